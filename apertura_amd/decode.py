@@ -1,0 +1,133 @@
+"""Torch-tensor front end of esda_decode (one decode step: append + attend + merge).
+
+Mirrors the reference's decode call pair -- ESKVCache::update (ESKVCache.mm:64-109)
+followed by the SDPA call of ESAttention.mm:188 -- as one call.  Tensors are torch
+CUDA (HIP) tensors; torch is only the allocator and stream provider here.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from ._lib import DecodeArgs, DecodeDesc, check, lib
+
+STAGE_ATTEND = 1
+STAGE_MERGE = 2
+
+
+@dataclass
+class DecodeStep:
+    """Shapes and cache mode of a decode step (esda_decode_desc).
+
+    Caches are [B, Hkv, cap, D] bf16 views (any sequence / head strides, rows dense).
+    ``ring`` selects slot = pos mod cap with a sliding ``window``; otherwise row =
+    pos - row_base.  ``kv_shared`` means V aliases K (attention_k_eq_v)."""
+
+    batch: int
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    cap: int
+    window: int = 0
+    ring: bool = False
+    kv_shared: bool = False
+    scale: float = 1.0
+    max_visible: int = 0
+    split_rows: int = 0
+    seq_stride: int | None = None
+    head_stride: int | None = None
+
+    def desc(self) -> DecodeDesc:
+        hs = self.head_stride if self.head_stride is not None else self.cap * self.head_dim
+        ss = self.seq_stride if self.seq_stride is not None else self.num_kv_heads * hs
+        return DecodeDesc(self.batch, self.num_q_heads, self.num_kv_heads, self.head_dim,
+                          self.cap, self.window, 1 if self.ring else 0, 1 if self.kv_shared else 0,
+                          ss, hs, self.max_visible, self.split_rows, self.scale)
+
+    @classmethod
+    def for_cache(cls, cache: torch.Tensor, num_q_heads: int, **kw) -> "DecodeStep":
+        B, Hkv, cap, D = cache.shape
+        if cache.stride(3) != 1 or cache.stride(2) != D:
+            raise ValueError("cache rows must be dense ([B, Hkv, cap, D] with unit inner strides)")
+        return cls(batch=B, num_q_heads=num_q_heads, num_kv_heads=Hkv, head_dim=D, cap=cap,
+                   seq_stride=cache.stride(0), head_stride=cache.stride(1), **kw)
+
+
+def workspace_bytes(step: DecodeStep) -> int:
+    n = ctypes.c_size_t(0)
+    d = step.desc()
+    check(lib().esda_decode_workspace_size(ctypes.byref(d), ctypes.byref(n)))
+    return int(n.value)
+
+
+def new_workspace(step: DecodeStep, device) -> torch.Tensor:
+    """Workspace for ``step`` with its status word zeroed (the only part that needs
+    initialising; the kernels keep it at zero unless a sequence is out of range)."""
+    return torch.zeros(workspace_bytes(step), dtype=torch.uint8, device=device)
+
+
+def _dev_ptr(t: torch.Tensor | None, dtype=None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("esda tensors must live in GPU memory")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"expected {dtype}, got {t.dtype}")
+    return t.data_ptr()
+
+
+def _stream_ptr(stream) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def decode_step(step: DecodeStep, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor | None,
+                k_cache: torch.Tensor, v_cache: torch.Tensor | None, pos: torch.Tensor,
+                row_base: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None, stream=None,
+                stages: int = STAGE_ATTEND | STAGE_MERGE) -> torch.Tensor:
+    """Append the new rows and attend; returns out [B, Hq, D] bf16."""
+    bf = torch.bfloat16
+    if q.shape != (step.batch, step.num_q_heads, step.head_dim) or not q.is_contiguous():
+        raise ValueError(f"q must be contiguous [B, Hq, D], got {tuple(q.shape)}")
+    if k_new.shape != (step.batch, step.num_kv_heads, step.head_dim) or not k_new.is_contiguous():
+        raise ValueError("k_new must be contiguous [B, Hkv, D]")
+    if v_new is not None and (v_new.shape != k_new.shape or not v_new.is_contiguous()):
+        raise ValueError("v_new must be contiguous [B, Hkv, D]")
+    if pos.dtype != torch.int32 or pos.shape != (step.batch,):
+        raise ValueError("pos must be int32 [B]")
+    if out is None:
+        out = torch.empty_like(q)
+    if workspace is None:
+        workspace = new_workspace(step, q.device)
+    vc = k_cache if (v_cache is None or step.kv_shared) else v_cache
+    args = DecodeArgs(_dev_ptr(q, bf), _dev_ptr(k_new, bf),
+                      _dev_ptr(v_new, bf) if (v_new is not None and not step.kv_shared) else None,
+                      _dev_ptr(k_cache, bf), _dev_ptr(vc, bf), _dev_ptr(pos),
+                      _dev_ptr(row_base), _dev_ptr(out, bf), _dev_ptr(workspace),
+                      workspace.numel() * workspace.element_size())
+    d = step.desc()
+    check(lib().esda_decode_stages(ctypes.byref(d), ctypes.byref(args), stages, _stream_ptr(stream)))
+    return out
+
+
+def decode_status(step: DecodeStep, workspace: torch.Tensor, stream=None) -> int:
+    """Number of sequences the kernels skipped (position outside the cache) since the
+    last call; clears the counter."""
+    n = ctypes.c_int32(0)
+    d = step.desc()
+    check(lib().esda_decode_status(ctypes.byref(d), _dev_ptr(workspace), ctypes.byref(n),
+                                   _stream_ptr(stream)))
+    return int(n.value)
+
+
+def kv_append(cache: torch.Tensor, src: torch.Tensor, row0: torch.Tensor, stream=None) -> None:
+    """Copy src [B, Hkv, n, D] into cache rows row0[b] .. row0[b]+n-1 (slice_update)."""
+    B, Hkv, cap, D = cache.shape
+    if src.shape[:2] != (B, Hkv) or src.shape[3] != D or not src.is_contiguous():
+        raise ValueError("src must be contiguous [B, Hkv, n, D]")
+    check(lib().esda_kv_append(_dev_ptr(cache, torch.bfloat16), cache.stride(0), cache.stride(1),
+                               B, Hkv, D, cap, _dev_ptr(src, torch.bfloat16), src.shape[2],
+                               _dev_ptr(row0), _stream_ptr(stream)))

@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Decode-attention bench on one MI355X (gfx950).
+
+Workload (default, BASELINE config 4 -- the north-star case): Gemma-4-31B global-layer
+decode step, B=1, Hq=32, Hkv=4 (GQA 8), head_dim 512, attention_k_eq_v (one K=V
+buffer), 131072 visible rows (rows 0..131070 cached + the new token appended at
+131071), scale 1/sqrt(512).  One step = esda_decode: fused append + split-K attention
++ merge, with every input already resident in HBM.
+
+Printed: ONE JSON line.  value = algorithmic HBM bytes per step / step time (GB/s);
+algorithmic bytes = visible rows x row bytes (K only under k_eq_v) + q read + out
+write + new-row read and write.  `roofline` prices the dominant kernel (the split-K
+attend kernel, timed alone with HIP events on the launch stream); `cpu_baseline` times
+the CPU oracle's reference-rounding restatement on the same inputs.
+
+  python bench.py [--steps K] [--warmup W] [--workload c4|c2|c1|c3] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+PEAK_HBM_GBS = 8000.0
+
+
+def _die_multi_gpu(n: int) -> None:
+    print(json.dumps({"error": f"--gpus {n}: this build measures one GPU only; the decode "
+                      "path shards by sequence / kv head with no exchange (see DESIGN.md)"}))
+    sys.exit(2)
+
+
+WORKLOADS = {
+    # name: (B, Hq, Hkv, D, cap, window, ring, shared, pos_fn, scale)
+    "c1": dict(B=1, Hq=16, Hkv=8, D=256, cap=1024, window=1024, ring=False, shared=False,
+               pos=lambda rng, B: [1023], scale=1 / 16),
+    "c2": dict(B=1, Hq=32, Hkv=4, D=512, cap=8448, window=0, ring=False, shared=True,
+               pos=lambda rng, B: [8192], scale=512 ** -0.5),
+    "c3": dict(B=8, Hq=32, Hkv=16, D=256, cap=1024, window=1024, ring=True, shared=False,
+               pos=lambda rng, B: [int(x) for x in rng.integers(2048, 32769, size=B)], scale=1 / 16),
+    "c4": dict(B=1, Hq=32, Hkv=4, D=512, cap=131072, window=0, ring=False, shared=True,
+               pos=lambda rng, B: [131071], scale=512 ** -0.5),
+}
+
+
+def visible_rows(w, pos):
+    out = []
+    for p in pos:
+        lo = max(0, p - w["window"] + 1) if w["window"] else 0
+        out.append(p - lo + 1)
+    return out
+
+
+def algorithmic_bytes(w, pos) -> int:
+    row = w["D"] * 2 * (1 if w["shared"] else 2)
+    kv = sum(visible_rows(w, pos)) * w["Hkv"] * row
+    q_o = 2 * w["B"] * w["Hq"] * w["D"] * 2
+    append = 2 * w["B"] * w["Hkv"] * row  # new-row read + cache write
+    return kv + q_o + append
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c4", choices=sorted(WORKLOADS))
+    ap.add_argument("--split-rows", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        _die_multi_gpu(max(args.gpus, int(os.environ.get("WORLD_SIZE", "1"))))
+
+    import numpy as np
+    import torch
+
+    from apertura_amd.decode import DecodeStep, STAGE_ATTEND, decode_step, new_workspace
+
+    w = WORKLOADS[args.workload]
+    rng = np.random.default_rng(1234)
+    pos = w["pos"](rng, w["B"])
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+
+    def rms_bf16(shape):
+        x = torch.randn(shape, device=dev, dtype=torch.float32, generator=gen)
+        x = x * torch.rsqrt(x.square().mean(-1, keepdim=True) + 1e-6)
+        return x.to(torch.bfloat16)
+
+    B, Hq, Hkv, D, cap = w["B"], w["Hq"], w["Hkv"], w["D"], w["cap"]
+    q = rms_bf16((B, Hq, D))
+    k_cache = rms_bf16((B, Hkv, cap, D))
+    v_cache = k_cache if w["shared"] else rms_bf16((B, Hkv, cap, D))
+    k_new = rms_bf16((B, Hkv, D))
+    v_new = None if w["shared"] else rms_bf16((B, Hkv, D))
+    pos_d = torch.tensor(pos, dtype=torch.int32, device=dev)
+    step = DecodeStep.for_cache(k_cache, Hq, window=w["window"], ring=w["ring"],
+                                kv_shared=w["shared"], scale=w["scale"], split_rows=args.split_rows)
+    ws = new_workspace(step, dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+
+    def run(stages=3):
+        decode_step(step, q, k_new, v_new, k_cache, v_cache, pos_d, out=out, workspace=ws,
+                    stream=stream, stages=stages)
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+
+    # Whole step (append + attend + merge), K steps between two events.
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+
+    # Dominant kernel alone (split-K attend with the fused append), same stream.
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a0.record(stream)
+    for _ in range(args.steps):
+        run(STAGE_ATTEND)
+    a1.record(stream)
+    torch.cuda.synchronize()
+    ms_attend = a0.elapsed_time(a1) / args.steps
+
+    nbytes = algorithmic_bytes(w, pos)
+    gbs = nbytes / (ms_step * 1e-3) / 1e9
+    gbs_attend = nbytes / (ms_attend * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(w, pos, q, k_cache, v_cache, k_new, v_new, args.cpu_threads)
+
+    line = {
+        "metric": "decode-attn HBM GB/s (and us/step) at Gemma-4-31B shapes, 1 GPU",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "us_per_step": round(ms_step * 1e3, 3),
+        "pct_of_hbm_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) rows, unit-RMS, bf16)",
+        "config": {
+            "workload": {"c4": "C4 global k_eq_v decode, L=131072", "c2": "C2 global k_eq_v decode, L=8193",
+                         "c1": "C1 local decode, L=1024", "c3": "C3 local ring decode, B=8"}[args.workload],
+            "batch": B, "num_q_heads": Hq, "num_kv_heads": Hkv, "head_dim": D,
+            "visible_rows": visible_rows(w, pos), "kv_shared": w["shared"],
+            "window": w["window"], "ring": w["ring"], "split_rows": step.split_rows or "auto",
+            "algorithmic_bytes_per_step": nbytes,
+        },
+        "roofline": {
+            "bound": "hbm", "kernel": "attend_kernel<D,kv_shared> (split-K + fused append)",
+            "achieved": round(gbs_attend, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs_attend / PEAK_HBM_GBS, 4), "traffic": None,
+            "kernel_us": round(ms_attend * 1e3, 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline(w, pos, q, k_cache, v_cache, k_new, v_new, threads: int):
+    """CPU oracle (reference-rounding restatement of ESAttention.mm:136-165) on the same
+    inputs, after the same append; timed for ~10-30 s of CPU work over repeats."""
+    import numpy as np
+    import torch
+
+    root = os.path.dirname(os.path.abspath(__file__))
+    sys.path.insert(0, root)
+    from oracle import oracle as orc
+
+    def host(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+
+    B, Hq, Hkv, D, cap = w["B"], w["Hq"], w["Hkv"], w["D"], w["cap"]
+    step = orc.Step(B=B, Hq=Hq, Hkv=Hkv, D=D, cap=cap, window=w["window"], ring=w["ring"],
+                    scale=w["scale"])
+    qh = host(q).reshape(B, Hq, D)
+    kc = host(k_cache)
+    vc = kc if w["shared"] else host(v_cache)
+    kn = host(k_new).reshape(B, Hkv, D)
+    vn = kn if w["shared"] else host(v_new).reshape(B, Hkv, D)
+    orc.append(step, kc, None if w["shared"] else vc, kn, None if w["shared"] else vn, pos)
+    reps, t_total = 0, 0.0
+    while t_total < 10.0 and reps < 50:
+        t0 = time.perf_counter()
+        orc.decode_refround(step, qh, kc, vc, pos, threads=threads)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    sec = t_total / reps
+    nbytes = algorithmic_bytes(w, pos)
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "us_per_step": round(sec * 1e6, 1),
+            "cores": threads, "kind": "port",
+            "sample": f"full workload step x{reps} repeats ({t_total:.1f} s), reference-rounding "
+                      f"oracle (MLX CPU path unavailable offline); host {os.cpu_count()} cpus visible"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

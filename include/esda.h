@@ -1,0 +1,119 @@
+/*
+ * esda.h -- C ABI of the MI355X (gfx950) decode-attention library libesda.so.
+ *
+ * One decode step of Gemma-4 attention: append the new token's K/V row into the
+ * cache and attend the single query over the visible rows, split-K across the
+ * GPU, merged in fp32.  Plain pointers and sizes only; every device pointer is
+ * caller-owned; every call takes an explicit HIP stream (NULL = default stream).
+ * Functions return ESDA_OK or an error code; esda_last_error() gives the message
+ * of the calling thread's last failure.
+ *
+ * Which reference interface each entry point replaces (paths in the Apertura tree):
+ *   esda_decode            ESKVCache::update (ESKVCache.mm:64-109, prealloc append)
+ *                          followed by mx::fast::scaled_dot_product_attention at
+ *                          ESAttention.mm:188 (decode, seq == 1); the additive mask of
+ *                          ESGemma4TextModel.mm:68-83 + alignMask (ESAttention.mm:17-22)
+ *                          becomes in-kernel index math from (pos, window, cap).
+ *   esda_kv_append         the slice_update append alone (ESKVCache.mm:97-98,
+ *                          ESKVCache.mm:498 for updateRaw), for multi-row appends.
+ *   esda_*_workspace_size  sizes the split partials the reference kept in MLX
+ *                          temporaries (ESDecodeAttn.mm:444-452).
+ */
+#ifndef APERTURA_ESDA_H
+#define APERTURA_ESDA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ESDA_OK 0
+#define ESDA_ERR_INVALID_ARGUMENT 1 /* the reference throws std::invalid_argument */
+#define ESDA_ERR_RUNTIME 2          /* the reference throws std::runtime_error     */
+#define ESDA_ERR_HIP 3              /* a HIP runtime call failed                   */
+#define ESDA_ERR_WORKSPACE 4        /* workspace missing or too small              */
+#define ESDA_ERR_DEVICE 5           /* no gfx950 device / library not usable       */
+
+/* Shape and cache mode of one decode step.
+ *
+ * Cache element (b, kvh, row, d) lives at cache[b*seq_stride + kvh*head_stride +
+ * row*head_dim + d] (bf16), the reference's [kvHeads, capacity, headDim] slot per
+ * sequence (ESKVCache.h:183-192) with a leading sequence index.
+ *
+ * pos[b] is the absolute position of the new token of sequence b.
+ *   ring == 0 (linear rows): the row of absolute position p is p - row_base[b]
+ *             (row_base NULL = 0; after a compaction row 0 holds position row_base).
+ *   ring == 1 (ring buffer): the row of absolute position p is p mod cap;
+ *             requires 0 < window <= cap.
+ * Visible positions (ESGemma4TextModel.mm:68-83): kj <= pos and, when window > 0,
+ * kj > pos - window; in linear mode also kj >= row_base[b].
+ * GQA: query head h reads kv head h / (num_q_heads / num_kv_heads) (ESOps.h:64-68). */
+typedef struct esda_decode_desc {
+    int32_t batch;        /* B                                              */
+    int32_t num_q_heads;  /* Hq                                             */
+    int32_t num_kv_heads; /* Hkv; Hq / Hkv <= 16                            */
+    int32_t head_dim;     /* 128, 256 or 512                                */
+    int32_t cap;          /* rows per (sequence, kv head)                   */
+    int32_t window;       /* 0 = full causal, > 0 = sliding window          */
+    int32_t ring;         /* 0 = linear rows, 1 = ring buffer               */
+    int32_t kv_shared;    /* 1 = V aliases K (attention_k_eq_v, one buffer) */
+    int64_t seq_stride;   /* elements; >= num_kv_heads * head_stride        */
+    int64_t head_stride;  /* elements; >= cap * head_dim, multiple of 8     */
+    int32_t max_visible;  /* upper bound on visible rows (0 = from cap/window) */
+    int32_t split_rows;   /* rows per split (0 = automatic; multiple of 64) */
+    float scale;          /* softmax scale (the model uses 1.0)             */
+} esda_decode_desc;
+
+typedef struct esda_decode_args {
+    const void *q;          /* [B, Hq, D] bf16, 16-byte aligned              */
+    const void *k_new;      /* [B, Hkv, D] bf16                              */
+    const void *v_new;      /* [B, Hkv, D] bf16; ignored when kv_shared      */
+    void *k_cache;          /* bf16 cache (see layout above)                 */
+    void *v_cache;          /* bf16 cache; must equal k_cache when kv_shared */
+    const int32_t *pos;     /* [B] int32, device memory                      */
+    const int32_t *row_base;/* [B] int32, device memory, or NULL             */
+    void *out;              /* [B, Hq, D] bf16                               */
+    void *workspace;        /* device scratch of esda_decode_workspace_size;
+                               zero its first 256 bytes once before first use */
+    size_t workspace_bytes;
+} esda_decode_args;
+
+/* Bytes of device workspace esda_decode needs for this description. */
+int esda_decode_workspace_size(const esda_decode_desc *desc, size_t *bytes);
+
+/* Append + attend + merge for one decode step (two kernel launches on `stream`).
+ * Replaces ESKVCache::update + SDPA at ESAttention.mm:105 and :188. */
+int esda_decode(const esda_decode_desc *desc, const esda_decode_args *args, void *stream);
+
+/* Stage selector for esda_decode_stages (a profiling aid: the bench times the
+ * split kernel alone).  esda_decode == both stages. */
+#define ESDA_STAGE_ATTEND 1 /* fused append + split-K partials */
+#define ESDA_STAGE_MERGE 2  /* cross-split fp32 merge -> bf16 out */
+int esda_decode_stages(const esda_decode_desc *desc, const esda_decode_args *args, int stages,
+                       void *stream);
+
+/* Reads (synchronously) and clears the device status word the kernels set when a
+ * sequence's position is outside its cache (such a sequence is skipped: nothing is
+ * written for it).  *bad_sequences receives the count flagged since the last call. */
+int esda_decode_status(const esda_decode_desc *desc, void *workspace, int32_t *bad_sequences,
+                       void *stream);
+
+/* Copy n_new rows per (sequence, kv head) into a linear cache at rows
+ * row0[b] .. row0[b]+n_new-1: the reference's slice_update append
+ * (ESKVCache.mm:97-98).  src: [B, Hkv, n_new, D] bf16. */
+int esda_kv_append(void *cache, int64_t seq_stride, int64_t head_stride, int32_t batch,
+                   int32_t num_kv_heads, int32_t head_dim, int32_t cap, const void *src,
+                   int32_t n_new, const int32_t *row0, void *stream);
+
+/* Message of the calling thread's last error ("" if none). */
+const char *esda_last_error(void);
+
+/* Library version (major*10000 + minor*100 + patch). */
+int esda_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

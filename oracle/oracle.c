@@ -1,0 +1,427 @@
+/*
+ * oracle.c -- CPU restatement of Apertura's decode-attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): loaded by tests/, smoke() and the
+ * cpu_baseline leg of bench.py; never by the product library.
+ *
+ * Parity status of each function is recorded in oracle.h and pinned by
+ * tests/test_oracle.py.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+static int32_t g_fault = 0;
+void orc_set_fault(int32_t fault) { g_fault = fault; }
+
+/* ------------------------------------------------------------------ bf16 */
+
+uint16_t orc_f32_to_bf16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu))
+        return (uint16_t) ((u >> 16) | 0x0040u); /* quiet NaN */
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7fffu + lsb; /* round to nearest, ties to even */
+    return (uint16_t) (u >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t h) {
+    uint32_t u = ((uint32_t) h) << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+void orc_f32_to_bf16_n(const float *x, uint16_t *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_f32_to_bf16(x[i]);
+}
+
+void orc_bf16_to_f32_n(const uint16_t *x, float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_bf16_to_f32(x[i]);
+}
+
+/* ------------------------------------------------------- visibility rule */
+
+static int desc_ok(const orc_desc *d) {
+    if (!d || d->B <= 0 || d->Hq <= 0 || d->Hkv <= 0 || d->D <= 0 || d->cap <= 0) return 0;
+    if (d->Hq % d->Hkv) return 0;
+    if (d->window < 0) return 0;
+    if (d->ring && (d->window <= 0 || d->window > d->cap)) return 0;
+    if (d->head_stride < (int64_t) d->cap * d->D) return 0;
+    if (d->seq_stride < (int64_t) d->Hkv * d->head_stride) return 0;
+    return 1;
+}
+
+/* Row holding absolute position p (ESKVCache.mm:97: the new row lands at row len;
+ * ring mode: slot p mod cap). */
+static int32_t row_of(const orc_desc *d, int32_t p, int32_t row_base) {
+    return d->ring ? (p % d->cap) : (p - row_base);
+}
+
+/* Key kj is visible to query qAbs iff kj <= qAbs and, for sliding layers,
+ * kj > qAbs - window (ESGemma4TextModel.mm:68-83).  Eviction keeps exactly those
+ * rows (ESKVCache.mm:104), so the visible set is the contiguous absolute range
+ * [lo, pos]. */
+int32_t orc_visible(const orc_desc *d, int32_t pos, int32_t row_base, int32_t *rows_out) {
+    if (!desc_ok(d) || pos < 0) return -1;
+    int32_t lo = 0;
+    if (d->window > 0) {
+        lo = pos - d->window + 1;
+        if (g_fault == 2) lo = pos - d->window; /* planted off-by-one */
+        if (lo < 0) lo = 0;
+    }
+    if (!d->ring) {
+        if (lo < row_base) lo = row_base;
+        if (pos - row_base >= d->cap) return -1;
+    } else if (d->window == 0 && pos >= d->cap) {
+        return -1;
+    }
+    int32_t n = 0;
+    for (int32_t p = lo; p <= pos; ++p) rows_out[n++] = row_of(d, p, row_base);
+    return n;
+}
+
+/* ---------------------------------------------------------------- append */
+
+int32_t orc_append(const orc_desc *d, uint16_t *k_cache, uint16_t *v_cache,
+                   const uint16_t *k_new, const uint16_t *v_new,
+                   const int32_t *pos, const int32_t *row_base) {
+    if (!desc_ok(d)) return -1;
+    if (g_fault == 4) return 0; /* planted: append dropped */
+    for (int32_t b = 0; b < d->B; ++b) {
+        int32_t rb = row_base ? row_base[b] : 0;
+        int32_t r = row_of(d, pos[b], rb);
+        if (r < 0 || r >= d->cap) return -1;
+        for (int32_t h = 0; h < d->Hkv; ++h) {
+            size_t dst = (size_t) b * d->seq_stride + (size_t) h * d->head_stride + (size_t) r * d->D;
+            size_t src = ((size_t) b * d->Hkv + h) * d->D;
+            memcpy(k_cache + dst, k_new + src, (size_t) d->D * 2);
+            if (v_cache != k_cache && v_new) memcpy(v_cache + dst, v_new + src, (size_t) d->D * 2);
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------ thread fan-out */
+
+typedef struct {
+    void (*fn)(void *ctx, int64_t item);
+    void *ctx;
+    int64_t n_items;
+    int64_t next;
+    pthread_mutex_t mu;
+} pool_t;
+
+static void *pool_worker(void *arg) {
+    pool_t *p = (pool_t *) arg;
+    for (;;) {
+        pthread_mutex_lock(&p->mu);
+        int64_t it = p->next++;
+        pthread_mutex_unlock(&p->mu);
+        if (it >= p->n_items) break;
+        p->fn(p->ctx, it);
+    }
+    return NULL;
+}
+
+static void run_items(void (*fn)(void *, int64_t), void *ctx, int64_t n_items, int32_t nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    if ((int64_t) nthreads > n_items) nthreads = (int32_t) (n_items > 0 ? n_items : 1);
+    pool_t p;
+    p.fn = fn; p.ctx = ctx; p.n_items = n_items; p.next = 0;
+    pthread_mutex_init(&p.mu, NULL);
+    if (nthreads == 1) {
+        pool_worker(&p);
+    } else {
+        pthread_t th[256];
+        for (int32_t i = 0; i < nthreads; ++i) pthread_create(&th[i], NULL, pool_worker, &p);
+        for (int32_t i = 0; i < nthreads; ++i) pthread_join(th[i], NULL);
+    }
+    pthread_mutex_destroy(&p.mu);
+}
+
+/* GQA: query head h reads kv head h / (Hq/Hkv) -- kv-major contiguous groups
+ * (ESOps.h:64-68, pinned by ESPrimitivesTests.mm:118-128). */
+static int32_t kv_of(const orc_desc *d, int32_t h) {
+    int32_t g = d->Hq / d->Hkv;
+    if (g_fault == 1) return h % d->Hkv; /* planted: interleaved mapping */
+    return h / g;
+}
+
+static float eff_scale(const orc_desc *d) { return g_fault == 3 ? 1.0f : d->scale; }
+
+typedef struct {
+    const orc_desc *d;
+    const uint16_t *q, *k, *v;
+    const int32_t *pos, *row_base;
+    void *out;
+    int32_t nsplit;
+    int32_t status;
+} job_t;
+
+static int32_t *alloc_rows(const orc_desc *d) {
+    return (int32_t *) malloc(sizeof(int32_t) * ((size_t) d->cap + 1));
+}
+
+/* ------------------------------------------------------------ fp64 mode */
+
+static void item_f64(void *ctx, int64_t it) {
+    job_t *j = (job_t *) ctx;
+    const orc_desc *d = j->d;
+    const int32_t b = (int32_t) (it / d->Hq), h = (int32_t) (it % d->Hq), D = d->D;
+    const int32_t kvh = kv_of(d, h);
+    int32_t *rows = alloc_rows(d);
+    double *out = (double *) j->out + ((size_t) b * d->Hq + h) * D;
+    int32_t n = orc_visible(d, j->pos[b], j->row_base ? j->row_base[b] : 0, rows);
+    if (n <= 0) { j->status = -1; free(rows); return; }
+    double *qd = (double *) malloc(sizeof(double) * D);
+    double *s = (double *) malloc(sizeof(double) * n);
+    const uint16_t *qh = j->q + ((size_t) b * d->Hq + h) * D;
+    for (int32_t i = 0; i < D; ++i) qd[i] = orc_bf16_to_f32(qh[i]);
+    const size_t base = (size_t) b * d->seq_stride + (size_t) kvh * d->head_stride;
+    double mx = -INFINITY;
+    for (int32_t t = 0; t < n; ++t) {
+        const uint16_t *kr = j->k + base + (size_t) rows[t] * D;
+        double acc = 0.0;
+        for (int32_t i = 0; i < D; ++i) acc += qd[i] * (double) orc_bf16_to_f32(kr[i]);
+        s[t] = acc * (double) eff_scale(d);
+        if (s[t] > mx) mx = s[t];
+    }
+    double den = 0.0;
+    for (int32_t t = 0; t < n; ++t) { s[t] = exp(s[t] - mx); den += s[t]; }
+    for (int32_t i = 0; i < D; ++i) out[i] = 0.0;
+    for (int32_t t = 0; t < n; ++t) {
+        const uint16_t *vr = j->v + base + (size_t) rows[t] * D;
+        const double w = s[t] / den;
+        for (int32_t i = 0; i < D; ++i) out[i] += w * (double) orc_bf16_to_f32(vr[i]);
+    }
+    free(qd); free(s); free(rows);
+}
+
+int32_t orc_decode_f64(const orc_desc *d, const uint16_t *q, const uint16_t *k_cache,
+                       const uint16_t *v_cache, const int32_t *pos, const int32_t *row_base,
+                       double *out, int32_t nthreads) {
+    if (!desc_ok(d)) return -1;
+    job_t j = {d, q, k_cache, v_cache, pos, row_base, out, 0, 0};
+    run_items(item_f64, &j, (int64_t) d->B * d->Hq, nthreads);
+    return j.status;
+}
+
+/* ------------------------------------------------- reference-rounding mode */
+
+static float bf(float x) { return orc_bf16_to_f32(orc_f32_to_bf16(x)); }
+
+/* ESAttention.mm:136-165, per query head:
+ *   scores = bf16(q . K^T)                   (:153, bf16 matmul, f32 accumulation)
+ *   scores = bf16(scores * bf16(scaling))    (:154, only when scaling != 1)
+ *   sf = f32(scores) + mask                  (:156-157; masked keys contribute 0)
+ *   w = bf16(softmax_precise(sf))            (:158-159)
+ *   out = bf16(w . V)                        (:161, f32 accumulation)            */
+static void item_refround(void *ctx, int64_t it) {
+    job_t *j = (job_t *) ctx;
+    const orc_desc *d = j->d;
+    const int32_t b = (int32_t) (it / d->Hq), h = (int32_t) (it % d->Hq), D = d->D;
+    const int32_t kvh = kv_of(d, h);
+    int32_t *rows = alloc_rows(d);
+    uint16_t *out = (uint16_t *) j->out + ((size_t) b * d->Hq + h) * D;
+    int32_t n = orc_visible(d, j->pos[b], j->row_base ? j->row_base[b] : 0, rows);
+    if (n <= 0) { j->status = -1; free(rows); return; }
+    float *qf = (float *) malloc(sizeof(float) * D);
+    float *s = (float *) malloc(sizeof(float) * n);
+    float *acc = (float *) malloc(sizeof(float) * D);
+    const uint16_t *qh = j->q + ((size_t) b * d->Hq + h) * D;
+    for (int32_t i = 0; i < D; ++i) qf[i] = orc_bf16_to_f32(qh[i]);
+    const size_t base = (size_t) b * d->seq_stride + (size_t) kvh * d->head_stride;
+    const float sc = eff_scale(d);
+    const float scb = bf(sc);
+    float mx = -INFINITY;
+    for (int32_t t = 0; t < n; ++t) {
+        const uint16_t *kr = j->k + base + (size_t) rows[t] * D;
+        float a = 0.0f;
+        for (int32_t i = 0; i < D; ++i) a += qf[i] * orc_bf16_to_f32(kr[i]);
+        float sv = bf(a);
+        if (sc != 1.0f) sv = bf(sv * scb);
+        s[t] = sv;
+        if (sv > mx) mx = sv;
+    }
+    float den = 0.0f;
+    for (int32_t t = 0; t < n; ++t) { s[t] = expf(s[t] - mx); den += s[t]; }
+    for (int32_t t = 0; t < n; ++t) s[t] = bf(s[t] / den);
+    for (int32_t i = 0; i < D; ++i) acc[i] = 0.0f;
+    for (int32_t t = 0; t < n; ++t) {
+        const uint16_t *vr = j->v + base + (size_t) rows[t] * D;
+        const float w = s[t];
+        for (int32_t i = 0; i < D; ++i) acc[i] += w * orc_bf16_to_f32(vr[i]);
+    }
+    for (int32_t i = 0; i < D; ++i) out[i] = orc_f32_to_bf16(acc[i]);
+    free(qf); free(s); free(acc); free(rows);
+}
+
+int32_t orc_decode_refround(const orc_desc *d, const uint16_t *q, const uint16_t *k_cache,
+                            const uint16_t *v_cache, const int32_t *pos,
+                            const int32_t *row_base, uint16_t *out, int32_t nthreads) {
+    if (!desc_ok(d)) return -1;
+    job_t j = {d, q, k_cache, v_cache, pos, row_base, out, 0, 0};
+    run_items(item_refround, &j, (int64_t) d->B * d->Hq, nthreads);
+    return j.status;
+}
+
+/* ----------------------------------------------------------- split-K mode */
+
+/* Online softmax per split as in ESDecodeAttn.mm:44-110 (m starts at -3e38, l at 0,
+ * acc = acc*corr + e*v), then the merge of ESDecodeAttn.mm:253-273:
+ *   mMax = max_s m_s;  w_s = exp(m_s - mMax);  O = sum_s acc_s w_s / sum_s l_s w_s. */
+static void item_splitk(void *ctx, int64_t it) {
+    job_t *j = (job_t *) ctx;
+    const orc_desc *d = j->d;
+    const int32_t b = (int32_t) (it / d->Hq), h = (int32_t) (it % d->Hq), D = d->D;
+    const int32_t kvh = kv_of(d, h), S = j->nsplit;
+    int32_t *rows = alloc_rows(d);
+    float *out = (float *) j->out + ((size_t) b * d->Hq + h) * D;
+    int32_t n = orc_visible(d, j->pos[b], j->row_base ? j->row_base[b] : 0, rows);
+    if (n <= 0 || S <= 0) { j->status = -1; free(rows); return; }
+    float *qf = (float *) malloc(sizeof(float) * D);
+    float *acc = (float *) malloc(sizeof(float) * (size_t) S * D);
+    float *ms = (float *) malloc(sizeof(float) * S);
+    float *ls = (float *) malloc(sizeof(float) * S);
+    const uint16_t *qh = j->q + ((size_t) b * d->Hq + h) * D;
+    for (int32_t i = 0; i < D; ++i) qf[i] = orc_bf16_to_f32(qh[i]);
+    const size_t base = (size_t) b * d->seq_stride + (size_t) kvh * d->head_stride;
+    const int32_t per = (n + S - 1) / S;
+    const float sc = eff_scale(d);
+    for (int32_t s = 0; s < S; ++s) {
+        float m = -3.0e38f, l = 0.0f;
+        float *a = acc + (size_t) s * D;
+        for (int32_t i = 0; i < D; ++i) a[i] = 0.0f;
+        const int32_t r0 = s * per, r1 = (r0 + per < n) ? r0 + per : n;
+        for (int32_t t = r0; t < r1; ++t) {
+            const uint16_t *kr = j->k + base + (size_t) rows[t] * D;
+            const uint16_t *vr = j->v + base + (size_t) rows[t] * D;
+            float dot = 0.0f;
+            for (int32_t i = 0; i < D; ++i) dot += qf[i] * orc_bf16_to_f32(kr[i]);
+            const float score = dot * sc;
+            const float mNew = score > m ? score : m;
+            const float corr = expf(m - mNew), e = expf(score - mNew);
+            l = l * corr + e;
+            for (int32_t i = 0; i < D; ++i) a[i] = a[i] * corr + e * orc_bf16_to_f32(vr[i]);
+            m = mNew;
+        }
+        ms[s] = m; ls[s] = l;
+    }
+    float mMax = -3.0e38f;
+    for (int32_t s = 0; s < S; ++s) if (ms[s] > mMax) mMax = ms[s];
+    float lTot = 0.0f;
+    for (int32_t s = 0; s < S; ++s) { ms[s] = expf(ms[s] - mMax); lTot += ls[s] * ms[s]; }
+    for (int32_t i = 0; i < D; ++i) {
+        float a = 0.0f;
+        for (int32_t s = 0; s < S; ++s) a += acc[(size_t) s * D + i] * ms[s];
+        out[i] = a / lTot;
+    }
+    free(qf); free(acc); free(ms); free(ls); free(rows);
+}
+
+int32_t orc_decode_splitk(const orc_desc *d, const uint16_t *q, const uint16_t *k_cache,
+                          const uint16_t *v_cache, const int32_t *pos, const int32_t *row_base,
+                          int32_t nsplit, float *out, int32_t nthreads) {
+    if (!desc_ok(d) || nsplit <= 0) return -1;
+    job_t j = {d, q, k_cache, v_cache, pos, row_base, out, nsplit, 0};
+    run_items(item_splitk, &j, (int64_t) d->B * d->Hq, nthreads);
+    return j.status;
+}
+
+/* ------------------------------------------------------ norms and rope */
+
+void orc_rope_inv_freq(int32_t head_dim, float theta, float partial, float *inv_freq) {
+    const int32_t half = head_dim / 2;
+    int32_t angles = (int32_t) ((double) partial * head_dim / 2.0);
+    if (angles > half) angles = half;
+    for (int32_t i = 0; i < half; ++i) inv_freq[i] = 0.0f;
+    for (int32_t i = 0; i < angles; ++i)
+        inv_freq[i] = (float) (1.0 / pow((double) theta, (double) (2 * i) / (double) head_dim));
+}
+
+void orc_rms_norm_rows(const uint16_t *x, const uint16_t *w, int64_t rows, int32_t n,
+                       float eps, uint16_t *y) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint16_t *xr = x + r * n;
+        float ss = 0.0f;
+        for (int32_t i = 0; i < n; ++i) { float v = orc_bf16_to_f32(xr[i]); ss += v * v; }
+        const float inv = 1.0f / sqrtf(ss / (float) n + eps);
+        for (int32_t i = 0; i < n; ++i) {
+            float v = orc_bf16_to_f32(xr[i]) * inv;
+            if (w) v *= orc_bf16_to_f32(w[i]);
+            y[r * n + i] = orc_f32_to_bf16(v);
+        }
+    }
+}
+
+/* ------------------------------------------------------------ raw-K mode */
+
+typedef struct {
+    const uint16_t *q, *raw, *kw;
+    const float *inv_freq;
+    int32_t Hkv, len, pitch;
+    float eps, scale;
+    double *out;
+} raw_job_t;
+
+/* One query head over all len rows of its kv head.  Reconstruction follows
+ * ESDecodeAttn.mm:51-93: rinv = rsqrt(mean(kraw^2) + eps); cos/sin of the fp32
+ * angle t*invfreq[f] rounded to bf16; K = bf16(rope(kraw*rinv*kw)) with pairs
+ * (d, d+256) for d < 64; V = kraw*rinv (ESDecodeAttn.mm:106).  Attention in fp64. */
+static void item_raw(void *ctx, int64_t it) {
+    raw_job_t *j = (raw_job_t *) ctx;
+    const int32_t h = (int32_t) it, kvh = h / 8, D = 512;
+    double qd[512], acc[512];
+    for (int32_t i = 0; i < D; ++i) { qd[i] = orc_bf16_to_f32(j->q[(size_t) h * D + i]); acc[i] = 0.0; }
+    double *s = (double *) malloc(sizeof(double) * j->len);
+    double *rv = (double *) malloc(sizeof(double) * j->len);
+    double mx = -INFINITY;
+    for (int32_t t = 0; t < j->len; ++t) {
+        const uint16_t *xr = j->raw + ((size_t) kvh * j->pitch + t) * D;
+        double ss = 0.0;
+        for (int32_t i = 0; i < D; ++i) { double v = orc_bf16_to_f32(xr[i]); ss += v * v; }
+        const float rinv = 1.0f / sqrtf((float) (ss / 512.0) + j->eps);
+        rv[t] = rinv;
+        double dot = 0.0;
+        for (int32_t dd = 0; dd < D; ++dd) {
+            const float kn = orc_bf16_to_f32(xr[dd]) * rinv * orc_bf16_to_f32(j->kw[dd]);
+            float kd = kn;
+            const int32_t f = dd & 255;
+            if (f < 64) {
+                const float a = (float) t * j->inv_freq[f];
+                const float c = bf(cosf(a)), sn = bf(sinf(a));
+                const int32_t pd = dd < 256 ? dd + 256 : dd - 256;
+                const float kn2 = orc_bf16_to_f32(xr[pd]) * rinv * orc_bf16_to_f32(j->kw[pd]);
+                const float sgn = (g_fault == 5) ? -1.0f : 1.0f;
+                kd = dd < 256 ? kn * c - sgn * kn2 * sn : kn * c + sgn * kn2 * sn;
+            }
+            dot += qd[dd] * (double) bf(kd);
+        }
+        s[t] = dot * (double) j->scale;
+        if (s[t] > mx) mx = s[t];
+    }
+    double den = 0.0;
+    for (int32_t t = 0; t < j->len; ++t) { s[t] = exp(s[t] - mx); den += s[t]; }
+    for (int32_t t = 0; t < j->len; ++t) {
+        const uint16_t *xr = j->raw + ((size_t) kvh * j->pitch + t) * D;
+        const double w = s[t] / den * rv[t];
+        for (int32_t i = 0; i < D; ++i) acc[i] += w * (double) orc_bf16_to_f32(xr[i]);
+    }
+    for (int32_t i = 0; i < D; ++i) j->out[(size_t) h * D + i] = acc[i];
+    free(s); free(rv);
+}
+
+int32_t orc_decode_raw_f64(const uint16_t *q, const uint16_t *raw, int32_t Hkv, int32_t len,
+                           int32_t pitch, const uint16_t *kw, float eps, const float *inv_freq,
+                           float scale, double *out, int32_t nthreads) {
+    if (Hkv <= 0 || len <= 0 || pitch < len) return -1;
+    raw_job_t j = {q, raw, kw, inv_freq, Hkv, len, pitch, eps, scale, out};
+    run_items(item_raw, &j, (int64_t) Hkv * 8, nthreads);
+    return 0;
+}

@@ -1,0 +1,227 @@
+"""ctypes front end of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY.  Loaded by tests/, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` as the checker / CPU baseline; the product
+package ``apertura_amd`` never imports it.
+
+Every array argument is a numpy array; bf16 tensors travel as ``np.uint16`` bit
+patterns.  See ``oracle.h`` for which reference file:line each function restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build() -> str:
+    """Compile liboracle.so from oracle.c (gcc, no GPU)."""
+    import subprocess
+
+    subprocess.run(["make", "-s", "-B", "-C", _HERE, "liboracle.so"], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class Desc(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32), ("Hq", ctypes.c_int32), ("Hkv", ctypes.c_int32),
+        ("D", ctypes.c_int32), ("cap", ctypes.c_int32), ("window", ctypes.c_int32),
+        ("ring", ctypes.c_int32), ("seq_stride", ctypes.c_int64),
+        ("head_stride", ctypes.c_int64), ("scale", ctypes.c_float),
+    ]
+
+
+_P = ctypes.c_void_p
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    i32 = ctypes.c_int32
+    L.orc_f32_to_bf16_n.argtypes = [_P, _P, ctypes.c_size_t]
+    L.orc_bf16_to_f32_n.argtypes = [_P, _P, ctypes.c_size_t]
+    L.orc_visible.argtypes = [ctypes.POINTER(Desc), i32, i32, _P]
+    L.orc_visible.restype = i32
+    L.orc_append.argtypes = [ctypes.POINTER(Desc), _P, _P, _P, _P, _P, _P]
+    L.orc_append.restype = i32
+    for name in ("orc_decode_f64", "orc_decode_refround"):
+        f = getattr(L, name)
+        f.argtypes = [ctypes.POINTER(Desc), _P, _P, _P, _P, _P, _P, i32]
+        f.restype = i32
+    L.orc_decode_splitk.argtypes = [ctypes.POINTER(Desc), _P, _P, _P, _P, _P, i32, _P, i32]
+    L.orc_decode_splitk.restype = i32
+    L.orc_rope_inv_freq.argtypes = [i32, ctypes.c_float, ctypes.c_float, _P]
+    L.orc_rms_norm_rows.argtypes = [_P, _P, ctypes.c_int64, i32, ctypes.c_float, _P]
+    L.orc_decode_raw_f64.argtypes = [_P, _P, i32, i32, i32, _P, ctypes.c_float, _P,
+                                     ctypes.c_float, _P, i32]
+    L.orc_decode_raw_f64.restype = i32
+    L.orc_set_fault.argtypes = [i32]
+
+
+def _ptr(a: np.ndarray | None) -> int | None:
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def _threads(n: int | None) -> int:
+    return int(n) if n else min(os.cpu_count() or 1, 16)
+
+
+# ----------------------------------------------------------------- bf16 helpers
+
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_f32_to_bf16_n(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def from_bf16(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().orc_bf16_to_f32_n(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+# ---------------------------------------------------------------- descriptions
+
+@dataclass
+class Step:
+    """One decode step's shapes and cache mode (mirrors orc_desc)."""
+
+    B: int
+    Hq: int
+    Hkv: int
+    D: int
+    cap: int
+    window: int = 0
+    ring: bool = False
+    scale: float = 1.0
+    seq_stride: int | None = None
+    head_stride: int | None = None
+
+    def desc(self) -> Desc:
+        hs = self.head_stride if self.head_stride is not None else self.cap * self.D
+        ss = self.seq_stride if self.seq_stride is not None else self.Hkv * hs
+        return Desc(self.B, self.Hq, self.Hkv, self.D, self.cap, self.window,
+                    1 if self.ring else 0, ss, hs, self.scale)
+
+    def cache_elems(self) -> int:
+        d = self.desc()
+        return int(d.seq_stride) * self.B
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int32))
+
+
+def visible(step: Step, pos: int, row_base: int = 0) -> np.ndarray:
+    rows = np.empty(step.cap + 1, dtype=np.int32)
+    d = step.desc()
+    n = lib().orc_visible(ctypes.byref(d), int(pos), int(row_base), _ptr(rows))
+    if n < 0:
+        raise ValueError("invalid step description")
+    return rows[:n].copy()
+
+
+def append(step: Step, k_cache: np.ndarray, v_cache: np.ndarray | None, k_new: np.ndarray,
+           v_new: np.ndarray | None, pos, row_base=None) -> None:
+    """In-place append of the new rows (v_cache None or identical = shared buffer)."""
+    d = step.desc()
+    vc = k_cache if v_cache is None else v_cache
+    rc = lib().orc_append(ctypes.byref(d), _ptr(k_cache), _ptr(vc), _ptr(k_new),
+                          _ptr(v_new), _ptr(_i32(pos)),
+                          None if row_base is None else _ptr(_i32(row_base)))
+    if rc != 0:
+        raise ValueError("orc_append rejected the description")
+
+
+def _decode(fn: str, step: Step, q, k_cache, v_cache, pos, row_base, out, threads, *extra):
+    d = step.desc()
+    vc = k_cache if v_cache is None else v_cache
+    pos_a = _i32(pos)
+    rb_a = None if row_base is None else _i32(row_base)
+    args = [ctypes.byref(d), _ptr(q), _ptr(k_cache), _ptr(vc), _ptr(pos_a), _ptr(rb_a)]
+    if fn == "orc_decode_splitk":
+        args.append(ctypes.c_int32(extra[0]))
+    args += [_ptr(out), _threads(threads)]
+    rc = getattr(lib(), fn)(*args)
+    if rc != 0:
+        raise ValueError(f"{fn} rejected the description")
+    return out
+
+
+def decode_f64(step: Step, q, k_cache, v_cache, pos, row_base=None, threads=None) -> np.ndarray:
+    out = np.empty((step.B, step.Hq, step.D), dtype=np.float64)
+    return _decode("orc_decode_f64", step, q, k_cache, v_cache, pos, row_base, out, threads)
+
+
+def decode_refround(step: Step, q, k_cache, v_cache, pos, row_base=None, threads=None) -> np.ndarray:
+    out = np.empty((step.B, step.Hq, step.D), dtype=np.uint16)
+    return _decode("orc_decode_refround", step, q, k_cache, v_cache, pos, row_base, out, threads)
+
+
+def decode_splitk(step: Step, q, k_cache, v_cache, pos, nsplit: int, row_base=None,
+                  threads=None) -> np.ndarray:
+    out = np.empty((step.B, step.Hq, step.D), dtype=np.float32)
+    return _decode("orc_decode_splitk", step, q, k_cache, v_cache, pos, row_base, out,
+                   threads, nsplit)
+
+
+def rope_inv_freq(head_dim: int, theta: float, partial: float) -> np.ndarray:
+    out = np.empty(head_dim // 2, dtype=np.float32)
+    lib().orc_rope_inv_freq(head_dim, ctypes.c_float(theta), ctypes.c_float(partial), _ptr(out))
+    return out
+
+
+def rms_norm_rows(x: np.ndarray, w: np.ndarray | None, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    n = x.shape[-1]
+    y = np.empty_like(x)
+    lib().orc_rms_norm_rows(_ptr(x), _ptr(w), x.size // n, n, ctypes.c_float(eps), _ptr(y))
+    return y
+
+
+def decode_raw_f64(q, raw, len_: int, kw, eps: float, inv_freq, scale: float = 1.0,
+                   threads=None) -> np.ndarray:
+    Hkv, pitch, D = raw.shape
+    assert D == 512 and q.shape == (Hkv * 8, 512)
+    out = np.empty((Hkv * 8, 512), dtype=np.float64)
+    inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    rc = lib().orc_decode_raw_f64(_ptr(q), _ptr(raw), Hkv, int(len_), pitch, _ptr(kw),
+                                  ctypes.c_float(eps), _ptr(inv), ctypes.c_float(scale),
+                                  _ptr(out), _threads(threads))
+    if rc != 0:
+        raise ValueError("orc_decode_raw_f64 rejected the shapes")
+    return out
+
+
+class planted_fault:
+    """Context manager that plants a mistake in the oracle (CPU self-tests only)."""
+
+    def __init__(self, code: int):
+        self.code = code
+
+    def __enter__(self):
+        lib().orc_set_fault(self.code)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_fault(0)
+        return False

@@ -1,0 +1,216 @@
+"""GPU parity of esda_decode (fused append + split-K attention + merge) against the
+CPU oracle, called through the C ABI (apertura_amd.decode -> libesda.so).
+
+Bar (north star): max-abs-err <= 2e-2 and mean-abs-err <= 2e-3 against the fp64
+oracle and against the reference-rounding oracle; the cache bytes after the append
+must equal the oracle's append bit for bit (every byte of the cache is compared).
+Configs C1-C4 run at their full sizes.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from _synth import make_step_inputs, plant_peaked_keys
+
+pytestmark = pytest.mark.gpu
+
+TOL_MAX, TOL_MEAN = 2e-2, 2e-3
+
+
+def _dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def _host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def run_case(name, *, B, Hq, Hkv, D, cap, pos, window=0, ring=False, shared=False, scale=None,
+             row_base=None, seed=0, split_rows=0, head_pad=0, seq_pad=0, peaks=0, bump=4.0,
+             refround=True, max_visible=0):
+    from apertura_amd.decode import DecodeStep, decode_status, decode_step, new_workspace
+    print(f"\n[case] {name}: B={B} Hq={Hq} Hkv={Hkv} D={D} cap={cap} window={window} "
+          f"ring={ring} shared={shared} pos={list(pos)[:4]} split_rows={split_rows}", flush=True)
+    scale = D ** -0.5 if scale is None else scale
+    hs = cap * D + head_pad
+    ss = Hkv * hs + seq_pad
+    step = orc.Step(B=B, Hq=Hq, Hkv=Hkv, D=D, cap=cap, window=window, ring=ring, scale=scale,
+                    seq_stride=ss, head_stride=hs)
+    q, kc, vc, kn, vn = make_step_inputs(step, seed, pos, shared_kv=shared)
+    if peaks:
+        plant_peaked_keys(step, q, kc, pos, peaks, bump, seed + 1, row_base)
+    dstep = DecodeStep(batch=B, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D, cap=cap,
+                       window=window, ring=ring, kv_shared=shared, scale=scale,
+                       seq_stride=ss, head_stride=hs, split_rows=split_rows,
+                       max_visible=max_visible)
+    q_d, kn_d = _dev(q), _dev(kn)
+    vn_d = None if shared else _dev(vn)
+    kc_d = _dev(kc)
+    vc_d = kc_d if shared else _dev(vc)
+    pos_d = torch.tensor(list(pos), dtype=torch.int32, device="cuda")
+    rb_d = None if row_base is None else torch.tensor(list(row_base), dtype=torch.int32, device="cuda")
+    ws = new_workspace(dstep, "cuda")
+    out = decode_step(dstep, q_d.view(B, Hq, D), kn_d.view(B, Hkv, D),
+                      None if vn_d is None else vn_d.view(B, Hkv, D), kc_d, vc_d, pos_d, rb_d,
+                      workspace=ws)
+    torch.cuda.synchronize()
+    assert decode_status(dstep, ws) == 0
+    # oracle: append, then attend
+    orc.append(step, kc, None if shared else vc, kn, None if shared else vn, list(pos), row_base)
+    got_k = _host(kc_d)
+    assert np.array_equal(got_k, kc), "K cache bytes differ after the append"
+    if not shared:
+        assert np.array_equal(_host(vc_d), vc), "V cache bytes differ after the append"
+    vref = kc if shared else vc
+    ref = orc.decode_f64(step, q, kc, vref, list(pos), row_base)
+    o = orc.from_bf16(_host(out)).reshape(B, Hq, D).astype(np.float64)
+    err = np.abs(o - ref)
+    print(f"[case] {name}: max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
+    assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN
+    if refround:
+        rr = orc.from_bf16(orc.decode_refround(step, q, kc, vref, list(pos), row_base)).astype(np.float64)
+        e2 = np.abs(o - rr.reshape(B, Hq, D))
+        assert e2.max() <= TOL_MAX and e2.mean() <= TOL_MEAN
+    return o, ref
+
+
+# ------------------------------------------------------------------ BASELINE configs
+
+def test_c1_local_b1_gqa2_d256():
+    run_case("C1", B=1, Hq=16, Hkv=8, D=256, cap=1024, window=1024, pos=[1023], scale=1 / 16)
+
+
+def test_c2_global_k_eq_v_d512_8192():
+    run_case("C2", B=1, Hq=32, Hkv=4, D=512, cap=8448, pos=[8192], shared=True)
+
+
+def test_c3_local_ring_b8():
+    rng = np.random.default_rng(33)
+    pos = [int(x) for x in rng.integers(2048, 32769, size=8)]
+    run_case("C3", B=8, Hq=32, Hkv=16, D=256, cap=1024, window=1024, ring=True, pos=pos,
+             scale=1 / 16, seed=3)
+
+
+def test_c4_global_k_eq_v_131072_peaked():
+    run_case("C4", B=1, Hq=32, Hkv=4, D=512, cap=131072, pos=[131071], shared=True, peaks=64,
+             bump=4.0, seed=4, refround=False)
+
+
+# ------------------------------------------------------------------ edge cases
+
+EDGE = [
+    dict(name="single_visible_row", B=1, Hq=8, Hkv=1, D=512, cap=64, pos=[0], shared=True),
+    dict(name="ragged_17_rows", B=1, Hq=8, Hkv=2, D=256, cap=64, pos=[16]),
+    dict(name="window_smaller_than_tile", B=2, Hq=4, Hkv=2, D=128, cap=300, window=5, pos=[299, 3]),
+    dict(name="ring_early_sequence", B=3, Hq=16, Hkv=8, D=256, cap=1024, window=1024, ring=True,
+         pos=[0, 5, 1500]),
+    dict(name="ring_window_below_cap", B=2, Hq=8, Hkv=4, D=256, cap=64, window=40, ring=True,
+         pos=[100, 39]),
+    dict(name="gqa1", B=2, Hq=4, Hkv=4, D=256, cap=200, pos=[199, 77]),
+    dict(name="gqa16", B=1, Hq=32, Hkv=2, D=512, cap=600, pos=[555], shared=True),
+    dict(name="gqa16_separate_v", B=1, Hq=16, Hkv=1, D=512, cap=333, pos=[332]),
+    dict(name="linear_row_base_window", B=2, Hq=16, Hkv=8, D=256, cap=1536, window=1024,
+         pos=[5000, 2000], row_base=[5000 - 1100, 1500]),
+    dict(name="padded_strides", B=3, Hq=8, Hkv=2, D=256, cap=100, pos=[99, 50, 7], head_pad=24,
+         seq_pad=40),
+    dict(name="mixed_lengths_global", B=4, Hq=32, Hkv=4, D=512, cap=3000, pos=[2999, 1, 1024, 777],
+         shared=True),
+    dict(name="split64", B=1, Hq=32, Hkv=4, D=512, cap=2000, pos=[1999], shared=True, split_rows=64),
+    dict(name="split_odd", B=1, Hq=16, Hkv=8, D=256, cap=1000, window=700, pos=[999], split_rows=208),
+    dict(name="max_visible_hint", B=2, Hq=32, Hkv=4, D=512, cap=4096, pos=[700, 900], shared=True,
+         max_visible=901),
+    dict(name="scale_one_in_model", B=1, Hq=32, Hkv=4, D=512, cap=512, pos=[511], shared=True,
+         scale=1.0),
+    dict(name="dominant_key", B=1, Hq=8, Hkv=1, D=256, cap=2048, pos=[2047], peaks=1, bump=30.0),
+]
+
+
+@pytest.mark.parametrize("case", EDGE, ids=[c["name"] for c in EDGE])
+def test_edge_case(case):
+    run_case(**case)
+
+
+def test_split_count_does_not_change_result_beyond_rounding():
+    a, ref = run_case("split_auto", B=1, Hq=32, Hkv=4, D=512, cap=4096, pos=[4095], shared=True, seed=9)
+    b, _ = run_case("split_64", B=1, Hq=32, Hkv=4, D=512, cap=4096, pos=[4095], shared=True, seed=9,
+                    split_rows=64)
+    assert np.abs(a - b).max() <= 2 * TOL_MAX / 4
+
+
+def test_repeated_launch_is_deterministic():
+    a, _ = run_case("det_a", B=2, Hq=16, Hkv=8, D=256, cap=1024, window=1024, ring=True,
+                    pos=[3000, 4000], seed=12, refround=False)
+    b, _ = run_case("det_b", B=2, Hq=16, Hkv=8, D=256, cap=1024, window=1024, ring=True,
+                    pos=[3000, 4000], seed=12, refround=False)
+    assert np.array_equal(a, b)
+
+
+def test_consecutive_steps_feed_the_cache():
+    """Three decode steps in a row on one cache: each step's append is visible to the next."""
+    from apertura_amd.decode import DecodeStep, decode_step, new_workspace
+    B, Hq, Hkv, D, cap, W = 2, 16, 8, 256, 64, 48
+    step = orc.Step(B=B, Hq=Hq, Hkv=Hkv, D=D, cap=cap, window=W, ring=True, scale=1 / 16)
+    q, kc, vc, _, _ = make_step_inputs(step, 21, [0, 0])
+    dstep = DecodeStep(batch=B, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D, cap=cap, window=W,
+                       ring=True, scale=1 / 16)
+    kc_d, vc_d = _dev(kc), _dev(vc)
+    ws = new_workspace(dstep, "cuda")
+    rng = np.random.default_rng(5)
+    from _synth import rms_rows
+    for it, pos in enumerate(([60, 10], [61, 11], [62, 12])):
+        print(f"\n[case] consecutive step {it} pos={pos}", flush=True)
+        kn, vn = rms_rows(rng, (B, Hkv, D)), rms_rows(rng, (B, Hkv, D))
+        out = decode_step(dstep, _dev(q).view(B, Hq, D), _dev(kn).view(B, Hkv, D),
+                          _dev(vn).view(B, Hkv, D), kc_d, vc_d,
+                          torch.tensor(pos, dtype=torch.int32, device="cuda"), workspace=ws)
+        torch.cuda.synchronize()
+        orc.append(step, kc, vc, kn, vn, pos)
+        assert np.array_equal(_host(kc_d), kc) and np.array_equal(_host(vc_d), vc)
+        ref = orc.decode_f64(step, q, kc, vc, pos)
+        o = orc.from_bf16(_host(out)).reshape(B, Hq, D)
+        assert np.abs(o - ref).max() <= TOL_MAX
+
+
+def test_out_of_range_position_is_flagged_and_skipped():
+    from apertura_amd.decode import DecodeStep, decode_status, decode_step, new_workspace
+    B, Hq, Hkv, D, cap = 2, 8, 2, 128, 32
+    step = orc.Step(B=B, Hq=Hq, Hkv=Hkv, D=D, cap=cap, scale=D ** -0.5)
+    q, kc, vc, kn, vn = make_step_inputs(step, 8, [5, 40])
+    dstep = DecodeStep(batch=B, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D, cap=cap, scale=D ** -0.5)
+    kc_d, vc_d = _dev(kc), _dev(vc)
+    ws = new_workspace(dstep, "cuda")
+    out = torch.zeros(B, Hq, D, dtype=torch.bfloat16, device="cuda")
+    print("\n[case] out-of-range position (sequence 1 at pos 40 > cap 32)", flush=True)
+    decode_step(dstep, _dev(q).view(B, Hq, D), _dev(kn).view(B, Hkv, D), _dev(vn).view(B, Hkv, D),
+                kc_d, vc_d, torch.tensor([5, 40], dtype=torch.int32, device="cuda"), out=out,
+                workspace=ws)
+    torch.cuda.synchronize()
+    assert decode_status(dstep, ws) == 1
+    assert decode_status(dstep, ws) == 0  # cleared
+    # sequence 0 is appended and attended; sequence 1 untouched
+    kc_exp = kc.copy()
+    vc_exp = vc.copy()
+    one = orc.Step(B=1, Hq=Hq, Hkv=Hkv, D=D, cap=cap, scale=D ** -0.5)
+    half = len(kc) // 2
+    orc.append(one, kc_exp[:half], vc_exp[:half], kn[:1], vn[:1], [5])
+    assert np.array_equal(_host(kc_d), kc_exp) and np.array_equal(_host(vc_d), vc_exp)
+    o = _host(out).reshape(B, Hq, D)
+    assert np.all(o[1] == 0)
+
+
+def test_kv_append_multi_row_bit_exact():
+    from apertura_amd.decode import kv_append
+    B, Hkv, cap, D, n = 2, 4, 100, 512, 7
+    rng = np.random.default_rng(2)
+    cache = rng.integers(0, 65535, size=(B, Hkv, cap, D), dtype=np.uint16)
+    src = rng.integers(0, 65535, size=(B, Hkv, n, D), dtype=np.uint16)
+    row0 = [10, 93]
+    c_d = _dev(cache).view(B, Hkv, cap, D)
+    print("\n[case] kv_append 7 rows", flush=True)
+    kv_append(c_d, _dev(src).view(B, Hkv, n, D), torch.tensor(row0, dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    exp = cache.copy()
+    for b in range(B):
+        exp[b, :, row0[b]:row0[b] + n] = src[b]
+    assert np.array_equal(_host(c_d).reshape(B, Hkv, cap, D), exp)

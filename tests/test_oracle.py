@@ -1,0 +1,447 @@
+"""Pins of the CPU oracle (oracle/liboracle.so) -- CPU only.
+
+The reference holds no attention goldens (its fixtures are gitignored and need the
+31B weights), so each oracle function is pinned by something other than itself:
+
+  bf16 rounding      torch's RNE bf16 conversion + hand-computed tie cases
+  visibility rule    HF transformers masking_utils (causal / sliding-window mask
+                     functions, the rule ESGemma4TextModel.mm:68-83 restates)
+  append             numpy row assignment; every other byte unchanged
+  decode_f64         HF transformers gemma4 eager_attention_forward in fp64 (library),
+                     closed forms (single key, q = 0, identical keys, dominant key),
+                     invariants (permutation / ring-vs-linear, masked rows inert,
+                     score shift)
+  GQA order          ESPrimitivesTests.mm:118-128 (repeatKV is kv-major: [h0,h0,h1,h1])
+  decode_refround    within the north-star tolerance of fp64; bit-level spot checks
+                     of its rounding points on a hand-computed case
+  decode_splitk      S = 1 vs many splits vs fp64 (split invariance)
+  rope inv_freq      ESPrimitivesTests.mm:130-139, 191-210 (zero tail, full rotation)
+  rms norm           ESPrimitivesTests.mm:93-116 (unit weight, weightless [2,2,2,2])
+  raw-K decode       HF apply_rotary_pos_emb + rms norm composition feeding decode_f64
+
+Planted-mistake tests (orc_set_fault) show that a plausible bug in the oracle is
+caught by at least one pin.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from _synth import make_step_inputs, rms_rows
+
+TOL_MAX, TOL_MEAN = 2e-2, 2e-3
+
+
+# --------------------------------------------------------------------- bf16
+
+def test_bf16_round_matches_torch():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(100_000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 100_000),
+        np.array([0.0, -0.0, 1.0, -1.0, 3.0e38, -3.0e38, 1e-40, np.inf, -np.inf], np.float32),
+    ]).astype(np.float32)
+    ours = orc.to_bf16(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(ours, theirs)
+
+
+def test_bf16_ties_to_even():
+    one = np.float32(1.0)
+    ulp = np.float32(2.0 ** -7)  # bf16 spacing at 1.0
+    vals = np.array([one + ulp / 2, one + 3 * ulp / 2, one + ulp / 2 + np.float32(2 ** -20)],
+                    np.float32)
+    got = orc.to_bf16(vals)
+    assert list(got) == [0x3F80, 0x3F82, 0x3F81]
+    assert np.isnan(orc.from_bf16(orc.to_bf16(np.array([np.nan], np.float32))))[0]
+
+
+# -------------------------------------------------------------- visibility
+
+def _hf_mask_fn(window: int):
+    from transformers import masking_utils as mu
+    return mu.sliding_window_causal_mask_function(window) if window else mu.causal_mask_function
+
+
+def _hf_allowed(window: int, pos: int, kv_positions) -> list:
+    fn = _hf_mask_fn(window)
+    z = torch.tensor(0)
+    ok = fn(z, z, torch.tensor(pos), torch.as_tensor(list(kv_positions), dtype=torch.long))
+    return ok.tolist()
+
+
+def _hf_visible(pos: int, window: int, n_pos: int):
+    ok = _hf_allowed(window, pos, range(n_pos))
+    return [kv for kv in range(n_pos) if ok[kv]]
+
+
+@pytest.mark.parametrize("pos,window", [(0, 0), (5, 0), (1023, 1024), (1024, 1024),
+                                        (3000, 1024), (7, 3), (2, 3), (4095, 512)])
+def test_visible_linear_matches_hf_mask(pos, window):
+    step = orc.Step(B=1, Hq=2, Hkv=1, D=8, cap=pos + 1, window=window)
+    rows = orc.visible(step, pos)
+    assert list(rows) == _hf_visible(pos, window, pos + 1)
+
+
+@pytest.mark.parametrize("pos,window,cap", [(0, 4, 4), (3, 4, 4), (10, 4, 4), (10, 3, 8),
+                                            (2048, 1024, 1024), (32767, 1024, 1024)])
+def test_visible_ring_matches_hf_mask(pos, window, cap):
+    step = orc.Step(B=1, Hq=2, Hkv=1, D=8, cap=cap, window=window, ring=True)
+    rows = orc.visible(step, pos)
+    want = [p % cap for p in _hf_visible(pos, window, pos + 1)]
+    assert list(rows) == want
+    assert len(set(rows)) == len(rows)  # no slot twice
+
+
+def test_visible_linear_row_base():
+    # After a compaction the buffer's row 0 holds absolute position row_base
+    # (ESKVCache.mm:76-94); rows below the window are gone, rows in it are re-based.
+    step = orc.Step(B=1, Hq=2, Hkv=1, D=8, cap=1536, window=1024)
+    rows = orc.visible(step, 5000, row_base=5000 - 1100)
+    assert rows[0] == 5000 - 1023 - (5000 - 1100) and rows[-1] == 1100 and len(rows) == 1024
+
+
+def test_visible_rejects_bad_descriptions():
+    with pytest.raises(ValueError):
+        orc.visible(orc.Step(B=1, Hq=2, Hkv=1, D=8, cap=4, window=0, ring=True), 3)
+    with pytest.raises(ValueError):
+        orc.visible(orc.Step(B=1, Hq=2, Hkv=1, D=8, cap=4, window=8, ring=True), 3)
+    with pytest.raises(ValueError):
+        orc.visible(orc.Step(B=1, Hq=3, Hkv=2, D=8, cap=4), 3)
+    with pytest.raises(ValueError):
+        orc.visible(orc.Step(B=1, Hq=2, Hkv=1, D=8, cap=4), 4)  # linear overflow
+
+
+# ------------------------------------------------------------------- append
+
+@pytest.mark.parametrize("ring,shared", [(False, False), (True, False), (False, True)])
+def test_append_writes_exactly_one_row(ring, shared):
+    step = orc.Step(B=3, Hq=4, Hkv=2, D=16, cap=8, window=8 if ring else 0, ring=ring,
+                    head_stride=8 * 16 + 16, seq_stride=2 * (8 * 16 + 16) + 32)
+    pos = [3, 7, 13] if ring else [0, 4, 7]
+    q, kc, vc, kn, vn = make_step_inputs(step, 11, pos, shared_kv=shared)
+    k0, v0 = kc.copy(), vc.copy()
+    orc.append(step, kc, None if shared else vc, kn, None if shared else vn, pos)
+    k_exp = k0.copy()
+    v_exp = v0.copy()
+    d = step.desc()
+    for b in range(step.B):
+        r = pos[b] % step.cap if ring else pos[b]
+        for h in range(step.Hkv):
+            off = b * d.seq_stride + h * d.head_stride + r * step.D
+            k_exp[off:off + step.D] = kn[b, h]
+            v_exp[off:off + step.D] = (kn if shared else vn)[b, h]
+    np.testing.assert_array_equal(kc, k_exp)
+    if not shared:
+        np.testing.assert_array_equal(vc, v_exp)
+
+
+# ---------------------------------------------------------------- fp64 mode
+
+def _hf_attention_f64(step, q, kc, vc, pos):
+    """transformers' gemma4 eager_attention_forward in fp64 over the full cache rows
+    with an HF-rule additive mask on absolute positions."""
+    from transformers.models.gemma4.modeling_gemma4 import eager_attention_forward
+    d = step.desc()
+    G = step.Hq // step.Hkv
+
+    class M(torch.nn.Module):
+        num_key_value_groups = G
+        head_dim = step.D
+        training = False
+
+    outs = []
+    for b in range(step.B):
+        # positions held by the cache, derived without the oracle: linear rows hold
+        # p = row; ring slot j holds the newest p <= pos with p = j (mod cap)
+        if step.ring:
+            held = [(pos[b] - ((pos[b] - j) % step.cap), j) for j in range(step.cap)]
+            held = sorted((p, j) for p, j in held if p >= 0)
+        else:
+            held = [(p, p) for p in range(pos[b] + 1)]
+        K = np.empty((step.Hkv, len(held), step.D), np.float64)
+        V = np.empty_like(K)
+        for h in range(step.Hkv):
+            base = b * d.seq_stride + h * d.head_stride
+            for t, (_, r) in enumerate(held):
+                K[h, t] = orc.from_bf16(kc[base + r * step.D: base + (r + 1) * step.D])
+                V[h, t] = orc.from_bf16(vc[base + r * step.D: base + (r + 1) * step.D])
+        ok = _hf_allowed(step.window, pos[b], [p for p, _ in held])
+        mask = torch.tensor([[0.0 if a else -1e30 for a in ok]], dtype=torch.float64)
+        Q = torch.from_numpy(orc.from_bf16(q[b]).astype(np.float64))[None, :, None, :]
+        o, _ = eager_attention_forward(M(), Q, torch.from_numpy(K)[None], torch.from_numpy(V)[None],
+                                       mask[None, None], scaling=step.scale)
+        outs.append(o[0, 0].numpy())
+    return np.stack(outs)
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(B=1, Hq=16, Hkv=8, D=64, cap=40, window=0, ring=False, pos=[39], shared=False),
+    dict(B=2, Hq=8, Hkv=1, D=64, cap=64, window=0, ring=False, pos=[10, 63], shared=True),
+    dict(B=2, Hq=4, Hkv=2, D=32, cap=16, window=16, ring=True, pos=[40, 9], shared=False),
+    dict(B=1, Hq=4, Hkv=2, D=32, cap=64, window=10, ring=False, pos=[50], shared=False),
+])
+def test_f64_matches_hf_eager_attention(cfg):
+    step = orc.Step(B=cfg["B"], Hq=cfg["Hq"], Hkv=cfg["Hkv"], D=cfg["D"], cap=cfg["cap"],
+                    window=cfg["window"], ring=cfg["ring"], scale=cfg["D"] ** -0.5)
+    q, kc, vc, kn, vn = make_step_inputs(step, 3, cfg["pos"], shared_kv=cfg["shared"])
+    orc.append(step, kc, None if cfg["shared"] else vc, kn, None if cfg["shared"] else vn,
+               cfg["pos"])
+    ours = orc.decode_f64(step, q, kc, vc, cfg["pos"])
+    ref = _hf_attention_f64(step, q, kc, vc, cfg["pos"])
+    # HF's eager softmax runs in fp32 (dtype=torch.float32) even for fp64 inputs.
+    np.testing.assert_allclose(ours, ref, rtol=0, atol=2e-6)
+
+
+def _one_step(D=32, Hq=4, Hkv=2, cap=12, pos=None, scale=None, ring=False, window=0, seed=5):
+    step = orc.Step(B=1, Hq=Hq, Hkv=Hkv, D=D, cap=cap, ring=ring, window=window,
+                    scale=scale if scale is not None else D ** -0.5)
+    pos = [cap - 1] if pos is None else pos
+    return step, make_step_inputs(step, seed, pos), pos
+
+
+def test_closed_form_single_key_returns_v_row():
+    step, (q, kc, vc, kn, vn), _ = _one_step(cap=4, pos=[0])
+    orc.append(step, kc, vc, kn, vn, [0])
+    out = orc.decode_f64(step, q, kc, vc, [0])
+    for h in range(step.Hq):
+        np.testing.assert_array_equal(out[0, h], orc.from_bf16(vn[0, h // 2]).astype(np.float64))
+
+
+def test_closed_form_zero_query_is_mean_of_visible_v():
+    step, (q, kc, vc, kn, vn), pos = _one_step(cap=64, pos=[40], window=17)
+    q[:] = 0
+    orc.append(step, kc, vc, kn, vn, pos)
+    out = orc.decode_f64(step, q, kc, vc, pos)
+    d = step.desc()
+    for h in range(step.Hq):
+        base = (h // 2) * d.head_stride
+        rows = range(40 - 16, 41)
+        mean = np.mean([orc.from_bf16(vc[base + r * 32: base + r * 32 + 32]) for r in rows], axis=0)
+        np.testing.assert_allclose(out[0, h], mean, atol=1e-12)
+
+
+def test_closed_form_identical_keys_uniform_weights():
+    step, (q, kc, vc, kn, vn), pos = _one_step(cap=20, pos=[19])
+    d = step.desc()
+    for h in range(step.Hkv):
+        base = h * d.head_stride
+        for r in range(20):
+            kc[base + r * 32: base + r * 32 + 32] = kn[0, h]
+    orc.append(step, kc, vc, kn, vn, pos)
+    out = orc.decode_f64(step, q, kc, vc, pos)
+    for h in range(step.Hq):
+        base = (h // 2) * d.head_stride
+        mean = np.mean([orc.from_bf16(vc[base + r * 32: base + r * 32 + 32]) for r in range(20)], 0)
+        np.testing.assert_allclose(out[0, h], mean, atol=1e-12)
+
+
+def test_closed_form_dominant_key_wins():
+    step, (q, kc, vc, kn, vn), pos = _one_step(D=32, Hq=2, Hkv=1, cap=30, pos=[29], scale=1.0)
+    d = step.desc()
+    r = 7
+    kc[r * 32:(r + 1) * 32] = orc.to_bf16(orc.from_bf16(q[0, 0]) * 50.0)
+    orc.append(step, kc, vc, kn, vn, pos)
+    out = orc.decode_f64(step, q, kc, vc, pos)
+    np.testing.assert_allclose(out[0, 0], orc.from_bf16(vc[r * 32:(r + 1) * 32]), atol=1e-9)
+
+
+def test_invariant_non_visible_rows_are_inert():
+    step, (q, kc, vc, kn, vn), pos = _one_step(cap=64, pos=[50], window=8)
+    orc.append(step, kc, vc, kn, vn, pos)
+    a = orc.decode_f64(step, q, kc, vc, pos)
+    d = step.desc()
+    vis = set(orc.visible(step, 50))
+    rng = np.random.default_rng(9)
+    for h in range(step.Hkv):
+        for r in range(64):
+            if r not in vis:
+                o = h * d.head_stride + r * 32
+                kc[o:o + 32] = orc.to_bf16(rng.standard_normal(32).astype(np.float32) * 100)
+                vc[o:o + 32] = orc.to_bf16(rng.standard_normal(32).astype(np.float32) * 100)
+    b = orc.decode_f64(step, q, kc, vc, pos)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_invariant_ring_equals_linear_layout():
+    D, W, pos = 32, 16, 45
+    lin = orc.Step(B=1, Hq=4, Hkv=2, D=D, cap=pos + 1, window=W, scale=0.3)
+    ring = orc.Step(B=1, Hq=4, Hkv=2, D=D, cap=W, window=W, ring=True, scale=0.3)
+    q, kc, vc, kn, vn = make_step_inputs(lin, 21, [pos])
+    orc.append(lin, kc, vc, kn, vn, [pos])
+    kr = np.zeros(ring.cache_elems(), np.uint16)
+    vr = np.zeros_like(kr)
+    for h in range(2):
+        for p in range(pos - W + 1, pos + 1):
+            src = h * lin.desc().head_stride + p * D
+            dst = h * ring.desc().head_stride + (p % W) * D
+            kr[dst:dst + D] = kc[src:src + D]
+            vr[dst:dst + D] = vc[src:src + D]
+    a = orc.decode_f64(lin, q, kc, vc, [pos])
+    b = orc.decode_f64(ring, q, kr, vr, [pos])
+    np.testing.assert_allclose(a, b, atol=1e-13)
+
+
+def test_gqa_order_is_kv_major():
+    # ESPrimitivesTests.mm:118-128: repeatKV([h0, h1], 2) == [h0, h0, h1, h1].
+    step = orc.Step(B=1, Hq=4, Hkv=2, D=8, cap=3, scale=1.0)
+    q = orc.to_bf16(np.zeros((1, 4, 8), np.float32))
+    kc = orc.to_bf16(np.zeros(step.cache_elems(), np.float32))
+    vc = kc.copy()
+    d = step.desc()
+    for h in range(2):
+        vc[h * d.head_stride: h * d.head_stride + 3 * 8] = orc.to_bf16(np.full(24, float(h), np.float32))
+    out = orc.decode_f64(step, q, kc, vc, [2])
+    np.testing.assert_array_equal(out[0, :, 0], [0.0, 0.0, 1.0, 1.0])
+
+
+# ------------------------------------------------- refround and split-K modes
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_refround_within_tolerance_of_f64(shared):
+    step = orc.Step(B=2, Hq=8, Hkv=2, D=128, cap=300, scale=128 ** -0.5)
+    pos = [299, 120]
+    q, kc, vc, kn, vn = make_step_inputs(step, 13, pos, shared_kv=shared)
+    orc.append(step, kc, None if shared else vc, kn, None if shared else vn, pos)
+    ref = orc.decode_f64(step, q, kc, vc, pos)
+    rr = orc.from_bf16(orc.decode_refround(step, q, kc, vc, pos)).astype(np.float64)
+    err = np.abs(rr - ref)
+    assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN
+    assert err.max() > 0  # it really rounds
+
+
+def test_refround_rounding_points_hand_case():
+    # Two keys, D=2: q=(1,0), k0=(1,0), k1=(0,0), v0=(1,0), v1=(0,1), scale 1.
+    # scores bf16(1), bf16(0); softmax = (e/(e+1), 1/(e+1)) -> bf16 each;
+    # out = bf16(w0*v0 + w1*v1).
+    step = orc.Step(B=1, Hq=1, Hkv=1, D=2, cap=2, scale=1.0)
+    q = orc.to_bf16(np.array([[[1.0, 0.0]]], np.float32))
+    kc = orc.to_bf16(np.array([1.0, 0.0, 0.0, 0.0], np.float32))
+    vc = orc.to_bf16(np.array([1.0, 0.0, 0.0, 1.0], np.float32))
+    out = orc.from_bf16(orc.decode_refround(step, q, kc, vc, [1]))[0, 0]
+    e = np.float32(np.e)
+    w0 = orc.from_bf16(orc.to_bf16(np.array([np.float32(1) / (np.float32(1) + np.exp(np.float32(-1)))], np.float32)))[0]
+    w1 = orc.from_bf16(orc.to_bf16(np.array([np.exp(np.float32(-1)) / (np.float32(1) + np.exp(np.float32(-1)))], np.float32)))[0]
+    assert out[0] == orc.from_bf16(orc.to_bf16(np.array([w0], np.float32)))[0]
+    assert out[1] == orc.from_bf16(orc.to_bf16(np.array([w1], np.float32)))[0]
+    assert abs(out[0] - e / (e + 1)) < 4e-3
+
+
+@pytest.mark.parametrize("nsplit", [1, 2, 7, 64])
+def test_splitk_is_split_invariant(nsplit):
+    step = orc.Step(B=1, Hq=8, Hkv=1, D=64, cap=500, scale=0.125)
+    pos = [499]
+    q, kc, vc, kn, vn = make_step_inputs(step, 17, pos, shared_kv=True)
+    orc.append(step, kc, None, kn, None, pos)
+    ref = orc.decode_f64(step, q, kc, kc, pos)
+    sk = orc.decode_splitk(step, q, kc, kc, pos, nsplit).astype(np.float64)
+    assert np.abs(sk - ref).max() < 1e-5
+
+
+def test_splitk_peaked_keys_merge():
+    # A few keys with +8 logits concentrated in one split: the merge must weight
+    # that split by exp(m_s - mMax) (empty/low splits vanish) -- ESDecodeAttn.mm:253-273.
+    step = orc.Step(B=1, Hq=2, Hkv=1, D=64, cap=1000, scale=1.0 / 8)
+    pos = [999]
+    q, kc, vc, kn, vn = make_step_inputs(step, 19, pos, shared_kv=True)
+    qd = orc.from_bf16(q[0, 0]).astype(np.float64)
+    alpha = 8.0 / (step.scale * np.linalg.norm(qd))  # raises head 0's logit by +8
+    for r in (3, 5, 8):
+        k = orc.from_bf16(kc[r * 64:(r + 1) * 64]) + alpha * qd / np.linalg.norm(qd)
+        kc[r * 64:(r + 1) * 64] = orc.to_bf16(k.astype(np.float32))
+    orc.append(step, kc, None, kn, None, pos)
+    ref = orc.decode_f64(step, q, kc, kc, pos)
+    sk = orc.decode_splitk(step, q, kc, kc, pos, 100).astype(np.float64)
+    assert np.abs(sk - ref).max() < 1e-5
+
+
+# ----------------------------------------------------------- rope and norms
+
+def test_rope_proportional_zero_tail():
+    # ESPrimitivesTests.mm:191-210: head_dim 512, partial 0.25 -> 64 real freqs, 192 zeros.
+    inv = orc.rope_inv_freq(512, 1.0e6, 0.25)
+    assert inv.shape == (256,)
+    assert np.all(inv[64:] == 0) and np.all(inv[:64] > 0)
+    assert inv[0] == 1.0 and abs(np.sin(1.0 * inv[0])) > 1e-3
+    # HF default rope: inv_freq = 1 / base ** (arange(0, dim, 2) / dim) over the rotated dims
+    ref = 1.0 / (1.0e6 ** (np.arange(0, 128, 2, dtype=np.float64) / 512))
+    np.testing.assert_allclose(inv[:64], ref.astype(np.float32), rtol=1e-6)
+
+
+def test_rope_local_full_rotation():
+    # ESPrimitivesTests.mm:130-139: full rotation, position 0 -> cos 1, sin 0.
+    inv = orc.rope_inv_freq(8, 1.0e4, 1.0)
+    assert np.all(inv > 0) and inv.shape == (4,)
+    assert np.all(np.cos(0.0 * inv) == 1.0) and np.all(np.sin(0.0 * inv) == 0.0)
+
+
+def test_rms_norm_weightless_and_unit_weight():
+    # ESPrimitivesTests.mm:107-116 and :93-105.
+    y = orc.from_bf16(orc.rms_norm_rows(orc.to_bf16(np.full((1, 4), 2.0, np.float32)), None, 1e-6))
+    assert np.all(np.abs(y - 1.0) <= 1e-3)
+    x = orc.to_bf16((np.arange(8, dtype=np.float32) - 3.0)[None])
+    y = orc.from_bf16(orc.rms_norm_rows(x, orc.to_bf16(np.ones(8, np.float32)), 1e-6))
+    assert abs(float(np.mean(y.astype(np.float64) ** 2)) - 1.0) <= 1e-2
+
+
+# --------------------------------------------------------------- raw-K mode
+
+def _hf_raw_reference(q, raw, len_, kw, eps, inv, scale):
+    """K = bf16(rope(rmsnorm_w(kraw))) with HF's apply_rotary_pos_emb / rotate_half on
+    bf16-rounded cos/sin; V = rmsnorm(kraw) without weight; fp64 attention."""
+    from transformers.models.gemma4.modeling_gemma4 import rotate_half
+    Hkv, pitch, D = raw.shape
+    x = torch.from_numpy(orc.from_bf16(raw[:, :len_]))
+    ss = (x.double() ** 2).sum(-1, keepdim=True)
+    rinv = 1.0 / torch.sqrt((ss / 512.0).float() + eps)
+    kn = x * rinv * torch.from_numpy(orc.from_bf16(kw))
+    pos_ = torch.arange(len_, dtype=torch.float32)[:, None]
+    freqs = pos_ * torch.from_numpy(inv)[None, :256]
+    emb = torch.cat([freqs, freqs], -1)
+    c = torch.cos(emb).to(torch.bfloat16).float()
+    s = torch.sin(emb).to(torch.bfloat16).float()
+    k = (kn * c + rotate_half(kn) * s).to(torch.bfloat16).double()
+    v = (x * rinv).double()
+    qq = torch.from_numpy(orc.from_bf16(q)).double().view(Hkv, 8, D)
+    sc = torch.einsum("hgd,htd->hgt", qq, k) * scale
+    w = torch.softmax(sc, -1)
+    return torch.einsum("hgt,htd->hgd", w, v).reshape(Hkv * 8, D).numpy()
+
+
+def test_raw_decode_matches_hf_rope_composition():
+    rng = np.random.default_rng(23)
+    Hkv, pitch, L = 1, 80, 70
+    raw = orc.to_bf16(rng.standard_normal((Hkv, pitch, 512)).astype(np.float32) * 3)
+    q = rms_rows(rng, (8, 512))
+    kw = orc.to_bf16((1.0 + 0.1 * rng.standard_normal(512)).astype(np.float32))
+    inv = orc.rope_inv_freq(512, 1.0e6, 0.25)
+    ours = orc.decode_raw_f64(q, raw, L, kw, 1e-6, inv, scale=512 ** -0.5)
+    ref = _hf_raw_reference(q, raw, L, kw, 1e-6, inv, 512 ** -0.5)
+    assert np.abs(ours - ref).max() < 2e-3
+
+
+# ------------------------------------------------------------ planted faults
+
+def _pins_fail(fn) -> bool:
+    try:
+        fn()
+    except AssertionError:
+        return True
+    return False
+
+
+@pytest.mark.parametrize("fault,pin", [
+    (1, lambda: test_gqa_order_is_kv_major()),
+    (1, lambda: test_f64_matches_hf_eager_attention(dict(B=1, Hq=16, Hkv=8, D=64, cap=40,
+                                                         window=0, ring=False, pos=[39],
+                                                         shared=False))),
+    (2, lambda: test_visible_linear_matches_hf_mask(3000, 1024)),
+    (3, lambda: test_f64_matches_hf_eager_attention(dict(B=1, Hq=4, Hkv=2, D=32, cap=64,
+                                                         window=10, ring=False, pos=[50],
+                                                         shared=False))),
+    (4, lambda: test_append_writes_exactly_one_row(False, False)),
+    (5, lambda: test_raw_decode_matches_hf_rope_composition()),
+])
+def test_planted_fault_is_caught(fault, pin):
+    with orc.planted_fault(fault):
+        assert _pins_fail(pin), f"planted fault {fault} went unnoticed"
+    pin()  # and the clean oracle passes again
