@@ -26,8 +26,9 @@
 //       base plus an immediate offset, so no address registers stay live).
 //   With attention_k_eq_v the V tile *is* the K registers: one HBM read per row.
 //
-// The new token's row is read from k_new/v_new by the lane that owns it and stored
-// into the cache by the same lane (bit-exact copy); no other workgroup reads that row.
+// The new token's row is copied from k_new/v_new into the cache by the workgroup whose
+// split ends at it (bit-exact copy); that workgroup's own loads read the row from
+// k_new/v_new and no other workgroup reads it, so the copy needs no ordering.
 
 #include <hip/hip_runtime.h>
 
@@ -36,6 +37,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <utility>
 
 #include "esda.h"
 
@@ -45,10 +47,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kTile = 16;
+constexpr int kTile = 16;          // MFMA row block; split sizes are multiples of it
 constexpr int kMaxGroup = 16;
 constexpr int kTargetGroups = 512;  // workgroups per launch the split heuristic aims for
 constexpr float kLog2e = 1.4426950408889634f;
@@ -94,55 +95,148 @@ struct AttendParams {
     float scale_log2e;
 };
 
-// LDS row stride of a staged tile: 16 bytes of padding shift consecutive rows by 4
-// banks, so 16 rows x 16-byte writes cover all banks and the 4 rows a column gather
-// touches at once (rows 4g+e) fall into disjoint 8-dword windows.
-template <int D>
-constexpr int lds_row_bytes() { return D * 2 + 16; }
-
+// Max over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48): two
+// permlane swaps exchange 16-lane rows and 32-lane halves without touching LDS.
 __device__ __forceinline__ float wave_max_across_groups(float x) {
-    x = fmaxf(x, __shfl_xor(x, 16));
-    x = fmaxf(x, __shfl_xor(x, 32));
-    return x;
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = fmaxf(__builtin_bit_cast(float, s16[0]), __builtin_bit_cast(float, s16[1]));
+    const unsigned v = __builtin_bit_cast(unsigned, x);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return fmaxf(__builtin_bit_cast(float, s32[0]), __builtin_bit_cast(float, s32[1]));
 }
 
-__device__ __forceinline__ void lds_fence() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
+// The running max is only raised (and O rescaled) once a score exceeds it by this
+// much in log2 units; until then probabilities may reach 2^8 before normalisation,
+// far from fp32 / bf16 limits, and the final division by l is unchanged.
+constexpr float kRescaleSlack = 8.0f;
 
-template <int D, bool SHARED>
-struct TileRegs {
-    uint4 k[D / 32];
-    uint4 v[SHARED ? 1 : D / 32];
+
+// ---------------------------------------------------------------- LDS ring layout
+//
+// A workgroup streams its rows through a ring of NS stages of 16 rows in LDS.  Rows
+// arrive by LDS DMA (global_load_lds_dwordx4: 64 lanes x 16 B land contiguously at
+// M0 + 16*lane), non-temporal, so in-flight data costs no registers and each
+// instruction reads 1 KB of contiguous HBM.  One instruction carries RPI = 512/D rows:
+// instruction i of a stage holds rows i + q*NI (q < RPI) in a 1040-byte block (1 KB +
+// 16 B pad).  Sub-row q is rotated by q*ROT chunks of 16 B, ROT being a whole number of
+// per-wave dim slices, which keeps every 128-bit row read and every 16-bit column
+// gather free of bank conflicts while all addresses stay base + immediate.
+template <int D, bool SHARED, int NW>
+struct Ring {
+    static constexpr int RPI = 512 / D;                     // rows per DMA instruction
+    static constexpr int NI = 16 / RPI;                     // DMA instructions per stage
+    static constexpr int CPR = D / 8;                       // 16-byte chunks per row
+    static constexpr int BLK = 1040;                        // LDS bytes per DMA block
+    static constexpr int TB = NI * BLK;                     // one tensor's stage
+    static constexpr int SB = (SHARED ? 1 : 2) * TB;        // stage bytes (K [+ V])
+    static constexpr int DW = D / NW;                       // dims per wave
+    static constexpr int SL = DW / 8;                       // chunks per wave slice
+    static constexpr int ROT = RPI > 1 ? (16 / RPI) / SL : 0;  // sub-row rotation, slices
+    static constexpr int KKW = DW / 32;                     // QK k-steps per wave
+    static constexpr int DTW = DW / 16;                     // PV dim tiles per wave
+    static constexpr int DPT = NI / NW;                     // DMA per wave per tensor
+    static constexpr int DPW = DPT * (SHARED ? 1 : 2);      // DMA per wave per stage
+    static constexpr int XB = 2 * NW * 64 * 16;             // score-exchange bytes
+    static constexpr int NS_ = (156 * 1024 - XB) / SB;
+    static constexpr int NS = NS_ > 16 ? 16 : NS_;          // stages in the ring
+    static_assert(DW % 32 == 0 && NI % NW == 0, "wave slices must cover whole MFMA steps");
+    static_assert(RPI == 1 || (16 / RPI) % SL == 0, "rotation must be whole slices");
+    static_assert(NS >= 4, "the ring needs at least 4 stages");
+    static_assert((NS - 3) * DPW <= 60, "vmcnt holds at most 63 outstanding loads");
+    // Byte offset of (row r, chunk cin of wave slice ws) inside a tensor stage.
+    __device__ static __forceinline__ int off(int r, int ws, int cin) {
+        const int i = r % NI, q = r / NI;
+        return i * BLK + q * 2 * D + (((ws + q * ROT) % NW) * SL + cin) * 16;
+    }
 };
 
-template <int D, bool SHARED>
-__device__ __forceinline__ void load_tile(TileRegs<D, SHARED> &t, const uint16_t *ksrc,
-                                          const uint16_t *vsrc, int lg) {
-#pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk)
-        t.k[kk] = *reinterpret_cast<const uint4 *>(ksrc + kk * 32 + lg * 8);
-    if constexpr (!SHARED) {
-#pragma unroll
-        for (int kk = 0; kk < D / 32; ++kk)
-            t.v[kk] = *reinterpret_cast<const uint4 *>(vsrc + kk * 32 + lg * 8);
-    }
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
+// lgkmcnt[11:8], vmcnt[5:4] at [15:14]).
+#define ESDA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+
+// Workgroup barrier for LDS hand-offs.  __syncthreads() would also drain every
+// outstanding global load (vmcnt(0)), which would empty the DMA ring each stage; the
+// ring's own vmcnt waits precede this barrier instead.  The memory clobber keeps the
+// compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#endif
 }
 
-template <int D, bool SHARED>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(1, 1)))
+// One 64-lane x 16-byte LDS DMA (global_load_lds_dwordx4, non-temporal): lane l's 16
+// bytes from `src` land at LDS byte address lds + 16*l.  Issued from inline assembly so
+// that the compiler does not track it: the ring accounts for these loads itself
+// (ESDA_WAIT_VM before each stage), and compiler-inserted waits would drain the ring.
+// M0 carries the LDS base; nothing else in these kernels uses M0.
+// (The guard keeps the gfx950 assembly out of hipcc's host pass.)
+__device__ __forceinline__ void lds_dma16(const void *src, unsigned lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const unsigned base = __builtin_amdgcn_readfirstlane(lds);  // wave-uniform by construction
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(base) : "memory");
+#endif
+}
+
+// Same DMA with a wave-uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset:
+// interior stages advance the base with scalar adds and reuse the lane offsets.
+__device__ __forceinline__ void lds_dma16_s(const void *sbase, unsigned voff, unsigned lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uintptr_t a = (uintptr_t) sbase;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned) a);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned) (a >> 32));
+    const uint64_t sb = ((uint64_t) hi << 32) | lo;
+    const unsigned base = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sb), "s"(base) : "memory");
+#endif
+}
+
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+    return (unsigned) (uintptr_t) (const __attribute__((address_space(3))) void *) p;
+}
+
+// Calls f(std::integral_constant<int, 0>) .. f(std::integral_constant<int, N-1>): a
+// guaranteed full unroll in which the index is a compile-time constant.
+template <class F, int... I>
+__device__ __forceinline__ void unroll_impl(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void unroll(F &&f) {
+    unroll_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int D, bool SHARED, int NW>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW)))
 void attend_kernel(AttendParams p) {
-    constexpr int KK = D / 32;
-    constexpr int DT = D / 16;
-    constexpr int RS = lds_row_bytes<D>();
-    // Per-wave V tile (16 padded rows); reused at the end for the cross-wave merge,
-    // which needs 2 * G * D floats <= 128 * D bytes < 4 * 16 * RS bytes.
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kWaves * kTile * RS];
-    __shared__ float lds_m[kWaves][kMaxGroup];
-    __shared__ float lds_l[kWaves][kMaxGroup];
+    using R = Ring<D, SHARED, NW>;
+    constexpr int NS = R::NS, DW = R::DW, KKW = R::KKW, DTW = R::DTW;
+    // Distinct arrays per stage: the compiler tracks DMA completion per LDS object, so a
+    // read of stage u only waits for stage u's DMA, never for the stages behind it.
+    __shared__ __attribute__((aligned(16))) unsigned char r0[R::SB], r1[R::SB], r2[R::SB], r3[R::SB],
+        r4[R::SB], r5[R::SB], r6[R::SB], r7[R::SB], r8[R::SB], r9[R::SB], r10[R::SB], r11[R::SB],
+        r12[R::SB], r13[R::SB], r14[R::SB], r15[R::SB];
+    // Stage buffer u (a compile-time index).
+    auto ring = [&](auto uc) -> unsigned char * {
+        constexpr int u = decltype(uc)::value % NS;
+        if constexpr (u == 0) return r0;
+        else if constexpr (u == 1) return r1;
+        else if constexpr (u == 2) return r2;
+        else if constexpr (u == 3) return r3;
+        else if constexpr (u == 4) return r4;
+        else if constexpr (u == 5) return r5;
+        else if constexpr (u == 6) return r6;
+        else if constexpr (u == 7) return r7;
+        else if constexpr (u == 8) return r8;
+        else if constexpr (u == 9) return r9;
+        else if constexpr (u == 10) return r10;
+        else if constexpr (u == 11) return r11;
+        else if constexpr (u == 12) return r12;
+        else if constexpr (u == 13) return r13;
+        else if constexpr (u == 14) return r14;
+        else return r15;
+    };
+    __shared__ f32x4 xch[2][NW][64];  // partial scores, double-buffered by stage parity
 
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -160,172 +254,188 @@ void attend_kernel(AttendParams p) {
     const int j1 = min(j0 + p.chunk, sv.nvis);
     if (split == p.S - 1 && j1 < sv.nvis && kvh == 0 && tid == 0) atomicAdd(p.status, 1);
 
-    // Q^T operand: lane l carries head l%16 of the group (zero when l%16 >= G).
-    bf16x8 qv[KK];
-    {
-        const bool qok = li < p.G;
-        const uint16_t *qrow = p.q + ((size_t) b * p.Hq + (size_t) kvh * p.G + (qok ? li : 0)) * D + lg * 8;
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            uint4 t = qok ? *reinterpret_cast<const uint4 *>(qrow + kk * 32) : make_uint4(0, 0, 0, 0);
-            qv[kk] = __builtin_bit_cast(bf16x8, t);
-        }
-    }
-
     const size_t head_off = (size_t) b * p.seq_stride + (size_t) kvh * p.head_stride;
     uint16_t *kbase = p.k_cache + head_off;
     uint16_t *vbase = p.v_cache + head_off;
     const uint16_t *knew = p.k_new + ((size_t) b * p.Hkv + kvh) * D;
     const uint16_t *vnew = SHARED ? knew : p.v_new + ((size_t) b * p.Hkv + kvh) * D;
-    unsigned char *wl = lds + wave * kTile * RS;
-    unsigned char *wr_base = wl + li * RS + lg * 16;       // + 64*kk
-    const unsigned char *gb[4];                              // + 32*dt
+
+    // Q^T operand for this wave's dim slice: lane (li, lg) = head li, dims
+    // wave*DW + 32kk + 8lg .. +8 (zero for heads >= G).
+    bf16x8 qv[KKW];
+    {
+        const bool qok = li < p.G;
+        const uint16_t *qrow = p.q + ((size_t) b * p.Hq + (size_t) kvh * p.G + (qok ? li : 0)) * D +
+                               wave * DW + lg * 8;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) gb[e] = wl + (4 * lg + e) * RS + 2 * li;
-
-    float m = -INFINITY, l = 0.0f;
-    f32x4 acc[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    const int ntile = (j1 - j0 + kTile - 1) / kTile;
-
-    // Row addressing for the tile starting at logical row jt: this lane loads row li.
-    auto row_src = [&](int jt, const uint16_t *&ks, const uint16_t *&vs, int &is_new) {
-        const int j = jt + li;
-        const int jj = j < j1 ? j : j1 - 1;  // clamp: masked rows read a visible row
-        int r = sv.first + jj;
-        if (r >= p.cap) r -= p.cap;
-        is_new = (j == sv.nvis - 1);
-        const bool from_new = (jj == sv.nvis - 1);
-        ks = from_new ? knew : kbase + (size_t) r * D;
-        vs = from_new ? vnew : vbase + (size_t) r * D;
-    };
-
-    // One register buffer per wave: a tile's registers are dead once its QK MFMAs have
-    // read them and its V rows sit in LDS, so the next tile's loads go into the same
-    // registers and stay in flight through this tile's softmax and PV.
-    TileRegs<D, SHARED> tr;
-    int t = wave;
-    int is_new = 0;
-    if (t < ntile) {
-        const uint16_t *ks, *vs;
-        row_src(j0 + t * kTile, ks, vs, is_new);
-        load_tile<D, SHARED>(tr, ks, vs, lg);
+        for (int kk = 0; kk < KKW; ++kk) {
+            const u32x4 t = qok ? *reinterpret_cast<const u32x4 *>(qrow + kk * 32) : u32x4{0u, 0u, 0u, 0u};
+            qv[kk] = __builtin_bit_cast(bf16x8, t);
+        }
     }
-    for (; t < ntile; t += kWaves) {
-        const int jt = j0 + t * kTile;
-        // Fused append: the owner of the new row copies it into the cache.
-        if (is_new) {
-            uint16_t *kd = kbase + (size_t) sv.newrow * D + lg * 8;
+    ESDA_WAIT_VM(0);  // Q is in registers before the ring starts counting its own loads
+
+    // DMA source slot of this lane: sub-row q, chunk c of the row (undoing the rotation).
+    const int dq = lane / R::CPR, dp = lane % R::CPR;
+    const int dchunk = ((((dp / R::SL) - dq * R::ROT) % NW + NW) % NW) * R::SL + dp % R::SL;
+    const int nst = (j1 - j0 + 15) / 16;
+    // Per-lane byte offsets of this wave's DMA slots inside a stage's row range.
+    unsigned dvoff[R::DPT];
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) *reinterpret_cast<uint4 *>(kd + kk * 32) = tr.k[kk];
+    for (int t = 0; t < R::DPT; ++t)
+        dvoff[t] = (unsigned) (((wave * R::DPT + t + dq * R::NI) * D + dchunk * 8) * 2);
+    auto dma = [&](int st, unsigned char *buf) {
+        const int jst = j0 + st * 16;
+        if (jst + 16 < j1 && sv.first + jst + 16 <= p.cap) {
+            // Interior stage: 16 consecutive cache rows, none clamped or new.
+            const uint16_t *kb = kbase + (size_t) (sv.first + jst) * D;
+            const uint16_t *vb = vbase + (size_t) (sv.first + jst) * D;
+#pragma unroll
+            for (int t = 0; t < R::DPT; ++t) {
+                const int i = wave * R::DPT + t;
+                lds_dma16_s(kb, dvoff[t], lds_addr(buf) + i * R::BLK);
+                if constexpr (!SHARED) lds_dma16_s(vb, dvoff[t], lds_addr(buf) + R::TB + i * R::BLK);
+            }
+            return;
+        }
+#pragma unroll
+        for (int t = 0; t < R::DPT; ++t) {
+            const int i = wave * R::DPT + t;            // DMA block of this stage
+            const int j = jst + i + dq * R::NI;         // logical row this lane feeds
+            const int jj = j < j1 ? j : j1 - 1;          // clamp: masked rows read a visible row
+            int r = sv.first + jj;
+            if (r >= p.cap) r -= p.cap;
+            const bool from_new = (jj == sv.nvis - 1);
+            const uint16_t *ks = (from_new ? knew : kbase + (size_t) r * D) + dchunk * 8;
+            lds_dma16(ks, lds_addr(buf) + i * R::BLK);
             if constexpr (!SHARED) {
-                uint16_t *vd = vbase + (size_t) sv.newrow * D + lg * 8;
-#pragma unroll
-                for (int kk = 0; kk < KK; ++kk) *reinterpret_cast<uint4 *>(vd + kk * 32) = tr.v[kk];
+                const uint16_t *vs = (from_new ? vnew : vbase + (size_t) r * D) + dchunk * 8;
+                lds_dma16(vs, lds_addr(buf) + R::TB + i * R::BLK);
             }
         }
-        // Scores S^T (keys x heads).
-        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+    };
+
+    // Per-lane LDS offsets: QK A operand (row li, this wave's slice, chunk 4kk + lg)
+    // and the V^T gather (row 4lg + e, dim wave*DW + 16dt + li).
+    // and the V^T transpose read (lane (li, lg) supplies row 4lg + li/4, dims
+    // wave*DW + 16dt + 4(li%4) .. +4; ds_read_b64_tr_b16 hands lane li of the group
+    // dim 16dt + li of rows 4lg .. 4lg+3, the PV A operand).
+    const int qk_off = R::off(li, wave, lg);                           // + 64*kk
+    const int tr_off = R::off(4 * lg + li / 4, wave, 0) + (li % 4) * 8;  // + 32*dt
+    constexpr int VOFF = SHARED ? 0 : R::TB;
+
+    float m = -INFINITY, l = 0.0f;
+    f32x4 acc[DTW];
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk)
-            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, tr.k[kk]), qv[kk], s, 0, 0, 0);
-        // V tile -> LDS (row li, dims 32kk+8lg..+8).
-        const uint4 *vsrc = SHARED ? tr.k : tr.v;
+    for (int dt = 0; dt < DTW; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Partial scores of stage st over this wave's dims, published for the other waves.
+    auto qk_partial = [&](const unsigned char *kb, int par) {
+        f32x4 sp = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk)
-            *reinterpret_cast<uint4 *>(wr_base + 64 * kk) = vsrc[kk];
-        // Next tile of this wave into the same registers.
-        if (t + kWaves < ntile) {
-            const uint16_t *ks, *vs;
-            row_src(jt + kWaves * kTile, ks, vs, is_new);
-            load_tile<D, SHARED>(tr, ks, vs, lg);
+        for (int kk = 0; kk < KKW; ++kk) {
+            const bf16x8 a = *reinterpret_cast<const bf16x8 *>(kb + qk_off + 64 * kk);
+            sp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qv[kk], sp, 0, 0, 0);
         }
-        // Online softmax (log2 domain); rows past the split end are masked.
-        float sc[4];
+        xch[par][wave][lane] = sp;
+    };
+
+    // Prologue: fill NS-1 stages, then publish stage 0's partial scores.
+    unroll<NS - 1>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        if (u < nst) dma(u, ring(uc));
+    });
+    if (nst - 1 >= NS - 2) {
+        ESDA_WAIT_VM((NS - 2) * R::DPW);
+    } else {
+        ESDA_WAIT_VM(0);
+    }
+    lds_barrier();
+    qk_partial(ring(std::integral_constant<int, 0>{}), 0);
+
+    // Iteration st: one barrier, after which (a) every wave's stage-st partial scores
+    // are in xch, (b) stage st+1 has landed from every wave's DMA, and (c) every wave is
+    // done with stage st-1's buffer, which is refilled at once.  The scores of stage
+    // st+1 are computed alongside stage st's PV, so the two dependency chains overlap.
+    auto stage = [&](int s0, auto uc) {
+        constexpr int u = decltype(uc)::value;
+        const int st = s0 + u;
+        if (st >= nst) return;
+        if (st + 1 < nst) {
+            // own DMA for stage st+1 done; stages st+2 .. st+NS-2 may stay in flight
+            if (nst - st - 2 >= NS - 3) {
+                ESDA_WAIT_VM((NS - 3) * R::DPW);
+            } else {
+                ESDA_WAIT_VM(0);
+            }
+        }
+        lds_barrier();
+        if (st + NS - 1 < nst) dma(st + NS - 1, ring(std::integral_constant<int, (u + NS - 1) % NS>{}));
+        f32x4 sc = xch[st & 1][0][lane];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int jk = jt + 4 * lg + r;
-            sc[r] = jk < j1 ? s[r] * p.scale_log2e : -INFINITY;
+        for (int w = 1; w < NW; ++w) sc += xch[st & 1][w][lane];
+        if (st + 1 < nst) qk_partial(ring(std::integral_constant<int, (u + 1) % NS>{}), (st + 1) & 1);
+        // Online softmax (log2 domain), identical in every wave; rows past the split
+        // end (last stage only) are masked.
+        const int jt = j0 + st * 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] *= p.scale_log2e;
+        if (jt + 16 > j1) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[r] = (jt + 4 * lg + r) < j1 ? sc[r] : -INFINITY;
         }
         const float tmax = wave_max_across_groups(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-        const float mnew = fmaxf(m, tmax);
-        if (__any(mnew > m)) {
+        if (__any(tmax > m + kRescaleSlack)) {
+            const float mnew = fmaxf(m, tmax);
             const float corr = __builtin_amdgcn_exp2f(m - mnew);
             l *= corr;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) acc[dt] *= corr;
+            for (int dt = 0; dt < DTW; ++dt) acc[dt] *= corr;
+            m = mnew;
         }
-        m = mnew;
-        bf16x4 pb;
+        short4v pbs;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pb[r] = (__bf16) __builtin_amdgcn_exp2f(sc[r] - m);
-        l += ((float) pb[0] + (float) pb[1]) + ((float) pb[2] + (float) pb[3]);
-        const short4v pbs = __builtin_bit_cast(short4v, pb);
-        lds_fence();
-        // O^T += V^T . P^T: lane (li, lg) gathers dim 16dt+li of rows 4lg+e.
+        for (int r = 0; r < 4; ++r) {
+            const __bf16 pr = (__bf16) __builtin_amdgcn_exp2f(sc[r] - m);
+            l += (float) pr;
+            pbs[r] = __builtin_bit_cast(short, pr);
+        }
+        // O^T (this wave's dims) += V^T . P^T
+        const unsigned char *vb = ring(uc) + VOFF;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            short4v a;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) a[e] = *reinterpret_cast<const short *>(gb[e] + 32 * dt);
+        for (int dt = 0; dt < DTW; ++dt) {
+            const short4v a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4v *) (vb + tr_off + 32 * dt));
             acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pbs, acc[dt], 0, 0, 0);
         }
-        lds_fence();
+    };
+    for (int s0 = 0; s0 < nst; s0 += NS) unroll<NS>([&](auto uc) { stage(s0, uc); });
+
+    // Fused append: the workgroup whose rows end at the new token copies k_new / v_new
+    // into its cache row (bit-exact).  Its own DMA reads that row from k_new / v_new and
+    // no other workgroup reads it; the copy runs after this workgroup's ring has
+    // drained, so no outstanding load is counted against the ring's waits.
+    if (wave == 0 && j1 == sv.nvis) {
+        for (int c = lane; c < D / 8; c += 64) {
+            *reinterpret_cast<u32x4 *>(kbase + (size_t) sv.newrow * D + c * 8) =
+                *reinterpret_cast<const u32x4 *>(knew + c * 8);
+            if constexpr (!SHARED)
+                *reinterpret_cast<u32x4 *>(vbase + (size_t) sv.newrow * D + c * 8) =
+                    *reinterpret_cast<const u32x4 *>(vnew + c * 8);
+        }
     }
 
-    // ---- merge the 4 waves of this workgroup (log2-domain max, fp32 sums)
+    // Partial of this split: every wave holds the same (m, l) and its own dim slice.
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
-    if (lg == 0) lds_m[wave][li] = m;
-    __syncthreads();
-    float mall = lds_m[0][li];
+    if (li < p.G) {
+        const size_t pidx = (((size_t) b * p.Hkv + kvh) * p.S + split) * p.G + li;
+        float *dst = p.part_acc + pidx * D + wave * DW;
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) mall = fmaxf(mall, lds_m[w][li]);
-    const float f = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - mall);
-    l *= f;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[dt] *= f;
-    if (lg == 0) lds_l[wave][li] = l;
-
-    float *slot = reinterpret_cast<float *>(lds);  // [2][G][D]
-    const bool hv = li < p.G;
-    auto put = [&](int s) {
-        if (hv) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-                *reinterpret_cast<f32x4 *>(slot + ((size_t) s * p.G + li) * D + 16 * dt + 4 * lg) = acc[dt];
-        }
-    };
-    auto take = [&](int s) {
-        if (hv) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-                acc[dt] += *reinterpret_cast<const f32x4 *>(slot + ((size_t) s * p.G + li) * D + 16 * dt + 4 * lg);
-        }
-    };
-    if (wave >= 2) put(wave - 2);
-    __syncthreads();
-    if (wave < 2) take(wave);
-    __syncthreads();
-    if (wave == 1) put(0);
-    __syncthreads();
-    if (wave == 0) {
-        take(0);
-        const size_t pidx = (((size_t) b * p.Hkv + kvh) * p.S + split) * p.G;
-        if (hv) {
-            float *dst = p.part_acc + (pidx + li) * D;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-                *reinterpret_cast<f32x4 *>(dst + 16 * dt + 4 * lg) = acc[dt];
-            if (lg == 0) {
-                float lt = 0.0f;
-#pragma unroll
-                for (int w = 0; w < kWaves; ++w) lt += lds_l[w][li];
-                p.part_ml[(pidx + li) * 2 + 0] = mall;
-                p.part_ml[(pidx + li) * 2 + 1] = lt;
-            }
+        for (int dt = 0; dt < DTW; ++dt) *reinterpret_cast<f32x4 *>(dst + 16 * dt + 4 * lg) = acc[dt];
+        if (wave == 0 && lg == 0) {
+            p.part_ml[pidx * 2 + 0] = m;
+            p.part_ml[pidx * 2 + 1] = l;
         }
     }
 }
@@ -337,31 +447,85 @@ struct MergeParams {
     int B, Hq, Hkv, G, D, cap, window, ring, S, chunk;
 };
 
+constexpr int kMergeThreads = 256;
+constexpr int kMergeDims = 128;     // output dims per merge workgroup (32 lanes x float4)
+constexpr int kMergeGroups = 8;     // split groups reduced in parallel
+constexpr int kMaxSplits = 4096;    // splits per (sequence, kv head) the merge accepts
+
+__device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const float w = __shfl_xor(v, o);
+        v = is_max ? fmaxf(v, w) : v + w;
+    }
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    v = red[0];
+    for (int w = 1; w < kMergeThreads / 64; ++w) v = is_max ? fmaxf(v, red[w]) : v + red[w];
+    return v;
+}
+
 // Cross-split merge (ESDecodeAttn.mm:253-273 restated in the log2 domain):
-// M = max_s m_s; O = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).  One thread per
-// output element; splits past the sequence's visible rows were never written.
-__global__ __launch_bounds__(64) void merge_kernel(MergeParams p) {
+// M = max_s m_s; O = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+// One workgroup per (sequence, query head, 128 output dims): the split weights are
+// computed once into LDS, then 8 split groups x 32 float4 lanes stream the partials in
+// parallel and reduce in LDS.  Splits past the sequence's visible rows were never
+// written and are not read.
+__global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
+    __shared__ float wS[kMaxSplits];
+    __shared__ float red[kMergeThreads / 64];
+    __shared__ f32x4 part[kMergeGroups][kMergeDims / 4];
     const int h = blockIdx.y, b = blockIdx.z;
-    const int d = blockIdx.x * 64 + threadIdx.x;
     const int kvh = h / p.G, g = h % p.G;
+    const int tid = threadIdx.x;
     const int pos = p.pos[b];
     const int base = p.row_base ? p.row_base[b] : 0;
     const SeqView sv = seq_view(pos, base, p.cap, p.window, p.ring);
-    if (!sv.ok || d >= p.D) return;
+    if (!sv.ok) return;
     int ns = (sv.nvis + p.chunk - 1) / p.chunk;
     if (ns > p.S) ns = p.S;
     const size_t pbase = ((size_t) b * p.Hkv + kvh) * p.S;
+
     float mx = -INFINITY;
-    for (int s = 0; s < ns; ++s) mx = fmaxf(mx, p.part_ml[((pbase + s) * p.G + g) * 2]);
-    float o = 0.0f, lt = 0.0f;
-    for (int s = 0; s < ns; ++s) {
+    for (int s = tid; s < ns; s += kMergeThreads) mx = fmaxf(mx, p.part_ml[((pbase + s) * p.G + g) * 2]);
+    mx = block_reduce(mx, red, true);
+    float lt = 0.0f;
+    for (int s = tid; s < ns; s += kMergeThreads) {
         const size_t ix = (pbase + s) * p.G + g;
         const float w = __builtin_amdgcn_exp2f(p.part_ml[ix * 2] - mx);
+        wS[s] = w;
         lt += p.part_ml[ix * 2 + 1] * w;
-        o += p.part_acc[ix * p.D + d] * w;
     }
-    const __bf16 r = (__bf16) (o / lt);
-    p.out[((size_t) b * p.Hq + h) * p.D + d] = __builtin_bit_cast(uint16_t, r);
+    lt = block_reduce(lt, red, false);  // its barriers also publish wS
+
+    const int dq = tid & 31, sg = tid >> 5;
+    const int d0 = blockIdx.x * kMergeDims + dq * 4;
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+    int s = sg;
+    for (; s + 3 * kMergeGroups < ns; s += 4 * kMergeGroups) {
+        f32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            v[u] = *reinterpret_cast<const f32x4 *>(p.part_acc + ((pbase + s + u * kMergeGroups) * p.G + g) * p.D + d0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) o += v[u] * wS[s + u * kMergeGroups];
+    }
+    for (; s < ns; s += kMergeGroups)
+        o += *reinterpret_cast<const f32x4 *>(p.part_acc + ((pbase + s) * p.G + g) * p.D + d0) * wS[s];
+    part[sg][dq] = o;
+    __syncthreads();
+    if (tid < kMergeDims / 4) {
+        f32x4 t = part[0][tid];
+#pragma unroll
+        for (int u = 1; u < kMergeGroups; ++u) t += part[u][tid];
+        const float inv = 1.0f / lt;
+        uint16_t *dst = p.out + ((size_t) b * p.Hq + h) * p.D + blockIdx.x * kMergeDims + tid * 4;
+        bf16x4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = (__bf16) (t[e] * inv);
+        *reinterpret_cast<uint2 *>(dst) = __builtin_bit_cast(uint2, r);
+    }
 }
 
 // Plain row copy for multi-row appends (slice_update at rows row0 .. row0 + n - 1).
@@ -457,7 +621,12 @@ int make_plan(const esda_decode_desc *d, Plan *pl) {
         if (c > 8192) c = 8192;
         chunk = (int) c;
     }
-    const int S = (maxvis + chunk - 1) / chunk;
+    int S = (maxvis + chunk - 1) / chunk;
+    if (S > kMaxSplits) {
+        chunk = (maxvis + kMaxSplits - 1) / kMaxSplits;
+        chunk = (chunk + kTile - 1) / kTile * kTile;
+        S = (maxvis + chunk - 1) / chunk;
+    }
     pl->G = G;
     pl->maxvis = maxvis;
     pl->chunk = chunk;
@@ -469,9 +638,14 @@ int make_plan(const esda_decode_desc *d, Plan *pl) {
     return ESDA_OK;
 }
 
+// Waves per workgroup (the head dim is split across them).
+template <int D>
+constexpr int ring_waves() { return 4; }
+
 template <int D, bool SHARED>
 hipError_t launch_attend(const AttendParams &ap, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((attend_kernel<D, SHARED>), grid, dim3(kThreads), 0, st, ap);
+    constexpr int NW = ring_waves<D>();
+    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW>), grid, dim3(64 * NW), 0, st, ap);
     return hipGetLastError();
 }
 
@@ -573,8 +747,8 @@ int esda_decode_stages(const esda_decode_desc *d, const esda_decode_args *a, int
         mp.ring = d->ring;
         mp.S = pl.S;
         mp.chunk = pl.chunk;
-        dim3 grid(d->head_dim / 64, d->num_q_heads, d->batch);
-        hipLaunchKernelGGL(merge_kernel, grid, dim3(64), 0, st, mp);
+        dim3 grid(d->head_dim / kMergeDims, d->num_q_heads, d->batch);
+        hipLaunchKernelGGL(merge_kernel, grid, dim3(kMergeThreads), 0, st, mp);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e, "merge_kernel launch");
     }

@@ -145,9 +145,10 @@ def append(step: Step, k_cache: np.ndarray, v_cache: np.ndarray | None, k_new: n
     """In-place append of the new rows (v_cache None or identical = shared buffer)."""
     d = step.desc()
     vc = k_cache if v_cache is None else v_cache
+    pos_a = _i32(pos)  # keep the converted arrays alive across the C call
+    rb_a = None if row_base is None else _i32(row_base)
     rc = lib().orc_append(ctypes.byref(d), _ptr(k_cache), _ptr(vc), _ptr(k_new),
-                          _ptr(v_new), _ptr(_i32(pos)),
-                          None if row_base is None else _ptr(_i32(row_base)))
+                          _ptr(v_new), _ptr(pos_a), _ptr(rb_a))
     if rc != 0:
         raise ValueError("orc_append rejected the description")
 

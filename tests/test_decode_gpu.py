@@ -120,8 +120,12 @@ EDGE = [
     dict(name="split_odd", B=1, Hq=16, Hkv=8, D=256, cap=1000, window=700, pos=[999], split_rows=208),
     dict(name="max_visible_hint", B=2, Hq=32, Hkv=4, D=512, cap=4096, pos=[700, 900], shared=True,
          max_visible=901),
+    # In-model scale 1.0 on unit-RMS q/k gives logits ~ |q||k| = 512: the reference
+    # composite's bf16 score rounding alone moves the output past the tolerance there
+    # (tests/test_oracle.py::test_refround_coarse_at_in_model_scale), so this case is
+    # gated against fp64 only.
     dict(name="scale_one_in_model", B=1, Hq=32, Hkv=4, D=512, cap=512, pos=[511], shared=True,
-         scale=1.0),
+         scale=1.0, refround=False),
     dict(name="dominant_key", B=1, Hq=8, Hkv=1, D=256, cap=2048, pos=[2047], peaks=1, bump=30.0),
 ]
 

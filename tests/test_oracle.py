@@ -445,3 +445,28 @@ def test_planted_fault_is_caught(fault, pin):
     with orc.planted_fault(fault):
         assert _pins_fail(pin), f"planted fault {fault} went unnoticed"
     pin()  # and the clean oracle passes again
+
+
+def test_append_with_row_base_writes_the_rebased_row():
+    # Regression: the row_base / pos arrays must stay alive across the C call.
+    step = orc.Step(B=2, Hq=4, Hkv=2, D=16, cap=64, window=32)
+    pos, rb = [100, 70], [60, 40]
+    q, kc, vc, kn, vn = make_step_inputs(step, 4, pos)
+    k0 = kc.copy()
+    orc.append(step, kc, vc, kn, vn, pos, rb)
+    d = step.desc()
+    changed = np.nonzero(kc != k0)[0]
+    rows = {(int(i // d.seq_stride), int((i % d.head_stride) // 16)) for i in changed}
+    assert rows <= {(0, 40), (1, 30)} and len(rows) == 2
+
+
+def test_refround_coarse_at_in_model_scale():
+    # Scale 1.0 (in-model, ESAttention.mm:56) on unit-RMS q/k at D=512: logits ~ 512, where
+    # one bf16 ulp of a score (ESAttention.mm:153) is 2..4 -- the reference composite's own
+    # rounding exceeds the 2e-2 bar, so GPU parity at this scale is gated on fp64 only.
+    step = orc.Step(B=1, Hq=8, Hkv=1, D=512, cap=512, scale=1.0)
+    q, kc, vc, kn, vn = make_step_inputs(step, 6, [511], shared_kv=True)
+    orc.append(step, kc, None, kn, None, [511])
+    ref = orc.decode_f64(step, q, kc, kc, [511])
+    rr = orc.from_bf16(orc.decode_refround(step, q, kc, kc, [511])).astype(np.float64)
+    assert np.abs(rr - ref).max() > TOL_MAX
