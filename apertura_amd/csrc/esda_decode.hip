@@ -51,7 +51,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 16;          // MFMA row block; split sizes are multiples of it
 constexpr int kMaxGroup = 16;
-constexpr int kTargetGroups = 512;  // workgroups per launch the split heuristic aims for
+constexpr int kTargetGroups = 256;  // one workgroup per MI355X CU (the ring LDS allows one per CU)
 constexpr float kLog2e = 1.4426950408889634f;
 
 // ------------------------------------------------------------------ per-sequence view
@@ -118,36 +118,33 @@ constexpr float kRescaleSlack = 8.0f;
 // arrive by LDS DMA (global_load_lds_dwordx4: 64 lanes x 16 B land contiguously at
 // M0 + 16*lane), non-temporal, so in-flight data costs no registers and each
 // instruction reads 1 KB of contiguous HBM.  One instruction carries RPI = 512/D rows:
-// instruction i of a stage holds rows i + q*NI (q < RPI) in a 1040-byte block (1 KB +
-// 16 B pad).  Sub-row q is rotated by q*ROT chunks of 16 B, ROT being a whole number of
-// per-wave dim slices, which keeps every 128-bit row read and every 16-bit column
-// gather free of bank conflicts while all addresses stay base + immediate.
+// instruction i of a stage holds rows i + q*NI (q < RPI) in a 1056-byte block (1 KB +
+// 32 B pad), sub-row q at +2D*q bytes.  The 32-byte pad (a measured choice: 16 B leaves
+// both the 128-bit row reads and the transpose reads 2-way bank-conflicted on gfx950)
+// makes both read patterns conflict-free with every address a base plus an immediate.
 template <int D, bool SHARED, int NW>
 struct Ring {
     static constexpr int RPI = 512 / D;                     // rows per DMA instruction
     static constexpr int NI = 16 / RPI;                     // DMA instructions per stage
     static constexpr int CPR = D / 8;                       // 16-byte chunks per row
-    static constexpr int BLK = 1040;                        // LDS bytes per DMA block
+    static constexpr int BLK = 1056;                        // LDS bytes per DMA block
     static constexpr int TB = NI * BLK;                     // one tensor's stage
     static constexpr int SB = (SHARED ? 1 : 2) * TB;        // stage bytes (K [+ V])
     static constexpr int DW = D / NW;                       // dims per wave
     static constexpr int SL = DW / 8;                       // chunks per wave slice
-    static constexpr int ROT = RPI > 1 ? (16 / RPI) / SL : 0;  // sub-row rotation, slices
     static constexpr int KKW = DW / 32;                     // QK k-steps per wave
     static constexpr int DTW = DW / 16;                     // PV dim tiles per wave
     static constexpr int DPT = NI / NW;                     // DMA per wave per tensor
     static constexpr int DPW = DPT * (SHARED ? 1 : 2);      // DMA per wave per stage
     static constexpr int XB = 2 * NW * 64 * 16;             // score-exchange bytes
-    static constexpr int NS_ = (156 * 1024 - XB) / SB;
+    static constexpr int NS_ = (160 * 1024 - XB - 256) / SB;
     static constexpr int NS = NS_ > 16 ? 16 : NS_;          // stages in the ring
     static_assert(DW % 32 == 0 && NI % NW == 0, "wave slices must cover whole MFMA steps");
-    static_assert(RPI == 1 || (16 / RPI) % SL == 0, "rotation must be whole slices");
     static_assert(NS >= 4, "the ring needs at least 4 stages");
     static_assert((NS - 3) * DPW <= 60, "vmcnt holds at most 63 outstanding loads");
     // Byte offset of (row r, chunk cin of wave slice ws) inside a tensor stage.
     __device__ static __forceinline__ int off(int r, int ws, int cin) {
-        const int i = r % NI, q = r / NI;
-        return i * BLK + q * 2 * D + (((ws + q * ROT) % NW) * SL + cin) * 16;
+        return (r % NI) * BLK + (r / NI) * 2 * D + (ws * SL + cin) * 16;
     }
 };
 
@@ -275,9 +272,8 @@ void attend_kernel(AttendParams p) {
     }
     ESDA_WAIT_VM(0);  // Q is in registers before the ring starts counting its own loads
 
-    // DMA source slot of this lane: sub-row q, chunk c of the row (undoing the rotation).
-    const int dq = lane / R::CPR, dp = lane % R::CPR;
-    const int dchunk = ((((dp / R::SL) - dq * R::ROT) % NW + NW) % NW) * R::SL + dp % R::SL;
+    // DMA source slot of this lane: sub-row dq, chunk dchunk of the row.
+    const int dq = lane / R::CPR, dchunk = lane % R::CPR;
     const int nst = (j1 - j0 + 15) / 16;
     // Per-lane byte offsets of this wave's DMA slots inside a stage's row range.
     unsigned dvoff[R::DPT];
@@ -468,14 +464,17 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
 
 // Cross-split merge (ESDecodeAttn.mm:253-273 restated in the log2 domain):
 // M = max_s m_s; O = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
-// One workgroup per (sequence, query head, 128 output dims): the split weights are
-// computed once into LDS, then 8 split groups x 32 float4 lanes stream the partials in
-// parallel and reduce in LDS.  Splits past the sequence's visible rows were never
-// written and are not read.
+// One workgroup per (sequence, query head, 128 output dims); 8 split groups x 32 float4
+// lanes.  Each thread issues its partial loads together with the (m, l) loads, so the
+// whole merge is one memory round trip; the per-split weights are then formed from the
+// block-wide max.  Splits past the sequence's visible rows were never written and are
+// not read.
+constexpr int kMergeRegs = 8;  // splits per thread held in registers (S <= 64 in one pass)
+
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
-    __shared__ float wS[kMaxSplits];
     __shared__ float red[kMergeThreads / 64];
     __shared__ f32x4 part[kMergeGroups][kMergeDims / 4];
+    __shared__ float lsum[kMergeGroups];
     const int h = blockIdx.y, b = blockIdx.z;
     const int kvh = h / p.G, g = h % p.G;
     const int tid = threadIdx.x;
@@ -486,40 +485,64 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
     int ns = (sv.nvis + p.chunk - 1) / p.chunk;
     if (ns > p.S) ns = p.S;
     const size_t pbase = ((size_t) b * p.Hkv + kvh) * p.S;
-
-    float mx = -INFINITY;
-    for (int s = tid; s < ns; s += kMergeThreads) mx = fmaxf(mx, p.part_ml[((pbase + s) * p.G + g) * 2]);
-    mx = block_reduce(mx, red, true);
-    float lt = 0.0f;
-    for (int s = tid; s < ns; s += kMergeThreads) {
-        const size_t ix = (pbase + s) * p.G + g;
-        const float w = __builtin_amdgcn_exp2f(p.part_ml[ix * 2] - mx);
-        wS[s] = w;
-        lt += p.part_ml[ix * 2 + 1] * w;
-    }
-    lt = block_reduce(lt, red, false);  // its barriers also publish wS
-
     const int dq = tid & 31, sg = tid >> 5;
     const int d0 = blockIdx.x * kMergeDims + dq * 4;
-    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-    int s = sg;
-    for (; s + 3 * kMergeGroups < ns; s += 4 * kMergeGroups) {
-        f32x4 v[4];
+
+    float mloc = -INFINITY;
+    float ms[kMergeRegs], ls[kMergeRegs];
+    f32x4 av[kMergeRegs];
+    // Fast path: every split this thread owns fits in registers (ns <= 64).
+    const bool in_regs = ns <= kMergeGroups * kMergeRegs;
+    if (in_regs) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            v[u] = *reinterpret_cast<const f32x4 *>(p.part_acc + ((pbase + s + u * kMergeGroups) * p.G + g) * p.D + d0);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) o += v[u] * wS[s + u * kMergeGroups];
+        for (int u = 0; u < kMergeRegs; ++u) {
+            const int s = sg + u * kMergeGroups;
+            if (s < ns) {
+                const size_t ix = (pbase + s) * p.G + g;
+                av[u] = *reinterpret_cast<const f32x4 *>(p.part_acc + ix * p.D + d0);
+                ms[u] = p.part_ml[ix * 2];
+                ls[u] = p.part_ml[ix * 2 + 1];
+            } else {
+                av[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                ms[u] = -INFINITY;
+                ls[u] = 0.0f;
+            }
+            mloc = fmaxf(mloc, ms[u]);
+        }
+    } else {
+        for (int s = sg; s < ns; s += kMergeGroups) mloc = fmaxf(mloc, p.part_ml[((pbase + s) * p.G + g) * 2]);
     }
-    for (; s < ns; s += kMergeGroups)
-        o += *reinterpret_cast<const f32x4 *>(p.part_acc + ((pbase + s) * p.G + g) * p.D + d0) * wS[s];
+    const float mx = block_reduce(mloc, red, true);
+
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+    float lt = 0.0f;
+    if (in_regs) {
+#pragma unroll
+        for (int u = 0; u < kMergeRegs; ++u) {
+            const float w = __builtin_amdgcn_exp2f(ms[u] - mx);  // 0 for absent splits
+            o += av[u] * w;
+            lt += ls[u] * w;
+        }
+    } else {
+        for (int s = sg; s < ns; s += kMergeGroups) {
+            const size_t ix = (pbase + s) * p.G + g;
+            const float w = __builtin_amdgcn_exp2f(p.part_ml[ix * 2] - mx);
+            o += *reinterpret_cast<const f32x4 *>(p.part_acc + ix * p.D + d0) * w;
+            lt += p.part_ml[ix * 2 + 1] * w;
+        }
+    }
     part[sg][dq] = o;
+    if (dq == 0) lsum[sg] = lt;
     __syncthreads();
     if (tid < kMergeDims / 4) {
         f32x4 t = part[0][tid];
+        float l = lsum[0];
 #pragma unroll
-        for (int u = 1; u < kMergeGroups; ++u) t += part[u][tid];
-        const float inv = 1.0f / lt;
+        for (int u = 1; u < kMergeGroups; ++u) {
+            t += part[u][tid];
+            l += lsum[u];
+        }
+        const float inv = 1.0f / l;
         uint16_t *dst = p.out + ((size_t) b * p.Hq + h) * p.D + blockIdx.x * kMergeDims + tid * 4;
         bf16x4 r;
 #pragma unroll

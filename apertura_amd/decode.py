@@ -131,3 +131,37 @@ def kv_append(cache: torch.Tensor, src: torch.Tensor, row0: torch.Tensor, stream
     check(lib().esda_kv_append(_dev_ptr(cache, torch.bfloat16), cache.stride(0), cache.stride(1),
                                B, Hkv, D, cap, _dev_ptr(src, torch.bfloat16), src.shape[2],
                                _dev_ptr(row0), _stream_ptr(stream)))
+
+
+class DecodeCall:
+    """A decode step with its C-ABI arguments marshalled once (the host-side cost of a
+    launch is then one ctypes call).  Tensors are referenced, not copied: refill q,
+    k_new, v_new and pos in place between calls.  Also usable under HIP graph capture
+    (the library issues only kernel launches on the given stream)."""
+
+    def __init__(self, step: DecodeStep, q, k_new, v_new, k_cache, v_cache, pos, row_base=None,
+                 out=None, workspace=None, stages: int = STAGE_ATTEND | STAGE_MERGE):
+        if out is None:
+            out = torch.empty_like(q)
+        if workspace is None:
+            workspace = new_workspace(step, q.device)
+        # validate once through the regular path (raises on any mismatch)
+        self._keep = (q, k_new, v_new, k_cache, v_cache, pos, row_base, out, workspace)
+        self.step, self.out, self.workspace, self.stages = step, out, workspace, stages
+        bf = torch.bfloat16
+        vc = k_cache if (v_cache is None or step.kv_shared) else v_cache
+        self._desc = step.desc()
+        self._args = DecodeArgs(_dev_ptr(q, bf), _dev_ptr(k_new, bf),
+                                _dev_ptr(v_new, bf) if (v_new is not None and not step.kv_shared) else None,
+                                _dev_ptr(k_cache, bf), _dev_ptr(vc, bf), _dev_ptr(pos),
+                                _dev_ptr(row_base), _dev_ptr(out, bf), _dev_ptr(workspace),
+                                workspace.numel() * workspace.element_size())
+        self._fn = lib().esda_decode_stages
+        self._pd, self._pa = ctypes.byref(self._desc), ctypes.byref(self._args)
+
+    def __call__(self, stream=None, stages: int | None = None) -> torch.Tensor:
+        rc = self._fn(self._pd, self._pa, self.stages if stages is None else stages,
+                      _stream_ptr(stream))
+        if rc:
+            check(rc)
+        return self.out
