@@ -13,7 +13,13 @@ write + new-row read and write.  `roofline` prices the dominant kernel (the spli
 attend kernel, timed alone with HIP events on the launch stream); `cpu_baseline` times
 the CPU oracle's reference-rounding restatement on the same inputs.
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c2|c1|c3] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c2|c1|c3|c5] [--no-cpu]
+
+Workload c5 is the full Gemma-4-31B-shaped attention step: 60 layers (every 6th
+global: D=512, Hkv=4, k_eq_v, linear caches; the rest local: D=256, Hkv=16, window
+1024 over a 1024-row ring), B=32, lengths ~ U[1024, 32768]; each layer appends and
+attends in order (one esda_decode per layer, 120 kernels per step, replayed from a HIP
+graph).  It reports total attention us per token step.
 """
 from __future__ import annotations
 
@@ -44,6 +50,16 @@ WORKLOADS = {
                pos=lambda rng, B: [131071], scale=512 ** -0.5),
 }
 
+# C5 layer types (ESModelConfig.mm:82-86: every 6th layer is global, the last one too).
+C5_LAYERS = 60
+C5_B = 32
+C5_LOCAL = dict(Hq=32, Hkv=16, D=256, cap=1024, window=1024, ring=True, shared=False, scale=1 / 16)
+C5_GLOBAL = dict(Hq=32, Hkv=4, D=512, window=0, ring=False, shared=True, scale=512 ** -0.5)
+
+
+def c5_is_global(layer: int) -> bool:
+    return layer % 6 == 5 or layer == C5_LAYERS - 1
+
 
 def visible_rows(w, pos):
     out = []
@@ -66,8 +82,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c4", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c4", choices=sorted(WORKLOADS) + ["c5"])
     ap.add_argument("--split-rows", type=int, default=0)
+    ap.add_argument("--local-split-rows", type=int, default=0, help="c5: split rows of local layers")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=16)
     args = ap.parse_args()
@@ -79,6 +96,8 @@ def main() -> int:
 
     from apertura_amd.decode import DecodeCall, DecodeStep, STAGE_ATTEND, new_workspace
 
+    if args.workload == "c5":
+        return bench_c5(args)
     w = WORKLOADS[args.workload]
     rng = np.random.default_rng(1234)
     pos = w["pos"](rng, w["B"])
@@ -181,6 +200,115 @@ def main() -> int:
             "kernel_us": round(ms_attend * 1e3, 3),
         },
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_c5(args) -> int:
+    """60-layer attention step at B=32 (see the module docstring)."""
+    import numpy as np
+    import torch
+
+    from apertura_amd.decode import DecodeCall, DecodeStep, STAGE_ATTEND
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(55)
+    lens = [int(x) for x in rng.integers(1024, 32769, size=C5_B)]
+    pos = [n - 1 for n in lens]
+    gcap = max(lens)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(55)
+
+    def rms_bf16(shape):
+        out = torch.empty(shape, device=dev, dtype=torch.bfloat16)
+        flat = out.view(-1, shape[-1])
+        for r0 in range(0, flat.shape[0], 1 << 20):
+            x = torch.randn((min(1 << 20, flat.shape[0] - r0), shape[-1]), device=dev, generator=gen)
+            flat[r0:r0 + x.shape[0]] = (x * torch.rsqrt(x.square().mean(-1, keepdim=True) + 1e-6)).bfloat16()
+        return out
+
+    pos_d = torch.tensor(pos, dtype=torch.int32, device=dev)
+    total_global_rows = sum(lens) * C5_GLOBAL["Hkv"]
+    g_split = args.split_rows or max(64, -(-total_global_rows // (4 * 256)) // 64 * 64)
+    l_split = args.local_split_rows
+    calls, kinds, nbytes = [], [], 0
+    shared_q = {}
+    for layer in range(C5_LAYERS):
+        t = C5_GLOBAL if c5_is_global(layer) else C5_LOCAL
+        cap = gcap if c5_is_global(layer) else t["cap"]
+        key = "g" if c5_is_global(layer) else "l"
+        if key not in shared_q:
+            shared_q[key] = (rms_bf16((C5_B, t["Hq"], t["D"])), rms_bf16((C5_B, t["Hkv"], t["D"])),
+                             None if t["shared"] else rms_bf16((C5_B, t["Hkv"], t["D"])))
+        q, kn, vn = shared_q[key]
+        kc = rms_bf16((C5_B, t["Hkv"], cap, t["D"]))
+        vc = kc if t["shared"] else rms_bf16((C5_B, t["Hkv"], cap, t["D"]))
+        step = DecodeStep.for_cache(kc, t["Hq"], window=t["window"], ring=t["ring"], kv_shared=t["shared"],
+                                    scale=t["scale"], split_rows=g_split if c5_is_global(layer) else l_split)
+        calls.append(DecodeCall(step, q, kn, vn, kc, vc, pos_d))
+        kinds.append(key)
+        vis = [min(n, t["window"]) if t["window"] else n for n in lens]
+        row = t["D"] * 2 * (1 if t["shared"] else 2)
+        nbytes += sum(vis) * t["Hkv"] * row + 2 * C5_B * t["Hq"] * t["D"] * 2 + 2 * C5_B * t["Hkv"] * row
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+
+    def step_all(stages=3, only=None):
+        for c, k in zip(calls, kinds):
+            if only is None or k == only:
+                c(stream, stages)
+
+    def graph_of(stages, only=None):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            step_all(stages, only)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=stream):
+                step_all(stages, only)
+        return g
+
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, args.warmup // 10)):
+            step_all()
+        ms_eager = timed(step_all, max(1, args.steps // 20))
+        g_full, g_att = graph_of(3), graph_of(STAGE_ATTEND)
+        ms_graph = timed(g_full.replay, max(2, args.steps // 10))
+        ms_att = timed(g_att.replay, max(2, args.steps // 10))
+        ms_local = timed(graph_of(3, "l").replay, max(2, args.steps // 10))
+        ms_global = timed(graph_of(3, "g").replay, max(2, args.steps // 10))
+    gbs = nbytes / (ms_graph * 1e-3) / 1e9
+    line = {
+        "metric": "decode-attn HBM GB/s (and us/step) at Gemma-4-31B shapes, 1 GPU",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": max(2, args.steps // 10), "warmup": args.warmup,
+        "ms_per_step": round(ms_graph, 6), "us_per_step": round(ms_graph * 1e3, 3),
+        "us_per_step_eager": round(ms_eager * 1e3, 3), "us_per_step_graph": round(ms_graph * 1e3, 3),
+        "timing": "HIP graph replay of the 60-layer step (120 kernels)",
+        "pct_of_hbm_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) rows, unit-RMS, bf16)",
+        "config": {"workload": "C5 Gemma-4-31B attention step: 60 layers (50 local D256 ring 1024, "
+                               "10 global D512 k_eq_v), B=32, len~U[1024,32768]",
+                   "batch": C5_B, "lengths_min_mean_max": [min(lens), sum(lens) // len(lens), max(lens)],
+                   "global_split_rows": g_split, "local_split_rows": l_split or "auto",
+                   "algorithmic_bytes_per_step": nbytes,
+                   "us_50_local_layers": round(ms_local * 1e3, 1), "us_10_global_layers": round(ms_global * 1e3, 1)},
+        "roofline": {"bound": "hbm", "kernel": "attend_kernel (all 60 layers, merges excluded)",
+                     "achieved": round(nbytes / (ms_att * 1e-3) / 1e9, 2), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(nbytes / (ms_att * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": None, "kernel_us": round(ms_att * 1e3, 3)},
+        "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
     return 0
