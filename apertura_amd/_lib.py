@@ -1,4 +1,5 @@
-"""ctypes binding of libesda.so (the C ABI declared in include/esda.h).
+"""ctypes binding of libesda.so (the C ABI declared in include/esda.h and
+include/esda_cache.h).
 
 The library is loaded from the package directory only (built in-tree by
 ``apertura_amd/build.py``); a missing library raises instead of falling back.
@@ -16,12 +17,20 @@ ESDA_OK = 0
 ERROR_NAMES = {1: "invalid argument", 2: "runtime error", 3: "HIP error", 4: "workspace",
                5: "device"}
 
-# Every symbol include/esda.h declares (checked by tests/test_abi.py).
+# Every function include/*.h declares (checked by tests/test_abi.py).
 EXPORTS = (
+    # include/esda.h
     "esda_decode_workspace_size", "esda_decode", "esda_decode_stages", "esda_decode_status",
-    "esda_kv_append",
-    "esda_last_error", "esda_version",
+    "esda_kv_append", "esda_decode_raw_workspace_size", "esda_decode_raw",
+    "esda_decode_raw_stages", "esda_fill_i32", "esda_last_error", "esda_version",
+    # include/esda_cache.h
+    "esda_cache_create", "esda_cache_destroy", "esda_cache_update", "esda_cache_update_raw",
+    "esda_cache_current", "esda_cache_decode", "esda_cache_decode_raw", "esda_cache_slot",
+    "esda_cache_seq_len", "esda_cache_mark_step", "esda_cache_reset", "esda_cache_save_snapshot",
+    "esda_cache_restore_snapshot", "esda_cache_mark_rewind_point", "esda_cache_rewind_to_mark",
+    "esda_decode_attn_global",
 )
+_VOID = ("esda_cache_destroy", "esda_cache_mark_step", "esda_cache_reset")
 
 
 class EsdaError(RuntimeError):
@@ -50,6 +59,33 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class RawDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32), ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("cap", ctypes.c_int32), ("seq_stride", ctypes.c_int64),
+        ("head_stride", ctypes.c_int64), ("max_visible", ctypes.c_int32),
+        ("split_rows", ctypes.c_int32), ("scale", ctypes.c_float), ("eps", ctypes.c_float),
+    ]
+
+
+class RawArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k_new", ctypes.c_void_p), ("raw_cache", ctypes.c_void_p),
+        ("pos", ctypes.c_void_p), ("kw", ctypes.c_void_p), ("inv_freq", ctypes.c_void_p),
+        ("out", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class View(ctypes.Structure):
+    """esda_view: element (h, r, d) at data[h*head_stride + r*head_dim + d]."""
+    _fields_ = [
+        ("data", ctypes.c_void_p), ("kv_heads", ctypes.c_int32), ("rows", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("head_stride", ctypes.c_int64),
+    ]
+
+
 def library_path() -> str:
     return _LIB_PATH
 
@@ -69,11 +105,36 @@ def lib() -> ctypes.CDLL:
                                          ctypes.c_int, P]
         L.esda_decode_status.argtypes = [ctypes.POINTER(DecodeDesc), P, ctypes.POINTER(i32), P]
         L.esda_kv_append.argtypes = [P, i64, i64, i32, i32, i32, i32, P, i32, P, P]
+        L.esda_decode_raw_workspace_size.argtypes = [ctypes.POINTER(RawDesc), ctypes.POINTER(sz)]
+        L.esda_decode_raw.argtypes = [ctypes.POINTER(RawDesc), ctypes.POINTER(RawArgs), P]
+        L.esda_decode_raw_stages.argtypes = [ctypes.POINTER(RawDesc), ctypes.POINTER(RawArgs),
+                                             ctypes.c_int, P]
+        L.esda_fill_i32.argtypes = [P, i32, i32, P]
         L.esda_last_error.restype = ctypes.c_char_p
         L.esda_last_error.argtypes = []
         L.esda_version.argtypes = []
+        f32, VP = ctypes.c_float, ctypes.POINTER(View)
+        pi32 = ctypes.POINTER(i32)
+        L.esda_cache_create.argtypes = [i32, ctypes.POINTER(P)]
+        L.esda_cache_destroy.argtypes = [P]
+        L.esda_cache_update.argtypes = [P, i32, P, P, i32, i32, i32, i32, i32, P, VP, VP]
+        L.esda_cache_update_raw.argtypes = [P, i32, P, i32, i32, i32, i32, P, VP, pi32, pi32]
+        L.esda_cache_current.argtypes = [P, i32, i32, VP, VP]
+        L.esda_cache_decode.argtypes = [P, i32, P, i32, P, P, i32, i32, i32, f32, P, P]
+        L.esda_cache_decode_raw.argtypes = [P, i32, P, i32, P, i32, P, f32, P, i32, P, P]
+        L.esda_cache_slot.argtypes = [P, i32, pi32, pi32, pi32, pi32]
+        L.esda_cache_seq_len.argtypes = [P]
+        L.esda_cache_mark_step.argtypes = [P, i32]
+        L.esda_cache_reset.argtypes = [P]
+        L.esda_cache_save_snapshot.argtypes = [P, ctypes.c_char_p, ctypes.c_char_p, i32]
+        L.esda_cache_restore_snapshot.argtypes = [P, ctypes.c_char_p, ctypes.c_char_p]
+        L.esda_cache_mark_rewind_point.argtypes = [P, i32]
+        L.esda_cache_rewind_to_mark.argtypes = [P]
+        L.esda_decode_attn_global.argtypes = [P, i32, P, i32, i32, i32, P, f32, P, i32, P, P]
         for name in EXPORTS:
-            if name not in ("esda_last_error", "esda_version"):
+            if name in _VOID:
+                getattr(L, name).restype = None
+            elif name not in ("esda_last_error", "esda_version"):
                 getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib

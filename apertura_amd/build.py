@@ -14,9 +14,16 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libesda.so")
-HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.environ.get("HIPCC", os.path.join(ROCM, "bin", "hipcc"))
+CXX = os.environ.get("CXX", "g++")
 
-SOURCES = ["esda_decode.hip", "esda_raw.hip", "es_api.cpp"]
+SOURCES = [
+    "esda_decode.hip",
+    "es/ESKVCache.cpp",
+    "es/ESDecodeAttn.cpp",
+    "es/es_capi.cpp",
+]
 
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -35,9 +42,12 @@ def build(verbose: bool = False) -> str:
     inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
     for src in sources():
         obj = os.path.join(CSRC, os.path.basename(src) + ".o")
+        # ES* C++ layer: host code only (HIP runtime API and the esda C ABI), built by
+        # the host compiler so no device code is generated for it.
         cmd = [HIPCC] + HIP_FLAGS + inc + ["-c", src, "-o", obj]
         if src.endswith(".cpp"):
-            cmd = [HIPCC, "-O2", "-std=c++17", "-fPIC"] + inc + ["-c", src, "-o", obj]
+            cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+                   "-I", os.path.join(ROCM, "include")] + inc + ["-c", src, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)

@@ -1,0 +1,185 @@
+"""Python front end of the ES* C++ layer (include/esda_cache.h): ``ESKVCache`` and
+``es_decode_attn_global`` with the reference's method names and argument meaning
+(Apertura ESKVCache.h:44-224, ESDecodeAttn.h:22-28).
+
+Row tensors are torch bf16 GPU tensors [kvHeads, n, headDim] with contiguous rows.
+Views returned by update / current are ``CacheView`` records (non-owning device
+pointers into the cache's buffers, valid until the slot next grows or is reset);
+``CacheView.torch()`` copies one out as a torch tensor.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from ._lib import View, check, lib
+from .decode import _dev_ptr, _stream_ptr
+
+
+@dataclass
+class CacheView:
+    data: int
+    kv_heads: int
+    rows: int
+    head_dim: int
+    head_stride: int  # elements
+
+    @classmethod
+    def of(cls, v: View) -> "CacheView":
+        return cls(int(v.data or 0), v.kv_heads, v.rows, v.head_dim, int(v.head_stride))
+
+    def torch(self, device="cuda") -> torch.Tensor:
+        """Copy of the viewed rows, [kv_heads, rows, head_dim] bf16 on `device`."""
+        out = torch.empty((self.kv_heads, self.rows, self.head_dim), dtype=torch.bfloat16, device=device)
+        _hip_copy_2d(out.data_ptr(), self.rows * self.head_dim * 2, self.data, self.head_stride * 2,
+                     self.rows * self.head_dim * 2, self.kv_heads)
+        return out
+
+
+_hip = None
+
+
+def _hip_copy_2d(dst: int, dpitch: int, src: int, spitch: int, width: int, height: int) -> None:
+    """Synchronous device-to-device 2-D copy through the HIP runtime torch already uses."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipMemcpy2D.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t,
+                                     ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int]
+        _hip.hipMemcpy2D.restype = ctypes.c_int
+    torch.cuda.synchronize()
+    rc = _hip.hipMemcpy2D(dst, dpitch, src, spitch, width, height, 3)  # hipMemcpyDeviceToDevice
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpy2D failed ({rc})")
+
+
+def _rows(t: torch.Tensor, what: str):
+    if t.dim() != 3 or t.dtype != torch.bfloat16 or not t.is_contiguous():
+        raise ValueError(f"{what} must be a contiguous bf16 [kvHeads, n, headDim] tensor")
+    return t.shape
+
+
+class ESKVCache:
+    """Per-layer KV storage on the GPU (the reference's ESKVCache)."""
+
+    kGrowChunk = 256
+
+    def __init__(self, num_layers: int):
+        h = ctypes.c_void_p()
+        check(lib().esda_cache_create(num_layers, ctypes.byref(h)))
+        self._h = h
+        self._num_layers = num_layers
+
+    def close(self) -> None:
+        if self._h:
+            lib().esda_cache_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def update(self, layer: int, k_new: torch.Tensor, v_new: torch.Tensor, max_keep: int = 0,
+               prealloc: bool = False, stream=None) -> tuple[CacheView, CacheView]:
+        kvh, n, hd = _rows(k_new, "k_new")
+        _rows(v_new, "v_new")
+        kv, vv = View(), View()
+        check(lib().esda_cache_update(self._h, layer, _dev_ptr(k_new), _dev_ptr(v_new), kvh, n, hd, max_keep,
+                                      1 if prealloc else 0, _stream_ptr(stream), ctypes.byref(kv),
+                                      ctypes.byref(vv)))
+        return CacheView.of(kv), CacheView.of(vv)
+
+    def update_raw(self, layer: int, k_new: torch.Tensor, prealloc: bool, stream=None):
+        """Returns (view, len, pitch) (ESKVCache::Raw without the buffer handle)."""
+        kvh, n, hd = _rows(k_new, "k_new")
+        v, ln, pitch = View(), ctypes.c_int32(), ctypes.c_int32()
+        check(lib().esda_cache_update_raw(self._h, layer, _dev_ptr(k_new), kvh, n, hd, 1 if prealloc else 0,
+                                          _stream_ptr(stream), ctypes.byref(v), ctypes.byref(ln),
+                                          ctypes.byref(pitch)))
+        return CacheView.of(v), int(ln.value), int(pitch.value)
+
+    def current(self, layer: int, prealloc: bool) -> tuple[CacheView, CacheView]:
+        kv, vv = View(), View()
+        check(lib().esda_cache_current(self._h, layer, 1 if prealloc else 0, ctypes.byref(kv), ctypes.byref(vv)))
+        return CacheView.of(kv), CacheView.of(vv)
+
+    def decode(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, max_keep: int,
+               scale: float, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """Fused append + attention of one decode step; v_new may be k_new itself
+        (attention_k_eq_v: one shared K=V buffer).  Returns [numQHeads, headDim] bf16."""
+        kvh, n, hd = _rows(k_new, "k_new")
+        _rows(v_new, "v_new")
+        if n != 1:
+            raise ValueError("decode appends exactly one row")
+        hq = q.numel() // hd
+        if out is None:
+            out = torch.empty((hq, hd), dtype=torch.bfloat16, device=q.device)
+        check(lib().esda_cache_decode(self._h, layer, _dev_ptr(q, torch.bfloat16), hq, _dev_ptr(k_new),
+                                      _dev_ptr(v_new), kvh, hd, max_keep, scale, _dev_ptr(out, torch.bfloat16),
+                                      _stream_ptr(stream)))
+        return out
+
+    def decode_raw(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, kw: torch.Tensor, eps: float,
+                   inv_freq, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """Fused updateRaw + esDecodeAttnGlobal of one decode step (head dim 512)."""
+        kvh, n, hd = _rows(k_new, "k_new")
+        if n != 1 or hd != 512:
+            raise ValueError("decode_raw appends one 512-dim row per kv head")
+        hq = q.numel() // 512
+        if out is None:
+            out = torch.empty((hq, 512), dtype=torch.bfloat16, device=q.device)
+        f = (ctypes.c_float * len(inv_freq))(*[float(x) for x in inv_freq])
+        check(lib().esda_cache_decode_raw(self._h, layer, _dev_ptr(q, torch.bfloat16), hq, _dev_ptr(k_new), kvh,
+                                          _dev_ptr(kw, torch.bfloat16), eps, f, len(inv_freq),
+                                          _dev_ptr(out, torch.bfloat16), _stream_ptr(stream)))
+        return out
+
+    def slot(self, layer: int) -> dict:
+        ln, st, cap, fl = (ctypes.c_int32() for _ in range(4))
+        check(lib().esda_cache_slot(self._h, layer, ctypes.byref(ln), ctypes.byref(st), ctypes.byref(cap),
+                                    ctypes.byref(fl)))
+        f = int(fl.value)
+        return {"len": int(ln.value), "start": int(st.value), "capacity": int(cap.value),
+                "lost": bool(f & 1), "shared": bool(f & 2), "raw": bool(f & 4)}
+
+    def seq_len(self) -> int:
+        return lib().esda_cache_seq_len(self._h)
+
+    def mark_step(self, n_new: int) -> None:
+        lib().esda_cache_mark_step(self._h, n_new)
+
+    def reset(self) -> None:
+        lib().esda_cache_reset(self._h)
+
+    # Not implemented by the library: the reference's failure values.
+    def save_snapshot(self, path: str, fingerprint: str, pos: int) -> bool:
+        return bool(lib().esda_cache_save_snapshot(self._h, path.encode(), fingerprint.encode(), pos))
+
+    def restore_snapshot(self, path: str, fingerprint: str) -> int:
+        return lib().esda_cache_restore_snapshot(self._h, path.encode(), fingerprint.encode())
+
+    def mark_rewind_point(self, pos: int) -> bool:
+        return bool(lib().esda_cache_mark_rewind_point(self._h, pos))
+
+    def rewind_to_mark(self) -> int:
+        return lib().esda_cache_rewind_to_mark(self._h)
+
+
+def es_decode_attn_global(q: torch.Tensor, raw_buf: torch.Tensor, length: int, pitch: int, kw: torch.Tensor,
+                          eps: float, inv_freq, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """esDecodeAttnGlobal: q [numQ, 512], raw_buf the unsliced [numKV, pitch, 512] buffer
+    whose rows 0 .. length-1 are attended; returns [numQ, 512] bf16."""
+    if raw_buf.dim() != 3 or not raw_buf.is_contiguous():
+        raise ValueError("raw_buf must be a contiguous [numKV, pitch, 512] tensor")
+    hq = q.numel() // 512
+    if out is None:
+        out = torch.empty((hq, 512), dtype=torch.bfloat16, device=q.device)
+    f = (ctypes.c_float * len(inv_freq))(*[float(x) for x in inv_freq])
+    check(lib().esda_decode_attn_global(_dev_ptr(q, torch.bfloat16), hq, _dev_ptr(raw_buf, torch.bfloat16),
+                                        raw_buf.shape[0], length, pitch, _dev_ptr(kw, torch.bfloat16), eps, f,
+                                        len(inv_freq), _dev_ptr(out, torch.bfloat16), _stream_ptr(stream)))
+    return out

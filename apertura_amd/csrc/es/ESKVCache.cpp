@@ -1,0 +1,425 @@
+// ESKVCache.cpp -- GPU KV cache with the reference's update / updateRaw / current /
+// reset behaviour (Apertura ESKVCache.mm:19-119, 458-504, 622-638).  Device work goes
+// through the HIP runtime (buffer copies) and the esda C ABI (decode kernels).
+#include "es/ESKVCache.h"
+
+#include <algorithm>
+#include <stdexcept>
+#include <string>
+
+#include "es/ESDecodeAttn.h"
+#include "esda.h"
+
+namespace es {
+namespace {
+
+int roundUpChunk(int n) {
+    return (n + ESKVCache::kGrowChunk - 1) / ESKVCache::kGrowChunk * ESKVCache::kGrowChunk;
+}
+
+void hipCheck(hipError_t e, const char *what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// esda status -> the exception type the reference throws for the same condition.
+void esdaCheck(int rc) {
+    if (rc == ESDA_OK) return;
+    if (rc == ESDA_ERR_INVALID_ARGUMENT) throw std::invalid_argument(esda_last_error());
+    throw std::runtime_error(esda_last_error());
+}
+
+// A [kvHeads, n, headDim] bf16 tensor whose rows are contiguous inside each head.
+void checkRows(const Tensor &t, const char *what) {
+    if (!t.defined() || t.dim() != 3 || t.dtype != Dtype::bf16)
+        throw std::invalid_argument(std::string(what) + ": expected a [kvHeads, n, headDim] bf16 tensor");
+    if (t.strides[2] != 1 || t.strides[1] != t.shape[2] || t.strides[0] < t.shape[1] * t.shape[2])
+        throw std::invalid_argument(std::string(what) + ": rows must be contiguous within each head");
+    if (t.shape[0] <= 0 || t.shape[1] <= 0 || t.shape[2] <= 0 || (t.shape[2] % 8))
+        throw std::invalid_argument(std::string(what) + ": empty tensor or headDim not a multiple of 8");
+}
+
+// dst[h, dr0 + i, :] = src[h, sr0 + i, :] for i < n and every head h.
+void copyRows(const Tensor &dst, int dr0, const Tensor &src, int sr0, int n, hipStream_t st) {
+    if (n <= 0) return;
+    const size_t rowBytes = (size_t) src.shape[2] * 2;
+    auto *d = static_cast<char *>(dst.data) + (size_t) dr0 * dst.strides[1] * 2;
+    auto *s = static_cast<const char *>(src.data) + (size_t) sr0 * src.strides[1] * 2;
+    hipCheck(hipMemcpy2DAsync(d, (size_t) dst.strides[0] * 2, s, (size_t) src.strides[0] * 2,
+                              (size_t) n * rowBytes, (size_t) src.shape[0], hipMemcpyDeviceToDevice, st),
+             "ESKVCache row copy");
+}
+
+Tensor zeros(const std::vector<int64_t> &shape, hipStream_t st) {
+    Tensor t = Tensor::empty(shape, Dtype::bf16);
+    hipCheck(hipMemsetAsync(t.data, 0, t.nbytes(), st), "ESKVCache zero fill");
+    return t;
+}
+
+// An owned copy of `src` (the reference stores the caller's array itself; here the
+// caller keeps ownership of its memory, so the value is copied).
+Tensor clone(const Tensor &src, hipStream_t st) {
+    Tensor t = Tensor::empty(src.shape, Dtype::bf16);
+    copyRows(t, 0, src, 0, (int) src.shape[1], st);
+    return t;
+}
+
+// Along the sequence axis: [a ; b] (a view-aware concatenate).
+Tensor concatRows(const Tensor &a, const Tensor &b, hipStream_t st) {
+    if (a.shape[0] != b.shape[0] || a.shape[2] != b.shape[2])
+        throw std::invalid_argument("ESKVCache::update: kv heads / head dim differ from the cached rows");
+    Tensor t = Tensor::empty({a.shape[0], a.shape[1] + b.shape[1], a.shape[2]}, Dtype::bf16);
+    copyRows(t, 0, a, 0, (int) a.shape[1], st);
+    copyRows(t, (int) a.shape[1], b, 0, (int) b.shape[1], st);
+    return t;
+}
+
+Tensor liveView(const Tensor &buf, int start, int len) {
+    if (start == 0 && len == buf.shape[1]) return buf;
+    return buf.slice(1, start, len);
+}
+
+}  // namespace
+
+ESKVCache::ESKVCache(int numLayers) : k_(numLayers), v_(numLayers), slots_(numLayers) {
+    if (numLayers <= 0) throw std::invalid_argument("ESKVCache: numLayers must be positive");
+}
+
+void ESKVCache::checkLayer(int layer) const {
+    if (layer < 0 || layer >= (int) slots_.size()) throw std::invalid_argument("ESKVCache: layer out of range");
+}
+
+const ESKVCache::Slot &ESKVCache::slotAt(int layer) const {
+    checkLayer(layer);
+    return slots_[layer];
+}
+
+int ESKVCache::slotCapacity(int layer) const {
+    const Slot &s = slotAt(layer);
+    return s.k ? (int) s.k->shape[1] : 0;
+}
+
+// Make room for nNew rows at s.len (ESKVCache.mm:74-94): when they do not fit, the live
+// range [start, len) moves to the front of a zeroed buffer of roundUpChunk(content +
+// nNew + kGrowChunk) rows.  Raw slots (no v) keep rows from 0 (ESKVCache.mm:490-496).
+void ESKVCache::growSlot(Slot &s, int nNew, hipStream_t st, bool compactStart) {
+    const int cap = (int) s.k->shape[1];
+    if (s.len + nNew <= cap) return;
+    const int from = compactStart ? s.start : 0;
+    const int content = s.len - from;
+    const int newCap = roundUpChunk(content + nNew + kGrowChunk);
+    const int64_t kvH = s.k->shape[0], hd = s.k->shape[2];
+    Tensor nk = zeros({kvH, newCap, hd}, st);
+    copyRows(nk, 0, *s.k, from, content, st);
+    std::optional<Tensor> nv;
+    if (s.v) {
+        if (s.shared) {
+            nv = nk;
+        } else {
+            nv = zeros({kvH, newCap, hd}, st);
+            copyRows(*nv, 0, *s.v, from, content, st);
+        }
+    }
+    // The old buffers may still be read by queued work: finish it before releasing them.
+    hipCheck(hipStreamSynchronize(st), "ESKVCache compaction");
+    s.k = nk;
+    s.v = nv;
+    if (compactStart) {
+        if (s.start > 0) s.lost = true;
+        s.len = content;
+        s.start = 0;
+    }
+}
+
+std::pair<Tensor, Tensor> ESKVCache::update(int layer, const Tensor &kNew, const Tensor &vNew, int maxKeep,
+                                            bool prealloc, hipStream_t st) {
+    checkLayer(layer);
+    checkRows(kNew, "ESKVCache::update kNew");
+    checkRows(vNew, "ESKVCache::update vNew");
+    if (kNew.shape[1] != vNew.shape[1])
+        throw std::invalid_argument("ESKVCache::update: kNew and vNew hold different row counts");
+    if (!prealloc) {
+        // Legacy mode (ESKVCache.mm:35-55): concat-grow, then keep the last maxKeep keys.
+        auto &K = k_[layer];
+        auto &V = v_[layer];
+        if (!K) {
+            K = clone(kNew, st);
+            V = clone(vNew, st);
+        } else {
+            K = concatRows(*K, kNew, st);
+            V = concatRows(*V, vNew, st);
+        }
+        if (maxKeep > 0 && K->shape[1] > maxKeep) {
+            const int len = (int) K->shape[1], vlen = (int) V->shape[1];
+            K = K->slice(1, len - maxKeep, len);
+            V = V->slice(1, vlen - maxKeep, vlen);
+        }
+        return {*K, *V};
+    }
+
+    Slot &s = slots_[layer];
+    // Mode-mismatch guard (ESKVCache.mm:59-62): raw rows are pre-norm, not K/V.
+    if (s.k && !s.v)
+        throw std::runtime_error("ESKVCache::update: slot holds raw-K content — not usable "
+                                 "by the composite path; re-prime the cache");
+    const bool aliased = kNew.data == vNew.data;
+    if (s.shared && !aliased)
+        throw std::runtime_error("ESKVCache::update: slot holds one shared K=V buffer; vNew must alias kNew");
+    const int nNew = (int) kNew.shape[1];
+    if (!s.k) {
+        // First append: capacity == content (ESKVCache.mm:69-73).  vNew aliasing kNew
+        // (attention_k_eq_v) starts one shared K=V buffer.
+        s.k = clone(kNew, st);
+        s.shared = aliased;
+        s.v = aliased ? *s.k : clone(vNew, st);
+        s.len = nNew;
+        s.start = 0;
+    } else {
+        if (kNew.shape[0] != s.k->shape[0] || kNew.shape[2] != s.k->shape[2])
+            throw std::invalid_argument("ESKVCache::update: kv heads / head dim differ from the slot");
+        growSlot(s, nNew, st, true);
+        // In-place append at row len (ESKVCache.mm:95-99).
+        copyRows(*s.k, s.len, kNew, 0, nNew, st);
+        if (!s.shared) copyRows(*s.v, s.len, vNew, 0, nNew, st);
+        s.len += nNew;
+    }
+    // Sliding-window eviction advances the logical start (ESKVCache.mm:102-104).
+    if (maxKeep > 0 && s.len - s.start > maxKeep) s.start = s.len - maxKeep;
+    return {liveView(*s.k, s.start, s.len), liveView(*s.v, s.start, s.len)};
+}
+
+std::pair<Tensor, Tensor> ESKVCache::current(int layer, bool prealloc) const {
+    checkLayer(layer);
+    if (!prealloc) {
+        if (!k_[layer]) throw std::runtime_error("ESKVCache::current: layer holds no rows");
+        return {*k_[layer], *v_[layer]};
+    }
+    const Slot &s = slots_[layer];
+    if (!s.k || !s.v) throw std::runtime_error("ESKVCache::current: layer holds no composite rows");
+    return {liveView(*s.k, s.start, s.len), liveView(*s.v, s.start, s.len)};
+}
+
+ESKVCache::Raw ESKVCache::updateRaw(int layer, const Tensor &kNew, bool prealloc, hipStream_t st) {
+    checkLayer(layer);
+    checkRows(kNew, "ESKVCache::updateRaw kNew");
+    const int nNew = (int) kNew.shape[1];
+    if (!prealloc) {
+        // Legacy concat-grow (ESKVCache.mm:460-466).
+        auto &K = k_[layer];
+        K = K ? concatRows(*K, kNew, st) : clone(kNew, st);
+        const int len = (int) K->shape[1];
+        return {*K, *K, len, len};
+    }
+    Slot &s = slots_[layer];
+    if (s.k && s.v)
+        throw std::runtime_error("ESKVCache::updateRaw: slot holds composite K/V content "
+                                 "(post-norm) — not derivable as raw; re-prime the cache");
+    if (!s.k) {
+        s.k = clone(kNew, st);
+        s.len = nNew;
+        s.start = 0;
+    } else {
+        if (kNew.shape[0] != s.k->shape[0] || kNew.shape[2] != s.k->shape[2])
+            throw std::invalid_argument("ESKVCache::updateRaw: kv heads / head dim differ from the slot");
+        growSlot(s, nNew, st, false);
+        copyRows(*s.k, s.len, kNew, 0, nNew, st);
+        s.len += nNew;
+    }
+    return {liveView(*s.k, 0, s.len), *s.k, s.len, (int) s.k->shape[1]};
+}
+
+void *ESKVCache::workspace(size_t bytes, hipStream_t st) {
+    if (!workspace_ || workspace_->nbytes() < bytes) {
+        if (workspace_) hipCheck(hipStreamSynchronize(st), "ESKVCache workspace growth");
+        const size_t n = std::max<size_t>(bytes, 1 << 20);
+        workspace_ = Tensor::empty({(int64_t) n}, Dtype::u8);
+        // The status word at the front starts at zero (esda workspace contract).
+        hipCheck(hipMemsetAsync(workspace_->data, 0, 256, st), "ESKVCache workspace clear");
+    }
+    return workspace_->data;
+}
+
+int *ESKVCache::positionWord(int layer, int value, hipStream_t st) {
+    if (!posDev_) posDev_ = Tensor::empty({(int64_t) slots_.size()}, Dtype::i32);
+    int32_t *p = static_cast<int32_t *>(posDev_->data) + layer;
+    esdaCheck(esda_fill_i32(p, value, 1, st));
+    return p;
+}
+
+Tensor ESKVCache::decode(int layer, const Tensor &q, const Tensor &kNew, const Tensor &vNew, int maxKeep,
+                         float scale, hipStream_t st, Tensor *out) {
+    checkLayer(layer);
+    checkRows(kNew, "ESKVCache::decode kNew");
+    checkRows(vNew, "ESKVCache::decode vNew");
+    if (kNew.shape[1] != 1 || vNew.shape != kNew.shape)
+        throw std::invalid_argument("ESKVCache::decode: kNew / vNew must be [kvHeads, 1, headDim]");
+    const int kvH = (int) kNew.shape[0], hd = (int) kNew.shape[2];
+    if (!q.defined() || q.dtype != Dtype::bf16 || !q.contiguous() || q.numel() % hd)
+        throw std::invalid_argument("ESKVCache::decode: q must be contiguous bf16 [numQHeads, headDim]");
+    const int Hq = (int) (q.numel() / hd);
+    Slot &s = slots_[layer];
+    if (s.k && !s.v)
+        throw std::runtime_error("ESKVCache::decode: slot holds raw-K content — not usable "
+                                 "by the composite path; re-prime the cache");
+    const bool aliased = kNew.data == vNew.data;
+    if (!s.k) {
+        // First row: capacity == content, as for the reference's first store.
+        s.k = Tensor::empty({kvH, 1, hd}, Dtype::bf16);
+        s.shared = aliased;
+        s.v = aliased ? *s.k : Tensor::empty({kvH, 1, hd}, Dtype::bf16);
+        s.len = 0;
+        s.start = 0;
+    } else {
+        if (kvH != s.k->shape[0] || hd != s.k->shape[2])
+            throw std::invalid_argument("ESKVCache::decode: kv heads / head dim differ from the slot");
+        if (s.shared && !aliased)
+            throw std::runtime_error("ESKVCache::decode: slot holds one shared K=V buffer; vNew must alias kNew");
+        growSlot(s, 1, st, true);
+    }
+    const int cap = (int) s.k->shape[1];
+    // Rows attended after the append: the live range the reference's update() leaves.
+    const int live = s.len + 1 - s.start;
+    const int w = maxKeep > 0 ? std::min(maxKeep, live) : live;
+
+    esda_decode_desc d{};
+    d.batch = 1;
+    d.num_q_heads = Hq;
+    d.num_kv_heads = kvH;
+    d.head_dim = hd;
+    d.cap = cap;
+    d.window = w;
+    d.ring = 0;
+    d.kv_shared = s.shared ? 1 : 0;
+    d.head_stride = (int64_t) cap * hd;
+    d.seq_stride = (int64_t) kvH * cap * hd;
+    d.max_visible = w;
+    d.split_rows = 0;
+    d.scale = scale;
+    size_t wsBytes = 0;
+    esdaCheck(esda_decode_workspace_size(&d, &wsBytes));
+
+    Tensor o;
+    if (out) {
+        if (out->dtype != Dtype::bf16 || !out->contiguous() || out->numel() != (int64_t) Hq * hd)
+            throw std::invalid_argument("ESKVCache::decode: out must be contiguous bf16 [numQHeads, headDim]");
+        o = *out;
+    } else {
+        o = Tensor::empty({Hq, hd}, Dtype::bf16);
+    }
+    esda_decode_args a{};
+    a.q = q.data;
+    a.k_new = kNew.data;
+    a.v_new = s.shared ? nullptr : vNew.data;
+    a.k_cache = s.k->data;
+    a.v_cache = s.v->data;
+    a.pos = positionWord(layer, s.len, st);
+    a.row_base = nullptr;
+    a.out = o.data;
+    a.workspace = workspace(wsBytes, st);
+    a.workspace_bytes = workspace_->nbytes();
+    esdaCheck(esda_decode(&d, &a, st));
+    s.len += 1;
+    if (maxKeep > 0 && s.len - s.start > maxKeep) s.start = s.len - maxKeep;
+    return o;
+}
+
+Tensor ESKVCache::decodeRaw(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
+                            const std::vector<float> &invFreq, hipStream_t st, Tensor *out) {
+    checkLayer(layer);
+    checkRows(kNew, "ESKVCache::decodeRaw kNew");
+    if (kNew.shape[1] != 1 || kNew.shape[2] != 512)
+        throw std::invalid_argument("ESKVCache::decodeRaw: kNew must be [kvHeads, 1, 512]");
+    if (invFreq.size() < 64)
+        throw std::invalid_argument("ESKVCache::decodeRaw: invFreq needs at least 64 entries");
+    const int kvH = (int) kNew.shape[0];
+    Slot &s = slots_[layer];
+    if (s.k && s.v)
+        throw std::runtime_error("ESKVCache::decodeRaw: slot holds composite K/V content "
+                                 "(post-norm) — not derivable as raw; re-prime the cache");
+    if (!s.k) {
+        s.k = Tensor::empty({kvH, 1, 512}, Dtype::bf16);
+        s.len = 0;
+        s.start = 0;
+    } else {
+        if (kvH != s.k->shape[0] || s.k->shape[2] != 512)
+            throw std::invalid_argument("ESKVCache::decodeRaw: kv heads / head dim differ from the slot");
+        growSlot(s, 1, st, false);
+    }
+    if (!invFreqDev_ || !std::equal(invFreqHost_.begin(), invFreqHost_.end(), invFreq.begin()) ||
+        invFreqHost_.size() != 64) {
+        if (invFreqDev_) hipCheck(hipStreamSynchronize(st), "ESKVCache rotary table");
+        invFreqHost_.assign(invFreq.begin(), invFreq.begin() + 64);
+        invFreqDev_ = Tensor::empty({64}, Dtype::f32);
+        hipCheck(hipMemcpyAsync(invFreqDev_->data, invFreqHost_.data(), 64 * sizeof(float),
+                                hipMemcpyHostToDevice, st),
+                 "ESKVCache rotary table upload");
+        hipCheck(hipStreamSynchronize(st), "ESKVCache rotary table upload");
+    }
+    if (!q.defined() || q.dtype != Dtype::bf16 || !q.contiguous() || q.numel() % 512)
+        throw std::invalid_argument("ESKVCache::decodeRaw: q must be contiguous bf16 [numQHeads, 512]");
+    if (!kw.defined() || kw.dtype != Dtype::bf16 || kw.numel() != 512 || !kw.contiguous())
+        throw std::invalid_argument("ESKVCache::decodeRaw: kw must be contiguous bf16 [512]");
+    const int Hq = (int) (q.numel() / 512);
+    const int cap = (int) s.k->shape[1];
+
+    esda_raw_desc d{};
+    d.batch = 1;
+    d.num_q_heads = Hq;
+    d.num_kv_heads = kvH;
+    d.head_dim = 512;
+    d.cap = cap;
+    d.head_stride = (int64_t) cap * 512;
+    d.seq_stride = (int64_t) kvH * cap * 512;
+    d.max_visible = s.len + 1;
+    d.split_rows = 0;
+    d.scale = 1.0f;
+    d.eps = eps;
+    size_t wsBytes = 0;
+    esdaCheck(esda_decode_raw_workspace_size(&d, &wsBytes));
+    Tensor o;
+    if (out) {
+        if (out->dtype != Dtype::bf16 || !out->contiguous() || out->numel() != (int64_t) Hq * 512)
+            throw std::invalid_argument("ESKVCache::decodeRaw: out must be contiguous bf16 [numQHeads, 512]");
+        o = *out;
+    } else {
+        o = Tensor::empty({Hq, 512}, Dtype::bf16);
+    }
+    esda_raw_args a{};
+    a.q = q.data;
+    a.k_new = kNew.data;
+    a.raw_cache = s.k->data;
+    a.pos = positionWord(layer, s.len, st);
+    a.kw = kw.data;
+    a.inv_freq = static_cast<const float *>(invFreqDev_->data);
+    a.out = o.data;
+    a.workspace = workspace(wsBytes, st);
+    a.workspace_bytes = workspace_->nbytes();
+    esdaCheck(esda_decode_raw(&d, &a, st));
+    s.len += 1;
+    return o;
+}
+
+void ESKVCache::markPrefix(int pos, const std::string &) {
+    if (pos < 4096)
+        throw std::invalid_argument("ESKVCache::markPrefix: marker positions below 4096 unsupported");
+    // Prefix markers feed the snapshot format, which this library does not implement.
+}
+
+bool ESKVCache::saveSnapshot(const std::string &, const std::string &, int) const { return false; }
+
+int ESKVCache::restoreSnapshot(const std::string &, const std::string &, RawMode,
+                               const std::function<std::string(int)> &) {
+    return -1;
+}
+
+bool ESKVCache::markRewindPoint(int) { return false; }
+
+int ESKVCache::rewindToMark() { return -1; }
+
+void ESKVCache::reset() {
+    for (auto &a : k_) a.reset();
+    for (auto &a : v_) a.reset();
+    for (auto &s : slots_) s = Slot{};
+    seqLen_ = 0;
+}
+
+}  // namespace es

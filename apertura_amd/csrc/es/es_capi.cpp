@@ -1,0 +1,191 @@
+// es_capi.cpp -- the C ABI of include/esda_cache.h over es::ESKVCache and
+// es::esDecodeAttnGlobal.  Exceptions are caught here and turned into status codes.
+#include <exception>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "es/ESDecodeAttn.h"
+#include "es/ESKVCache.h"
+#include "esda_cache.h"
+#include "esda_internal.h"
+
+struct esda_cache {
+    es::ESKVCache impl;
+    explicit esda_cache(int n) : impl(n) {}
+};
+
+namespace {
+
+template <class F>
+int guarded(F &&f) {
+    try {
+        f();
+        return ESDA_OK;
+    } catch (const std::invalid_argument &e) {
+        esda_detail::set_error(e.what());
+        return ESDA_ERR_INVALID_ARGUMENT;
+    } catch (const std::exception &e) {
+        esda_detail::set_error(e.what());
+        return ESDA_ERR_RUNTIME;
+    }
+}
+
+es::Tensor rows(const void *p, int kvH, int n, int hd) {
+    if (!p) throw std::invalid_argument("null tensor pointer");
+    if (kvH <= 0 || n <= 0 || hd <= 0) throw std::invalid_argument("tensor sizes must be positive");
+    return es::Tensor::wrap(const_cast<void *>(p), {kvH, n, hd}, es::Dtype::bf16);
+}
+
+void toView(const es::Tensor &t, esda_view *v) {
+    if (!v) return;
+    v->data = t.data;
+    v->kv_heads = (int32_t) t.shape[0];
+    v->rows = (int32_t) t.shape[1];
+    v->head_dim = (int32_t) t.shape[2];
+    v->head_stride = t.strides[0];
+}
+
+void needCache(const esda_cache *c) {
+    if (!c) throw std::invalid_argument("null cache handle");
+}
+
+hipStream_t asStream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+int esda_cache_create(int32_t num_layers, esda_cache **out) {
+    return guarded([&] {
+        if (!out) throw std::invalid_argument("esda_cache_create: null output");
+        *out = new esda_cache(num_layers);
+    });
+}
+
+void esda_cache_destroy(esda_cache *cache) { delete cache; }
+
+int esda_cache_update(esda_cache *cache, int32_t layer, const void *k_new, const void *v_new, int32_t kv_heads,
+                      int32_t n_new, int32_t head_dim, int32_t max_keep, int32_t prealloc, void *stream,
+                      esda_view *k_out, esda_view *v_out) {
+    return guarded([&] {
+        needCache(cache);
+        auto kv = cache->impl.update(layer, rows(k_new, kv_heads, n_new, head_dim),
+                                     rows(v_new, kv_heads, n_new, head_dim), max_keep, prealloc != 0,
+                                     asStream(stream));
+        toView(kv.first, k_out);
+        toView(kv.second, v_out);
+    });
+}
+
+int esda_cache_update_raw(esda_cache *cache, int32_t layer, const void *k_new, int32_t kv_heads, int32_t n_new,
+                          int32_t head_dim, int32_t prealloc, void *stream, esda_view *view, int32_t *len,
+                          int32_t *pitch) {
+    return guarded([&] {
+        needCache(cache);
+        auto r = cache->impl.updateRaw(layer, rows(k_new, kv_heads, n_new, head_dim), prealloc != 0,
+                                       asStream(stream));
+        toView(r.view, view);
+        if (len) *len = r.len;
+        if (pitch) *pitch = r.pitch;
+    });
+}
+
+int esda_cache_current(esda_cache *cache, int32_t layer, int32_t prealloc, esda_view *k_out, esda_view *v_out) {
+    return guarded([&] {
+        needCache(cache);
+        auto kv = cache->impl.current(layer, prealloc != 0);
+        toView(kv.first, k_out);
+        toView(kv.second, v_out);
+    });
+}
+
+int esda_cache_decode(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads, const void *k_new,
+                      const void *v_new, int32_t kv_heads, int32_t head_dim, int32_t max_keep, float scale,
+                      void *out, void *stream) {
+    return guarded([&] {
+        needCache(cache);
+        if (!q || !out || num_q_heads <= 0) throw std::invalid_argument("esda_cache_decode: null q / out");
+        es::Tensor qt = es::Tensor::wrap(const_cast<void *>(q), {num_q_heads, head_dim}, es::Dtype::bf16);
+        es::Tensor ot = es::Tensor::wrap(out, {num_q_heads, head_dim}, es::Dtype::bf16);
+        cache->impl.decode(layer, qt, rows(k_new, kv_heads, 1, head_dim), rows(v_new, kv_heads, 1, head_dim),
+                           max_keep, scale, asStream(stream), &ot);
+    });
+}
+
+int esda_cache_decode_raw(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads, const void *k_new,
+                          int32_t kv_heads, const void *kw, float eps, const float *inv_freq, int32_t n_freq,
+                          void *out, void *stream) {
+    return guarded([&] {
+        needCache(cache);
+        if (!q || !out || !kw || !inv_freq || num_q_heads <= 0 || n_freq < 0)
+            throw std::invalid_argument("esda_cache_decode_raw: null pointer");
+        es::Tensor qt = es::Tensor::wrap(const_cast<void *>(q), {num_q_heads, 512}, es::Dtype::bf16);
+        es::Tensor ot = es::Tensor::wrap(out, {num_q_heads, 512}, es::Dtype::bf16);
+        es::Tensor kwt = es::Tensor::wrap(const_cast<void *>(kw), {512}, es::Dtype::bf16);
+        std::vector<float> f(inv_freq, inv_freq + n_freq);
+        cache->impl.decodeRaw(layer, qt, rows(k_new, kv_heads, 1, 512), kwt, eps, f, asStream(stream), &ot);
+    });
+}
+
+int esda_cache_slot(esda_cache *cache, int32_t layer, int32_t *len, int32_t *start, int32_t *capacity,
+                    int32_t *flags) {
+    return guarded([&] {
+        needCache(cache);
+        if (len) *len = cache->impl.slotLen(layer);
+        if (start) *start = cache->impl.slotStart(layer);
+        if (capacity) *capacity = cache->impl.slotCapacity(layer);
+        if (flags) {
+            int f = 0;
+            if (cache->impl.slotLost(layer)) f |= 1;
+            if (cache->impl.slotShared(layer)) f |= 2;
+            if (cache->impl.slotRaw(layer)) f |= 4;
+            *flags = f;
+        }
+    });
+}
+
+int esda_cache_seq_len(const esda_cache *cache) { return cache ? cache->impl.seqLen() : -1; }
+
+void esda_cache_mark_step(esda_cache *cache, int32_t n_new) {
+    if (cache) cache->impl.markStep(n_new);
+}
+
+void esda_cache_reset(esda_cache *cache) {
+    if (cache) cache->impl.reset();
+}
+
+int esda_cache_save_snapshot(const esda_cache *cache, const char *path, const char *fingerprint, int32_t pos) {
+    if (!cache || !path || !fingerprint) return 0;
+    return cache->impl.saveSnapshot(path, fingerprint, pos) ? 1 : 0;
+}
+
+int esda_cache_restore_snapshot(esda_cache *cache, const char *path, const char *fingerprint) {
+    if (!cache || !path || !fingerprint) return -1;
+    return cache->impl.restoreSnapshot(path, fingerprint);
+}
+
+int esda_cache_mark_rewind_point(esda_cache *cache, int32_t pos) {
+    return cache && cache->impl.markRewindPoint(pos) ? 1 : 0;
+}
+
+int esda_cache_rewind_to_mark(esda_cache *cache) { return cache ? cache->impl.rewindToMark() : -1; }
+
+int esda_decode_attn_global(const void *q, int32_t num_q_heads, const void *raw_buf, int32_t num_kv_heads,
+                            int32_t len, int32_t pitch, const void *kw, float eps, const float *inv_freq,
+                            int32_t n_freq, void *out, void *stream) {
+    return guarded([&] {
+        if (!q || !raw_buf || !kw || !inv_freq || !out || n_freq < 0)
+            throw std::invalid_argument("esda_decode_attn_global: null pointer");
+        if (num_q_heads <= 0 || num_kv_heads <= 0 || pitch <= 0)
+            throw std::invalid_argument("esda_decode_attn_global: sizes must be positive");
+        es::Tensor qt = es::Tensor::wrap(const_cast<void *>(q), {num_q_heads, 512}, es::Dtype::bf16);
+        es::Tensor rb = es::Tensor::wrap(const_cast<void *>(raw_buf), {num_kv_heads, pitch, 512}, es::Dtype::bf16);
+        es::Tensor kwt = es::Tensor::wrap(const_cast<void *>(kw), {512}, es::Dtype::bf16);
+        es::Tensor ot = es::Tensor::wrap(out, {num_q_heads, 512}, es::Dtype::bf16);
+        std::vector<float> f(inv_freq, inv_freq + n_freq);
+        es::esDecodeAttnGlobal(qt, rb, len, pitch, kwt, eps, f, asStream(stream), &ot);
+    });
+}
+
+}  // extern "C"

@@ -40,6 +40,7 @@
 #include <utility>
 
 #include "esda.h"
+#include "esda_internal.h"
 
 namespace {
 
@@ -93,17 +94,30 @@ struct AttendParams {
     long long seq_stride, head_stride;
     int B, Hq, Hkv, G, cap, window, ring, S, chunk;
     float scale_log2e;
+    // raw-K mode only
+    const uint16_t *kw;
+    const float *inv_freq;
+    float eps;
 };
 
-// Max over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48): two
-// permlane swaps exchange 16-lane rows and 32-lane halves without touching LDS.
+// Max over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48) without
+// touching LDS.  v_permlane16_swap_b32 a, b exchanges the odd 16-lane rows of a with
+// the even rows of b (v_permlane32_swap_b32: the upper half of a with the lower half of
+// b); with a = b = x, max(a, b) is then the max over row pairs, and over halves.  The
+// swaps are written in assembly because this toolchain's builtins hand back the first
+// register for both results, which silently drops the partner row from the max.
 __device__ __forceinline__ float wave_max_across_groups(float x) {
-    const unsigned u = __builtin_bit_cast(unsigned, x);
-    const auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    x = fmaxf(__builtin_bit_cast(float, s16[0]), __builtin_bit_cast(float, s16[1]));
-    const unsigned v = __builtin_bit_cast(unsigned, x);
-    const auto s32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return fmaxf(__builtin_bit_cast(float, s32[0]), __builtin_bit_cast(float, s32[1]));
+#if defined(__HIP_DEVICE_COMPILE__)
+    unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    x = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    a = __builtin_bit_cast(unsigned, x);
+    b = a;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+#else
+    return x;
+#endif
 }
 
 // The running max is only raised (and O rescaled) once a score exceeds it by this
@@ -122,7 +136,8 @@ constexpr float kRescaleSlack = 8.0f;
 // 32 B pad), sub-row q at +2D*q bytes.  The 32-byte pad (a measured choice: 16 B leaves
 // both the 128-bit row reads and the transpose reads 2-way bank-conflicted on gfx950)
 // makes both read patterns conflict-free with every address a base plus an immediate.
-template <int D, bool SHARED, int NW>
+// EXTRA: LDS bytes the kernel variant needs beside the ring and the score exchange.
+template <int D, bool SHARED, int NW, int EXTRA = 0>
 struct Ring {
     static constexpr int RPI = 512 / D;                     // rows per DMA instruction
     static constexpr int NI = 16 / RPI;                     // DMA instructions per stage
@@ -137,7 +152,7 @@ struct Ring {
     static constexpr int DPT = NI / NW;                     // DMA per wave per tensor
     static constexpr int DPW = DPT * (SHARED ? 1 : 2);      // DMA per wave per stage
     static constexpr int XB = 2 * NW * 64 * 16;             // score-exchange bytes
-    static constexpr int NS_ = (160 * 1024 - XB - 256) / SB;
+    static constexpr int NS_ = (160 * 1024 - XB - 256 - EXTRA) / SB;
     static constexpr int NS = NS_ > 16 ? 16 : NS_;          // stages in the ring
     static_assert(DW % 32 == 0 && NI % NW == 0, "wave slices must cover whole MFMA steps");
     static_assert(NS >= 4, "the ring needs at least 4 stages");
@@ -203,11 +218,83 @@ __device__ __forceinline__ void unroll(F &&f) {
     unroll_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-template <int D, bool SHARED, int NW>
+// ------------------------------------------------------------ raw-K reconstruction
+//
+// Raw mode (ESDecodeAttn.mm:51-106): the cache holds pre-norm k_proj rows.  Per row,
+// rinv = rsqrt(mean(kraw^2) + eps); K = bf16(rope(kraw * rinv * kw)) with rotary pairs
+// (d, d + 256) for d < 64, whose cos / sin are those of the fp32 angle t * inv_freq[d]
+// rounded to bf16; V = kraw * rinv, with rinv folded into the softmax weight.
+
+constexpr int kRawDim = 512;
+constexpr int kRopePairs = 64;
+constexpr int kTabStride = 68;  // words per cos/sin table row: 64 + 4 (conflict-free 128-bit reads)
+constexpr int kRawExtraLds = 3 * 16 * 4 * 4 + 2 * 16 * kTabStride * 4;
+
+// Cody-Waite split of pi/2 (hi + mid + lo, each the nearest fp32 to what remains).
+constexpr float kTwoOverPi = 0.636619746685028076171875f;     // fp32(2/pi)
+constexpr float kPio2Hi = 1.57079637050628662109375f;         // fp32(pi/2)
+constexpr float kPio2Mid = -4.37113882867379300296306610107421875e-8f;
+constexpr float kPio2Lo = -1.715124510005881916757519826222e-15f;
+
+// cos and sin of an fp32 angle |a| < 2^20.  Reduction a = n*pi/2 + r in three FMA
+// steps (the first is exact: n*hi is a multiple of 2^-23 within 1 of a), then Taylor
+// polynomials on |r| <= pi/4 (truncation error < 2e-9), then the quadrant n mod 4.
+// Absolute error is a few 1e-8, far inside the bf16 rounding applied to the results.
+__device__ __forceinline__ void sincos_f32(float a, float &s, float &c) {
+    const float n = __builtin_rintf(a * kTwoOverPi);
+    float r = __builtin_fmaf(-n, kPio2Hi, a);
+    r = __builtin_fmaf(-n, kPio2Mid, r);
+    r = __builtin_fmaf(-n, kPio2Lo, r);
+    const float r2 = r * r;
+    float ps = __builtin_fmaf(r2, 1.0f / 362880.0f, -1.0f / 5040.0f);
+    ps = __builtin_fmaf(r2, ps, 1.0f / 120.0f);
+    ps = __builtin_fmaf(r2, ps, -1.0f / 6.0f);
+    const float sr = __builtin_fmaf(r * r2, ps, r);
+    float pc = __builtin_fmaf(r2, -1.0f / 3628800.0f, 1.0f / 40320.0f);
+    pc = __builtin_fmaf(r2, pc, -1.0f / 720.0f);
+    pc = __builtin_fmaf(r2, pc, 1.0f / 24.0f);
+    pc = __builtin_fmaf(r2, pc, -0.5f);
+    const float cr = __builtin_fmaf(r2, pc, 1.0f);
+    const int q = (int) n & 3;
+    s = (q & 1) ? cr : sr;
+    c = (q & 1) ? sr : cr;
+    if (q & 2) s = -s;
+    if ((q + 1) & 2) c = -c;
+}
+
+__device__ __forceinline__ float bf16_lo(unsigned w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_hi(unsigned w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// --------------------------------------------------------------------- attend kernel
+//
+// grid (splits, kv heads, sequences), NW = 4 waves per workgroup, one workgroup per
+// CU.  A workgroup owns `chunk` consecutive visible rows of one (sequence, kv head)
+// and streams them through the LDS ring in 16-row stages.  The head dim is split
+// across the waves: per stage, each wave forms partial scores S^T[16 rows x 16 heads]
+// over its dims with v_mfma_f32_16x16x32_bf16 (the GQA group is the MFMA N dimension,
+// zero-padded to 16, so each K/V byte is read from HBM once per group), the partials
+// are summed through LDS, every wave runs the same online softmax, and each wave
+// accumulates O^T for its own dims with v_mfma_f32_16x16x16_bf16 (V^T from LDS by
+// transpose reads).  One barrier per stage: the scores of stage s+1 are formed while
+// stage s is accumulated.  With attention_k_eq_v the V rows are the K rows in LDS.
+//
+// RAW (D = 512, one tensor): the QK operand is rebuilt from raw rows in registers.  The
+// row norms need all four waves' dims, so each stage's partial sums of squares (and its
+// cos/sin table) are published two stages ahead: in iteration s the waves publish
+// stage s+2's sums and table, form stage s+1's scores and accumulate stage s.
+//
+// The new token's row is copied from k_new/v_new into the cache by the workgroup whose
+// split ends at it (bit-exact copy); that workgroup's own loads read the row from
+// k_new/v_new and no other workgroup reads it, so the copy needs no ordering.
+template <int D, bool SHARED, int NW, bool RAW>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW)))
 void attend_kernel(AttendParams p) {
-    using R = Ring<D, SHARED, NW>;
+    static_assert(!RAW || (D == kRawDim && SHARED && NW == 4), "raw mode: one 512-dim stream, 4 waves");
+    using R = Ring<D, SHARED, NW, RAW ? kRawExtraLds : 0>;
     constexpr int NS = R::NS, DW = R::DW, KKW = R::KKW, DTW = R::DTW;
+    // Stages between the one being accumulated and the newest one that must have landed.
+    constexpr int AHEAD = RAW ? 2 : 1;
+    static_assert(NS >= AHEAD + 3, "the ring must hold the look-ahead stages and one in flight");
     // Distinct arrays per stage: the compiler tracks DMA completion per LDS object, so a
     // read of stage u only waits for stage u's DMA, never for the stages behind it.
     __shared__ __attribute__((aligned(16))) unsigned char r0[R::SB], r1[R::SB], r2[R::SB], r3[R::SB],
@@ -234,9 +321,15 @@ void attend_kernel(AttendParams p) {
         else return r15;
     };
     __shared__ f32x4 xch[2][NW][64];  // partial scores, double-buffered by stage parity
+    // Raw mode: per-row partial sums of squares xss[stage % 3][row][wave] and the cos/sin
+    // table xtab[stage % 2][row][pair] (bf16 cos in the low half, sin in the high half).
+    __shared__ __attribute__((aligned(16))) unsigned char rawlds[RAW ? kRawExtraLds : 16];
+    auto *xss = reinterpret_cast<float (*)[16][4]>(rawlds);
+    auto *xtab = reinterpret_cast<unsigned (*)[16][kTabStride]>(rawlds + 3 * 16 * 4 * 4);
 
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, lg = lane >> 4;
 
     const int pos = p.pos[b];
@@ -250,27 +343,47 @@ void attend_kernel(AttendParams p) {
     if (j0 >= sv.nvis) return;
     const int j1 = min(j0 + p.chunk, sv.nvis);
     if (split == p.S - 1 && j1 < sv.nvis && kvh == 0 && tid == 0) atomicAdd(p.status, 1);
+    const bool append = p.k_new != nullptr;
 
     const size_t head_off = (size_t) b * p.seq_stride + (size_t) kvh * p.head_stride;
     uint16_t *kbase = p.k_cache + head_off;
     uint16_t *vbase = p.v_cache + head_off;
-    const uint16_t *knew = p.k_new + ((size_t) b * p.Hkv + kvh) * D;
+    const uint16_t *knew = append ? p.k_new + ((size_t) b * p.Hkv + kvh) * D : nullptr;
     const uint16_t *vnew = SHARED ? knew : p.v_new + ((size_t) b * p.Hkv + kvh) * D;
 
-    // Q^T operand for this wave's dim slice: lane (li, lg) = head li, dims
-    // wave*DW + 32kk + 8lg .. +8 (zero for heads >= G).
+    // 32-dim chunk of the QK k-step kk of this wave.  Raw mode interleaves the waves so
+    // that each rotary pair (d, d + 256), d < 64, sits in one lane of wave 0 or 1.
+    auto qk_chunk = [&](int kk) { return RAW ? wave + 4 * kk : wave * KKW + kk; };
+
+    // Q^T operand for this wave's dims: lane (li, lg) = head li, dims 32*chunk + 8lg .. +8
+    // (zero for heads >= G).
     bf16x8 qv[KKW];
     {
         const bool qok = li < p.G;
-        const uint16_t *qrow = p.q + ((size_t) b * p.Hq + (size_t) kvh * p.G + (qok ? li : 0)) * D +
-                               wave * DW + lg * 8;
+        const uint16_t *qrow = p.q + ((size_t) b * p.Hq + (size_t) kvh * p.G + (qok ? li : 0)) * D + lg * 8;
 #pragma unroll
         for (int kk = 0; kk < KKW; ++kk) {
-            const u32x4 t = qok ? *reinterpret_cast<const u32x4 *>(qrow + kk * 32) : u32x4{0u, 0u, 0u, 0u};
+            const u32x4 t = qok ? *reinterpret_cast<const u32x4 *>(qrow + 32 * qk_chunk(kk)) : u32x4{0u, 0u, 0u, 0u};
             qv[kk] = __builtin_bit_cast(bf16x8, t);
         }
     }
-    ESDA_WAIT_VM(0);  // Q is in registers before the ring starts counting its own loads
+    // Raw mode: k-norm weights of the lane's QK dims, and the rotary frequencies of the
+    // four table entries this thread computes per stage (row tid/16, pairs 4(tid%16)..+4).
+    float kwf[RAW ? KKW : 1][8];
+    f32x4 invf = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (RAW) {
+#pragma unroll
+        for (int kk = 0; kk < KKW; ++kk) {
+            const u32x4 t = *reinterpret_cast<const u32x4 *>(p.kw + 32 * qk_chunk(kk) + 8 * lg);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kwf[kk][2 * e] = bf16_lo(t[e]);
+                kwf[kk][2 * e + 1] = bf16_hi(t[e]);
+            }
+        }
+        invf = *reinterpret_cast<const f32x4 *>(p.inv_freq + 4 * (tid & 15));
+    }
+    ESDA_WAIT_VM(0);  // operands are in registers before the ring starts counting its own loads
 
     // DMA source slot of this lane: sub-row dq, chunk dchunk of the row.
     const int dq = lane / R::CPR, dchunk = lane % R::CPR;
@@ -301,7 +414,7 @@ void attend_kernel(AttendParams p) {
             const int jj = j < j1 ? j : j1 - 1;          // clamp: masked rows read a visible row
             int r = sv.first + jj;
             if (r >= p.cap) r -= p.cap;
-            const bool from_new = (jj == sv.nvis - 1);
+            const bool from_new = append && (jj == sv.nvis - 1);
             const uint16_t *ks = (from_new ? knew : kbase + (size_t) r * D) + dchunk * 8;
             lds_dma16(ks, lds_addr(buf) + i * R::BLK);
             if constexpr (!SHARED) {
@@ -311,12 +424,11 @@ void attend_kernel(AttendParams p) {
         }
     };
 
-    // Per-lane LDS offsets: QK A operand (row li, this wave's slice, chunk 4kk + lg)
-    // and the V^T gather (row 4lg + e, dim wave*DW + 16dt + li).
-    // and the V^T transpose read (lane (li, lg) supplies row 4lg + li/4, dims
-    // wave*DW + 16dt + 4(li%4) .. +4; ds_read_b64_tr_b16 hands lane li of the group
-    // dim 16dt + li of rows 4lg .. 4lg+3, the PV A operand).
-    const int qk_off = R::off(li, wave, lg);                           // + 64*kk
+    // Per-lane LDS offsets: the QK A operand (row li, chunk qk_chunk(kk), 16 bytes at
+    // 8lg dims) and the V^T transpose read (lane (li, lg) supplies row 4lg + li/4, dims
+    // wave*DW + 16dt + 4(li%4) .. +4; ds_read_b64_tr_b16 hands lane li of the group dim
+    // 16dt + li of rows 4lg .. 4lg+3, the PV A operand).
+    const int qk_off = R::off(li, 0, 0) + lg * 16;                     // + 64*qk_chunk(kk)
     const int tr_off = R::off(4 * lg + li / 4, wave, 0) + (li % 4) * 8;  // + 32*dt
     constexpr int VOFF = SHARED ? 0 : R::TB;
 
@@ -325,42 +437,151 @@ void attend_kernel(AttendParams p) {
 #pragma unroll
     for (int dt = 0; dt < DTW; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Partial scores of stage st over this wave's dims, published for the other waves.
+    // Partial scores of a stage over this wave's dims, published for the other waves.
     auto qk_partial = [&](const unsigned char *kb, int par) {
         f32x4 sp = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int kk = 0; kk < KKW; ++kk) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8 *>(kb + qk_off + 64 * kk);
+            const bf16x8 a = *reinterpret_cast<const bf16x8 *>(kb + qk_off + 64 * qk_chunk(kk));
             sp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qv[kk], sp, 0, 0, 0);
         }
         xch[par][wave][lane] = sp;
     };
 
-    // Prologue: fill NS-1 stages, then publish stage 0's partial scores.
+    // ---- raw mode helpers
+    u32x4 araw[RAW ? KKW : 1];  // raw QK operand of the next stage to score
+    auto load_raw = [&](const unsigned char *kb) {
+#pragma unroll
+        for (int kk = 0; kk < (RAW ? KKW : 1); ++kk)
+            araw[kk] = *reinterpret_cast<const u32x4 *>(kb + qk_off + 64 * qk_chunk(kk));
+    };
+    // Partial sum of squares of row li over this wave's dims -> xss[buf][li][wave].
+    auto publish_ss = [&](int buf) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < (RAW ? KKW : 1); ++kk)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float x0 = bf16_lo(araw[kk][e]), x1 = bf16_hi(araw[kk][e]);
+                ss = __builtin_fmaf(x0, x0, ss);
+                ss = __builtin_fmaf(x1, x1, ss);
+            }
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        if (lg == 0) xss[buf][li][wave] = ss;
+    };
+    // cos/sin table of stage st: this thread's row tid/16, pairs 4(tid%16) .. +4.
+    auto publish_tab = [&](int st, int buf) {
+        const int row = tid >> 4;
+        const float t = (float) (sv.first + j0 + st * 16 + row);
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float s, c;
+            sincos_f32(t * invf[e], s, c);
+            const unsigned cb = __builtin_bit_cast(unsigned short, (__bf16) c);
+            const unsigned sb = __builtin_bit_cast(unsigned short, (__bf16) s);
+            w[e] = cb | (sb << 16);
+        }
+        *reinterpret_cast<u32x4 *>(&xtab[buf][row][4 * (tid & 15)]) = w;
+    };
+    // mean(kraw^2) + eps of a row; rinv = rsqrt of it.
+    auto row_ms = [&](int buf, int row) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(&xss[buf][row][0]);
+        return (v[0] + v[1] + v[2] + v[3]) * (1.0f / kRawDim) + p.eps;
+    };
+    // Scores of the stage held in araw: rebuild K in registers, then MFMA.
+    auto qk_raw = [&](int ssbuf, int tabbuf, int par) {
+        if constexpr (RAW) {
+            const float rinv = __builtin_amdgcn_rsqf(row_ms(ssbuf, li));
+            float kn[KKW][8];
+    #pragma unroll
+            for (int kk = 0; kk < KKW; ++kk)
+    #pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    kn[kk][2 * e] = bf16_lo(araw[kk][e]) * rinv * kwf[kk][2 * e];
+                    kn[kk][2 * e + 1] = bf16_hi(araw[kk][e]) * rinv * kwf[kk][2 * e + 1];
+                }
+            if (wave < 2) {
+                // chunk `wave` holds dims d = 32*wave + 8lg + e < 64, chunk wave + 8 their pairs.
+                const unsigned *tb = &xtab[tabbuf][li][32 * wave + 8 * lg];
+                const u32x4 t0 = *reinterpret_cast<const u32x4 *>(tb);
+                const u32x4 t1 = *reinterpret_cast<const u32x4 *>(tb + 4);
+    #pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const unsigned w = e < 4 ? t0[e] : t1[e - 4];
+                    const float c = bf16_lo(w), s = bf16_hi(w);
+                    const float lo = kn[0][e], hi = kn[2][e];
+                    kn[0][e] = lo * c - hi * s;
+                    kn[2][e] = hi * c + lo * s;
+                }
+            }
+            f32x4 sp = {0.0f, 0.0f, 0.0f, 0.0f};
+    #pragma unroll
+            for (int kk = 0; kk < KKW; ++kk) {
+                bf16x8 a;
+    #pragma unroll
+                for (int e = 0; e < 8; ++e) a[e] = (__bf16) kn[kk][e];
+                sp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qv[kk], sp, 0, 0, 0);
+            }
+            xch[par][wave][lane] = sp;
+        }
+    };
+
+    // Prologue: fill NS-1 stages; publish what iteration 0 needs.
     unroll<NS - 1>([&](auto uc) {
         constexpr int u = decltype(uc)::value;
         if (u < nst) dma(u, ring(uc));
     });
-    if (nst - 1 >= NS - 2) {
-        ESDA_WAIT_VM((NS - 2) * R::DPW);
+    if constexpr (RAW) {
+        // stages 0..2 landed (stage 2 for the first iteration's sums of squares)
+        if (nst - 1 >= NS - 2) {
+            ESDA_WAIT_VM((NS - 4) * R::DPW);
+        } else {
+            ESDA_WAIT_VM(0);
+        }
+        lds_barrier();
+        load_raw(ring(std::integral_constant<int, 0>{}));
+        publish_ss(0);
+        publish_tab(0, 0);
+        if (nst > 1) {
+            load_raw(ring(std::integral_constant<int, 1>{}));
+            publish_ss(1);
+            publish_tab(1, 1);
+        }
+        lds_barrier();
+        // scores of stage 0 (its raw operand is read again; araw keeps stage 1's)
+        {
+            u32x4 keep[KKW];
+#pragma unroll
+            for (int kk = 0; kk < KKW; ++kk) keep[kk] = araw[kk];
+            load_raw(ring(std::integral_constant<int, 0>{}));
+            qk_raw(0, 0, 0);
+#pragma unroll
+            for (int kk = 0; kk < KKW; ++kk) araw[kk] = keep[kk];
+        }
     } else {
-        ESDA_WAIT_VM(0);
+        if (nst - 1 >= NS - 2) {
+            ESDA_WAIT_VM((NS - 2) * R::DPW);
+        } else {
+            ESDA_WAIT_VM(0);
+        }
+        lds_barrier();
+        qk_partial(ring(std::integral_constant<int, 0>{}), 0);
     }
-    lds_barrier();
-    qk_partial(ring(std::integral_constant<int, 0>{}), 0);
 
     // Iteration st: one barrier, after which (a) every wave's stage-st partial scores
-    // are in xch, (b) stage st+1 has landed from every wave's DMA, and (c) every wave is
-    // done with stage st-1's buffer, which is refilled at once.  The scores of stage
+    // are in xch, (b) stage st+AHEAD has landed from every wave's DMA, and (c) every wave
+    // is done with stage st-1's buffer, which is refilled at once.  The scores of stage
     // st+1 are computed alongside stage st's PV, so the two dependency chains overlap.
     auto stage = [&](int s0, auto uc) {
         constexpr int u = decltype(uc)::value;
         const int st = s0 + u;
         if (st >= nst) return;
-        if (st + 1 < nst) {
-            // own DMA for stage st+1 done; stages st+2 .. st+NS-2 may stay in flight
-            if (nst - st - 2 >= NS - 3) {
-                ESDA_WAIT_VM((NS - 3) * R::DPW);
+        if (st + AHEAD < nst) {
+            // own DMA for stage st+AHEAD done; the stages behind it may stay in flight
+            if (nst - st - AHEAD - 1 >= NS - 2 - AHEAD) {
+                ESDA_WAIT_VM((NS - 2 - AHEAD) * R::DPW);
             } else {
                 ESDA_WAIT_VM(0);
             }
@@ -370,7 +591,16 @@ void attend_kernel(AttendParams p) {
         f32x4 sc = xch[st & 1][0][lane];
 #pragma unroll
         for (int w = 1; w < NW; ++w) sc += xch[st & 1][w][lane];
-        if (st + 1 < nst) qk_partial(ring(std::integral_constant<int, (u + 1) % NS>{}), (st + 1) & 1);
+        if constexpr (RAW) {
+            if (st + 1 < nst) qk_raw((st + 1) % 3, (st + 1) & 1, (st + 1) & 1);
+            if (st + 2 < nst) {
+                load_raw(ring(std::integral_constant<int, (u + 2) % NS>{}));
+                publish_ss((st + 2) % 3);
+                publish_tab(st + 2, st & 1);
+            }
+        } else {
+            if (st + 1 < nst) qk_partial(ring(std::integral_constant<int, (u + 1) % NS>{}), (st + 1) & 1);
+        }
         // Online softmax (log2 domain), identical in every wave; rows past the split
         // end (last stage only) are masked.
         const int jt = j0 + st * 16;
@@ -390,11 +620,26 @@ void attend_kernel(AttendParams p) {
             m = mnew;
         }
         short4v pbs;
+        if constexpr (RAW) {
+            // V = kraw * rinv enters through the weight: P = bf16(e * rinv).  l adds the
+            // same rounded weight divided by rinv (ms * rinv = 1 / rinv), so numerator and
+            // denominator carry identical rounding and a dominant row is reproduced exactly.
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const __bf16 pr = (__bf16) __builtin_amdgcn_exp2f(sc[r] - m);
-            l += (float) pr;
-            pbs[r] = __builtin_bit_cast(short, pr);
+            for (int r = 0; r < 4; ++r) {
+                const float e = __builtin_amdgcn_exp2f(sc[r] - m);
+                const float ms = row_ms(st % 3, 4 * lg + r);
+                const float rinv = __builtin_amdgcn_rsqf(ms);
+                const __bf16 pw = (__bf16) (e * rinv);
+                l += (float) pw * (ms * rinv);
+                pbs[r] = __builtin_bit_cast(short, pw);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const __bf16 pr = (__bf16) __builtin_amdgcn_exp2f(sc[r] - m);
+                l += (float) pr;
+                pbs[r] = __builtin_bit_cast(short, pr);
+            }
         }
         // O^T (this wave's dims) += V^T . P^T
         const unsigned char *vb = ring(uc) + VOFF;
@@ -411,7 +656,7 @@ void attend_kernel(AttendParams p) {
     // into its cache row (bit-exact).  Its own DMA reads that row from k_new / v_new and
     // no other workgroup reads it; the copy runs after this workgroup's ring has
     // drained, so no outstanding load is counted against the ring's waits.
-    if (wave == 0 && j1 == sv.nvis) {
+    if (append && wave == 0 && j1 == sv.nvis) {
         for (int c = lane; c < D / 8; c += 64) {
             *reinterpret_cast<u32x4 *>(kbase + (size_t) sv.newrow * D + c * 8) =
                 *reinterpret_cast<const u32x4 *>(knew + c * 8);
@@ -551,6 +796,11 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
     }
 }
 
+__global__ void fill_i32_kernel(int *dst, int value, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = value;
+}
+
 // Plain row copy for multi-row appends (slice_update at rows row0 .. row0 + n - 1).
 __global__ __launch_bounds__(256) void append_kernel(uint16_t *cache, long long seq_stride,
                                                       long long head_stride, int Hkv, int D,
@@ -576,6 +826,12 @@ __global__ __launch_bounds__(256) void append_kernel(uint16_t *cache, long long 
 // ------------------------------------------------------------------------ host side
 
 thread_local std::string g_err;
+
+}  // namespace
+
+void esda_detail::set_error(const std::string &msg) { g_err = msg; }
+
+namespace {
 
 int fail(int code, const std::string &msg) {
     g_err = msg;
@@ -665,10 +921,10 @@ int make_plan(const esda_decode_desc *d, Plan *pl) {
 template <int D>
 constexpr int ring_waves() { return 4; }
 
-template <int D, bool SHARED>
+template <int D, bool SHARED, bool RAW = false>
 hipError_t launch_attend(const AttendParams &ap, dim3 grid, hipStream_t st) {
     constexpr int NW = ring_waves<D>();
-    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW>), grid, dim3(64 * NW), 0, st, ap);
+    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW>), grid, dim3(64 * NW), 0, st, ap);
     return hipGetLastError();
 }
 
@@ -678,6 +934,82 @@ hipError_t dispatch_attend(int D, bool shared, const AttendParams &ap, dim3 grid
         case 256: return shared ? launch_attend<256, true>(ap, grid, st) : launch_attend<256, false>(ap, grid, st);
         default:  return shared ? launch_attend<512, true>(ap, grid, st) : launch_attend<512, false>(ap, grid, st);
     }
+}
+
+// The raw-mode step as a plain decode description: linear rows, full causal span, one
+// shared stream of 512-dim rows.
+int raw_as_decode(const esda_raw_desc *r, esda_decode_desc *d) {
+    if (!r) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw: null description");
+    if (r->head_dim != kRawDim) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw: head_dim must be 512");
+    if (!(r->eps >= 0.0f)) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw: eps must be >= 0");
+    std::memset(d, 0, sizeof(*d));
+    d->batch = r->batch;
+    d->num_q_heads = r->num_q_heads;
+    d->num_kv_heads = r->num_kv_heads;
+    d->head_dim = r->head_dim;
+    d->cap = r->cap;
+    d->window = 0;
+    d->ring = 0;
+    d->kv_shared = 1;
+    d->seq_stride = r->seq_stride;
+    d->head_stride = r->head_stride;
+    d->max_visible = r->max_visible;
+    d->split_rows = r->split_rows;
+    d->scale = r->scale;
+    return ESDA_OK;
+}
+
+// Launches the requested stages of one decode step (raw: the raw-K attend kernel).
+int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap_in, uint16_t *out,
+               void *workspace, int stages, bool raw, hipStream_t st) {
+    unsigned char *ws = static_cast<unsigned char *>(workspace);
+    float *part_ml = reinterpret_cast<float *>(ws + pl.off_ml);
+    float *part_acc = reinterpret_cast<float *>(ws + pl.off_acc);
+    if (stages & ESDA_STAGE_ATTEND) {
+        AttendParams ap = ap_in;
+        ap.part_acc = part_acc;
+        ap.part_ml = part_ml;
+        ap.status = reinterpret_cast<int *>(ws);
+        ap.seq_stride = d->seq_stride;
+        ap.head_stride = d->head_stride;
+        ap.B = d->batch;
+        ap.Hq = d->num_q_heads;
+        ap.Hkv = d->num_kv_heads;
+        ap.G = pl.G;
+        ap.cap = d->cap;
+        ap.window = d->window;
+        ap.ring = d->ring;
+        ap.S = pl.S;
+        ap.chunk = pl.chunk;
+        ap.scale_log2e = d->scale * kLog2e;
+        dim3 grid(pl.S, d->num_kv_heads, d->batch);
+        hipError_t e = raw ? launch_attend<kRawDim, true, true>(ap, grid, st)
+                           : dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
+        if (e != hipSuccess) return hip_fail(e, "attend_kernel launch");
+    }
+    if (stages & ESDA_STAGE_MERGE) {
+        MergeParams mp;
+        mp.part_acc = part_acc;
+        mp.part_ml = part_ml;
+        mp.pos = ap_in.pos;
+        mp.row_base = ap_in.row_base;
+        mp.out = out;
+        mp.B = d->batch;
+        mp.Hq = d->num_q_heads;
+        mp.Hkv = d->num_kv_heads;
+        mp.G = pl.G;
+        mp.D = d->head_dim;
+        mp.cap = d->cap;
+        mp.window = d->window;
+        mp.ring = d->ring;
+        mp.S = pl.S;
+        mp.chunk = pl.chunk;
+        dim3 grid(d->head_dim / kMergeDims, d->num_q_heads, d->batch);
+        hipLaunchKernelGGL(merge_kernel, grid, dim3(kMergeThreads), 0, st, mp);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(e, "merge_kernel launch");
+    }
+    return ESDA_OK;
 }
 
 }  // namespace
@@ -721,65 +1053,65 @@ int esda_decode_stages(const esda_decode_desc *d, const esda_decode_args *a, int
     rc = check_device();
     if (rc) return rc;
 
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    unsigned char *ws = static_cast<unsigned char *>(a->workspace);
-    float *part_ml = reinterpret_cast<float *>(ws + pl.off_ml);
-    float *part_acc = reinterpret_cast<float *>(ws + pl.off_acc);
-    if (stages & ESDA_STAGE_ATTEND) {
-        AttendParams ap;
-        ap.q = static_cast<const uint16_t *>(a->q);
-        ap.k_new = static_cast<const uint16_t *>(a->k_new);
-        ap.v_new = static_cast<const uint16_t *>(d->kv_shared ? a->k_new : a->v_new);
-        ap.k_cache = static_cast<uint16_t *>(a->k_cache);
-        ap.v_cache = static_cast<uint16_t *>(a->v_cache);
-        ap.pos = a->pos;
-        ap.row_base = a->row_base;
-        ap.part_acc = part_acc;
-        ap.part_ml = part_ml;
-        ap.status = reinterpret_cast<int *>(ws);
-        ap.seq_stride = d->seq_stride;
-        ap.head_stride = d->head_stride;
-        ap.B = d->batch;
-        ap.Hq = d->num_q_heads;
-        ap.Hkv = d->num_kv_heads;
-        ap.G = pl.G;
-        ap.cap = d->cap;
-        ap.window = d->window;
-        ap.ring = d->ring;
-        ap.S = pl.S;
-        ap.chunk = pl.chunk;
-        ap.scale_log2e = d->scale * kLog2e;
-        dim3 grid(pl.S, d->num_kv_heads, d->batch);
-        hipError_t e = dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
-        if (e != hipSuccess) return hip_fail(e, "attend_kernel launch");
-    }
-    if (stages & ESDA_STAGE_MERGE) {
-        MergeParams mp;
-        mp.part_acc = part_acc;
-        mp.part_ml = part_ml;
-        mp.pos = a->pos;
-        mp.row_base = a->row_base;
-        mp.out = static_cast<uint16_t *>(a->out);
-        mp.B = d->batch;
-        mp.Hq = d->num_q_heads;
-        mp.Hkv = d->num_kv_heads;
-        mp.G = pl.G;
-        mp.D = d->head_dim;
-        mp.cap = d->cap;
-        mp.window = d->window;
-        mp.ring = d->ring;
-        mp.S = pl.S;
-        mp.chunk = pl.chunk;
-        dim3 grid(d->head_dim / kMergeDims, d->num_q_heads, d->batch);
-        hipLaunchKernelGGL(merge_kernel, grid, dim3(kMergeThreads), 0, st, mp);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return hip_fail(e, "merge_kernel launch");
-    }
-    return ESDA_OK;
+    AttendParams ap{};
+    ap.q = static_cast<const uint16_t *>(a->q);
+    ap.k_new = static_cast<const uint16_t *>(a->k_new);
+    ap.v_new = static_cast<const uint16_t *>(d->kv_shared ? a->k_new : a->v_new);
+    ap.k_cache = static_cast<uint16_t *>(a->k_cache);
+    ap.v_cache = static_cast<uint16_t *>(a->v_cache);
+    ap.pos = a->pos;
+    ap.row_base = a->row_base;
+    return run_stages(d, pl, ap, static_cast<uint16_t *>(a->out), a->workspace, stages, false,
+                      reinterpret_cast<hipStream_t>(stream));
 }
 
 int esda_decode(const esda_decode_desc *desc, const esda_decode_args *args, void *stream) {
     return esda_decode_stages(desc, args, ESDA_STAGE_ATTEND | ESDA_STAGE_MERGE, stream);
+}
+
+int esda_decode_raw_workspace_size(const esda_raw_desc *desc, size_t *bytes) {
+    esda_decode_desc d;
+    int rc = raw_as_decode(desc, &d);
+    if (rc) return rc;
+    return esda_decode_workspace_size(&d, bytes);
+}
+
+int esda_decode_raw_stages(const esda_raw_desc *desc, const esda_raw_args *a, int stages, void *stream) {
+    esda_decode_desc d;
+    int rc = raw_as_decode(desc, &d);
+    if (rc) return rc;
+    Plan pl;
+    rc = make_plan(&d, &pl);
+    if (rc) return rc;
+    if (!a) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw: null arguments");
+    if (!a->q || !a->raw_cache || !a->pos || !a->kw || !a->inv_freq || !a->out)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw: null device pointer");
+    if (!aligned16(a->q) || (a->k_new && !aligned16(a->k_new)) || !aligned16(a->raw_cache) ||
+        !aligned16(a->kw) || !aligned16(a->inv_freq) || !aligned16(a->out))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw: tensors must be 16-byte aligned");
+    if (!a->workspace || a->workspace_bytes < pl.bytes || !aligned16(a->workspace))
+        return fail(ESDA_ERR_WORKSPACE, "esda_decode_raw: workspace missing or smaller than esda_decode_raw_workspace_size");
+    if ((stages & (ESDA_STAGE_ATTEND | ESDA_STAGE_MERGE)) == 0 || (stages & ~3))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_stages: bad stage mask");
+    rc = check_device();
+    if (rc) return rc;
+    AttendParams ap{};
+    ap.q = static_cast<const uint16_t *>(a->q);
+    ap.k_new = static_cast<const uint16_t *>(a->k_new);
+    ap.v_new = ap.k_new;
+    ap.k_cache = static_cast<uint16_t *>(a->raw_cache);
+    ap.v_cache = ap.k_cache;
+    ap.pos = a->pos;
+    ap.row_base = nullptr;
+    ap.kw = static_cast<const uint16_t *>(a->kw);
+    ap.inv_freq = a->inv_freq;
+    ap.eps = desc->eps;
+    return run_stages(&d, pl, ap, static_cast<uint16_t *>(a->out), a->workspace, stages, true,
+                      reinterpret_cast<hipStream_t>(stream));
+}
+
+int esda_decode_raw(const esda_raw_desc *desc, const esda_raw_args *args, void *stream) {
+    return esda_decode_raw_stages(desc, args, ESDA_STAGE_ATTEND | ESDA_STAGE_MERGE, stream);
 }
 
 int esda_decode_status(const esda_decode_desc *desc, void *workspace, int32_t *bad_sequences,
@@ -823,6 +1155,18 @@ int esda_kv_append(void *cache, int64_t seq_stride, int64_t head_stride, int32_t
                        nullptr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "append_kernel launch");
+    return ESDA_OK;
+}
+
+int esda_fill_i32(int32_t *dst, int32_t value, int32_t n, void *stream) {
+    if (!dst || n < 0) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_fill_i32: null pointer or negative count");
+    if (n == 0) return ESDA_OK;
+    int rc = check_device();
+    if (rc) return rc;
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((n + 255) / 256), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), dst, value, n);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "fill_i32_kernel launch");
     return ESDA_OK;
 }
 

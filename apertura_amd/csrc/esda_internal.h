@@ -1,0 +1,9 @@
+// esda_internal.h -- library-internal hooks shared by the HIP sources and the ES* C++
+// layer (not part of the public ABI).
+#pragma once
+#include <string>
+
+namespace esda_detail {
+// Sets the calling thread's esda_last_error() message.
+void set_error(const std::string &msg);
+}  // namespace esda_detail

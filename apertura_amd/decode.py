@@ -11,7 +11,7 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import DecodeArgs, DecodeDesc, check, lib
+from ._lib import DecodeArgs, DecodeDesc, RawArgs, RawDesc, check, lib
 
 STAGE_ATTEND = 1
 STAGE_MERGE = 2
@@ -162,6 +162,105 @@ class DecodeCall:
     def __call__(self, stream=None, stages: int | None = None) -> torch.Tensor:
         rc = self._fn(self._pd, self._pa, self.stages if stages is None else stages,
                       _stream_ptr(stream))
+        if rc:
+            check(rc)
+        return self.out
+
+
+# ----------------------------------------------------------------------- raw-K mode
+
+@dataclass
+class RawStep:
+    """Shapes of a raw-K decode step (esda_raw_desc): the cache holds pre-norm k_proj rows
+    [B, Hkv, cap, 512]; sequence b attends rows 0 .. pos[b] with K and V rebuilt from them
+    (ESDecodeAttn.mm:17-117)."""
+
+    batch: int
+    num_q_heads: int
+    num_kv_heads: int
+    cap: int
+    eps: float = 1e-6
+    scale: float = 1.0
+    max_visible: int = 0
+    split_rows: int = 0
+    seq_stride: int | None = None
+    head_stride: int | None = None
+    head_dim: int = 512
+
+    def desc(self) -> RawDesc:
+        hs = self.head_stride if self.head_stride is not None else self.cap * self.head_dim
+        ss = self.seq_stride if self.seq_stride is not None else self.num_kv_heads * hs
+        return RawDesc(self.batch, self.num_q_heads, self.num_kv_heads, self.head_dim, self.cap,
+                       ss, hs, self.max_visible, self.split_rows, self.scale, self.eps)
+
+    @classmethod
+    def for_cache(cls, cache: torch.Tensor, num_q_heads: int, **kw) -> "RawStep":
+        B, Hkv, cap, D = cache.shape
+        if D != 512 or cache.stride(3) != 1 or cache.stride(2) != D:
+            raise ValueError("raw cache rows must be dense [B, Hkv, cap, 512]")
+        return cls(batch=B, num_q_heads=num_q_heads, num_kv_heads=Hkv, cap=cap,
+                   seq_stride=cache.stride(0), head_stride=cache.stride(1), **kw)
+
+
+def raw_workspace_bytes(step: RawStep) -> int:
+    n = ctypes.c_size_t(0)
+    d = step.desc()
+    check(lib().esda_decode_raw_workspace_size(ctypes.byref(d), ctypes.byref(n)))
+    return int(n.value)
+
+
+def new_raw_workspace(step: RawStep, device) -> torch.Tensor:
+    return torch.zeros(raw_workspace_bytes(step), dtype=torch.uint8, device=device)
+
+
+def decode_raw(step: RawStep, q: torch.Tensor, k_new: torch.Tensor | None, raw_cache: torch.Tensor,
+               pos: torch.Tensor, kw: torch.Tensor, inv_freq: torch.Tensor,
+               out: torch.Tensor | None = None, workspace: torch.Tensor | None = None, stream=None,
+               stages: int = STAGE_ATTEND | STAGE_MERGE) -> torch.Tensor:
+    """Raw-K decode step: write k_new (raw rows, or None) at row pos[b], then attend rows
+    0 .. pos[b]; returns out [B, Hq, 512] bf16."""
+    bf = torch.bfloat16
+    if q.shape != (step.batch, step.num_q_heads, 512) or not q.is_contiguous():
+        raise ValueError("q must be contiguous [B, Hq, 512]")
+    if k_new is not None and (k_new.shape != (step.batch, step.num_kv_heads, 512) or not k_new.is_contiguous()):
+        raise ValueError("k_new must be contiguous [B, Hkv, 512]")
+    if pos.dtype != torch.int32 or pos.shape != (step.batch,):
+        raise ValueError("pos must be int32 [B]")
+    if kw.dtype != bf or kw.numel() != 512 or inv_freq.dtype != torch.float32 or inv_freq.numel() < 64:
+        raise ValueError("kw must be bf16 [512] and inv_freq f32 [>= 64]")
+    if out is None:
+        out = torch.empty_like(q)
+    if workspace is None:
+        workspace = new_raw_workspace(step, q.device)
+    args = RawArgs(_dev_ptr(q, bf), _dev_ptr(k_new, bf), _dev_ptr(raw_cache, bf), _dev_ptr(pos),
+                   _dev_ptr(kw, bf), _dev_ptr(inv_freq), _dev_ptr(out, bf), _dev_ptr(workspace),
+                   workspace.numel() * workspace.element_size())
+    d = step.desc()
+    check(lib().esda_decode_raw_stages(ctypes.byref(d), ctypes.byref(args), stages, _stream_ptr(stream)))
+    return out
+
+
+class RawCall:
+    """decode_raw with its arguments marshalled once (see DecodeCall)."""
+
+    def __init__(self, step: RawStep, q, k_new, raw_cache, pos, kw, inv_freq, out=None, workspace=None,
+                 stages: int = STAGE_ATTEND | STAGE_MERGE):
+        if out is None:
+            out = torch.empty_like(q)
+        if workspace is None:
+            workspace = new_raw_workspace(step, q.device)
+        self._keep = (q, k_new, raw_cache, pos, kw, inv_freq, out, workspace)
+        self.step, self.out, self.workspace, self.stages = step, out, workspace, stages
+        bf = torch.bfloat16
+        self._desc = step.desc()
+        self._args = RawArgs(_dev_ptr(q, bf), _dev_ptr(k_new, bf), _dev_ptr(raw_cache, bf), _dev_ptr(pos),
+                             _dev_ptr(kw, bf), _dev_ptr(inv_freq), _dev_ptr(out, bf), _dev_ptr(workspace),
+                             workspace.numel() * workspace.element_size())
+        self._fn = lib().esda_decode_raw_stages
+        self._pd, self._pa = ctypes.byref(self._desc), ctypes.byref(self._args)
+
+    def __call__(self, stream=None, stages: int | None = None) -> torch.Tensor:
+        rc = self._fn(self._pd, self._pa, self.stages if stages is None else stages, _stream_ptr(stream))
         if rc:
             check(rc)
         return self.out

@@ -48,6 +48,10 @@ WORKLOADS = {
                pos=lambda rng, B: [int(x) for x in rng.integers(2048, 32769, size=B)], scale=1 / 16),
     "c4": dict(B=1, Hq=32, Hkv=4, D=512, cap=131072, window=0, ring=False, shared=True,
                pos=lambda rng, B: [131071], scale=512 ** -0.5),
+    # C4's shape in raw-K mode (the reference's esDecodeAttnGlobal path): the cache holds
+    # pre-norm k_proj rows; K and V are rebuilt in the kernel; in-model scale 1.0.
+    "c4raw": dict(B=1, Hq=32, Hkv=4, D=512, cap=131072, window=0, ring=False, shared=True, raw=True,
+                  pos=lambda rng, B: [131071], scale=1.0),
 }
 
 # C5 layer types (ESModelConfig.mm:82-86: every 6th layer is global, the last one too).
@@ -87,6 +91,8 @@ def main() -> int:
     ap.add_argument("--local-split-rows", type=int, default=0, help="c5: split rows of local layers")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="time a plain device copy of MIB MiB instead (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         _die_multi_gpu(max(args.gpus, int(os.environ.get("WORLD_SIZE", "1"))))
@@ -94,8 +100,11 @@ def main() -> int:
     import numpy as np
     import torch
 
-    from apertura_amd.decode import DecodeCall, DecodeStep, STAGE_ATTEND, new_workspace
+    from apertura_amd.decode import (DecodeCall, DecodeStep, RawCall, RawStep, STAGE_ATTEND,
+                                     new_raw_workspace, new_workspace)
 
+    if args.calibrate_copy:
+        return calibrate_copy(args)
     if args.workload == "c5":
         return bench_c5(args)
     w = WORKLOADS[args.workload]
@@ -117,12 +126,25 @@ def main() -> int:
     k_new = rms_bf16((B, Hkv, D))
     v_new = None if w["shared"] else rms_bf16((B, Hkv, D))
     pos_d = torch.tensor(pos, dtype=torch.int32, device=dev)
-    step = DecodeStep.for_cache(k_cache, Hq, window=w["window"], ring=w["ring"],
-                                kv_shared=w["shared"], scale=w["scale"], split_rows=args.split_rows)
-    ws = new_workspace(step, dev)
     out = torch.empty_like(q)
     stream = torch.cuda.Stream()  # default priority (side stream for graph capture)
-    call = DecodeCall(step, q, k_new, v_new, k_cache, v_cache, pos_d, out=out, workspace=ws)
+    raw = None
+    if w.get("raw"):
+        # raw k_proj rows (not normalised), a k-norm weight and Gemma-4's global rotary table
+        k_cache.mul_(2.0)
+        k_new.mul_(2.0)
+        kw = (1.0 + 0.25 * torch.randn(D, device=dev, generator=gen)).to(torch.bfloat16)
+        inv_freq = torch.zeros(D // 2, dtype=torch.float32, device=dev)
+        inv_freq[:64] = 1.0 / (1.0e6 ** (torch.arange(64, dtype=torch.float64, device=dev) * 2 / D)).float()
+        step = RawStep.for_cache(k_cache, Hq, eps=1e-6, scale=w["scale"], split_rows=args.split_rows)
+        ws = new_raw_workspace(step, dev)
+        call = RawCall(step, q, k_new, k_cache, pos_d, kw, inv_freq, out=out, workspace=ws)
+        raw = (kw, inv_freq)
+    else:
+        step = DecodeStep.for_cache(k_cache, Hq, window=w["window"], ring=w["ring"],
+                                    kv_shared=w["shared"], scale=w["scale"], split_rows=args.split_rows)
+        ws = new_workspace(step, dev)
+        call = DecodeCall(step, q, k_new, v_new, k_cache, v_cache, pos_d, out=out, workspace=ws)
 
     def timed(fn, n):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -165,7 +187,10 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(w, pos, q, k_cache, v_cache, k_new, v_new, args.cpu_threads)
+        if raw is not None:
+            cpu = cpu_baseline_raw(w, pos, q, k_cache, raw[0], raw[1], args.cpu_threads)
+        else:
+            cpu = cpu_baseline(w, pos, q, k_cache, v_cache, k_new, v_new, args.cpu_threads)
 
     line = {
         "metric": "decode-attn HBM GB/s (and us/step) at Gemma-4-31B shapes, 1 GPU",
@@ -187,14 +212,17 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) rows, unit-RMS, bf16)",
         "config": {
             "workload": {"c4": "C4 global k_eq_v decode, L=131072", "c2": "C2 global k_eq_v decode, L=8193",
-                         "c1": "C1 local decode, L=1024", "c3": "C3 local ring decode, B=8"}[args.workload],
+                         "c1": "C1 local decode, L=1024", "c3": "C3 local ring decode, B=8",
+                         "c4raw": "C4 shape, raw-K mode (K/V rebuilt in-kernel), L=131072"}[args.workload],
             "batch": B, "num_q_heads": Hq, "num_kv_heads": Hkv, "head_dim": D,
             "visible_rows": visible_rows(w, pos), "kv_shared": w["shared"],
             "window": w["window"], "ring": w["ring"], "split_rows": step.split_rows or "auto",
             "algorithmic_bytes_per_step": nbytes,
         },
         "roofline": {
-            "bound": "hbm", "kernel": "attend_kernel<D,kv_shared> (split-K + fused append)",
+            "bound": "hbm",
+            "kernel": ("attend_kernel<512,shared,raw> (raw-K rebuild + split-K + fused append)" if raw is not None
+                       else "attend_kernel<D,kv_shared> (split-K + fused append)"),
             "achieved": round(gbs_attend, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(gbs_attend / PEAK_HBM_GBS, 4), "traffic": None,
             "kernel_us": round(ms_attend * 1e3, 3),
@@ -202,6 +230,29 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def calibrate_copy(args) -> int:
+    """A plain device-to-device copy of known size: the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    readings of this kernel give the factor between those counters and true HBM bytes."""
+    import torch
+
+    n = args.calibrate_copy << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(max(1, args.warmup)):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n,
+                      "us": round(ms * 1e3, 3), "GB/s": round(2 * n / (ms * 1e-3) / 1e9, 2)}), flush=True)
     return 0
 
 
@@ -348,6 +399,41 @@ def cpu_baseline(w, pos, q, k_cache, v_cache, k_new, v_new, threads: int):
             "cores": threads, "kind": "port",
             "sample": f"full workload step x{reps} repeats ({t_total:.1f} s), reference-rounding "
                       f"oracle (MLX CPU path unavailable offline); host {os.cpu_count()} cpus visible"}
+
+
+def cpu_baseline_raw(w, pos, q, k_cache, kw, inv_freq, threads: int):
+    """CPU oracle of the raw-K step (orc_decode_raw_f64: the reconstruction of
+    ESDecodeAttn.mm:17-117 in fp64) on a bounded sample: the first `rows` cached rows of
+    every kv head, repeated for >= 10 s; throughput in the step's bytes per row."""
+    import numpy as np
+    import torch
+
+    root = os.path.dirname(os.path.abspath(__file__))
+    sys.path.insert(0, root)
+    from oracle import oracle as orc
+
+    def host(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    B, Hq, Hkv, D = w["B"], w["Hq"], w["Hkv"], w["D"]
+    rows = 16384
+    qh = host(q).reshape(B, Hq, D)[0]
+    raw = np.ascontiguousarray(host(k_cache).reshape(B, Hkv, -1, D)[0, :, :rows])
+    kwh = host(kw).reshape(-1)
+    inv = inv_freq.detach().cpu().numpy()
+    reps, t_total = 0, 0.0
+    while t_total < 10.0 and reps < 50:
+        t0 = time.perf_counter()
+        orc.decode_raw_f64(qh, raw, rows, kwh, 1e-6, inv, w["scale"], threads=threads)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    sec = t_total / reps
+    nbytes = rows * Hkv * D * 2
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "us_per_step": None,
+            "cores": threads, "kind": "port",
+            "sample": f"{rows} of {visible_rows(w, pos)[0]} rows per kv head x{reps} repeats "
+                      f"({t_total:.1f} s), fp64 raw-K oracle (MLX CPU path unavailable offline); "
+                      f"host {os.cpu_count()} cpus visible"}
 
 
 if __name__ == "__main__":

@@ -1,0 +1,26 @@
+#pragma once
+//  ESDecodeAttn -- raw-K decode attention for the GLOBAL layers (head_dim 512) with the
+//  reference's signature (Apertura ESDecodeAttn.h:22-28), backed by esda_decode_raw.
+//  The kernel streams each cached raw k_proj row once and rebuilds in registers:
+//      rinv = rsqrt(mean(kraw^2) + eps)
+//      K    = bf16(rope(kraw * rinv * kw))   (rotary pairs (d, d + 256) for d < 64,
+//                                             cos / sin of the fp32 angle rounded to bf16)
+//      V    = kraw * rinv                    (folded into the softmax weight)
+//  then attends the query heads of each kv head, split-K, merged in fp32.
+#include "ESTensor.h"
+
+#include <vector>
+
+namespace es {
+
+// q:      [numQ, 512] bf16, query heads kv-major, post q-norm + RoPE.
+// rawBuf: the UNSLICED cache buffer [numKV, pitch, 512] bf16 of raw k_proj rows.
+// len:    live rows (attended: rows 0 .. len-1; row t has rotary position t).
+// kw:     k-norm weights [512] bf16.  invFreq: rotary table (>= 64 entries; the first
+//         64 are used, a zero tail is the identity).  Returns O [numQ, 512] bf16.
+// Throws std::invalid_argument on shape contracts (ESDecodeAttn.mm:419-422).
+Tensor esDecodeAttnGlobal(const Tensor &q, const Tensor &rawBuf, int len, int pitch, const Tensor &kw,
+                          float eps, const std::vector<float> &invFreq, hipStream_t stream = nullptr,
+                          Tensor *out = nullptr);
+
+}  // namespace es

@@ -1,0 +1,120 @@
+#pragma once
+//  ESKVCache -- per-layer key/value storage on the GPU with the reference's interface
+//  (Apertura ESKVCache.h:44-224).  Buffers are [kvHeads, capacity, headDim] bf16 per
+//  layer; update() appends along the sequence axis and returns the cached K/V as views.
+//  Two storage modes, selected per call as in the reference (ESKVCache.h:7-21):
+//    - legacy (prealloc=false): concat-grow, slice eviction (the bit-exact reference);
+//    - prealloc (prealloc=true): in-place appends into a buffer grown in kGrowChunk-row
+//      steps, a logical `start` cursor for sliding-window eviction, and compaction of the
+//      live range into a fresh buffer when the write cursor reaches capacity.
+//  decode() is the fused decode step of this library: the prealloc append and the
+//  attention of the new token in one GPU pass (esda_decode), replacing update()
+//  followed by SDPA at ESAttention.mm:105 and :188.
+//  KV snapshots, prefix markers, turn rewind, quantized / q8 storage and the compiled
+//  step mode are not implemented: their members keep the reference's signatures and
+//  return its failure values (-1 / false).
+//
+//  Every call takes a HIP stream (nullptr = the default stream).  Buffer growth and
+//  compaction synchronise that stream before the old buffer is released.  An instance
+//  is used from one thread at a time (the reference runs its engine on one thread).
+#include "ESTensor.h"
+
+#include <functional>
+#include <optional>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace es {
+
+class ESKVCache {
+public:
+    explicit ESKVCache(int numLayers);
+    ~ESKVCache() = default;
+    ESKVCache(const ESKVCache &) = delete;
+    ESKVCache &operator=(const ESKVCache &) = delete;
+
+    static constexpr int kGrowChunk = 256;
+
+    // Append kNew/vNew ([kvHeads, nNew, headDim] bf16, rows contiguous) for `layer`;
+    // returns the cached {K, V} as views [kvHeads, live, headDim].  maxKeep > 0 keeps
+    // only the last maxKeep keys (sliding-window eviction).  (ESKVCache.mm:19-110)
+    // Throws std::runtime_error when the slot holds raw-K content (ESKVCache.mm:59-62).
+    // In prealloc mode a slot first filled with vNew aliasing kNew keeps one shared K=V
+    // buffer (attention_k_eq_v); later appends to it must alias too.
+    std::pair<Tensor, Tensor> update(int layer, const Tensor &kNew, const Tensor &vNew, int maxKeep = 0,
+                                     bool prealloc = false, hipStream_t stream = nullptr);
+
+    // Raw-K storage: only the pre-norm k_proj rows, one stream (ESKVCache.mm:458-504).
+    // {live view [kvHeads, len, headDim], whole buffer, len, pitch (= buffer rows)}.
+    struct Raw {
+        Tensor view, buffer;
+        int len, pitch;
+    };
+    Raw updateRaw(int layer, const Tensor &kNew, bool prealloc, hipStream_t stream = nullptr);
+
+    // Fused decode step for `layer` (prealloc storage): appends the single new row of
+    // kNew/vNew ([kvHeads, 1, headDim]) and returns softmax(scale q K^T) V over the rows
+    // the reference would attend after update(maxKeep): [numQHeads, headDim] bf16 in
+    // `out` (allocated when null).  q: numQHeads*headDim bf16, query heads kv-major.
+    // vNew aliasing kNew (same data pointer) is attention_k_eq_v: a slot created that
+    // way keeps one shared K=V buffer, written and read once.
+    Tensor decode(int layer, const Tensor &q, const Tensor &kNew, const Tensor &vNew, int maxKeep,
+                  float scale, hipStream_t stream = nullptr, Tensor *out = nullptr);
+
+    // Fused raw-K decode step: updateRaw(layer, kNew, true) and esDecodeAttnGlobal over
+    // the slot in one GPU pass.  kNew: [kvHeads, 1, 512] raw k_proj rows.
+    Tensor decodeRaw(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
+                     const std::vector<float> &invFreq, hipStream_t stream = nullptr, Tensor *out = nullptr);
+
+    // The cached {K, V} without appending (ESKVCache.mm:112-119).
+    std::pair<Tensor, Tensor> current(int layer, bool prealloc) const;
+
+    // Not implemented (persistence, rewind, quantized storage): the reference's
+    // signatures (ESKVCache.h:102-174) with its failure results.
+    void markPrefix(int pos, const std::string &fingerprint);
+    bool saveSnapshot(const std::string &path, const std::string &fingerprint, int pos) const;
+    enum class RawMode { composite, raw, rawQ8, asStored };
+    int restoreSnapshot(const std::string &path, const std::string &fingerprint,
+                        RawMode mode = RawMode::asStored,
+                        const std::function<std::string(int)> &prefixFp = nullptr);
+    bool markRewindPoint(int pos);
+    int rewindToMark();
+    void clearRewindMark() {}
+
+    int seqLen() const { return seqLen_; }
+    void markStep(int nNew) { seqLen_ += nNew; }
+    void reset();
+
+    int numLayers() const { return (int) slots_.size(); }
+    // Prealloc slot bookkeeping (read-only).
+    int slotLen(int layer) const { return slotAt(layer).len; }
+    int slotStart(int layer) const { return slotAt(layer).start; }
+    int slotCapacity(int layer) const;
+    bool slotLost(int layer) const { return slotAt(layer).lost; }
+    bool slotShared(int layer) const { return slotAt(layer).shared; }
+    bool slotRaw(int layer) const { return slotAt(layer).k.has_value() && !slotAt(layer).v.has_value(); }
+
+private:
+    struct Slot {
+        std::optional<Tensor> k, v;  // v empty: raw-K content
+        int len = 0, start = 0;
+        bool lost = false;    // rows before `start` were discarded by a compaction
+        bool shared = false;  // v is the same buffer as k (attention_k_eq_v decode)
+    };
+    std::vector<std::optional<Tensor>> k_, v_;  // legacy storage
+    std::vector<Slot> slots_;                   // prealloc storage
+    int seqLen_ = 0;
+    std::optional<Tensor> posDev_;     // per-layer position words for decode()
+    std::optional<Tensor> workspace_;  // esda_decode / esda_decode_raw workspace
+    std::optional<Tensor> invFreqDev_; // rotary table of the last decodeRaw()
+    std::vector<float> invFreqHost_;
+
+    const Slot &slotAt(int layer) const;
+    void checkLayer(int layer) const;
+    void growSlot(Slot &s, int nNew, hipStream_t stream, bool compactStart);
+    void *workspace(size_t bytes, hipStream_t stream);
+    int *positionWord(int layer, int value, hipStream_t stream);
+};
+
+}  // namespace es

@@ -107,6 +107,59 @@ int esda_kv_append(void *cache, int64_t seq_stride, int64_t head_stride, int32_t
                    int32_t num_kv_heads, int32_t head_dim, int32_t cap, const void *src,
                    int32_t n_new, const int32_t *row0, void *stream);
 
+/* ---------------------------------------------------------------- raw-K mode
+ *
+ * Global layers with a raw-K cache: the cache holds only the pre-norm k_proj rows and
+ * the kernel rebuilds, per streamed row (ESDecodeAttn.mm:17-117):
+ *   rinv = rsqrt(mean(kraw^2) + eps)
+ *   K    = bf16(rope(kraw * rinv * kw)), rotary pairs (d, d + 256) for d < 64 at
+ *          rotary position = row index, cos / sin of the fp32 angle row*inv_freq[d]
+ *          rounded to bf16
+ *   V    = kraw * rinv (the factor is folded into the softmax weight)
+ * Linear rows, full causal span: sequence b attends rows 0 .. pos[b]. */
+typedef struct esda_raw_desc {
+    int32_t batch;        /* B                                          */
+    int32_t num_q_heads;  /* Hq                                         */
+    int32_t num_kv_heads; /* Hkv; Hq / Hkv <= 16                        */
+    int32_t head_dim;     /* must be 512                                */
+    int32_t cap;          /* rows per (sequence, kv head): the pitch     */
+    int64_t seq_stride;   /* elements; >= num_kv_heads * head_stride    */
+    int64_t head_stride;  /* elements; >= cap * 512, multiple of 8      */
+    int32_t max_visible;  /* upper bound on pos[b] + 1 (0 = cap)        */
+    int32_t split_rows;   /* rows per split (0 = automatic; multiple of 16) */
+    float scale;          /* softmax scale (the model uses 1.0)         */
+    float eps;            /* k-norm epsilon                             */
+} esda_raw_desc;
+
+typedef struct esda_raw_args {
+    const void *q;           /* [B, Hq, 512] bf16 (post q-norm + RoPE), 16-byte aligned */
+    const void *k_new;       /* [B, Hkv, 512] bf16 raw rows written to row pos[b] before
+                                attending, or NULL when the rows are already cached   */
+    void *raw_cache;         /* bf16 raw-K cache (layout as esda_decode_desc)          */
+    const int32_t *pos;      /* [B] int32, device memory: row of the newest token      */
+    const void *kw;          /* [512] bf16 k-norm weights                              */
+    const float *inv_freq;   /* [64] f32 rotary inverse frequencies                    */
+    void *out;               /* [B, Hq, 512] bf16                                      */
+    void *workspace;         /* esda_decode_raw_workspace_size bytes; first 256 zeroed once */
+    size_t workspace_bytes;
+} esda_raw_args;
+
+int esda_decode_raw_workspace_size(const esda_raw_desc *desc, size_t *bytes);
+
+/* Fused raw-K decode step (append + rebuild + attend + merge): replaces
+ * ESKVCache::updateRaw (ESKVCache.mm:458-504) followed by esDecodeAttnGlobal
+ * (ESDecodeAttn.mm:415-453) as called at ESAttention.mm:291-300. */
+int esda_decode_raw(const esda_raw_desc *desc, const esda_raw_args *args, void *stream);
+
+/* Stage-selectable form of esda_decode_raw (ESDA_STAGE_* as for esda_decode_stages). */
+int esda_decode_raw_stages(const esda_raw_desc *desc, const esda_raw_args *args, int stages,
+                           void *stream);
+
+/* dst[0 .. n-1] = value on `stream` (a kernel, so it may be captured in a graph): sets
+ * the per-sequence position words that replace the host-built additive mask upload of
+ * ESGemma4TextModel.mm:68-83 / ESAttention.mm:17-22. */
+int esda_fill_i32(int32_t *dst, int32_t value, int32_t n, void *stream);
+
 /* Message of the calling thread's last error ("" if none). */
 const char *esda_last_error(void);
 

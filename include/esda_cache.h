@@ -1,0 +1,102 @@
+/*
+ * esda_cache.h -- C ABI over the ES* C++ layer of libesda.so (headers under include/es): the
+ * reference's ESKVCache and esDecodeAttnGlobal behind an opaque handle, for FFI
+ * callers (ctypes, cgo, JNI) that cannot use the C++ classes.
+ *
+ * Every function returns ESDA_OK or an error code from esda.h; C++ exceptions never
+ * cross this boundary: std::invalid_argument becomes ESDA_ERR_INVALID_ARGUMENT and
+ * std::runtime_error ESDA_ERR_RUNTIME, with the message in esda_last_error().
+ * Row tensors are [kv_heads, n, head_dim] bf16 device memory with contiguous rows.
+ *
+ * Reference interfaces (Apertura tree):
+ *   esda_cache_create / destroy    ESKVCache(int numLayers)            ESKVCache.h:46
+ *   esda_cache_update              ESKVCache::update                   ESKVCache.h:57-58, ESKVCache.mm:19-110
+ *   esda_cache_update_raw          ESKVCache::updateRaw                ESKVCache.h:78-79, ESKVCache.mm:458-504
+ *   esda_cache_current             ESKVCache::current                  ESKVCache.h:117, ESKVCache.mm:112-119
+ *   esda_cache_decode              ESKVCache::update + SDPA decode     ESAttention.mm:105, :188
+ *   esda_cache_decode_raw          updateRaw + esDecodeAttnGlobal      ESAttention.mm:291-300
+ *   esda_cache_seq_len / mark_step ESKVCache::seqLen / markStep        ESKVCache.h:176-177
+ *   esda_cache_reset               ESKVCache::reset                    ESKVCache.h:178, ESKVCache.mm:622-638
+ *   esda_cache_save_snapshot, restore_snapshot, mark_rewind_point, rewind_to_mark:
+ *                                  ESKVCache.h:102-174; not implemented, they return the
+ *                                  reference's failure values (0 = false, -1)
+ *   esda_cache_slot                slot bookkeeping (len, start, capacity) for callers
+ *                                  and tests; the reference keeps it private (ESKVCache.h:183-192)
+ *   esda_decode_attn_global        esDecodeAttnGlobal                  ESDecodeAttn.h:27-28
+ */
+#ifndef APERTURA_ESDA_CACHE_H
+#define APERTURA_ESDA_CACHE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "esda.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct esda_cache esda_cache; /* opaque: one ESKVCache */
+
+/* A non-owning view of cached rows: element (h, r, d) at data[h*head_stride + r*head_dim + d]. */
+typedef struct esda_view {
+    void *data;
+    int32_t kv_heads;
+    int32_t rows;
+    int32_t head_dim;
+    int64_t head_stride; /* elements */
+} esda_view;
+
+int esda_cache_create(int32_t num_layers, esda_cache **out);
+void esda_cache_destroy(esda_cache *cache);
+
+/* prealloc: 0 = legacy concat mode, 1 = preallocated chunk-grown mode. */
+int esda_cache_update(esda_cache *cache, int32_t layer, const void *k_new, const void *v_new,
+                      int32_t kv_heads, int32_t n_new, int32_t head_dim, int32_t max_keep,
+                      int32_t prealloc, void *stream, esda_view *k_out, esda_view *v_out);
+
+int esda_cache_update_raw(esda_cache *cache, int32_t layer, const void *k_new, int32_t kv_heads,
+                          int32_t n_new, int32_t head_dim, int32_t prealloc, void *stream,
+                          esda_view *view, int32_t *len, int32_t *pitch);
+
+int esda_cache_current(esda_cache *cache, int32_t layer, int32_t prealloc, esda_view *k_out,
+                       esda_view *v_out);
+
+/* Fused decode step: append one row (v_new == k_new: one shared K=V buffer) and attend.
+ * q: [num_q_heads, head_dim] bf16; out: [num_q_heads, head_dim] bf16. */
+int esda_cache_decode(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads,
+                      const void *k_new, const void *v_new, int32_t kv_heads, int32_t head_dim,
+                      int32_t max_keep, float scale, void *out, void *stream);
+
+/* Fused raw-K decode step (head_dim 512): append one raw row and attend.  inv_freq is a
+ * host array of n_freq >= 64 floats (the first 64 are used). */
+int esda_cache_decode_raw(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads,
+                          const void *k_new, int32_t kv_heads, const void *kw, float eps,
+                          const float *inv_freq, int32_t n_freq, void *out, void *stream);
+
+/* flags: bit 0 = rows before start were discarded by a compaction, bit 1 = shared K=V
+ * buffer, bit 2 = raw-K content. */
+int esda_cache_slot(esda_cache *cache, int32_t layer, int32_t *len, int32_t *start,
+                    int32_t *capacity, int32_t *flags);
+
+int esda_cache_seq_len(const esda_cache *cache);
+void esda_cache_mark_step(esda_cache *cache, int32_t n_new);
+void esda_cache_reset(esda_cache *cache);
+
+int esda_cache_save_snapshot(const esda_cache *cache, const char *path, const char *fingerprint,
+                             int32_t pos);
+int esda_cache_restore_snapshot(esda_cache *cache, const char *path, const char *fingerprint);
+int esda_cache_mark_rewind_point(esda_cache *cache, int32_t pos);
+int esda_cache_rewind_to_mark(esda_cache *cache);
+
+/* esDecodeAttnGlobal: q [num_q_heads, 512], raw_buf the unsliced [num_kv_heads, pitch,
+ * 512] buffer, rows 0 .. len-1 attended (already appended); out [num_q_heads, 512]. */
+int esda_decode_attn_global(const void *q, int32_t num_q_heads, const void *raw_buf,
+                            int32_t num_kv_heads, int32_t len, int32_t pitch, const void *kw,
+                            float eps, const float *inv_freq, int32_t n_freq, void *out,
+                            void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,5 +1,5 @@
 """C-ABI checks that need no GPU: libesda.so loads, exports every function
-include/esda.h declares, and rejects bad descriptions before touching the device."""
+include/*.h declares, and rejects bad descriptions before touching the device."""
 import ctypes
 import os
 import re
@@ -13,13 +13,17 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _declared():
-    txt = open(os.path.join(ROOT, "include", "esda.h")).read()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(esda_\w+)\s*\(", txt, re.M)))
+    names = set()
+    for h in os.listdir(os.path.join(ROOT, "include")):
+        if h.endswith(".h"):
+            txt = open(os.path.join(ROOT, "include", h)).read()
+            names |= set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(esda_\w+)\s*\(", txt, re.M))
+    return sorted(names)
 
 
 def test_header_declares_and_library_exports_every_symbol():
     names = _declared()
-    assert "esda_decode" in names and len(names) >= 7
+    assert "esda_decode" in names and "esda_decode_raw" in names and "esda_cache_update" in names
     L = _lib.lib()
     for n in names:
         assert hasattr(L, n), f"libesda.so does not export {n}"
@@ -73,3 +77,44 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(ImportError):
         _lib.lib()
+
+
+# ------------------------------------------------ ES* layer handle (no device calls)
+
+def test_es_cache_handle_host_side_behaviour(tmp_path):
+    """Construction, step counting, the not-implemented members' failure values and
+    argument validation run on the host only."""
+    from apertura_amd.cache import ESKVCache
+    c = ESKVCache(4)
+    assert c.seq_len() == 0
+    c.mark_step(3)
+    assert c.seq_len() == 3
+    c.reset()
+    assert c.seq_len() == 0
+    assert c.save_snapshot(str(tmp_path / "s"), "fp", 1) is False
+    assert c.restore_snapshot(str(tmp_path / "s"), "fp") == -1
+    assert c.mark_rewind_point(1) is False and c.rewind_to_mark() == -1
+    assert c.slot(2) == {"len": 0, "start": 0, "capacity": 0, "lost": False, "shared": False, "raw": False}
+    with pytest.raises(_lib.EsdaError) as ei:
+        c.slot(4)
+    assert ei.value.code == 1
+    view = _lib.View()
+    rc = _lib.lib().esda_cache_update(c._h, 0, None, None, 2, 1, 128, 0, 1, None, ctypes.byref(view),
+                                      ctypes.byref(view))
+    assert rc == 1 and b"null" in _lib.lib().esda_last_error()
+    rc = _lib.lib().esda_cache_current(c._h, 1, 1, ctypes.byref(view), ctypes.byref(view))
+    assert rc == 2  # no rows yet: std::runtime_error
+    with pytest.raises(_lib.EsdaError):
+        ESKVCache(0)
+
+
+def test_raw_descriptions_are_validated_without_device():
+    from apertura_amd.decode import RawStep, raw_workspace_bytes
+    assert raw_workspace_bytes(RawStep(batch=1, num_q_heads=32, num_kv_heads=4, cap=131072)) > 256
+    for bad in (dict(head_dim=256), dict(num_q_heads=31), dict(cap=0), dict(eps=-1.0),
+                dict(split_rows=40)):
+        kw = dict(batch=1, num_q_heads=32, num_kv_heads=4, cap=1024)
+        kw.update(bad)
+        with pytest.raises(_lib.EsdaError) as ei:
+            raw_workspace_bytes(RawStep(**kw))
+        assert ei.value.code == 1

@@ -135,6 +135,17 @@ def test_edge_case(case):
     run_case(**case)
 
 
+@pytest.mark.parametrize("D", [256, 512])
+def test_huge_logit_gap_does_not_overflow(D):
+    """Keys scoring ~200 (natural-log units) above the rest: the running max must see
+    them wherever they sit in a 16-row stage (a cross-lane max that missed a lane group
+    would let exp2 of the unnormalised scores overflow to inf).  V rows stay unit-RMS
+    (separate V), so the absolute tolerance keeps its meaning."""
+    for seed in (31, 32, 33):
+        run_case(f"huge-gap-{seed}", B=1, Hq=32, Hkv=8, D=D, cap=2048, pos=[2047], shared=False,
+                 peaks=3, bump=200.0, seed=seed, split_rows=64, refround=False)
+
+
 def test_split_count_does_not_change_result_beyond_rounding():
     a, ref = run_case("split_auto", B=1, Hq=32, Hkv=4, D=512, cap=4096, pos=[4095], shared=True, seed=9)
     b, _ = run_case("split_64", B=1, Hq=32, Hkv=4, D=512, cap=4096, pos=[4095], shared=True, seed=9,

@@ -1,0 +1,218 @@
+"""GPU checks of the ES* C++ layer (ESKVCache through include/esda_cache.h).
+
+update() in both storage modes is compared byte for byte with a host model of the
+reference's semantics (concatenate along the sequence axis, keep the last maxKeep rows:
+ESKVCache.mm:35-55 and 64-109); decode() is compared with the CPU oracle on the rows
+that model says are live, across buffer growth and compaction; the mode-mismatch
+guards raise the reference's error class.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from _synth import rms_rows
+
+pytestmark = pytest.mark.gpu
+
+TOL_MAX, TOL_MEAN = 2e-2, 2e-3
+
+
+def _dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def _host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _view(v) -> np.ndarray:
+    return _host(v.torch())
+
+
+@pytest.mark.parametrize("max_keep", [0, 48])
+def test_update_modes_match_the_concat_model(max_keep):
+    from apertura_amd.cache import ESKVCache
+    rng = np.random.default_rng(max_keep + 1)
+    kvh, hd = 2, 128
+    cache = ESKVCache(2)
+    model_k = np.zeros((kvh, 0, hd), np.uint16)
+    model_v = np.zeros((kvh, 0, hd), np.uint16)
+    # a prefill of 70 rows, then single-row appends across two capacity growths
+    sizes = [70] + [1] * 500
+    for i, n in enumerate(sizes):
+        kn, vn = rms_rows(rng, (kvh, n, hd)), rms_rows(rng, (kvh, n, hd))
+        model_k = np.concatenate([model_k, kn], axis=1)
+        model_v = np.concatenate([model_v, vn], axis=1)
+        if max_keep and model_k.shape[1] > max_keep and n == 1:
+            model_k, model_v = model_k[:, -max_keep:], model_v[:, -max_keep:]
+        lk, lv = cache.update(0, _dev(kn), _dev(vn), max_keep if n == 1 else 0, prealloc=False)
+        pk, pv = cache.update(1, _dev(kn), _dev(vn), max_keep if n == 1 else 0, prealloc=True)
+        if i % 61 == 0 or i == len(sizes) - 1:
+            for v, m in ((lk, model_k), (lv, model_v), (pk, model_k), (pv, model_v)):
+                assert v.rows == m.shape[1]
+                assert np.array_equal(_view(v), m), f"step {i}: view differs from the model"
+    s = cache.slot(1)
+    assert s["len"] - s["start"] == model_k.shape[1]
+    assert s["capacity"] % 256 == 0 and s["capacity"] >= s["len"]
+    assert s["lost"] == bool(max_keep)  # a compaction dropped evicted rows only when sliding
+    ck, cv = cache.current(1, True)
+    assert np.array_equal(_view(ck), model_k) and np.array_equal(_view(cv), model_v)
+
+
+def test_first_prealloc_store_has_capacity_equal_to_content_then_grows_by_chunks():
+    from apertura_amd.cache import ESKVCache
+    rng = np.random.default_rng(3)
+    cache = ESKVCache(1)
+    kn = rms_rows(rng, (4, 100, 64))
+    cache.update(0, _dev(kn), _dev(kn), 0, prealloc=True)
+    assert cache.slot(0)["capacity"] == 100
+    one = rms_rows(rng, (4, 1, 64))
+    cache.update(0, _dev(one), _dev(one), 0, prealloc=True)
+    assert cache.slot(0)["capacity"] == 512  # roundUp(100 + 1 + 256, 256)
+
+
+def _decode_run(cache, layer, rng, *, kvh, hq, hd, shared, max_keep, steps, prefill, scale):
+    """Prefill with update(prealloc), then decode() steps, each checked against the oracle
+    on the live rows of the host model."""
+    model_k = rms_rows(rng, (kvh, prefill, hd)) if prefill else np.zeros((kvh, 0, hd), np.uint16)
+    model_v = model_k if shared else (rms_rows(rng, (kvh, prefill, hd)) if prefill else model_k.copy())
+    if prefill:
+        k_d = _dev(model_k)
+        cache.update(layer, k_d, k_d if shared else _dev(model_v), 0, prealloc=True)
+    worst = 0.0
+    for i in range(steps):
+        q = rms_rows(rng, (hq, hd))
+        kn = rms_rows(rng, (kvh, 1, hd))
+        vn = kn if shared else rms_rows(rng, (kvh, 1, hd))
+        kn_d = _dev(kn)
+        out = cache.decode(layer, _dev(q), kn_d, kn_d if shared else _dev(vn), max_keep, scale)
+        model_k = np.concatenate([model_k, kn], axis=1)
+        model_v = model_k if shared else np.concatenate([model_v, vn], axis=1)
+        if max_keep and model_k.shape[1] > max_keep:
+            model_k = model_k[:, -max_keep:]
+            model_v = model_k if shared else model_v[:, -max_keep:]
+        live = model_k.shape[1]
+        if i % 7 == 0 or i == steps - 1:
+            step = orc.Step(B=1, Hq=hq, Hkv=kvh, D=hd, cap=live, scale=scale)
+            ref = orc.decode_f64(step, q.reshape(1, hq, hd), np.ascontiguousarray(model_k).reshape(-1),
+                                 np.ascontiguousarray(model_v).reshape(-1), [live - 1])
+            o = orc.from_bf16(_host(out)).reshape(1, hq, hd).astype(np.float64)
+            err = np.abs(o - ref)
+            worst = max(worst, err.max())
+            assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN, f"step {i}"
+    ck, cv = cache.current(layer, True)
+    assert np.array_equal(_view(ck), model_k) and np.array_equal(_view(cv), model_v)
+    return worst
+
+
+def test_decode_sliding_layer_across_compaction():
+    from apertura_amd.cache import ESKVCache
+    cache = ESKVCache(1)
+    w = _decode_run(cache, 0, np.random.default_rng(5), kvh=4, hq=8, hd=256, shared=False, max_keep=96,
+                    steps=480, prefill=40, scale=1 / 16)
+    s = cache.slot(0)
+    assert s["len"] - s["start"] == 96 and s["lost"] and not s["shared"]
+    print(f"sliding worst max_abs {w:.3e}")
+
+
+def test_decode_global_k_eq_v_across_growth():
+    from apertura_amd.cache import ESKVCache
+    cache = ESKVCache(2)
+    w = _decode_run(cache, 1, np.random.default_rng(7), kvh=2, hq=16, hd=512, shared=True, max_keep=0,
+                    steps=300, prefill=230, scale=512 ** -0.5)
+    s = cache.slot(1)
+    assert s["len"] == 530 and s["start"] == 0 and s["shared"] and s["capacity"] >= 530
+    print(f"global worst max_abs {w:.3e}")
+
+
+def test_decode_on_an_empty_slot_starts_the_cache():
+    from apertura_amd.cache import ESKVCache
+    rng = np.random.default_rng(9)
+    cache = ESKVCache(1)
+    w = _decode_run(cache, 0, rng, kvh=1, hq=4, hd=128, shared=True, max_keep=0, steps=20, prefill=0,
+                    scale=1.0)
+    assert w <= TOL_MAX
+    s = cache.slot(0)
+    assert s["len"] == 20 and s["shared"]
+
+
+def test_mode_mismatch_guards_raise_runtime_error():
+    from apertura_amd import EsdaError
+    from apertura_amd.cache import ESKVCache
+    rng = np.random.default_rng(11)
+    cache = ESKVCache(2)
+    kv = _dev(rms_rows(rng, (2, 3, 512)))
+    cache.update(0, kv, kv, 0, prealloc=True)
+    with pytest.raises(EsdaError) as ei:
+        cache.update_raw(0, kv, True)
+    assert ei.value.code == 2 and "composite" in str(ei.value)
+    cache.update_raw(1, kv, True)
+    with pytest.raises(EsdaError) as ei:
+        cache.update(1, kv, kv, 0, prealloc=True)
+    assert ei.value.code == 2 and "raw-K" in str(ei.value)
+    with pytest.raises(EsdaError) as ei:
+        cache.decode(1, _dev(rms_rows(rng, (16, 512))), kv[:, :1].contiguous(), kv[:, :1].contiguous(), 0, 1.0)
+    assert ei.value.code == 2
+    assert cache.slot(1)["raw"] and not cache.slot(0)["raw"]
+    # a shared K=V slot refuses a distinct V row
+    c2 = ESKVCache(1)
+    one = _dev(rms_rows(rng, (2, 1, 128)))
+    c2.decode(0, _dev(rms_rows(rng, (4, 128))), one, one, 0, 1.0)
+    other = _dev(rms_rows(rng, (2, 1, 128)))
+    with pytest.raises(EsdaError) as ei:
+        c2.decode(0, _dev(rms_rows(rng, (4, 128))), one, other, 0, 1.0)
+    assert ei.value.code == 2
+
+
+def test_update_raw_layout_and_growth():
+    from apertura_amd.cache import ESKVCache
+    rng = np.random.default_rng(13)
+    cache = ESKVCache(1)
+    model = rms_rows(rng, (4, 300, 512))
+    view, ln, pitch = cache.update_raw(0, _dev(model), True)
+    assert (ln, pitch) == (300, 300)
+    for _ in range(3):
+        one = rms_rows(rng, (4, 1, 512))
+        view, ln, pitch = cache.update_raw(0, _dev(one), True)
+        model = np.concatenate([model, one], axis=1)
+    assert (ln, pitch) == (303, 768)  # roundUp(300 + 1 + 256, 256)
+    assert np.array_equal(_view(view), model)
+
+
+def test_decode_raw_through_the_cache_matches_oracle():
+    from apertura_amd.cache import ESKVCache
+    rng = np.random.default_rng(15)
+    kvh, hq, eps = 2, 16, 1e-6
+    inv = orc.rope_inv_freq(512, 1.0e6, 0.25)
+    kw = orc.to_bf16((1.0 + 0.2 * rng.standard_normal(512)).astype(np.float32))
+    kw_d = _dev(kw)
+    cache = ESKVCache(1)
+    model = orc.to_bf16(rng.standard_normal((kvh, 200, 512), dtype=np.float32) * 2.0)
+    cache.update_raw(0, _dev(model), True)
+    for i in range(70):
+        q = rms_rows(rng, (hq, 512))
+        one = orc.to_bf16(rng.standard_normal((kvh, 1, 512), dtype=np.float32) * 2.0)
+        out = cache.decode_raw(0, _dev(q), _dev(one), kw_d, eps, list(inv))
+        model = np.concatenate([model, one], axis=1)
+        if i % 10 == 0 or i == 69:
+            ref = orc.decode_raw_f64(q, np.ascontiguousarray(model), model.shape[1], kw, eps, inv, 1.0)
+            o = orc.from_bf16(_host(out)).reshape(hq, 512).astype(np.float64)
+            err = np.abs(o - ref)
+            assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN, f"step {i}"
+    view, ln, pitch = cache.update_raw(0, _dev(np.zeros((kvh, 1, 512), np.uint16)), True)
+    assert ln == 271 and np.array_equal(_view(view)[:, :270], model)
+
+
+def test_not_implemented_members_return_reference_failure_values(tmp_path):
+    from apertura_amd.cache import ESKVCache
+    cache = ESKVCache(3)
+    assert cache.save_snapshot(str(tmp_path / "kv.safetensors"), "fp", 10) is False
+    assert cache.restore_snapshot(str(tmp_path / "kv.safetensors"), "fp") == -1
+    assert cache.mark_rewind_point(5) is False
+    assert cache.rewind_to_mark() == -1
+    cache.mark_step(5)
+    cache.mark_step(2)
+    assert cache.seq_len() == 7
+    cache.reset()
+    assert cache.seq_len() == 0

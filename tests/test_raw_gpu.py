@@ -1,0 +1,151 @@
+"""GPU parity of the raw-K decode path (esda_decode_raw: fused raw-row append + in-kernel
+K/V reconstruction + split-K attention + merge) against the CPU oracle
+(orc_decode_raw_f64, the reconstruction of ESDecodeAttn.mm:17-117 evaluated in fp64
+after the kernel's rounding points), called through the C ABI.
+
+Bar: max-abs-err <= 2e-2 and mean-abs-err <= 2e-3; the raw cache after the append is
+compared byte for byte.  Raw rows are un-normalised k_proj outputs (scaled N(0, 1), so
+the per-row rsqrt matters), kw is a non-trivial k-norm weight, and the rotary table is
+Gemma-4's global one (theta 1e6, 64 of 256 pairs rotated, zero tail).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL_MAX, TOL_MEAN = 2e-2, 2e-3
+EPS = 1e-6
+
+
+def _dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def _host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _raw_inputs(rng, B, Hq, Hkv, cap, row_scale=3.0):
+    q = rng.standard_normal((B, Hq, 512), dtype=np.float32)
+    q = orc.to_bf16(q / np.sqrt(np.mean(q * q, axis=-1, keepdims=True) + EPS))
+    raw = np.empty((B, Hkv, cap, 512), dtype=np.uint16)
+    for b in range(B):
+        for h in range(Hkv):
+            # per-row scales spread over [0.5, 1.5] * row_scale: rinv differs row to row
+            s = row_scale * (0.5 + rng.random((cap, 1), dtype=np.float32))
+            raw[b, h] = orc.to_bf16(rng.standard_normal((cap, 512), dtype=np.float32) * s)
+    kn = orc.to_bf16(rng.standard_normal((B, Hkv, 512), dtype=np.float32) * row_scale)
+    kw = orc.to_bf16((1.0 + 0.25 * rng.standard_normal(512)).astype(np.float32))
+    return q, raw, kn, kw
+
+
+def _check(name, o, ref):
+    err = np.abs(o - ref)
+    print(f"[raw] {name}: max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
+    assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN, name
+    return err
+
+
+def run_raw(name, *, B=1, Hq=32, Hkv=4, cap, pos, scale=1.0, seed=0, split_rows=0, append=True,
+            theta=1.0e6, partial=0.25, fault=0):
+    from apertura_amd.decode import RawStep, decode_raw, new_raw_workspace
+    print(f"\n[raw] {name}: B={B} Hq={Hq} Hkv={Hkv} cap={cap} pos={list(pos)[:4]} scale={scale} "
+          f"append={append} split_rows={split_rows}", flush=True)
+    rng = np.random.default_rng(seed)
+    q, raw, kn, kw = _raw_inputs(rng, B, Hq, Hkv, cap)
+    inv = orc.rope_inv_freq(512, theta, partial)
+    step = RawStep(batch=B, num_q_heads=Hq, num_kv_heads=Hkv, cap=cap, eps=EPS, scale=scale,
+                   split_rows=split_rows)
+    raw_d = _dev(raw)
+    out = decode_raw(step, _dev(q), _dev(kn) if append else None, raw_d,
+                     torch.tensor(list(pos), dtype=torch.int32, device="cuda"), _dev(kw),
+                     torch.from_numpy(inv).cuda(), workspace=new_raw_workspace(step, "cuda"))
+    torch.cuda.synchronize()
+    if append:
+        for b in range(B):
+            raw[b, :, pos[b]] = kn[b]
+    assert np.array_equal(_host(raw_d), raw), "raw cache bytes differ after the append"
+    o = orc.from_bf16(_host(out)).reshape(B, Hq, 512).astype(np.float64)
+    errs = []
+    for b in range(B):
+        with orc.planted_fault(fault):
+            ref = orc.decode_raw_f64(q[b], np.ascontiguousarray(raw[b]), pos[b] + 1, kw, EPS, inv, scale)
+        if fault:
+            errs.append(np.abs(o[b] - ref))
+        else:
+            errs.append(_check(f"{name} b={b}", o[b], ref))
+    return o, errs
+
+
+def test_raw_small_with_append():
+    run_raw("small", cap=512, pos=[299], scale=512 ** -0.5)
+
+
+def test_raw_in_model_scale_one():
+    run_raw("scale1", cap=1024, pos=[1000], scale=1.0, seed=3)
+
+
+def test_raw_long_context_131072():
+    """The C4 shape in raw mode: 131072 rows, all visible, 64 splits per kv head."""
+    run_raw("c4-raw", cap=131072, pos=[131071], scale=512 ** -0.5, seed=5)
+
+
+def test_raw_batched_ragged_positions():
+    run_raw("batched", B=3, cap=4096, pos=[17, 2500, 4095], scale=512 ** -0.5, seed=7)
+
+
+def test_raw_no_append_reads_cached_rows():
+    run_raw("no-append", cap=2048, pos=[1500], append=False, seed=9)
+
+
+@pytest.mark.parametrize("split_rows", [16, 48, 512])
+def test_raw_split_sizes(split_rows):
+    run_raw(f"split{split_rows}", cap=1024, pos=[777], split_rows=split_rows, seed=11)
+
+
+def test_raw_zero_tail_rotary_table():
+    """partial 1/8: only 32 pairs rotate, the rest of the 64 used entries are zero."""
+    run_raw("tail", cap=512, pos=[511], partial=0.125, seed=13)
+
+
+def test_raw_single_row():
+    run_raw("one-row", cap=64, pos=[0], seed=15)
+
+
+def test_raw_rope_sign_fault_is_detected():
+    """The parity check is sensitive to the rotation: against an oracle with the RoPE
+    sign flipped (a planted mistake, on the CPU) the GPU result is far off."""
+    _, errs = run_raw("rope-fault", cap=2048, pos=[2047], scale=1.0, seed=17, fault=5)
+    assert max(e.max() for e in errs) > 10 * TOL_MAX
+
+
+def test_raw_repeated_launch_is_deterministic():
+    from apertura_amd.decode import RawStep, decode_raw, new_raw_workspace
+    rng = np.random.default_rng(21)
+    q, raw, kn, kw = _raw_inputs(rng, 1, 32, 4, 8192)
+    step = RawStep(batch=1, num_q_heads=32, num_kv_heads=4, cap=8192, eps=EPS)
+    args = (_dev(q), None, _dev(raw), torch.tensor([8191], dtype=torch.int32, device="cuda"), _dev(kw),
+            torch.from_numpy(orc.rope_inv_freq(512, 1e6, 0.25)).cuda())
+    ws = new_raw_workspace(step, "cuda")
+    a = decode_raw(step, *args, workspace=ws).clone()
+    b = decode_raw(step, *args, workspace=ws).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_es_decode_attn_global_matches_oracle():
+    """esDecodeAttnGlobal signature (ES* C++ layer): rows already appended, pitch > len."""
+    from apertura_amd.cache import es_decode_attn_global
+    rng = np.random.default_rng(23)
+    Hkv, pitch, length = 4, 1280, 1000
+    q, raw, _, kw = _raw_inputs(rng, 1, 8 * Hkv, Hkv, pitch)
+    inv = orc.rope_inv_freq(512, 1.0e6, 0.25)
+    raw_d = _dev(raw[0])
+    out = es_decode_attn_global(_dev(q[0]), raw_d, length, pitch, _dev(kw), EPS, list(inv))
+    torch.cuda.synchronize()
+    assert np.array_equal(_host(raw_d), raw[0])
+    ref = orc.decode_raw_f64(q[0], np.ascontiguousarray(raw[0]), length, kw, EPS, inv, 1.0)
+    _check("esDecodeAttnGlobal", orc.from_bf16(_host(out)).reshape(8 * Hkv, 512).astype(np.float64), ref)
