@@ -48,6 +48,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 16;          // MFMA row block; split sizes are multiples of it
@@ -228,7 +230,7 @@ __device__ __forceinline__ void unroll(F &&f) {
 constexpr int kRawDim = 512;
 constexpr int kRopePairs = 64;
 constexpr int kTabStride = 68;  // words per cos/sin table row: 64 + 4 (conflict-free 128-bit reads)
-constexpr int kRawExtraLds = 3 * 16 * 4 * 4 + 2 * 16 * kTabStride * 4;
+constexpr int kRawExtraLds = 3 * 16 * 4 * 4 + 2 * 16 * kTabStride * 4 + 2 * 2 * 16 * 4;
 
 // Cody-Waite split of pi/2 (hi + mid + lo, each the nearest fp32 to what remains).
 constexpr float kTwoOverPi = 0.636619746685028076171875f;     // fp32(2/pi)
@@ -321,11 +323,14 @@ void attend_kernel(AttendParams p) {
         else return r15;
     };
     __shared__ f32x4 xch[2][NW][64];  // partial scores, double-buffered by stage parity
-    // Raw mode: per-row partial sums of squares xss[stage % 3][row][wave] and the cos/sin
-    // table xtab[stage % 2][row][pair] (bf16 cos in the low half, sin in the high half).
+    // Raw mode: per-row partial sums of squares xss[stage % 3][row][wave], the cos/sin
+    // table xtab[stage % 2][row][pair] (bf16 cos in the low half, sin in the high half)
+    // and the per-row norm factors xr.
     __shared__ __attribute__((aligned(16))) unsigned char rawlds[RAW ? kRawExtraLds : 16];
     auto *xss = reinterpret_cast<float (*)[16][4]>(rawlds);
     auto *xtab = reinterpret_cast<unsigned (*)[16][kTabStride]>(rawlds + 3 * 16 * 4 * 4);
+    // xr[stage % 2][0][row] = rinv, xr[stage % 2][1][row] = 1 / rinv
+    auto *xr = reinterpret_cast<float (*)[2][16]>(rawlds + 3 * 16 * 4 * 4 + 2 * 16 * kTabStride * 4);
 
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -455,20 +460,23 @@ void attend_kernel(AttendParams p) {
         for (int kk = 0; kk < (RAW ? KKW : 1); ++kk)
             araw[kk] = *reinterpret_cast<const u32x4 *>(kb + qk_off + 64 * qk_chunk(kk));
     };
-    // Partial sum of squares of row li over this wave's dims -> xss[buf][li][wave].
+    // Partial sum of squares of row li over this wave's dims -> xss[buf][li][wave]: the
+    // diagonal of the stage's 16x16 Gram matrix over those dims.  The A and B operands of
+    // v_mfma_f32_16x16x32_bf16 take the same lane data (row li, dims 8lg..+8 of each
+    // chunk), and products of bf16 values are exact in the fp32 accumulation.
     auto publish_ss = [&](int buf) {
-        float ss = 0.0f;
+        if constexpr (RAW) {
+            f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kk = 0; kk < (RAW ? KKW : 1); ++kk)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float x0 = bf16_lo(araw[kk][e]), x1 = bf16_hi(araw[kk][e]);
-                ss = __builtin_fmaf(x0, x0, ss);
-                ss = __builtin_fmaf(x1, x1, ss);
+            for (int kk = 0; kk < KKW; ++kk) {
+                const bf16x8 a = __builtin_bit_cast(bf16x8, araw[kk]);
+                g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, a, g, 0, 0, 0);
             }
-        ss += __shfl_xor(ss, 16);
-        ss += __shfl_xor(ss, 32);
-        if (lg == 0) xss[buf][li][wave] = ss;
+            // C layout: lane (li, lg) holds C[4lg + i][li]; row li's diagonal entry is
+            // register li - 4lg of the lanes with lg == li / 4.
+            const int i = li - 4 * lg;
+            if (i >= 0 && i < 4) xss[buf][li][wave] = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
+        }
     };
     // cos/sin table of stage st: this thread's row tid/16, pairs 4(tid%16) .. +4.
     auto publish_tab = [&](int st, int buf) {
@@ -479,9 +487,7 @@ void attend_kernel(AttendParams p) {
         for (int e = 0; e < 4; ++e) {
             float s, c;
             sincos_f32(t * invf[e], s, c);
-            const unsigned cb = __builtin_bit_cast(unsigned short, (__bf16) c);
-            const unsigned sb = __builtin_bit_cast(unsigned short, (__bf16) s);
-            w[e] = cb | (sb << 16);
+            w[e] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{c, s}, bf16x2));
         }
         *reinterpret_cast<u32x4 *>(&xtab[buf][row][4 * (tid & 15)]) = w;
     };
@@ -493,7 +499,13 @@ void attend_kernel(AttendParams p) {
     // Scores of the stage held in araw: rebuild K in registers, then MFMA.
     auto qk_raw = [&](int ssbuf, int tabbuf, int par) {
         if constexpr (RAW) {
-            const float rinv = __builtin_amdgcn_rsqf(row_ms(ssbuf, li));
+            const float ms = row_ms(ssbuf, li);
+            const float rinv = __builtin_amdgcn_rsqf(ms);
+            // rinv and 1/rinv (= ms * rinv) of the row, for the stage's softmax weights.
+            if (wave == 0 && lg == 0) {
+                xr[par][0][li] = rinv;
+                xr[par][1][li] = ms * rinv;
+            }
             float kn[KKW][8];
     #pragma unroll
             for (int kk = 0; kk < KKW; ++kk)
@@ -591,25 +603,22 @@ void attend_kernel(AttendParams p) {
         f32x4 sc = xch[st & 1][0][lane];
 #pragma unroll
         for (int w = 1; w < NW; ++w) sc += xch[st & 1][w][lane];
+        // The look-ahead work runs unconditionally (one basic block with the softmax, so
+        // the two interleave): past the last stage it reads stale but in-bounds LDS and
+        // writes exchange slots that are never read again.
         if constexpr (RAW) {
-            if (st + 1 < nst) qk_raw((st + 1) % 3, (st + 1) & 1, (st + 1) & 1);
-            if (st + 2 < nst) {
-                load_raw(ring(std::integral_constant<int, (u + 2) % NS>{}));
-                publish_ss((st + 2) % 3);
-                publish_tab(st + 2, st & 1);
-            }
+            qk_raw((st + 1) % 3, (st + 1) & 1, (st + 1) & 1);
+            load_raw(ring(std::integral_constant<int, (u + 2) % NS>{}));
+            publish_ss((st + 2) % 3);
+            publish_tab(st + 2, st & 1);
         } else {
-            if (st + 1 < nst) qk_partial(ring(std::integral_constant<int, (u + 1) % NS>{}), (st + 1) & 1);
+            qk_partial(ring(std::integral_constant<int, (u + 1) % NS>{}), (st + 1) & 1);
         }
         // Online softmax (log2 domain), identical in every wave; rows past the split
         // end (last stage only) are masked.
         const int jt = j0 + st * 16;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[r] *= p.scale_log2e;
-        if (jt + 16 > j1) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sc[r] = (jt + 4 * lg + r) < j1 ? sc[r] : -INFINITY;
-        }
+        for (int r = 0; r < 4; ++r) sc[r] = (jt + 4 * lg + r) < j1 ? sc[r] * p.scale_log2e : -INFINITY;
         const float tmax = wave_max_across_groups(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
         if (__any(tmax > m + kRescaleSlack)) {
             const float mnew = fmaxf(m, tmax);
@@ -624,13 +633,13 @@ void attend_kernel(AttendParams p) {
             // V = kraw * rinv enters through the weight: P = bf16(e * rinv).  l adds the
             // same rounded weight divided by rinv (ms * rinv = 1 / rinv), so numerator and
             // denominator carry identical rounding and a dominant row is reproduced exactly.
+            const f32x4 ri = *reinterpret_cast<const f32x4 *>(&xr[st & 1][0][4 * lg]);
+            const f32x4 rn = *reinterpret_cast<const f32x4 *>(&xr[st & 1][1][4 * lg]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float e = __builtin_amdgcn_exp2f(sc[r] - m);
-                const float ms = row_ms(st % 3, 4 * lg + r);
-                const float rinv = __builtin_amdgcn_rsqf(ms);
-                const __bf16 pw = (__bf16) (e * rinv);
-                l += (float) pw * (ms * rinv);
+                const __bf16 pw = (__bf16) (e * ri[r]);
+                l += (float) pw * rn[r];
                 pbs[r] = __builtin_bit_cast(short, pw);
             }
         } else {
