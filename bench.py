@@ -224,13 +224,28 @@ def main() -> int:
             "kernel": ("attend_kernel<512,shared,raw> (raw-K rebuild + split-K + fused append)" if raw is not None
                        else "attend_kernel<D,kv_shared> (split-K + fused append)"),
             "achieved": round(gbs_attend, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(gbs_attend / PEAK_HBM_GBS, 4), "traffic": None,
+            "frac": round(gbs_attend / PEAK_HBM_GBS, 4), "traffic": profiled_traffic(args.workload),
+            "traffic_source": f"profiles/attend_{args.workload}.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
             "kernel_us": round(ms_attend * 1e3, 3),
         },
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def profiled_traffic(workload: str):
+    """HBM bytes per attend launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    (calibrated against a plain copy), as recorded in profiles/attend_<workload>.md; None
+    when that workload has no profile."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"attend_{workload}.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def calibrate_copy(args) -> int:
