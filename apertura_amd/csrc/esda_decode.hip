@@ -4,31 +4,20 @@
 // Reference behaviour (Apertura tree): ESKVCache::update prealloc append
 // (ESKVCache.mm:64-109) followed by mx::fast::scaled_dot_product_attention at
 // ESAttention.mm:188, with the visibility rule of ESGemma4TextModel.mm:68-83 and the
-// split merge of ESDecodeAttn.mm:253-273.
+// split merge of ESDecodeAttn.mm:253-273; in raw-K mode, ESKVCache::updateRaw
+// (ESKVCache.mm:458-504) followed by esDecodeAttnGlobal (ESDecodeAttn.mm:17-117, 415-453).
 //
-// Work decomposition
-//   grid (splits, kv heads, sequences), 256 threads = 4 waves per workgroup.  A
-//   workgroup owns `chunk` consecutive visible rows of one (sequence, kv head); its
-//   waves take 16-row tiles round-robin, each with its own online-softmax state, and
-//   merge in LDS at the end.  The whole GQA group (G <= 16 query heads) is one MFMA
-//   N dimension, so every K/V byte is read from HBM once per group.
-//
-// Per 16-row tile (one wave):
-//   S^T[16 keys x 16 heads] = K[16 x D] . Q^T[D x 16]   v_mfma_f32_16x16x32_bf16, D/32 steps
-//       K comes straight from the 128-bit global loads (A operand: lane l holds row
-//       l%16, dims 32k+8(l/16)..+8); Q^T sits in VGPRs for the whole kernel.
-//   online softmax in the C layout (lane l: head l%16, keys 4(l/16)+r): the tile max
-//       needs two cross-lane exchanges; the rescale of O runs only when a max grows.
-//   O^T[D x 16] += V^T[D x 16 keys] . P^T[16 keys x 16]   v_mfma_f32_16x16x16_bf16, D/16
-//       P^T is already in B-operand layout (same lane, same keys); V^T is gathered from
-//       an LDS copy of the tile whose rows are padded by 16 bytes (conflict-free for the
-//       128-bit row writes and the 16-bit column gathers; every address is a per-lane
-//       base plus an immediate offset, so no address registers stay live).
-//   With attention_k_eq_v the V tile *is* the K registers: one HBM read per row.
-//
-// The new token's row is copied from k_new/v_new into the cache by the workgroup whose
-// split ends at it (bit-exact copy); that workgroup's own loads read the row from
-// k_new/v_new and no other workgroup reads it, so the copy needs no ordering.
+// Kernels
+//   attend_kernel  grid (splits, kv heads, sequences), 4 waves, one workgroup per CU.  A
+//                  workgroup streams `chunk` visible rows of one (sequence, kv head)
+//                  through an LDS ring filled by LDS DMA, splits the head dim across its
+//                  waves for the QK and PV MFMAs (the GQA group is the MFMA N dimension),
+//                  runs an fp32 online softmax and writes (m, l, acc) partials.  The
+//                  workgroup whose split ends at the new token also copies its row into
+//                  the cache.  Details at the kernel.
+//   merge_kernel   reduces the partials of all splits per (sequence, query head).
+//   append_kernel  multi-row append (slice_update) for prefill-style callers.
+// The C ABI (include/esda.h) is at the end of the file.
 
 #include <hip/hip_runtime.h>
 
