@@ -44,6 +44,9 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kTile = 16;          // MFMA row block; split sizes are multiples of it
 constexpr int kMaxGroup = 16;
 constexpr int kTargetGroups = 256;  // one workgroup per MI355X CU (the ring LDS allows one per CU)
+constexpr int kMinRows = 64;        // fewest rows per workgroup the automatic plan gives
+constexpr int kMaxGroups = 16384;   // workgroups per launch
+constexpr int kMaxBatch = 256;      // sequences per call (one per thread of the prefix scan)
 constexpr float kLog2e = 1.4426950408889634f;
 
 // ------------------------------------------------------------------ per-sequence view
@@ -83,8 +86,12 @@ struct AttendParams {
     float *part_acc, *part_ml;
     int *status;
     long long seq_stride, head_stride;
-    int B, Hq, Hkv, G, cap, window, ring, S, chunk;
+    int B, Hq, Hkv, G, cap, window, ring;
+    int balanced;      // 1: W balanced shares of all rows; 0: grid (S, Hkv, B) of chunk-row splits
+    int W, S, chunk;
     float scale_log2e;
+    long long *table;  // balanced: prefix sums of visible rows per sequence, for the merge
+    uint16_t *out;     // written directly for (sequence, kv head) pairs of one segment
     // raw-K mode only
     const uint16_t *kw;
     const float *inv_freq;
@@ -193,6 +200,16 @@ __device__ __forceinline__ void lds_dma16_s(const void *sbase, unsigned voff, un
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sb), "s"(base) : "memory");
 #endif
 }
+
+// a / b for non-negative a, b > 0: 32-bit division when both fit (the common case),
+// which is far shorter than the 64-bit sequence.
+__device__ __forceinline__ long long udiv64(long long a, long long b) {
+    if (((unsigned long long) a | (unsigned long long) b) >> 32 == 0) return (long long) ((unsigned) a / (unsigned) b);
+    return (long long) ((unsigned long long) a / (unsigned long long) b);
+}
+
+// A value that is the same in every lane, as a scalar.
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 __device__ __forceinline__ unsigned lds_addr(const void *p) {
     return (unsigned) (uintptr_t) (const __attribute__((address_space(3))) void *) p;
@@ -321,22 +338,15 @@ void attend_kernel(AttendParams p) {
     // xr[stage % 2][0][row] = rinv, xr[stage % 2][1][row] = 1 / rinv
     auto *xr = reinterpret_cast<float (*)[2][16]>(rawlds + 3 * 16 * 4 * 4 + 2 * 16 * kTabStride * 4);
 
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int wg = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, lg = lane >> 4;
 
-    const int pos = p.pos[b];
-    const int base = p.row_base ? p.row_base[b] : 0;
-    const SeqView sv = seq_view(pos, base, p.cap, p.window, p.ring);
-    if (!sv.ok) {
-        if (split == 0 && kvh == 0 && tid == 0) atomicAdd(p.status, 1);
-        return;
-    }
-    const int j0 = split * p.chunk;
-    if (j0 >= sv.nvis) return;
-    const int j1 = min(j0 + p.chunk, sv.nvis);
-    if (split == p.S - 1 && j1 < sv.nvis && kvh == 0 && tid == 0) atomicAdd(p.status, 1);
+    // One segment: rows [j0, j1) of (sequence b, kv head kvh).  `slot` indexes its partial;
+    // `direct` means the segment is the whole (b, kvh) and writes the output itself.
+    auto segment = [&](const int b, const int kvh, const int j0, const int j1, const SeqView sv,
+                       const size_t slot, const bool direct) {
     const bool append = p.k_new != nullptr;
 
     const size_t head_off = (size_t) b * p.seq_stride + (size_t) kvh * p.head_stride;
@@ -667,8 +677,24 @@ void attend_kernel(AttendParams p) {
     // Partial of this split: every wave holds the same (m, l) and its own dim slice.
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
+    if (direct) {
+        // The only segment of this (sequence, kv head): normalise here, with the merge's
+        // arithmetic (acc * (1 / l), then bf16); the merge skips this pair.
+        if (li < p.G) {
+            const float inv = 1.0f / l;
+            uint16_t *dst = p.out + ((size_t) b * p.Hq + (size_t) kvh * p.G + li) * D + wave * DW;
+#pragma unroll
+            for (int dt = 0; dt < DTW; ++dt) {
+                bf16x4 r;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) r[e] = (__bf16) (acc[dt][e] * inv);
+                *reinterpret_cast<uint2 *>(dst + 16 * dt + 4 * lg) = __builtin_bit_cast(uint2, r);
+            }
+        }
+        return;
+    }
     if (li < p.G) {
-        const size_t pidx = (((size_t) b * p.Hkv + kvh) * p.S + split) * p.G + li;
+        const size_t pidx = slot * p.G + li;
         float *dst = p.part_acc + pidx * D + wave * DW;
 #pragma unroll
         for (int dt = 0; dt < DTW; ++dt) *reinterpret_cast<f32x4 *>(dst + 16 * dt + 4 * lg) = acc[dt];
@@ -677,19 +703,150 @@ void attend_kernel(AttendParams p) {
             p.part_ml[pidx * 2 + 1] = l;
         }
     }
+    };
+
+    if (!p.balanced) {
+        // Fixed splits (uniform lengths: one sequence, or windowed local layers): workgroup
+        // (split, kvh, b) takes rows [split * chunk, (split + 1) * chunk) of its pair.
+        const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+        const SeqView sv = seq_view(p.pos[b], p.row_base ? p.row_base[b] : 0, p.cap, p.window, p.ring);
+        if (!sv.ok) {
+            if (split == 0 && kvh == 0 && tid == 0) atomicAdd(p.status, 1);
+            return;
+        }
+        const int j0 = split * p.chunk;
+        if (j0 >= sv.nvis) return;
+        const int j1 = min(j0 + p.chunk, sv.nvis);
+        // rows past the last split (max_visible below the real length) are reported
+        if (split == p.S - 1 && j1 < sv.nvis && kvh == 0 && tid == 0) atomicAdd(p.status, 1);
+        segment(b, kvh, j0, j1, sv, ((size_t) b * p.Hkv + kvh) * p.S + split, j0 == 0 && j1 == sv.nvis);
+        return;
+    }
+
+    // Balanced shares (ragged batches).
+    // Visible rows of every sequence and their exclusive prefix sums (the rows that
+    // precede sequence b in the linearised order).  Up to 64 sequences every wave scans
+    // the batch in its own lanes (no LDS, no barrier); larger batches (up to 256, one per
+    // thread) go through LDS.
+    __shared__ long long s_pref[kMaxBatch + 1];
+    __shared__ long long s_wtot[NW];
+    const bool single = p.B == 1;
+    const bool wave_scan = p.B <= 64;
+    long long w_incl = 0, w_nv = 0;  // wave scan: lane t's inclusive sum and rows of sequence t
+    SeqView w_view{0, 0, 0, 0};
+    long long rows_seq = 0;          // sum of visible rows over the batch
+    if (single) {
+        // one sequence: its view straight from the (wave-uniform) position word
+        w_view = seq_view(p.pos[0], p.row_base ? p.row_base[0] : 0, p.cap, p.window, p.ring);
+        rows_seq = w_view.ok ? w_view.nvis : 0;
+        if (wg == 0 && tid == 0) {
+            if (!w_view.ok) atomicAdd(p.status, 1);
+            p.table[0] = 0;
+            p.table[1] = rows_seq;
+        }
+    } else {
+        const int t = wave_scan ? lane : tid;
+        SeqView v{0, 0, 0, 0};
+        if (t < p.B) v = seq_view(p.pos[t], p.row_base ? p.row_base[t] : 0, p.cap, p.window, p.ring);
+        const long long nv = v.ok ? v.nvis : 0;
+        long long x = nv;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const long long y = __shfl_up(x, o);
+            if (lane >= o) x += y;
+        }
+        if (wave_scan) {
+            w_incl = x;
+            w_nv = nv;
+            w_view = v;
+            rows_seq = __shfl(x, 63);
+            if (wg == 0 && wave == 0) {
+                if (t < p.B && !v.ok) atomicAdd(p.status, 1);
+                if (t < p.B) p.table[t] = x - nv;
+                if (t == 0) p.table[p.B] = rows_seq;
+            }
+        } else {
+            if (lane == 63) s_wtot[wave] = x;
+            __syncthreads();  // no DMA is in flight yet
+            long long off = 0;
+            for (int i = 0; i < wave; ++i) off += s_wtot[i];
+            if (tid < p.B) s_pref[tid + 1] = off + x;
+            if (tid == 0) s_pref[0] = 0;
+            if (wg == 0 && tid < p.B && !v.ok) atomicAdd(p.status, 1);
+            __syncthreads();
+            // B + 1 entries (B may be 256 = one per thread): the total goes in separately
+            if (wg == 0 && tid < p.B) p.table[tid] = s_pref[tid];
+            if (wg == 0 && tid == 0) p.table[p.B] = s_pref[p.B];
+            rows_seq = s_pref[p.B];
+        }
+    }
+    const long long rows_total = rows_seq * p.Hkv;
+    // Rows before sequence b (b <= B) and its view; the same in every lane.
+    auto lane64 = [](long long v, int l) {
+        const unsigned lo = __builtin_amdgcn_readlane((unsigned) v, l);
+        const unsigned hi = __builtin_amdgcn_readlane((unsigned) ((unsigned long long) v >> 32), l);
+        return (long long) (((unsigned long long) hi << 32) | lo);
+    };
+    auto pref_at = [&](int b) -> long long {
+        if (single) return b == 0 ? 0 : rows_seq;
+        if (!wave_scan) return s_pref[b];
+        return b >= p.B ? rows_seq : lane64(w_incl - w_nv, b);
+    };
+    auto view_at = [&](int b) -> SeqView {
+        if (single) return w_view;
+        if (!wave_scan) return seq_view(p.pos[b], p.row_base ? p.row_base[b] : 0, p.cap, p.window, p.ring);
+        return SeqView{__builtin_amdgcn_readlane(w_view.nvis, b), __builtin_amdgcn_readlane(w_view.first, b),
+                       __builtin_amdgcn_readlane(w_view.newrow, b), __builtin_amdgcn_readlane(w_view.ok, b)};
+    };
+
+    // This workgroup's share of all visible rows, linearised as (sequence, kv head, row):
+    // [rows_total * wg / W, rows_total * (wg + 1) / W).  It covers one or more segments; the
+    // partial of workgroup wg for pair u = b * Hkv + kvh goes to slot u + wg, so the slots
+    // of one pair are consecutive and distinct pairs never share a slot.
+    const long long lo = udiv64(rows_total * wg, p.W), hi = udiv64(rows_total * (wg + 1), p.W);
+    long long x = lo;
+    int b = 0;
+    while (x < hi) {
+        // the sequence holding row x (x < rows_total): the count of sequences that end at
+        // or before it
+        if (single) {
+            b = 0;
+        } else if (wave_scan) {
+            b = __popcll(__ballot(lane < p.B && w_incl * p.Hkv <= x));
+        } else {
+            while (pref_at(b + 1) * p.Hkv <= x) ++b;
+        }
+        const long long pb = pref_at(b);
+        const long long sb = pb * p.Hkv;
+        const int n = (int) (pref_at(b + 1) - pb);
+        const int kvh = (int) udiv64(x - sb, n);
+        const int j0 = (int) (x - sb - (long long) kvh * n);
+        const long long pair_end = sb + (long long) (kvh + 1) * n;
+        const long long seg_end = pair_end < hi ? pair_end : hi;
+        const int j1 = j0 + (int) (seg_end - x);
+        const SeqView v = view_at(b);
+        // Every value of the segment is the same in all lanes (computed from LDS and kernel
+        // arguments); saying so keeps the ring's control flow and addresses scalar.
+        const SeqView sv{uniform(v.nvis), uniform(v.first), uniform(v.newrow), uniform(v.ok)};
+        const int ub = uniform(b), ukvh = uniform(kvh), uj0 = uniform(j0), uj1 = uniform(j1);
+        segment(ub, ukvh, uj0, uj1, sv, (size_t) ub * p.Hkv + ukvh + wg, uj0 == 0 && uj1 == n);
+        lds_barrier();  // every wave is done with the ring before the next segment refills it
+        x = seg_end;
+    }
 }
 
 struct MergeParams {
     const float *part_acc, *part_ml;
+    const long long *table;
     const int *pos, *row_base;
     uint16_t *out;
-    int B, Hq, Hkv, G, D, cap, window, ring, S, chunk;
+    int B, Hq, Hkv, G, D, cap, window, ring;
+    int balanced, W, S, chunk;
 };
 
 constexpr int kMergeThreads = 256;
 constexpr int kMergeDims = 128;     // output dims per merge workgroup (32 lanes x float4)
 constexpr int kMergeGroups = 8;     // split groups reduced in parallel
-constexpr int kMaxSplits = 4096;    // splits per (sequence, kv head) the merge accepts
 
 __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) {
     for (int o = 32; o > 0; o >>= 1) {
@@ -710,8 +867,7 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
 // One workgroup per (sequence, query head, 128 output dims); 8 split groups x 32 float4
 // lanes.  Each thread issues its partial loads together with the (m, l) loads, so the
 // whole merge is one memory round trip; the per-split weights are then formed from the
-// block-wide max.  Splits past the sequence's visible rows were never written and are
-// not read.
+// block-wide max.
 constexpr int kMergeRegs = 8;  // splits per thread held in registers (S <= 64 in one pass)
 
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
@@ -721,13 +877,30 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
     const int h = blockIdx.y, b = blockIdx.z;
     const int kvh = h / p.G, g = h % p.G;
     const int tid = threadIdx.x;
-    const int pos = p.pos[b];
-    const int base = p.row_base ? p.row_base[b] : 0;
-    const SeqView sv = seq_view(pos, base, p.cap, p.window, p.ring);
-    if (!sv.ok) return;
-    int ns = (sv.nvis + p.chunk - 1) / p.chunk;
-    if (ns > p.S) ns = p.S;
-    const size_t pbase = ((size_t) b * p.Hkv + kvh) * p.S;
+    int ns;
+    size_t pbase;
+    if (p.balanced) {
+        // The attend workgroups that covered pair (b, kvh): those holding its first and
+        // last rows in the linearised (sequence, kv head, row) order, each range
+        // [rows_total * w / W, rows_total * (w + 1) / W).
+        const long long n = p.table[b + 1] - p.table[b];
+        const long long rows_total = p.table[p.B] * p.Hkv;
+        if (n <= 0 || rows_total <= 0) return;
+        const long long first = p.table[b] * p.Hkv + (long long) kvh * n, last = first + n - 1;
+        if (first < 0 || last >= rows_total) return;  // inconsistent table: read nothing
+        const int w0 = (int) udiv64((first + 1) * p.W - 1, rows_total);
+        const int w1 = (int) udiv64((last + 1) * p.W - 1, rows_total);
+        if (w0 < 0 || w1 >= p.W || w0 > w1) return;
+        ns = w1 - w0 + 1;
+        pbase = (size_t) b * p.Hkv + kvh + w0;
+    } else {
+        const SeqView sv = seq_view(p.pos[b], p.row_base ? p.row_base[b] : 0, p.cap, p.window, p.ring);
+        if (!sv.ok) return;
+        ns = (sv.nvis + p.chunk - 1) / p.chunk;
+        if (ns > p.S) ns = p.S;
+        pbase = ((size_t) b * p.Hkv + kvh) * p.S;
+    }
+    if (ns <= 1) return;  // one workgroup covered the pair and wrote the output itself
     const int dq = tid & 31, sg = tid >> 5;
     const int d0 = blockIdx.x * kMergeDims + dq * 4;
 
@@ -862,14 +1035,16 @@ int check_device() {
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
 struct Plan {
-    int G, maxvis, chunk, S;
-    size_t off_ml, off_acc, bytes;
+    int G, maxvis, balanced, W, S, chunk;
+    size_t off_table, off_ml, off_acc, bytes;
 };
 
 int make_plan(const esda_decode_desc *d, Plan *pl) {
     if (!d) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: null description");
     if (d->batch <= 0 || d->num_q_heads <= 0 || d->num_kv_heads <= 0)
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: batch and head counts must be positive");
+    if (d->batch > kMaxBatch)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: at most 256 sequences per call");
     if (d->head_dim != 128 && d->head_dim != 256 && d->head_dim != 512)
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: head_dim must be 128, 256 or 512");
     if (d->num_q_heads % d->num_kv_heads)
@@ -889,27 +1064,49 @@ int make_plan(const esda_decode_desc *d, Plan *pl) {
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: split_rows must be a multiple of 16");
     int bound = d->ring ? d->window : (d->window > 0 ? std::min(d->window, d->cap) : d->cap);
     int maxvis = d->max_visible > 0 ? std::min(d->max_visible, bound) : bound;
-    int chunk = d->split_rows;
-    if (chunk == 0) {
-        const double rows = (double) maxvis * d->batch * d->num_kv_heads;
-        long long c = (long long) std::ceil(rows / kTargetGroups);
-        c = (c + 63) / 64 * 64;
-        if (c < 64) c = 64;
-        if (c > 8192) c = 8192;
-        chunk = (int) c;
-    }
-    int S = (maxvis + chunk - 1) / chunk;
-    if (S > kMaxSplits) {
-        chunk = (maxvis + kMaxSplits - 1) / kMaxSplits;
-        chunk = (chunk + kTile - 1) / kTile * kTile;
-        S = (maxvis + chunk - 1) / chunk;
-    }
+    // Work split.  Sizing uses the upper bound on rows (the kernels see the real ones).
+    // Automatic: about one workgroup per CU, no fewer than 64 rows each; split_rows > 0
+    // asks for that many rows per workgroup.
+    const long long rows_max = (long long) maxvis * d->batch * d->num_kv_heads;
+    const long long per = d->split_rows > 0 ? d->split_rows : kMinRows;
+    // Several full-causal sequences have ragged lengths: workgroups then take balanced
+    // shares of all rows (the kernel scans the lengths).  Otherwise (one sequence, or
+    // windowed local layers whose lengths are nearly equal) a plain grid of fixed splits
+    // per (sequence, kv head) starts faster.
+    pl->balanced = d->batch > 1 && !d->ring;
     pl->G = G;
     pl->maxvis = maxvis;
-    pl->chunk = chunk;
-    pl->S = S;
-    const size_t parts = (size_t) d->batch * d->num_kv_heads * S * G;
-    pl->off_ml = 256;
+    size_t slots;
+    if (pl->balanced) {
+        long long W = (rows_max + per - 1) / per;
+        if (d->split_rows == 0 && W > kTargetGroups) W = kTargetGroups;
+        if (W > kMaxGroups) W = kMaxGroups;
+        if (W < 1) W = 1;
+        pl->W = (int) W;
+        pl->S = pl->chunk = 0;
+        slots = (size_t) d->batch * d->num_kv_heads + (size_t) W;  // pair u's partial from workgroup w at u + w
+    } else {
+        long long chunk = d->split_rows;
+        if (chunk == 0) {
+            chunk = (rows_max + kTargetGroups - 1) / kTargetGroups;
+            chunk = (chunk + kMinRows - 1) / kMinRows * kMinRows;
+            if (chunk < kMinRows) chunk = kMinRows;
+            if (chunk > 8192) chunk = 8192;
+        }
+        long long S = (maxvis + chunk - 1) / chunk;
+        if (S > kMaxGroups) {
+            chunk = (maxvis + kMaxGroups - 1) / kMaxGroups;
+            chunk = (chunk + kTile - 1) / kTile * kTile;
+            S = (maxvis + chunk - 1) / chunk;
+        }
+        pl->W = 0;
+        pl->S = (int) S;
+        pl->chunk = (int) chunk;
+        slots = (size_t) d->batch * d->num_kv_heads * S;
+    }
+    const size_t parts = slots * G;
+    pl->off_table = 256;
+    pl->off_ml = pl->off_table + (((size_t) (d->batch + 1) * sizeof(long long) + 255) / 256) * 256;
     pl->off_acc = pl->off_ml + ((parts * 2 * sizeof(float) + 255) / 256) * 256;
     pl->bytes = pl->off_acc + parts * d->head_dim * sizeof(float);
     return ESDA_OK;
@@ -961,6 +1158,7 @@ int raw_as_decode(const esda_raw_desc *r, esda_decode_desc *d) {
 int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap_in, uint16_t *out,
                void *workspace, int stages, bool raw, hipStream_t st) {
     unsigned char *ws = static_cast<unsigned char *>(workspace);
+    long long *table = reinterpret_cast<long long *>(ws + pl.off_table);
     float *part_ml = reinterpret_cast<float *>(ws + pl.off_ml);
     float *part_acc = reinterpret_cast<float *>(ws + pl.off_acc);
     if (stages & ESDA_STAGE_ATTEND) {
@@ -977,10 +1175,14 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         ap.cap = d->cap;
         ap.window = d->window;
         ap.ring = d->ring;
+        ap.balanced = pl.balanced;
+        ap.W = pl.W;
         ap.S = pl.S;
         ap.chunk = pl.chunk;
+        ap.table = table;
         ap.scale_log2e = d->scale * kLog2e;
-        dim3 grid(pl.S, d->num_kv_heads, d->batch);
+        ap.out = out;
+        const dim3 grid = pl.balanced ? dim3(pl.W) : dim3(pl.S, d->num_kv_heads, d->batch);
         hipError_t e = raw ? launch_attend<kRawDim, true, true>(ap, grid, st)
                            : dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
         if (e != hipSuccess) return hip_fail(e, "attend_kernel launch");
@@ -989,6 +1191,7 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         MergeParams mp;
         mp.part_acc = part_acc;
         mp.part_ml = part_ml;
+        mp.table = table;
         mp.pos = ap_in.pos;
         mp.row_base = ap_in.row_base;
         mp.out = out;
@@ -1000,6 +1203,8 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         mp.cap = d->cap;
         mp.window = d->window;
         mp.ring = d->ring;
+        mp.balanced = pl.balanced;
+        mp.W = pl.W;
         mp.S = pl.S;
         mp.chunk = pl.chunk;
         dim3 grid(d->head_dim / kMergeDims, d->num_q_heads, d->batch);

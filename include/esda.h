@@ -62,7 +62,7 @@ typedef struct esda_decode_desc {
     int64_t seq_stride;   /* elements; >= num_kv_heads * head_stride        */
     int64_t head_stride;  /* elements; >= cap * head_dim, multiple of 8     */
     int32_t max_visible;  /* upper bound on visible rows (0 = from cap/window) */
-    int32_t split_rows;   /* rows per split (0 = automatic; multiple of 64) */
+    int32_t split_rows;   /* rows per workgroup (0 = automatic; multiple of 16) */
     float scale;          /* softmax scale (the model uses 1.0)             */
 } esda_decode_desc;
 
@@ -88,7 +88,10 @@ int esda_decode_workspace_size(const esda_decode_desc *desc, size_t *bytes);
 int esda_decode(const esda_decode_desc *desc, const esda_decode_args *args, void *stream);
 
 /* Stage selector for esda_decode_stages (a profiling aid: the bench times the
- * split kernel alone).  esda_decode == both stages. */
+ * split kernel alone).  esda_decode == both stages.  When the plan has one split per
+ * (sequence, kv head) -- split_rows >= max_visible, or automatically when batch *
+ * num_kv_heads fills the GPU -- the attend stage writes `out` itself and the merge stage
+ * launches nothing. */
 #define ESDA_STAGE_ATTEND 1 /* fused append + split-K partials */
 #define ESDA_STAGE_MERGE 2  /* cross-split fp32 merge -> bf16 out */
 int esda_decode_stages(const esda_decode_desc *desc, const esda_decode_args *args, int stages,

@@ -120,6 +120,17 @@ EDGE = [
     dict(name="split_odd", B=1, Hq=16, Hkv=8, D=256, cap=1000, window=700, pos=[999], split_rows=208),
     dict(name="max_visible_hint", B=2, Hq=32, Hkv=4, D=512, cap=4096, pos=[700, 900], shared=True,
          max_visible=901),
+    # a hint below the real lengths only sizes the work split: every row is still attended
+    dict(name="max_visible_hint_too_small", B=2, Hq=32, Hkv=4, D=512, cap=4096, pos=[3000, 900],
+         shared=True, max_visible=100),
+    # ragged batches: workgroups take equal shares of all rows, so one workgroup may span the
+    # end of one (sequence, kv head) and the start of the next
+    dict(name="ragged_batch_16", B=16, Hq=32, Hkv=4, D=512, cap=4096, shared=True,
+         pos=[int(x) for x in np.random.default_rng(77).integers(16, 4096, 16)]),
+    dict(name="many_tiny_sequences", B=64, Hq=8, Hkv=2, D=128, cap=64,
+         pos=[int(x) for x in np.random.default_rng(78).integers(0, 64, 64)]),
+    dict(name="max_batch_256", B=256, Hq=4, Hkv=1, D=256, cap=48, window=32, ring=True,
+         pos=[int(x) for x in np.random.default_rng(79).integers(0, 5000, 256)]),
     # In-model scale 1.0 on unit-RMS q/k gives logits ~ |q||k| = 512: the reference
     # composite's bf16 score rounding alone moves the output past the tolerance there
     # (tests/test_oracle.py::test_refround_coarse_at_in_model_scale), so this case is
