@@ -150,7 +150,9 @@ struct Ring {
     static constexpr int DPT = NI / NW;                     // DMA per wave per tensor
     static constexpr int DPW = DPT * (SHARED ? 1 : 2);      // DMA per wave per stage
     static constexpr int XB = 2 * NW * 64 * 16;             // score-exchange bytes
-    static constexpr int NS_ = (160 * 1024 - XB - 256 - EXTRA) / SB;
+    // reserve: kernel arguments' spill room (256 B) and the batch prefix scan (int64 per
+    // sequence + one per wave)
+    static constexpr int NS_ = (160 * 1024 - XB - 256 - ((kMaxBatch + 1) + NW) * 8 - EXTRA) / SB;
     static constexpr int NS = NS_ > 16 ? 16 : NS_;          // stages in the ring
     static_assert(DW % 32 == 0 && NI % NW == 0, "wave slices must cover whole MFMA steps");
     static_assert(NS >= 4, "the ring needs at least 4 stages");
@@ -236,7 +238,9 @@ __device__ __forceinline__ void unroll(F &&f) {
 constexpr int kRawDim = 512;
 constexpr int kRopePairs = 64;
 constexpr int kTabStride = 68;  // words per cos/sin table row: 64 + 4 (conflict-free 128-bit reads)
-constexpr int kRawExtraLds = 3 * 16 * 4 * 4 + 2 * 16 * kTabStride * 4 + 2 * 2 * 16 * 4;
+// LDS of the raw-mode exchanges for NW waves: row sums of squares [3][16][NW], the
+// cos/sin tables [2][16][kTabStride], the row norm factors [2][2][16].
+constexpr int raw_extra_lds(int nw) { return 3 * 16 * nw * 4 + 2 * 16 * kTabStride * 4 + 2 * 2 * 16 * 4; }
 
 // Cody-Waite split of pi/2 (hi + mid + lo, each the nearest fp32 to what remains).
 constexpr float kTwoOverPi = 0.636619746685028076171875f;     // fp32(2/pi)
@@ -297,8 +301,8 @@ __device__ __forceinline__ float bf16_hi(unsigned w) { return __builtin_bit_cast
 template <int D, bool SHARED, int NW, bool RAW>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW)))
 void attend_kernel(AttendParams p) {
-    static_assert(!RAW || (D == kRawDim && SHARED && NW == 4), "raw mode: one 512-dim stream, 4 waves");
-    using R = Ring<D, SHARED, NW, RAW ? kRawExtraLds : 0>;
+    static_assert(!RAW || (D == kRawDim && SHARED && (NW == 4 || NW == 8)), "raw mode: one 512-dim stream, 4 or 8 waves");
+    using R = Ring<D, SHARED, NW, RAW ? raw_extra_lds(NW) : 0>;
     constexpr int NS = R::NS, DW = R::DW, KKW = R::KKW, DTW = R::DTW;
     // Stages between the one being accumulated and the newest one that must have landed.
     constexpr int AHEAD = RAW ? 2 : 1;
@@ -332,11 +336,14 @@ void attend_kernel(AttendParams p) {
     // Raw mode: per-row partial sums of squares xss[stage % 3][row][wave], the cos/sin
     // table xtab[stage % 2][row][pair] (bf16 cos in the low half, sin in the high half)
     // and the per-row norm factors xr.
-    __shared__ __attribute__((aligned(16))) unsigned char rawlds[RAW ? kRawExtraLds : 16];
-    auto *xss = reinterpret_cast<float (*)[16][4]>(rawlds);
-    auto *xtab = reinterpret_cast<unsigned (*)[16][kTabStride]>(rawlds + 3 * 16 * 4 * 4);
+    __shared__ __attribute__((aligned(16))) unsigned char rawlds[RAW ? raw_extra_lds(NW) : 16];
+    auto *xss = reinterpret_cast<float (*)[16][NW]>(rawlds);
+    auto *xtab = reinterpret_cast<unsigned (*)[16][kTabStride]>(rawlds + 3 * 16 * NW * 4);
     // xr[stage % 2][0][row] = rinv, xr[stage % 2][1][row] = 1 / rinv
-    auto *xr = reinterpret_cast<float (*)[2][16]>(rawlds + 3 * 16 * 4 * 4 + 2 * 16 * kTabStride * 4);
+    auto *xr = reinterpret_cast<float (*)[2][16]>(rawlds + 3 * 16 * NW * 4 + 2 * 16 * kTabStride * 4);
+    // cos/sin table entries per thread per stage (16 rows x 64 pairs over 64*NW threads)
+    constexpr int EPT = 1024 / (64 * NW);
+    constexpr int TPR = 64 / EPT;  // threads per table row
 
     const int wg = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -357,7 +364,9 @@ void attend_kernel(AttendParams p) {
 
     // 32-dim chunk of the QK k-step kk of this wave.  Raw mode interleaves the waves so
     // that each rotary pair (d, d + 256), d < 64, sits in one lane of wave 0 or 1.
-    auto qk_chunk = [&](int kk) { return RAW ? wave + 4 * kk : wave * KKW + kk; };
+    auto qk_chunk = [&](int kk) { return RAW ? wave + NW * kk : wave * KKW + kk; };
+    // k-step holding the rotary partners (chunk + 8) of the chunk at k-step 0
+    constexpr int KP = 8 / NW;
 
     // Q^T operand for this wave's dims: lane (li, lg) = head li, dims 32*chunk + 8lg .. +8
     // (zero for heads >= G).
@@ -374,7 +383,7 @@ void attend_kernel(AttendParams p) {
     // Raw mode: k-norm weights of the lane's QK dims, and the rotary frequencies of the
     // four table entries this thread computes per stage (row tid/16, pairs 4(tid%16)..+4).
     float kwf[RAW ? KKW : 1][8];
-    f32x4 invf = {0.0f, 0.0f, 0.0f, 0.0f};
+    float invf[RAW ? EPT : 1] = {};
     if constexpr (RAW) {
 #pragma unroll
         for (int kk = 0; kk < KKW; ++kk) {
@@ -385,7 +394,8 @@ void attend_kernel(AttendParams p) {
                 kwf[kk][2 * e + 1] = bf16_hi(t[e]);
             }
         }
-        invf = *reinterpret_cast<const f32x4 *>(p.inv_freq + 4 * (tid & 15));
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) invf[e] = p.inv_freq[EPT * (tid % TPR) + e];
     }
     ESDA_WAIT_VM(0);  // operands are in registers before the ring starts counting its own loads
 
@@ -477,23 +487,35 @@ void attend_kernel(AttendParams p) {
             if (i >= 0 && i < 4) xss[buf][li][wave] = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
         }
     };
-    // cos/sin table of stage st: this thread's row tid/16, pairs 4(tid%16) .. +4.
+    // cos/sin table of stage st: this thread's row tid / TPR, pairs EPT*(tid % TPR) .. +EPT.
     auto publish_tab = [&](int st, int buf) {
-        const int row = tid >> 4;
-        const float t = (float) (sv.first + j0 + st * 16 + row);
-        u32x4 w;
+        if constexpr (RAW) {
+            const int row = tid / TPR;
+            const float t = (float) (sv.first + j0 + st * 16 + row);
+            unsigned w[EPT];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float s, c;
-            sincos_f32(t * invf[e], s, c);
-            w[e] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{c, s}, bf16x2));
+            for (int e = 0; e < EPT; ++e) {
+                float s, c;
+                sincos_f32(t * invf[e], s, c);
+                w[e] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{c, s}, bf16x2));
+            }
+            unsigned *dst = &xtab[buf][row][EPT * (tid % TPR)];
+            if constexpr (EPT == 4) {
+                *reinterpret_cast<u32x4 *>(dst) = u32x4{w[0], w[1], w[2], w[3]};
+            } else {
+                *reinterpret_cast<uint2 *>(dst) = uint2{w[0], w[1]};
+            }
         }
-        *reinterpret_cast<u32x4 *>(&xtab[buf][row][4 * (tid & 15)]) = w;
     };
     // mean(kraw^2) + eps of a row; rinv = rsqrt of it.
     auto row_ms = [&](int buf, int row) {
-        const f32x4 v = *reinterpret_cast<const f32x4 *>(&xss[buf][row][0]);
-        return (v[0] + v[1] + v[2] + v[3]) * (1.0f / kRawDim) + p.eps;
+        float sum = 0.0f;
+#pragma unroll
+        for (int q4 = 0; q4 < NW; q4 += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(&xss[buf][row][q4]);
+            sum += (v[0] + v[1]) + (v[2] + v[3]);
+        }
+        return sum * (1.0f / kRawDim) + p.eps;
     };
     // Scores of the stage held in araw: rebuild K in registers, then MFMA.
     auto qk_raw = [&](int ssbuf, int tabbuf, int par) {
@@ -514,7 +536,8 @@ void attend_kernel(AttendParams p) {
                     kn[kk][2 * e + 1] = bf16_hi(araw[kk][e]) * rinv * kwf[kk][2 * e + 1];
                 }
             if (wave < 2) {
-                // chunk `wave` holds dims d = 32*wave + 8lg + e < 64, chunk wave + 8 their pairs.
+                // chunk `wave` (k-step 0) holds dims d = 32*wave + 8lg + e < 64; chunk wave + 8
+                // (k-step KP) their rotary partners.
                 const unsigned *tb = &xtab[tabbuf][li][32 * wave + 8 * lg];
                 const u32x4 t0 = *reinterpret_cast<const u32x4 *>(tb);
                 const u32x4 t1 = *reinterpret_cast<const u32x4 *>(tb + 4);
@@ -522,9 +545,9 @@ void attend_kernel(AttendParams p) {
                 for (int e = 0; e < 8; ++e) {
                     const unsigned w = e < 4 ? t0[e] : t1[e - 4];
                     const float c = bf16_lo(w), s = bf16_hi(w);
-                    const float lo = kn[0][e], hi = kn[2][e];
+                    const float lo = kn[0][e], hi = kn[KP][e];
                     kn[0][e] = lo * c - hi * s;
-                    kn[2][e] = hi * c + lo * s;
+                    kn[KP][e] = hi * c + lo * s;
                 }
             }
             f32x4 sp = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1116,9 +1139,13 @@ int make_plan(const esda_decode_desc *d, Plan *pl) {
 template <int D>
 constexpr int ring_waves() { return 4; }
 
+// Raw mode: 8 waves, two per SIMD, so one wave's dependency stalls overlap the other's
+// reconstruction work.
+constexpr int kRawWaves = 8;
+
 template <int D, bool SHARED, bool RAW = false>
 hipError_t launch_attend(const AttendParams &ap, dim3 grid, hipStream_t st) {
-    constexpr int NW = ring_waves<D>();
+    constexpr int NW = RAW ? kRawWaves : ring_waves<D>();
     hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW>), grid, dim3(64 * NW), 0, st, ap);
     return hipGetLastError();
 }
