@@ -1,7 +1,8 @@
 """Build libesda.so (HIP, gfx950) in-tree with hipcc.
 
 Every HIP source is compiled with packed-FP32 instructions disabled (the compiler
-would otherwise form v_pk_*_f32 from ordinary float code).  The host pass prints a
+would otherwise form v_pk_*_f32 from ordinary float code) and the AMDGPU iterative-ILP
+instruction scheduler.  The host pass prints a
 harmless warning that it does not know that feature.
 """
 from __future__ import annotations
@@ -28,6 +29,10 @@ SOURCES = [
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # The default scheduler serialises the attend loop's LDS reads behind their uses when
+    # the loop is nested (the balanced split's segment walk); the iterative ILP strategy
+    # keeps them overlapped in every copy.
+    "-mllvm", "-amdgpu-sched-strategy=iterative-ilp",
     "-Wno-unused-command-line-argument",
 ]
 

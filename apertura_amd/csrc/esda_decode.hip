@@ -299,7 +299,10 @@ __device__ __forceinline__ float bf16_hi(unsigned w) { return __builtin_bit_cast
 // split ends at it (bit-exact copy); that workgroup's own loads read the row from
 // k_new/v_new and no other workgroup reads it, so the copy needs no ordering.
 template <int D, bool SHARED, int NW, bool RAW>
-__global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW)))
+// The LDS ring allows one workgroup per CU, i.e. NW/4 waves per SIMD: telling the
+// compiler so lifts the register limit it would otherwise keep for higher occupancy,
+// which it meets by serialising LDS reads behind their uses.
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void attend_kernel(AttendParams p) {
     static_assert(!RAW || (D == kRawDim && SHARED && (NW == 4 || NW == 8)), "raw mode: one 512-dim stream, 4 or 8 waves");
     using R = Ring<D, SHARED, NW, RAW ? raw_extra_lds(NW) : 0>;
