@@ -72,10 +72,12 @@ class Toy:
     def out(self, li, x, o_bf16):
         return x + _f(o_bf16).reshape(-1) @ self.w[li]["o"]
 
-    def logits(self, x):
-        # O(1) logits over the vocabulary, so top-2 margins are small enough for attention
-        # errors to matter (a tied head on unit-RMS rows would give margins in the hundreds)
-        return _rms(x) @ self.emb.T / np.sqrt(HIDDEN)
+    def logits(self, x, token):
+        # The head reads what the two attention layers added to the residual stream (the
+        # input embedding subtracted): with it left in, the input token's own logit wins
+        # every step by ~20 and the argmax would not depend on attention at all.  These
+        # logits are O(1) with a median top-2 margin of ~0.3, and the greedy tokens vary.
+        return _rms(x - self.emb[token]) @ self.emb.T / np.sqrt(HIDDEN)
 
 
 def _oracle_attend(L, q, kc, vc):
@@ -102,7 +104,7 @@ def test_greedy_argmax_agreement_in_a_random_init_model():
         host_k.append(k)
         host_v.append(v)
     token = int(rng.integers(VOCAB))
-    agree, margins = 0, []
+    agree, margins, dlogit, tokens = 0, [], [], set()
     for _ in range(steps):
         x_ref = toy.emb[token].copy()
         x_gpu = toy.emb[token].copy()
@@ -120,14 +122,25 @@ def test_greedy_argmax_agreement_in_a_random_init_model():
             kd = _dev(kg[:, None])
             o = cache.decode(li, _dev(qg), kd, kd if L["shared"] else _dev(vg[:, None]), L["window"], 1.0)
             x_gpu = toy.out(li, x_gpu, _host(o))
-        lr, lg = toy.logits(x_ref), toy.logits(x_gpu)
+        lr, lg = toy.logits(x_ref, token), toy.logits(x_gpu, token)
         top = np.sort(lr)[-2:]
         margins.append(float(top[1] - top[0]))
+        dlogit.append(float(np.abs(lr - lg).max()))
         agree += int(np.argmax(lr) == np.argmax(lg))
         token = int(np.argmax(lr))  # teacher forcing from the oracle path
-    print(f"greedy agreement {agree}/{steps}; smallest top-2 margin {min(margins):.4f}")
-    # a flip is acceptable only where the oracle's own top-2 margin is within rounding noise
-    assert agree >= steps - sum(m < 0.05 for m in margins)
+        tokens.add(token)
+    print(f"greedy agreement {agree}/{steps}; {len(tokens)} distinct tokens; smallest top-2 "
+          f"margin {min(margins):.4f}; max |logit diff| {max(dlogit):.4f}")
+    # the test is only meaningful if the argmax moves with the attention output
+    assert len(tokens) >= steps // 2
+    # The two residual streams (and so the appended K/V rows) drift apart by rounding over
+    # the 64 steps: the fp64 oracle against the reference-rounding one drifts by up to 0.3
+    # in a logit on this toy.  The fp64 oracle with a planted fault in place of the GPU
+    # path (sliding window one row too long, kv heads swapped, the appended row not
+    # attended) moves a logit by 1.6 to 5.9 here, so the drift bound is 1.0; a flip is
+    # acceptable only where the oracle's own top-2 margin is below 0.1.
+    assert max(dlogit) < 1.0
+    assert agree >= steps - sum(m < 0.1 for m in margins)
     # the sliding layer kept exactly its window; the global layer every row
     assert cache.slot(0)["len"] - cache.slot(0)["start"] == LAYERS[0]["window"]
     assert cache.slot(1)["len"] == prefill + steps and cache.slot(1)["shared"]
