@@ -8,9 +8,10 @@
 // (ESKVCache.mm:458-504) followed by esDecodeAttnGlobal (ESDecodeAttn.mm:17-117, 415-453).
 //
 // Kernels
-//   attend_kernel  grid (splits, kv heads, sequences), 4 waves, one workgroup per CU.  A
-//                  workgroup streams `chunk` visible rows of one (sequence, kv head)
-//                  through an LDS ring filled by LDS DMA, splits the head dim across its
+//   attend_kernel  grid (splits, kv heads, sequences) or balanced shares of a ragged
+//                  batch; 4 or 8 waves, one workgroup per CU.  A workgroup streams
+//                  visible rows of one (sequence, kv head) -- or of 2 or 4 kv heads
+//                  packed together -- through an LDS ring filled by LDS DMA, splits the head dim across its
 //                  waves for the QK and PV MFMAs (the GQA group is the MFMA N dimension),
 //                  runs an fp32 online softmax and writes (m, l, acc) partials.  The
 //                  workgroup whose split ends at the new token also copies its row into
@@ -86,7 +87,10 @@ struct AttendParams {
     float *part_acc, *part_ml;
     int *status;
     long long seq_stride, head_stride;
+    // Hkv and G count packed kv heads: a workgroup serves pk consecutive kv heads of one
+    // sequence (gk query heads each) as one group of G = pk * gk query heads.
     int B, Hq, Hkv, G, cap, window, ring;
+    int pk, gk;
     int balanced;      // 1: W balanced shares of all rows; 0: grid (S, Hkv, B) of chunk-row splits
     int W, S, chunk;
     float scale_log2e;
@@ -279,9 +283,15 @@ __device__ __forceinline__ float bf16_hi(unsigned w) { return __builtin_bit_cast
 
 // --------------------------------------------------------------------- attend kernel
 //
-// grid (splits, kv heads, sequences), NW = 4 waves per workgroup, one workgroup per
+// grid (splits, kv heads, sequences), NW = 4 or 8 waves per workgroup, one workgroup per
 // CU.  A workgroup owns `chunk` consecutive visible rows of one (sequence, kv head)
-// and streams them through the LDS ring in 16-row stages.  The head dim is split
+// and streams them through the LDS ring in 16-row stages.  When each pair needs one
+// split and pairs are plentiful, pk = 2 or 4 kv heads of a sequence share a workgroup:
+// a stage then holds 16 / pk rows of each, their query heads fill the MFMA N dimension
+// side by side, and scores of a head against another kv head's rows are masked.
+// Ragged batches use balanced shares instead: workgroup w takes rows
+// [total * w / W, total * (w + 1) / W) of all visible rows linearised by (sequence, kv
+// head, row), one segment per pair it touches.  The head dim is split
 // across the waves: per stage, each wave forms partial scores S^T[16 rows x 16 heads]
 // over its dims with v_mfma_f32_16x16x32_bf16 (the GQA group is the MFMA N dimension,
 // zero-padded to 16, so each K/V byte is read from HBM once per group), the partials
@@ -353,17 +363,28 @@ void attend_kernel(AttendParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, lg = lane >> 4;
 
-    // One segment: rows [j0, j1) of (sequence b, kv head kvh).  `slot` indexes its partial;
-    // `direct` means the segment is the whole (b, kvh) and writes the output itself.
+    // Packed kv heads: a stage holds RPP = 16 / pk rows of each of the pk kv heads (stage
+    // row r belongs to kv head r / RPP, row r % RPP of the stage's row range).  pk is 1, 2
+    // or 4 and the same in every lane.
+    const int pk = uniform(p.pk);
+    const int lrpp = 4 - __builtin_ctz(pk), RPP = 1 << lrpp;
+    // Query head li belongs to kv head li / gk of the group (padding heads li >= G take
+    // the last); the C rows 4lg .. 4lg+3 of this lane come from one kv head (RPP >= 4).
+    const bool hmatch = ((4 * lg) >> lrpp) == min(li / p.gk, pk - 1);
+    const int jl = (4 * lg) & (RPP - 1);
+
+    // One segment: rows [j0, j1) of (sequence b, packed kv head kvh).  `slot` indexes its
+    // partial; `direct` means the segment is the whole pair and writes the output itself.
     auto segment = [&](const int b, const int kvh, const int j0, const int j1, const SeqView sv,
                        const size_t slot, const bool direct) {
     const bool append = p.k_new != nullptr;
 
-    const size_t head_off = (size_t) b * p.seq_stride + (size_t) kvh * p.head_stride;
+    // kv head kvh * pk + i of sequence b sits at head_off + i * head_stride
+    const size_t head_off = (size_t) b * p.seq_stride + (size_t) kvh * pk * p.head_stride;
     uint16_t *kbase = p.k_cache + head_off;
     uint16_t *vbase = p.v_cache + head_off;
-    const uint16_t *knew = append ? p.k_new + ((size_t) b * p.Hkv + kvh) * D : nullptr;
-    const uint16_t *vnew = SHARED ? knew : p.v_new + ((size_t) b * p.Hkv + kvh) * D;
+    const uint16_t *knew = append ? p.k_new + ((size_t) b * p.Hkv + kvh) * pk * D : nullptr;
+    const uint16_t *vnew = SHARED ? knew : p.v_new + ((size_t) b * p.Hkv + kvh) * pk * D;
 
     // 32-dim chunk of the QK k-step kk of this wave.  Raw mode interleaves the waves so
     // that each rotary pair (d, d + 256), d < 64, sits in one lane of wave 0 or 1.
@@ -404,16 +425,19 @@ void attend_kernel(AttendParams p) {
 
     // DMA source slot of this lane: sub-row dq, chunk dchunk of the row.
     const int dq = lane / R::CPR, dchunk = lane % R::CPR;
-    const int nst = (j1 - j0 + 15) / 16;
-    // Per-lane byte offsets of this wave's DMA slots inside a stage's row range.
+    const int nst = (j1 - j0 + RPP - 1) >> lrpp;
+    // Per-lane byte offsets of this wave's DMA slots inside a stage's row range (stage row
+    // r: kv head r / RPP of the group, row r % RPP; below 2^31 bytes, checked by the host).
     unsigned dvoff[R::DPT];
 #pragma unroll
-    for (int t = 0; t < R::DPT; ++t)
-        dvoff[t] = (unsigned) (((wave * R::DPT + t + dq * R::NI) * D + dchunk * 8) * 2);
+    for (int t = 0; t < R::DPT; ++t) {
+        const int r = wave * R::DPT + t + dq * R::NI;
+        dvoff[t] = (unsigned) ((((size_t) (r >> lrpp) * p.head_stride) + (size_t) (r & (RPP - 1)) * D + dchunk * 8) * 2);
+    }
     auto dma = [&](int st, unsigned char *buf) {
-        const int jst = j0 + st * 16;
-        if (jst + 16 < j1 && sv.first + jst + 16 <= p.cap) {
-            // Interior stage: 16 consecutive cache rows, none clamped or new.
+        const int jst = j0 + st * RPP;
+        if (jst + RPP < j1 && sv.first + jst + RPP <= p.cap) {
+            // Interior stage: RPP consecutive cache rows per kv head, none clamped or new.
             const uint16_t *kb = kbase + (size_t) (sv.first + jst) * D;
             const uint16_t *vb = vbase + (size_t) (sv.first + jst) * D;
 #pragma unroll
@@ -427,15 +451,18 @@ void attend_kernel(AttendParams p) {
 #pragma unroll
         for (int t = 0; t < R::DPT; ++t) {
             const int i = wave * R::DPT + t;            // DMA block of this stage
-            const int j = jst + i + dq * R::NI;         // logical row this lane feeds
+            const int sr = i + dq * R::NI;              // stage row this lane feeds
+            const int pr = sr >> lrpp;                  // its kv head within the group
+            const int j = jst + (sr & (RPP - 1));       // its logical row
             const int jj = j < j1 ? j : j1 - 1;          // clamp: masked rows read a visible row
             int r = sv.first + jj;
             if (r >= p.cap) r -= p.cap;
             const bool from_new = append && (jj == sv.nvis - 1);
-            const uint16_t *ks = (from_new ? knew : kbase + (size_t) r * D) + dchunk * 8;
+            const size_t hoff = (size_t) pr * p.head_stride + (size_t) r * D;
+            const uint16_t *ks = (from_new ? knew + pr * D : kbase + hoff) + dchunk * 8;
             lds_dma16(ks, lds_addr(buf) + i * R::BLK);
             if constexpr (!SHARED) {
-                const uint16_t *vs = (from_new ? vnew : vbase + (size_t) r * D) + dchunk * 8;
+                const uint16_t *vs = (from_new ? vnew + pr * D : vbase + hoff) + dchunk * 8;
                 lds_dma16(vs, lds_addr(buf) + R::TB + i * R::BLK);
             }
         }
@@ -640,10 +667,10 @@ void attend_kernel(AttendParams p) {
             qk_partial(ring(std::integral_constant<int, (u + 1) % NS>{}), (st + 1) & 1);
         }
         // Online softmax (log2 domain), identical in every wave; rows past the split
-        // end (last stage only) are masked.
-        const int jt = j0 + st * 16;
+        // end (last stage only) and rows of another kv head of the group are masked.
+        const int jt = j0 + st * RPP + jl;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[r] = (jt + 4 * lg + r) < j1 ? sc[r] * p.scale_log2e : -INFINITY;
+        for (int r = 0; r < 4; ++r) sc[r] = hmatch && (jt + r) < j1 ? sc[r] * p.scale_log2e : -INFINITY;
         const float tmax = wave_max_across_groups(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
         if (__any(tmax > m + kRescaleSlack)) {
             const float mnew = fmaxf(m, tmax);
@@ -690,13 +717,16 @@ void attend_kernel(AttendParams p) {
     // into its cache row (bit-exact).  Its own DMA reads that row from k_new / v_new and
     // no other workgroup reads it; the copy runs after this workgroup's ring has
     // drained, so no outstanding load is counted against the ring's waits.
-    if (append && wave == 0 && j1 == sv.nvis) {
-        for (int c = lane; c < D / 8; c += 64) {
-            *reinterpret_cast<u32x4 *>(kbase + (size_t) sv.newrow * D + c * 8) =
-                *reinterpret_cast<const u32x4 *>(knew + c * 8);
-            if constexpr (!SHARED)
-                *reinterpret_cast<u32x4 *>(vbase + (size_t) sv.newrow * D + c * 8) =
-                    *reinterpret_cast<const u32x4 *>(vnew + c * 8);
+    if (append && j1 == sv.nvis) {
+        for (int pr = wave; pr < pk; pr += NW) {  // wave pr copies kv head pr of the group
+            const size_t row = (size_t) pr * p.head_stride + (size_t) sv.newrow * D;
+            for (int c = lane; c < D / 8; c += 64) {
+                *reinterpret_cast<u32x4 *>(kbase + row + c * 8) =
+                    *reinterpret_cast<const u32x4 *>(knew + pr * D + c * 8);
+                if constexpr (!SHARED)
+                    *reinterpret_cast<u32x4 *>(vbase + row + c * 8) =
+                        *reinterpret_cast<const u32x4 *>(vnew + pr * D + c * 8);
+            }
         }
     }
 
@@ -1062,10 +1092,26 @@ bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 
 struct Plan {
     int G, maxvis, balanced, W, S, chunk;
+    int pk;  // kv heads packed per workgroup (the kernels see Hkv / pk heads of G * pk)
     size_t off_table, off_ml, off_acc, bytes;
 };
 
-int make_plan(const esda_decode_desc *d, Plan *pl) {
+// Kv heads per workgroup for a grid of one split per (sequence, kv head): with several
+// workgroups' worth of pairs per CU, packing pk kv heads (pk * G <= 16 query heads, the
+// MFMA's N dimension) gives each workgroup one pk-times longer stream instead of pk short
+// ones, each of which would pay the ring's fill and drain.  Local layers (G = 2) at C5's
+// batch: 512 pairs -> 256 workgroups of two kv heads.
+int choose_pack(const esda_decode_desc *d, int G, long long S) {
+    const long long pairs = (long long) d->batch * d->num_kv_heads;
+    int pk = 1;
+    while (pk < 4 && S == 1 && G * pk * 2 <= kMaxGroup && d->num_kv_heads % (pk * 2) == 0 &&
+           pairs / (pk * 2) >= kTargetGroups &&
+           (long long) d->head_stride * 2 * (pk * 2) + 16LL * d->head_dim * 2 < (1LL << 31))
+        pk *= 2;
+    return pk;
+}
+
+int make_plan(const esda_decode_desc *d, Plan *pl, bool allow_pack = true) {
     if (!d) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: null description");
     if (d->batch <= 0 || d->num_q_heads <= 0 || d->num_kv_heads <= 0)
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: batch and head counts must be positive");
@@ -1102,6 +1148,7 @@ int make_plan(const esda_decode_desc *d, Plan *pl) {
     pl->balanced = d->batch > 1 && !d->ring;
     pl->G = G;
     pl->maxvis = maxvis;
+    pl->pk = 1;
     size_t slots;
     if (pl->balanced) {
         long long W = (rows_max + per - 1) / per;
@@ -1128,9 +1175,10 @@ int make_plan(const esda_decode_desc *d, Plan *pl) {
         pl->W = 0;
         pl->S = (int) S;
         pl->chunk = (int) chunk;
-        slots = (size_t) d->batch * d->num_kv_heads * S;
+        if (allow_pack && d->split_rows == 0) pl->pk = choose_pack(d, G, S);
+        slots = (size_t) d->batch * (d->num_kv_heads / pl->pk) * S;
     }
-    const size_t parts = slots * G;
+    const size_t parts = slots * G * pl->pk;
     pl->off_table = 256;
     pl->off_ml = pl->off_table + (((size_t) (d->batch + 1) * sizeof(long long) + 255) / 256) * 256;
     pl->off_acc = pl->off_ml + ((parts * 2 * sizeof(float) + 255) / 256) * 256;
@@ -1138,9 +1186,13 @@ int make_plan(const esda_decode_desc *d, Plan *pl) {
     return ESDA_OK;
 }
 
-// Waves per workgroup (the head dim is split across them).
+// Waves per workgroup (the head dim is split across them).  D = 256: 8 waves, two per
+// SIMD, so one wave's softmax and exchange latency overlaps the other's MFMAs (measured:
+// C3 attend 25.3 -> 24.0 us, C5 local layers -2.3%).  D = 512 keeps 4: its 8-wave form
+// loses a ring stage to the larger score exchange and runs C4 ~6% slower.  D = 128 has
+// too few dims for 8 waves of 32-dim MFMA steps.
 template <int D>
-constexpr int ring_waves() { return 4; }
+constexpr int ring_waves() { return D == 256 ? 8 : 4; }
 
 // Raw mode: 8 waves, two per SIMD, so one wave's dependency stalls overlap the other's
 // reconstruction work.
@@ -1200,8 +1252,10 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         ap.head_stride = d->head_stride;
         ap.B = d->batch;
         ap.Hq = d->num_q_heads;
-        ap.Hkv = d->num_kv_heads;
-        ap.G = pl.G;
+        ap.Hkv = d->num_kv_heads / pl.pk;
+        ap.G = pl.G * pl.pk;
+        ap.pk = pl.pk;
+        ap.gk = pl.G;
         ap.cap = d->cap;
         ap.window = d->window;
         ap.ring = d->ring;
@@ -1212,12 +1266,13 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         ap.table = table;
         ap.scale_log2e = d->scale * kLog2e;
         ap.out = out;
-        const dim3 grid = pl.balanced ? dim3(pl.W) : dim3(pl.S, d->num_kv_heads, d->batch);
+        const dim3 grid = pl.balanced ? dim3(pl.W) : dim3(pl.S, d->num_kv_heads / pl.pk, d->batch);
         hipError_t e = raw ? launch_attend<kRawDim, true, true>(ap, grid, st)
                            : dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
         if (e != hipSuccess) return hip_fail(e, "attend_kernel launch");
     }
-    if (stages & ESDA_STAGE_MERGE) {
+    // One split per pair: the attend workgroups wrote every output themselves.
+    if ((stages & ESDA_STAGE_MERGE) && !(!pl.balanced && pl.S == 1)) {
         MergeParams mp;
         mp.part_acc = part_acc;
         mp.part_ml = part_ml;
@@ -1227,8 +1282,8 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         mp.out = out;
         mp.B = d->batch;
         mp.Hq = d->num_q_heads;
-        mp.Hkv = d->num_kv_heads;
-        mp.G = pl.G;
+        mp.Hkv = d->num_kv_heads / pl.pk;
+        mp.G = pl.G * pl.pk;
         mp.D = d->head_dim;
         mp.cap = d->cap;
         mp.window = d->window;
@@ -1306,7 +1361,12 @@ int esda_decode_raw_workspace_size(const esda_raw_desc *desc, size_t *bytes) {
     esda_decode_desc d;
     int rc = raw_as_decode(desc, &d);
     if (rc) return rc;
-    return esda_decode_workspace_size(&d, bytes);
+    Plan pl;
+    rc = make_plan(&d, &pl, /*allow_pack=*/false);
+    if (rc) return rc;
+    if (!bytes) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_workspace_size: null output");
+    *bytes = pl.bytes;
+    return ESDA_OK;
 }
 
 int esda_decode_raw_stages(const esda_raw_desc *desc, const esda_raw_args *a, int stages, void *stream) {
@@ -1314,7 +1374,7 @@ int esda_decode_raw_stages(const esda_raw_desc *desc, const esda_raw_args *a, in
     int rc = raw_as_decode(desc, &d);
     if (rc) return rc;
     Plan pl;
-    rc = make_plan(&d, &pl);
+    rc = make_plan(&d, &pl, /*allow_pack=*/false);  // the raw rebuild runs 16-row stages of one kv head
     if (rc) return rc;
     if (!a) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw: null arguments");
     if (!a->q || !a->raw_cache || !a->pos || !a->kw || !a->inv_freq || !a->out)
