@@ -856,10 +856,15 @@ void attend_kernel(AttendParams p) {
     };
 
     // This workgroup's share of all visible rows, linearised as (sequence, kv head, row):
-    // [rows_total * wg / W, rows_total * (wg + 1) / W).  It covers one or more segments; the
-    // partial of workgroup wg for pair u = b * Hkv + kvh goes to slot u + wg, so the slots
-    // of one pair are consecutive and distinct pairs never share a slot.
-    const long long lo = udiv64(rows_total * wg, p.W), hi = udiv64(rows_total * (wg + 1), p.W);
+    // [rows_total * wg / Wr, rows_total * (wg + 1) / Wr) with Wr = min(W, rows_total), so
+    // that every share holds at least one row (W is sized from the bound on rows; early in
+    // a long cache fewer rows are visible) and workgroups wg >= Wr have nothing to do.  A
+    // share covers one or more segments; the partial of workgroup wg for pair
+    // u = b * Hkv + kvh goes to slot u + wg, so the slots of one pair are consecutive and
+    // distinct pairs never share a slot.
+    const int Wr = (int) (rows_total < p.W ? rows_total : p.W);
+    if (wg >= Wr) return;
+    const long long lo = udiv64(rows_total * wg, Wr), hi = udiv64(rows_total * (wg + 1), Wr);
     long long x = lo;
     int b = 0;
     while (x < hi) {
@@ -944,9 +949,12 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
         if (n <= 0 || rows_total <= 0) return;
         const long long first = p.table[b] * p.Hkv + (long long) kvh * n, last = first + n - 1;
         if (first < 0 || last >= rows_total) return;  // inconsistent table: read nothing
-        const int w0 = (int) udiv64((first + 1) * p.W - 1, rows_total);
-        const int w1 = (int) udiv64((last + 1) * p.W - 1, rows_total);
-        if (w0 < 0 || w1 >= p.W || w0 > w1) return;
+        // the attend kernel's share count: every one of workgroups w0 .. w1 holds rows of
+        // the pair and wrote its slot
+        const long long Wr = rows_total < p.W ? rows_total : p.W;
+        const int w0 = (int) udiv64((first + 1) * Wr - 1, rows_total);
+        const int w1 = (int) udiv64((last + 1) * Wr - 1, rows_total);
+        if (w0 < 0 || w1 >= Wr || w0 > w1) return;
         ns = w1 - w0 + 1;
         pbase = (size_t) b * p.Hkv + kvh + w0;
     } else {

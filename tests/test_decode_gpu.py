@@ -28,8 +28,8 @@ def _host(t: torch.Tensor) -> np.ndarray:
 
 def run_case(name, *, B, Hq, Hkv, D, cap, pos, window=0, ring=False, shared=False, scale=None,
              row_base=None, seed=0, split_rows=0, head_pad=0, seq_pad=0, peaks=0, bump=4.0,
-             refround=True, max_visible=0):
-    from apertura_amd.decode import DecodeStep, decode_status, decode_step, new_workspace
+             refround=True, max_visible=0, workspace=None):
+    from apertura_amd.decode import DecodeStep, decode_status, decode_step, new_workspace, workspace_bytes
     print(f"\n[case] {name}: B={B} Hq={Hq} Hkv={Hkv} D={D} cap={cap} window={window} "
           f"ring={ring} shared={shared} pos={list(pos)[:4]} split_rows={split_rows}", flush=True)
     scale = D ** -0.5 if scale is None else scale
@@ -50,7 +50,11 @@ def run_case(name, *, B, Hq, Hkv, D, cap, pos, window=0, ring=False, shared=Fals
     vc_d = kc_d if shared else _dev(vc)
     pos_d = torch.tensor(list(pos), dtype=torch.int32, device="cuda")
     rb_d = None if row_base is None else torch.tensor(list(row_base), dtype=torch.int32, device="cuda")
-    ws = new_workspace(dstep, "cuda")
+    if workspace is None:
+        ws = new_workspace(dstep, "cuda")
+    else:
+        assert workspace.numel() >= workspace_bytes(dstep)
+        ws = workspace
     out = decode_step(dstep, q_d.view(B, Hq, D), kn_d.view(B, Hkv, D),
                       None if vn_d is None else vn_d.view(B, Hkv, D), kc_d, vc_d, pos_d, rb_d,
                       workspace=ws)
@@ -138,6 +142,14 @@ EDGE = [
     # end of one (sequence, kv head) and the start of the next
     dict(name="ragged_batch_16", B=16, Hq=32, Hkv=4, D=512, cap=4096, shared=True,
          pos=[int(x) for x in np.random.default_rng(77).integers(16, 4096, 16)]),
+    # fewer visible rows than the plan's workgroups (sized from the cap): every workgroup
+    # share must still hold a row, or a merge would read partials nobody wrote
+    dict(name="balanced_fewer_rows_than_workgroups", B=2, Hq=8, Hkv=4, D=128, cap=8192, pos=[5, 9]),
+    dict(name="balanced_three_tiny_sequences", B=3, Hq=8, Hkv=4, D=256, cap=2048, pos=[0, 1, 3]),
+    # one long pair split over many workgroups, a mid pair over a few and a short one in
+    # one workgroup (written directly)
+    dict(name="balanced_merge_kinds_mixed", B=3, Hq=16, Hkv=2, D=512, cap=60032, shared=True,
+         pos=[60000, 100, 3000]),
     dict(name="many_tiny_sequences", B=64, Hq=8, Hkv=2, D=128, cap=64,
          pos=[int(x) for x in np.random.default_rng(78).integers(0, 64, 64)]),
     dict(name="max_batch_256", B=256, Hq=4, Hkv=1, D=256, cap=48, window=32, ring=True,
@@ -166,6 +178,27 @@ def test_huge_logit_gap_does_not_overflow(D):
     for seed in (31, 32, 33):
         run_case(f"huge-gap-{seed}", B=1, Hq=32, Hkv=8, D=D, cap=2048, pos=[2047], shared=False,
                  peaks=3, bump=200.0, seed=seed, split_rows=64, refround=False)
+
+
+def test_one_workspace_across_plans():
+    """One workspace serves steps of different shapes in turn, as the cache layer's single
+    workspace serves every layer: no plan may depend on what another left in it."""
+    from apertura_amd.decode import DecodeStep, workspace_bytes
+    shapes = [
+        dict(name="ws-ring-b8", B=8, Hq=32, Hkv=16, D=256, cap=1024, window=1024, ring=True,
+             pos=[3000 + 111 * i for i in range(8)], scale=1 / 16, seed=41),
+        dict(name="ws-balanced", B=4, Hq=32, Hkv=4, D=512, cap=3000, shared=True,
+             pos=[2999, 40, 1500, 700], seed=42),
+        dict(name="ws-grid-b1", B=1, Hq=16, Hkv=8, D=256, cap=1024, window=1024, pos=[1023], seed=43),
+    ]
+    need = max(workspace_bytes(DecodeStep(batch=c["B"], num_q_heads=c["Hq"], num_kv_heads=c["Hkv"],
+                                          head_dim=c["D"], cap=c["cap"], window=c.get("window", 0),
+                                          ring=c.get("ring", False), kv_shared=c.get("shared", False),
+                                          scale=1.0, seq_stride=c["Hkv"] * c["cap"] * c["D"],
+                                          head_stride=c["cap"] * c["D"])) for c in shapes)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    for c in shapes + shapes[::-1] + shapes:
+        run_case(**c, workspace=ws)
 
 
 def test_split_count_does_not_change_result_beyond_rounding():
