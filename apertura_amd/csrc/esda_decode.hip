@@ -931,6 +931,37 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
 // block-wide max.
 constexpr int kMergeRegs = 8;  // splits per thread held in registers (S <= 64 in one pass)
 
+// The splits that hold partials of pair (b, kvh): their count ns (0 when the sequence
+// is skipped) and the slot of the first, as the attend kernel laid them out.
+__device__ __forceinline__ int pair_splits(const MergeParams &p, int b, int kvh, size_t &pbase) {
+    int ns;
+    if (p.balanced) {
+        // The attend workgroups that covered pair (b, kvh): those holding its first and
+        // last rows in the linearised (sequence, kv head, row) order, each range
+        // [rows_total * w / Wr, rows_total * (w + 1) / Wr).
+        const long long n = p.table[b + 1] - p.table[b];
+        const long long rows_total = p.table[p.B] * p.Hkv;
+        if (n <= 0 || rows_total <= 0) return 0;
+        const long long first = p.table[b] * p.Hkv + (long long) kvh * n, last = first + n - 1;
+        if (first < 0 || last >= rows_total) return 0;  // inconsistent table: read nothing
+        // the attend kernel's share count: every one of workgroups w0 .. w1 holds rows of
+        // the pair and wrote its slot
+        const long long Wr = rows_total < p.W ? rows_total : p.W;
+        const int w0 = (int) udiv64((first + 1) * Wr - 1, rows_total);
+        const int w1 = (int) udiv64((last + 1) * Wr - 1, rows_total);
+        if (w0 < 0 || w1 >= Wr || w0 > w1) return 0;
+        ns = w1 - w0 + 1;
+        pbase = (size_t) b * p.Hkv + kvh + w0;
+    } else {
+        const SeqView sv = seq_view(p.pos[b], p.row_base ? p.row_base[b] : 0, p.cap, p.window, p.ring);
+        if (!sv.ok) return 0;
+        ns = (sv.nvis + p.chunk - 1) / p.chunk;
+        if (ns > p.S) ns = p.S;
+        pbase = ((size_t) b * p.Hkv + kvh) * p.S;
+    }
+    return ns;
+}
+
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
     __shared__ float red[kMergeThreads / 64];
     __shared__ f32x4 part[kMergeGroups][kMergeDims / 4];
@@ -938,32 +969,8 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
     const int h = blockIdx.y, b = blockIdx.z;
     const int kvh = h / p.G, g = h % p.G;
     const int tid = threadIdx.x;
-    int ns;
     size_t pbase;
-    if (p.balanced) {
-        // The attend workgroups that covered pair (b, kvh): those holding its first and
-        // last rows in the linearised (sequence, kv head, row) order, each range
-        // [rows_total * w / W, rows_total * (w + 1) / W).
-        const long long n = p.table[b + 1] - p.table[b];
-        const long long rows_total = p.table[p.B] * p.Hkv;
-        if (n <= 0 || rows_total <= 0) return;
-        const long long first = p.table[b] * p.Hkv + (long long) kvh * n, last = first + n - 1;
-        if (first < 0 || last >= rows_total) return;  // inconsistent table: read nothing
-        // the attend kernel's share count: every one of workgroups w0 .. w1 holds rows of
-        // the pair and wrote its slot
-        const long long Wr = rows_total < p.W ? rows_total : p.W;
-        const int w0 = (int) udiv64((first + 1) * Wr - 1, rows_total);
-        const int w1 = (int) udiv64((last + 1) * Wr - 1, rows_total);
-        if (w0 < 0 || w1 >= Wr || w0 > w1) return;
-        ns = w1 - w0 + 1;
-        pbase = (size_t) b * p.Hkv + kvh + w0;
-    } else {
-        const SeqView sv = seq_view(p.pos[b], p.row_base ? p.row_base[b] : 0, p.cap, p.window, p.ring);
-        if (!sv.ok) return;
-        ns = (sv.nvis + p.chunk - 1) / p.chunk;
-        if (ns > p.S) ns = p.S;
-        pbase = ((size_t) b * p.Hkv + kvh) * p.S;
-    }
+    const int ns = pair_splits(p, b, kvh, pbase);
     if (ns <= 1) return;  // one workgroup covered the pair and wrote the output itself
     const int dq = tid & 31, sg = tid >> 5;
     const int d0 = blockIdx.x * kMergeDims + dq * 4;
@@ -1029,6 +1036,62 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
         for (int e = 0; e < 4; ++e) r[e] = (__bf16) (t[e] * inv);
         *reinterpret_cast<uint2 *>(dst) = __builtin_bit_cast(uint2, r);
     }
+}
+
+// Merge for pairs of few splits (balanced shares): one thread per (sequence,
+// query head, 4 output dims), no barriers.  Splits are read 8 at a time -- the loads of
+// a chunk issue together, so up to 8 splits cost one memory round trip -- with the
+// running max raised per chunk (same result as merge_kernel up to summation order).
+constexpr int kMergeRowsThreads = 256;
+constexpr int kMergeRowsChunk = 8;
+
+__global__ __launch_bounds__(kMergeRowsThreads) void merge_rows_kernel(MergeParams p) {
+    const int D4 = p.D / 4;
+    const int t = blockIdx.x * kMergeRowsThreads + threadIdx.x;
+    const int b = blockIdx.y;
+    if (t >= p.Hq * D4) return;
+    const int h = t / D4, d4 = t - (t / D4) * D4;
+    const int kvh = h / p.G, g = h % p.G;
+    size_t pbase;
+    const int ns = pair_splits(p, b, kvh, pbase);
+    if (ns <= 1) return;  // written by the attend kernel, or skipped
+    float mx = -INFINITY, lt = 0.0f;
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < ns; s0 += kMergeRowsChunk) {
+        float mv[kMergeRowsChunk], lv[kMergeRowsChunk];
+        f32x4 av[kMergeRowsChunk];
+#pragma unroll
+        for (int u = 0; u < kMergeRowsChunk; ++u) {
+            mv[u] = -INFINITY;
+            lv[u] = 0.0f;
+            av[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (s0 + u < ns) {
+                const size_t ix = (pbase + s0 + u) * p.G + g;
+                mv[u] = p.part_ml[ix * 2];
+                lv[u] = p.part_ml[ix * 2 + 1];
+                av[u] = *reinterpret_cast<const f32x4 *>(p.part_acc + ix * p.D + d4 * 4);
+            }
+        }
+        float cm = mv[0];
+#pragma unroll
+        for (int u = 1; u < kMergeRowsChunk; ++u) cm = fmaxf(cm, mv[u]);
+        const float mn = fmaxf(mx, cm);
+        const float c = __builtin_amdgcn_exp2f(mx - mn);  // 0 on the first chunk
+        o *= c;
+        lt *= c;
+#pragma unroll
+        for (int u = 0; u < kMergeRowsChunk; ++u) {
+            const float w = __builtin_amdgcn_exp2f(mv[u] - mn);  // 0 for absent splits
+            o += av[u] * w;
+            lt += lv[u] * w;
+        }
+        mx = mn;
+    }
+    const float inv = 1.0f / lt;
+    bf16x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = (__bf16) (o[e] * inv);
+    *reinterpret_cast<uint2 *>(p.out + ((size_t) b * p.Hq + h) * p.D + d4 * 4) = __builtin_bit_cast(uint2, r);
 }
 
 __global__ void fill_i32_kernel(int *dst, int value, int n) {
@@ -1300,8 +1363,18 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         mp.W = pl.W;
         mp.S = pl.S;
         mp.chunk = pl.chunk;
-        dim3 grid(d->head_dim / kMergeDims, d->num_q_heads, d->batch);
-        hipLaunchKernelGGL(merge_kernel, grid, dim3(kMergeThreads), 0, st, mp);
+        if (pl.balanced) {
+            // Balanced shares give each pair a few splits: thread-per-output merge (C5's
+            // global layers: 11 -> 4.4 us).  Grids keep merge_kernel, whose workgroups
+            // reduce 8 splits side by side (at C1's 16 splits over 8 pairs the rows
+            // kernel would run 4 workgroups and two round trips: 9.0 -> 11.8 us a step).
+            const int threads = d->num_q_heads * (d->head_dim / 4);
+            dim3 grid((threads + kMergeRowsThreads - 1) / kMergeRowsThreads, d->batch);
+            hipLaunchKernelGGL(merge_rows_kernel, grid, dim3(kMergeRowsThreads), 0, st, mp);
+        } else {
+            dim3 grid(d->head_dim / kMergeDims, d->num_q_heads, d->batch);
+            hipLaunchKernelGGL(merge_kernel, grid, dim3(kMergeThreads), 0, st, mp);
+        }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e, "merge_kernel launch");
     }
