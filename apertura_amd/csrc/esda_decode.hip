@@ -308,13 +308,17 @@ __device__ __forceinline__ float bf16_hi(unsigned w) { return __builtin_bit_cast
 // The new token's row is copied from k_new/v_new into the cache by the workgroup whose
 // split ends at it (bit-exact copy); that workgroup's own loads read the row from
 // k_new/v_new and no other workgroup reads it, so the copy needs no ordering.
-template <int D, bool SHARED, int NW, bool RAW>
+// RPK (raw mode): kv heads per workgroup, 1 or 2 (the host's pk).  With 2, a stage holds 8
+// rows of each of two kv heads of one sequence at the same 8 positions, so the cos/sin
+// table of a stage has 8 rows instead of 16: half the table work per stage.
+template <int D, bool SHARED, int NW, bool RAW, int RPK = 1>
 // The LDS ring allows one workgroup per CU, i.e. NW/4 waves per SIMD: telling the
 // compiler so lifts the register limit it would otherwise keep for higher occupancy,
 // which it meets by serialising LDS reads behind their uses.
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void attend_kernel(AttendParams p) {
     static_assert(!RAW || (D == kRawDim && SHARED && (NW == 4 || NW == 8)), "raw mode: one 512-dim stream, 4 or 8 waves");
+    static_assert(RPK == 1 || (RAW && RPK == 2), "kv-head packing is a runtime choice outside raw mode");
     using R = Ring<D, SHARED, NW, RAW ? raw_extra_lds(NW) : 0>;
     constexpr int NS = R::NS, DW = R::DW, KKW = R::KKW, DTW = R::DTW;
     // Stages between the one being accumulated and the newest one that must have landed.
@@ -354,8 +358,10 @@ void attend_kernel(AttendParams p) {
     auto *xtab = reinterpret_cast<unsigned (*)[16][kTabStride]>(rawlds + 3 * 16 * NW * 4);
     // xr[stage % 2][0][row] = rinv, xr[stage % 2][1][row] = 1 / rinv
     auto *xr = reinterpret_cast<float (*)[2][16]>(rawlds + 3 * 16 * NW * 4 + 2 * 16 * kTabStride * 4);
-    // cos/sin table entries per thread per stage (16 rows x 64 pairs over 64*NW threads)
-    constexpr int EPT = 1024 / (64 * NW);
+    // cos/sin table of a stage: TR rows (one per position) x 64 pairs over 64*NW threads
+    constexpr int TR = 16 / RPK;
+    constexpr int EPT = TR * 64 / (64 * NW);
+    static_assert(EPT >= 1, "every thread computes at least one table entry");
     constexpr int TPR = 64 / EPT;  // threads per table row
 
     const int wg = blockIdx.x;
@@ -521,7 +527,7 @@ void attend_kernel(AttendParams p) {
     auto publish_tab = [&](int st, int buf) {
         if constexpr (RAW) {
             const int row = tid / TPR;
-            const float t = (float) (sv.first + j0 + st * 16 + row);
+            const float t = (float) (sv.first + j0 + st * TR + row);
             unsigned w[EPT];
 #pragma unroll
             for (int e = 0; e < EPT; ++e) {
@@ -530,10 +536,13 @@ void attend_kernel(AttendParams p) {
                 w[e] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{c, s}, bf16x2));
             }
             unsigned *dst = &xtab[buf][row][EPT * (tid % TPR)];
+            static_assert(EPT == 1 || EPT == 2 || EPT == 4, "table entries per thread");
             if constexpr (EPT == 4) {
                 *reinterpret_cast<u32x4 *>(dst) = u32x4{w[0], w[1], w[2], w[3]};
-            } else {
+            } else if constexpr (EPT == 2) {
                 *reinterpret_cast<uint2 *>(dst) = uint2{w[0], w[1]};
+            } else {
+                *dst = w[0];
             }
         }
     };
@@ -568,7 +577,7 @@ void attend_kernel(AttendParams p) {
             if (wave < 2) {
                 // chunk `wave` (k-step 0) holds dims d = 32*wave + 8lg + e < 64; chunk wave + 8
                 // (k-step KP) their rotary partners.
-                const unsigned *tb = &xtab[tabbuf][li][32 * wave + 8 * lg];
+                const unsigned *tb = &xtab[tabbuf][li & (TR - 1)][32 * wave + 8 * lg];
                 const u32x4 t0 = *reinterpret_cast<const u32x4 *>(tb);
                 const u32x4 t1 = *reinterpret_cast<const u32x4 *>(tb + 4);
     #pragma unroll
@@ -929,7 +938,9 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
 // lanes.  Each thread issues its partial loads together with the (m, l) loads, so the
 // whole merge is one memory round trip; the per-split weights are then formed from the
 // block-wide max.
-constexpr int kMergeRegs = 8;  // splits per thread held in registers (S <= 64 in one pass)
+// REGS: splits per thread held in registers (S <= 8 * REGS in one pass): 8, or 16 for
+// the raw-K C4 shape, which packs two kv heads into 128 splits (the larger register set
+// costs the 64-split merges ~0.6 us).
 
 // The splits that hold partials of pair (b, kvh): their count ns (0 when the sequence
 // is skipped) and the slot of the first, as the attend kernel laid them out.
@@ -962,6 +973,7 @@ __device__ __forceinline__ int pair_splits(const MergeParams &p, int b, int kvh,
     return ns;
 }
 
+template <int REGS>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
     __shared__ float red[kMergeThreads / 64];
     __shared__ f32x4 part[kMergeGroups][kMergeDims / 4];
@@ -976,13 +988,13 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
     const int d0 = blockIdx.x * kMergeDims + dq * 4;
 
     float mloc = -INFINITY;
-    float ms[kMergeRegs], ls[kMergeRegs];
-    f32x4 av[kMergeRegs];
-    // Fast path: every split this thread owns fits in registers (ns <= 64).
-    const bool in_regs = ns <= kMergeGroups * kMergeRegs;
+    float ms[REGS], ls[REGS];
+    f32x4 av[REGS];
+    // Fast path: every split this thread owns fits in registers.
+    const bool in_regs = ns <= kMergeGroups * REGS;
     if (in_regs) {
 #pragma unroll
-        for (int u = 0; u < kMergeRegs; ++u) {
+        for (int u = 0; u < REGS; ++u) {
             const int s = sg + u * kMergeGroups;
             if (s < ns) {
                 const size_t ix = (pbase + s) * p.G + g;
@@ -1005,7 +1017,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
     float lt = 0.0f;
     if (in_regs) {
 #pragma unroll
-        for (int u = 0; u < kMergeRegs; ++u) {
+        for (int u = 0; u < REGS; ++u) {
             const float w = __builtin_amdgcn_exp2f(ms[u] - mx);  // 0 for absent splits
             o += av[u] * w;
             lt += ls[u] * w;
@@ -1182,7 +1194,9 @@ int choose_pack(const esda_decode_desc *d, int G, long long S) {
     return pk;
 }
 
-int make_plan(const esda_decode_desc *d, Plan *pl, bool allow_pack = true) {
+// raw: the raw-K kernel packs two kv heads whenever their query heads fit the MFMA's N
+// dimension (their rows share positions, so they share the stage's cos/sin table).
+int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
     if (!d) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: null description");
     if (d->batch <= 0 || d->num_q_heads <= 0 || d->num_kv_heads <= 0)
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: batch and head counts must be positive");
@@ -1207,10 +1221,15 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool allow_pack = true) {
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: split_rows must be a multiple of 16");
     int bound = d->ring ? d->window : (d->window > 0 ? std::min(d->window, d->cap) : d->cap);
     int maxvis = d->max_visible > 0 ? std::min(d->max_visible, bound) : bound;
-    // Work split.  Sizing uses the upper bound on rows (the kernels see the real ones).
+    pl->pk = 1;
+    if (raw && G * 2 <= kMaxGroup && d->num_kv_heads % 2 == 0 &&
+        (long long) d->head_stride * 2 * 2 + 16LL * d->head_dim * 2 < (1LL << 31))
+        pl->pk = 2;
+    // Work split.  Sizing uses the upper bound on rows (the kernels see the real ones),
+    // counted per packed kv head (a row of a pk-packed head is pk cache rows).
     // Automatic: about one workgroup per CU, no fewer than 64 rows each; split_rows > 0
     // asks for that many rows per workgroup.
-    const long long rows_max = (long long) maxvis * d->batch * d->num_kv_heads;
+    const long long rows_max = (long long) maxvis * d->batch * (d->num_kv_heads / pl->pk);
     const long long per = d->split_rows > 0 ? d->split_rows : kMinRows;
     // Several full-causal sequences have ragged lengths: workgroups then take balanced
     // shares of all rows (the kernel scans the lengths).  Otherwise (one sequence, or
@@ -1219,7 +1238,6 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool allow_pack = true) {
     pl->balanced = d->batch > 1 && !d->ring;
     pl->G = G;
     pl->maxvis = maxvis;
-    pl->pk = 1;
     size_t slots;
     if (pl->balanced) {
         long long W = (rows_max + per - 1) / per;
@@ -1228,7 +1246,7 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool allow_pack = true) {
         if (W < 1) W = 1;
         pl->W = (int) W;
         pl->S = pl->chunk = 0;
-        slots = (size_t) d->batch * d->num_kv_heads + (size_t) W;  // pair u's partial from workgroup w at u + w
+        slots = (size_t) d->batch * (d->num_kv_heads / pl->pk) + (size_t) W;  // pair u's partial from workgroup w at u + w
     } else {
         long long chunk = d->split_rows;
         if (chunk == 0) {
@@ -1246,7 +1264,7 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool allow_pack = true) {
         pl->W = 0;
         pl->S = (int) S;
         pl->chunk = (int) chunk;
-        if (allow_pack && d->split_rows == 0) pl->pk = choose_pack(d, G, S);
+        if (!raw && d->split_rows == 0) pl->pk = choose_pack(d, G, S);
         slots = (size_t) d->batch * (d->num_kv_heads / pl->pk) * S;
     }
     const size_t parts = slots * G * pl->pk;
@@ -1269,10 +1287,10 @@ constexpr int ring_waves() { return D == 256 ? 8 : 4; }
 // reconstruction work.
 constexpr int kRawWaves = 8;
 
-template <int D, bool SHARED, bool RAW = false>
+template <int D, bool SHARED, bool RAW = false, int RPK = 1>
 hipError_t launch_attend(const AttendParams &ap, dim3 grid, hipStream_t st) {
     constexpr int NW = RAW ? kRawWaves : ring_waves<D>();
-    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW>), grid, dim3(64 * NW), 0, st, ap);
+    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW, RPK>), grid, dim3(64 * NW), 0, st, ap);
     return hipGetLastError();
 }
 
@@ -1338,8 +1356,9 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         ap.scale_log2e = d->scale * kLog2e;
         ap.out = out;
         const dim3 grid = pl.balanced ? dim3(pl.W) : dim3(pl.S, d->num_kv_heads / pl.pk, d->batch);
-        hipError_t e = raw ? launch_attend<kRawDim, true, true>(ap, grid, st)
-                           : dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
+        hipError_t e = !raw            ? dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st)
+                       : pl.pk == 2    ? launch_attend<kRawDim, true, true, 2>(ap, grid, st)
+                                       : launch_attend<kRawDim, true, true, 1>(ap, grid, st);
         if (e != hipSuccess) return hip_fail(e, "attend_kernel launch");
     }
     // One split per pair: the attend workgroups wrote every output themselves.
@@ -1373,7 +1392,10 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
             hipLaunchKernelGGL(merge_rows_kernel, grid, dim3(kMergeRowsThreads), 0, st, mp);
         } else {
             dim3 grid(d->head_dim / kMergeDims, d->num_q_heads, d->batch);
-            hipLaunchKernelGGL(merge_kernel, grid, dim3(kMergeThreads), 0, st, mp);
+            if (pl.S <= kMergeGroups * 8)
+                hipLaunchKernelGGL(merge_kernel<8>, grid, dim3(kMergeThreads), 0, st, mp);
+            else
+                hipLaunchKernelGGL(merge_kernel<16>, grid, dim3(kMergeThreads), 0, st, mp);
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e, "merge_kernel launch");
@@ -1443,7 +1465,7 @@ int esda_decode_raw_workspace_size(const esda_raw_desc *desc, size_t *bytes) {
     int rc = raw_as_decode(desc, &d);
     if (rc) return rc;
     Plan pl;
-    rc = make_plan(&d, &pl, /*allow_pack=*/false);
+    rc = make_plan(&d, &pl, /*raw=*/true);
     if (rc) return rc;
     if (!bytes) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_workspace_size: null output");
     *bytes = pl.bytes;
@@ -1455,7 +1477,7 @@ int esda_decode_raw_stages(const esda_raw_desc *desc, const esda_raw_args *a, in
     int rc = raw_as_decode(desc, &d);
     if (rc) return rc;
     Plan pl;
-    rc = make_plan(&d, &pl, /*allow_pack=*/false);  // the raw rebuild runs 16-row stages of one kv head
+    rc = make_plan(&d, &pl, /*raw=*/true);
     if (rc) return rc;
     if (!a) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw: null arguments");
     if (!a->q || !a->raw_cache || !a->pos || !a->kw || !a->inv_freq || !a->out)

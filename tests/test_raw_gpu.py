@@ -97,6 +97,16 @@ def test_raw_batched_ragged_positions():
     run_raw("batched", B=3, cap=4096, pos=[17, 2500, 4095], scale=512 ** -0.5, seed=7)
 
 
+def test_raw_unpacked_odd_kv_heads():
+    """Three kv heads cannot pair up: one kv head per workgroup (16 rows per stage)."""
+    run_raw("unpacked-hkv3", B=2, Hq=24, Hkv=3, cap=1024, pos=[1000, 333], scale=512 ** -0.5, seed=19)
+
+
+def test_raw_unpacked_single_kv_head():
+    """One kv head (8 query heads, the reference kernel's group): nothing to pair with."""
+    run_raw("unpacked-hkv1", Hq=8, Hkv=1, cap=1500, pos=[1499], scale=512 ** -0.5, seed=21)
+
+
 def test_raw_no_append_reads_cached_rows():
     run_raw("no-append", cap=2048, pos=[1500], append=False, seed=9)
 
