@@ -25,12 +25,17 @@ EXPORTS = (
     "esda_decode_raw_stages", "esda_fill_i32", "esda_last_error", "esda_version",
     # include/esda_cache.h
     "esda_cache_create", "esda_cache_destroy", "esda_cache_update", "esda_cache_update_raw",
-    "esda_cache_current", "esda_cache_decode", "esda_cache_decode_raw", "esda_cache_slot",
+    "esda_cache_current", "esda_cache_current_raw", "esda_cache_decode", "esda_cache_decode_raw", "esda_cache_slot",
     "esda_cache_seq_len", "esda_cache_mark_step", "esda_cache_reset", "esda_cache_save_snapshot",
-    "esda_cache_restore_snapshot", "esda_cache_mark_rewind_point", "esda_cache_rewind_to_mark",
+    "esda_cache_restore_snapshot", "esda_cache_restore_snapshot_ex", "esda_cache_mark_prefix",
+    "esda_cache_mark_rewind_point", "esda_cache_rewind_to_mark", "esda_cache_clear_rewind_mark",
     "esda_decode_attn_global",
 )
-_VOID = ("esda_cache_destroy", "esda_cache_mark_step", "esda_cache_reset")
+_VOID = ("esda_cache_destroy", "esda_cache_mark_step", "esda_cache_reset", "esda_cache_clear_rewind_mark")
+
+# const char *(*)(int32_t pos, void *user): the caller's prefix fingerprint at a marker
+# (declared returning void *: the callback hands back the address of a buffer it keeps alive)
+PREFIX_FP_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p)
 
 
 class EsdaError(RuntimeError):
@@ -120,6 +125,7 @@ def lib() -> ctypes.CDLL:
         L.esda_cache_update.argtypes = [P, i32, P, P, i32, i32, i32, i32, i32, P, VP, VP]
         L.esda_cache_update_raw.argtypes = [P, i32, P, i32, i32, i32, i32, P, VP, pi32, pi32]
         L.esda_cache_current.argtypes = [P, i32, i32, VP, VP]
+        L.esda_cache_current_raw.argtypes = [P, i32, VP, pi32, pi32]
         L.esda_cache_decode.argtypes = [P, i32, P, i32, P, P, i32, i32, i32, f32, P, P]
         L.esda_cache_decode_raw.argtypes = [P, i32, P, i32, P, i32, P, f32, P, i32, P, P]
         L.esda_cache_slot.argtypes = [P, i32, pi32, pi32, pi32, pi32]
@@ -128,6 +134,9 @@ def lib() -> ctypes.CDLL:
         L.esda_cache_reset.argtypes = [P]
         L.esda_cache_save_snapshot.argtypes = [P, ctypes.c_char_p, ctypes.c_char_p, i32]
         L.esda_cache_restore_snapshot.argtypes = [P, ctypes.c_char_p, ctypes.c_char_p]
+        L.esda_cache_restore_snapshot_ex.argtypes = [P, ctypes.c_char_p, ctypes.c_char_p, i32, PREFIX_FP_FN, P]
+        L.esda_cache_mark_prefix.argtypes = [P, i32, ctypes.c_char_p]
+        L.esda_cache_clear_rewind_mark.argtypes = [P]
         L.esda_cache_mark_rewind_point.argtypes = [P, i32]
         L.esda_cache_rewind_to_mark.argtypes = [P]
         L.esda_decode_attn_global.argtypes = [P, i32, P, i32, i32, i32, P, f32, P, i32, P, P]

@@ -23,6 +23,7 @@ SOURCES = [
     "esda_decode.hip",
     "es/ESKVCache.cpp",
     "es/ESDecodeAttn.cpp",
+    "es/ESSnapshot.cpp",
     "es/es_capi.cpp",
 ]
 

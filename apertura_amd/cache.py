@@ -107,6 +107,12 @@ class ESKVCache:
         check(lib().esda_cache_current(self._h, layer, 1 if prealloc else 0, ctypes.byref(kv), ctypes.byref(vv)))
         return CacheView.of(kv), CacheView.of(vv)
 
+    def current_raw(self, layer: int):
+        """(view, len, pitch) of a prealloc raw-K slot without appending."""
+        v, ln, pitch = View(), ctypes.c_int32(), ctypes.c_int32()
+        check(lib().esda_cache_current_raw(self._h, layer, ctypes.byref(v), ctypes.byref(ln), ctypes.byref(pitch)))
+        return CacheView.of(v), int(ln.value), int(pitch.value)
+
     def decode(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, max_keep: int,
                scale: float, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
         """Fused append + attention of one decode step; v_new may be k_new itself
@@ -155,18 +161,38 @@ class ESKVCache:
     def reset(self) -> None:
         lib().esda_cache_reset(self._h)
 
-    # Not implemented by the library: the reference's failure values.
+    # Persistence and rewind (ESKVCache.h:102-174).
+    RAW_MODES = {"composite": 0, "raw": 1, "rawQ8": 2, "asStored": 3}
+
     def save_snapshot(self, path: str, fingerprint: str, pos: int) -> bool:
         return bool(lib().esda_cache_save_snapshot(self._h, path.encode(), fingerprint.encode(), pos))
 
-    def restore_snapshot(self, path: str, fingerprint: str) -> int:
-        return lib().esda_cache_restore_snapshot(self._h, path.encode(), fingerprint.encode())
+    def restore_snapshot(self, path: str, fingerprint: str, mode: str = "asStored", prefix_fp=None) -> int:
+        """Restored position or -1.  prefix_fp(pos) -> the caller's prefix fingerprint at a
+        marker position ("" = none)."""
+        from ._lib import PREFIX_FP_FN
+        keep = []
+
+        def cb(pos, _user):
+            buf = ctypes.create_string_buffer((prefix_fp(int(pos)) or "").encode())
+            keep.append(buf)  # alive until the restore returns
+            return ctypes.addressof(buf)
+
+        fn = PREFIX_FP_FN(cb) if prefix_fp is not None else PREFIX_FP_FN()
+        return lib().esda_cache_restore_snapshot_ex(self._h, path.encode(), fingerprint.encode(),
+                                                    self.RAW_MODES[mode], fn, None)
+
+    def mark_prefix(self, pos: int, fingerprint: str) -> None:
+        check(lib().esda_cache_mark_prefix(self._h, pos, fingerprint.encode()))
 
     def mark_rewind_point(self, pos: int) -> bool:
         return bool(lib().esda_cache_mark_rewind_point(self._h, pos))
 
     def rewind_to_mark(self) -> int:
         return lib().esda_cache_rewind_to_mark(self._h)
+
+    def clear_rewind_mark(self) -> None:
+        lib().esda_cache_clear_rewind_mark(self._h)
 
 
 def es_decode_attn_global(q: torch.Tensor, raw_buf: torch.Tensor, length: int, pitch: int, kw: torch.Tensor,

@@ -198,6 +198,13 @@ std::pair<Tensor, Tensor> ESKVCache::current(int layer, bool prealloc) const {
     return {liveView(*s.k, s.start, s.len), liveView(*s.v, s.start, s.len)};
 }
 
+ESKVCache::Raw ESKVCache::currentRaw(int layer) const {
+    checkLayer(layer);
+    const Slot &s = slots_[layer];
+    if (!s.k || s.v) throw std::runtime_error("ESKVCache::currentRaw: layer holds no raw rows");
+    return {liveView(*s.k, s.start, s.len), *s.k, s.len, (int) s.k->shape[1]};
+}
+
 ESKVCache::Raw ESKVCache::updateRaw(int layer, const Tensor &kNew, bool prealloc, hipStream_t st) {
     checkLayer(layer);
     checkRows(kNew, "ESKVCache::updateRaw kNew");
@@ -398,27 +405,12 @@ Tensor ESKVCache::decodeRaw(int layer, const Tensor &q, const Tensor &kNew, cons
     return o;
 }
 
-void ESKVCache::markPrefix(int pos, const std::string &) {
-    if (pos < 4096)
-        throw std::invalid_argument("ESKVCache::markPrefix: marker positions below 4096 unsupported");
-    // Prefix markers feed the snapshot format, which this library does not implement.
-}
-
-bool ESKVCache::saveSnapshot(const std::string &, const std::string &, int) const { return false; }
-
-int ESKVCache::restoreSnapshot(const std::string &, const std::string &, RawMode,
-                               const std::function<std::string(int)> &) {
-    return -1;
-}
-
-bool ESKVCache::markRewindPoint(int) { return false; }
-
-int ESKVCache::rewindToMark() { return -1; }
-
 void ESKVCache::reset() {
     for (auto &a : k_) a.reset();
     for (auto &a : v_) a.reset();
     for (auto &s : slots_) s = Slot{};
+    markers_.clear();
+    rewindMark_.reset();
     seqLen_ = 0;
 }
 

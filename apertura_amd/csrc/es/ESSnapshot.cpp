@@ -1,0 +1,709 @@
+// ESSnapshot.cpp -- KV snapshot persistence, prefix markers and in-memory turn rewind for
+// es::ESKVCache (Apertura ESKVCache.mm:121-456, ESKVCache.h:102-174).
+//
+// File format: safetensors, the layout the reference writes through mx::save_safetensors:
+// an 8-byte little-endian header length N, N bytes of JSON ({"__metadata__": {string:
+// string}, "<name>": {"dtype", "shape", "data_offsets": [begin, end]}}), then the bytes the
+// offsets index (row-major).  Tensors: k_<i> / v_<i> ([kvHeads, live rows, headDim] bf16;
+// raw-K layers k_<i> only); q8 raw layers rq_<i> (u8) + rs_<i> / rb_<i> (f32 [kvHeads, rows,
+// 1]); marker windows m<j>_k_<i> / m<j>_v_<i>.  Metadata: fingerprint, pos, layers,
+// marker_count, marker_<j>_pos, marker_<j>_fp; this library adds shared_<i> = "1" for a
+// layer whose V is its K buffer (attention_k_eq_v decode), written as two equal tensors so
+// that the reference's reader sees an ordinary k/v layer.
+//
+// Device <-> host copies are synchronous: snapshots and marks are rare, and each begins
+// with a device-wide synchronisation so that appends queued on any stream have landed.
+#include "es/ESKVCache.h"
+
+#include <algorithm>
+#include <cerrno>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace es {
+namespace {
+
+void hipOk(hipError_t e, const char *what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int chunkUp(int n) {
+    return (n + ESKVCache::kGrowChunk - 1) / ESKVCache::kGrowChunk * ESKVCache::kGrowChunk;
+}
+
+// ------------------------------------------------------------------ safetensors I/O
+
+struct StTensor {
+    std::string dtype;             // "BF16", "F32", "U8", ...
+    std::vector<int64_t> shape;
+    std::vector<uint8_t> bytes;    // row-major payload
+};
+
+size_t stDtypeSize(const std::string &d) {
+    if (d == "BF16" || d == "F16" || d == "I16" || d == "U16") return 2;
+    if (d == "F32" || d == "I32" || d == "U32") return 4;
+    if (d == "F64" || d == "I64" || d == "U64") return 8;
+    if (d == "U8" || d == "I8" || d == "BOOL" || d == "F8_E4M3" || d == "F8_E5M2") return 1;
+    return 0;
+}
+
+// The subset of JSON a safetensors header uses: objects, arrays, strings, integers (and,
+// for robustness, other numbers, true / false / null).
+struct Json {
+    enum Kind { Null, Bool, Int, Num, Str, Arr, Obj } kind = Null;
+    int64_t i = 0;
+    std::string s;
+    std::vector<Json> arr;
+    std::vector<std::pair<std::string, Json>> obj;
+    const Json *get(const std::string &key) const {
+        for (const auto &kv : obj)
+            if (kv.first == key) return &kv.second;
+        return nullptr;
+    }
+};
+
+class JsonReader {
+public:
+    JsonReader(const char *b, const char *e) : p_(b), e_(e) {}
+    bool parse(Json &out) {
+        if (!value(out, 0)) return false;
+        ws();
+        return p_ == e_;
+    }
+
+private:
+    const char *p_, *e_;
+    void ws() {
+        while (p_ < e_ && (*p_ == ' ' || *p_ == '\t' || *p_ == '\n' || *p_ == '\r')) ++p_;
+    }
+    bool lit(const char *w) {
+        const size_t n = std::strlen(w);
+        if ((size_t) (e_ - p_) < n || std::strncmp(p_, w, n) != 0) return false;
+        p_ += n;
+        return true;
+    }
+    static void utf8(std::string &o, unsigned c) {
+        if (c < 0x80) {
+            o += (char) c;
+        } else if (c < 0x800) {
+            o += (char) (0xC0 | (c >> 6));
+            o += (char) (0x80 | (c & 0x3F));
+        } else if (c < 0x10000) {
+            o += (char) (0xE0 | (c >> 12));
+            o += (char) (0x80 | ((c >> 6) & 0x3F));
+            o += (char) (0x80 | (c & 0x3F));
+        } else {
+            o += (char) (0xF0 | (c >> 18));
+            o += (char) (0x80 | ((c >> 12) & 0x3F));
+            o += (char) (0x80 | ((c >> 6) & 0x3F));
+            o += (char) (0x80 | (c & 0x3F));
+        }
+    }
+    bool hex4(unsigned &c) {
+        if (e_ - p_ < 4) return false;
+        c = 0;
+        for (int k = 0; k < 4; ++k) {
+            const char h = *p_++;
+            c <<= 4;
+            if (h >= '0' && h <= '9') c |= (unsigned) (h - '0');
+            else if (h >= 'a' && h <= 'f') c |= (unsigned) (h - 'a' + 10);
+            else if (h >= 'A' && h <= 'F') c |= (unsigned) (h - 'A' + 10);
+            else return false;
+        }
+        return true;
+    }
+    bool str(std::string &o) {
+        if (p_ >= e_ || *p_ != '"') return false;
+        ++p_;
+        while (p_ < e_ && *p_ != '"') {
+            const char c = *p_++;
+            if ((unsigned char) c < 0x20) return false;
+            if (c != '\\') {
+                o += c;
+                continue;
+            }
+            if (p_ >= e_) return false;
+            const char x = *p_++;
+            switch (x) {
+                case '"': o += '"'; break;
+                case '\\': o += '\\'; break;
+                case '/': o += '/'; break;
+                case 'b': o += '\b'; break;
+                case 'f': o += '\f'; break;
+                case 'n': o += '\n'; break;
+                case 'r': o += '\r'; break;
+                case 't': o += '\t'; break;
+                case 'u': {
+                    unsigned c1;
+                    if (!hex4(c1)) return false;
+                    if (c1 >= 0xD800 && c1 < 0xDC00) {  // surrogate pair
+                        unsigned c2;
+                        if (!lit("\\u") || !hex4(c2) || c2 < 0xDC00 || c2 >= 0xE000) return false;
+                        c1 = 0x10000 + ((c1 - 0xD800) << 10) + (c2 - 0xDC00);
+                    }
+                    utf8(o, c1);
+                    break;
+                }
+                default: return false;
+            }
+        }
+        if (p_ >= e_) return false;
+        ++p_;
+        return true;
+    }
+    bool value(Json &v, int depth) {
+        if (depth > 16) return false;
+        ws();
+        if (p_ >= e_) return false;
+        const char c = *p_;
+        if (c == '{') {
+            ++p_;
+            v.kind = Json::Obj;
+            ws();
+            if (p_ < e_ && *p_ == '}') { ++p_; return true; }
+            for (;;) {
+                ws();
+                std::string k;
+                if (!str(k)) return false;
+                ws();
+                if (p_ >= e_ || *p_ != ':') return false;
+                ++p_;
+                Json x;
+                if (!value(x, depth + 1)) return false;
+                v.obj.emplace_back(std::move(k), std::move(x));
+                ws();
+                if (p_ < e_ && *p_ == ',') { ++p_; continue; }
+                if (p_ < e_ && *p_ == '}') { ++p_; return true; }
+                return false;
+            }
+        }
+        if (c == '[') {
+            ++p_;
+            v.kind = Json::Arr;
+            ws();
+            if (p_ < e_ && *p_ == ']') { ++p_; return true; }
+            for (;;) {
+                Json x;
+                if (!value(x, depth + 1)) return false;
+                v.arr.push_back(std::move(x));
+                ws();
+                if (p_ < e_ && *p_ == ',') { ++p_; continue; }
+                if (p_ < e_ && *p_ == ']') { ++p_; return true; }
+                return false;
+            }
+        }
+        if (c == '"') {
+            v.kind = Json::Str;
+            return str(v.s);
+        }
+        if (lit("true")) { v.kind = Json::Bool; v.i = 1; return true; }
+        if (lit("false")) { v.kind = Json::Bool; v.i = 0; return true; }
+        if (lit("null")) { v.kind = Json::Null; return true; }
+        // number: integers exactly, anything else only recognised
+        const char *b = p_;
+        if (p_ < e_ && *p_ == '-') ++p_;
+        bool integral = true, digits = false;
+        while (p_ < e_ && ((*p_ >= '0' && *p_ <= '9') || *p_ == '.' || *p_ == 'e' || *p_ == 'E' ||
+                           *p_ == '+' || *p_ == '-')) {
+            if (*p_ >= '0' && *p_ <= '9') digits = true;
+            else integral = false;
+            ++p_;
+        }
+        if (!digits) return false;
+        if (integral) {
+            const std::string t(b, p_);
+            errno = 0;
+            char *end = nullptr;
+            const long long x = std::strtoll(t.c_str(), &end, 10);
+            if (errno || !end || *end) return false;
+            v.kind = Json::Int;
+            v.i = x;
+        } else {
+            v.kind = Json::Num;
+        }
+        return true;
+    }
+};
+
+std::string jsonEscape(const std::string &s) {
+    std::string o = "\"";
+    for (unsigned char c : s) {
+        if (c == '"') o += "\\\"";
+        else if (c == '\\') o += "\\\\";
+        else if (c < 0x20) {
+            char buf[8];
+            std::snprintf(buf, sizeof buf, "\\u%04x", c);
+            o += buf;
+        } else {
+            o += (char) c;
+        }
+    }
+    return o + "\"";
+}
+
+// Writes `path` (through path + ".tmp", renamed on success).  Tensor names must be unique.
+bool writeSafetensors(const std::string &path, const std::vector<std::pair<std::string, StTensor>> &ts,
+                      const std::map<std::string, std::string> &meta) {
+    std::string h = "{\"__metadata__\":{";
+    bool first = true;
+    for (const auto &kv : meta) {
+        h += (first ? "" : ",") + jsonEscape(kv.first) + ":" + jsonEscape(kv.second);
+        first = false;
+    }
+    h += "}";
+    uint64_t off = 0;
+    for (const auto &t : ts) {
+        h += "," + jsonEscape(t.first) + ":{\"dtype\":" + jsonEscape(t.second.dtype) + ",\"shape\":[";
+        for (size_t i = 0; i < t.second.shape.size(); ++i)
+            h += (i ? "," : "") + std::to_string(t.second.shape[i]);
+        h += "],\"data_offsets\":[" + std::to_string(off) + "," + std::to_string(off + t.second.bytes.size()) + "]}";
+        off += t.second.bytes.size();
+    }
+    h += "}";
+    while (h.size() % 8) h += ' ';  // the data section starts 8-byte aligned
+    const std::string tmp = path + ".tmp";
+    std::FILE *f = std::fopen(tmp.c_str(), "wb");
+    if (!f) return false;
+    uint8_t len[8];
+    const uint64_t n = h.size();
+    for (int i = 0; i < 8; ++i) len[i] = (uint8_t) (n >> (8 * i));
+    bool ok = std::fwrite(len, 1, 8, f) == 8 && std::fwrite(h.data(), 1, h.size(), f) == h.size();
+    for (const auto &t : ts)
+        ok = ok && (t.second.bytes.empty() ||
+                    std::fwrite(t.second.bytes.data(), 1, t.second.bytes.size(), f) == t.second.bytes.size());
+    ok = (std::fclose(f) == 0) && ok;
+    if (!ok || std::rename(tmp.c_str(), path.c_str()) != 0) {
+        std::remove(tmp.c_str());
+        return false;
+    }
+    return true;
+}
+
+// Reads and validates a whole file: every tensor's dtype is known, its offsets lie inside
+// the data section and span exactly numel * dtype size.  false on any defect.
+bool readSafetensors(const std::string &path, std::map<std::string, StTensor> &out,
+                     std::map<std::string, std::string> &meta) {
+    std::FILE *f = std::fopen(path.c_str(), "rb");
+    if (!f) return false;
+    struct Closer {
+        std::FILE *f;
+        ~Closer() { std::fclose(f); }
+    } closer{f};
+    if (std::fseek(f, 0, SEEK_END) != 0) return false;
+    const long long fileSize = std::ftell(f);
+    if (fileSize < 8 || std::fseek(f, 0, SEEK_SET) != 0) return false;
+    uint8_t len[8];
+    if (std::fread(len, 1, 8, f) != 8) return false;
+    uint64_t n = 0;
+    for (int i = 0; i < 8; ++i) n |= (uint64_t) len[i] << (8 * i);
+    if (n == 0 || n > (uint64_t) (fileSize - 8) || n > (100u << 20)) return false;
+    std::string h(n, '\0');
+    if (std::fread(&h[0], 1, n, f) != n) return false;
+    Json root;
+    if (!JsonReader(h.data(), h.data() + h.size()).parse(root) || root.kind != Json::Obj) return false;
+    const uint64_t dataSize = (uint64_t) fileSize - 8 - n;
+    for (const auto &kv : root.obj) {
+        if (kv.first == "__metadata__") {
+            if (kv.second.kind != Json::Obj) return false;
+            for (const auto &m : kv.second.obj) {
+                if (m.second.kind != Json::Str) return false;
+                meta[m.first] = m.second.s;
+            }
+            continue;
+        }
+        const Json &t = kv.second;
+        const Json *dt = t.get("dtype"), *sh = t.get("shape"), *of = t.get("data_offsets");
+        if (t.kind != Json::Obj || !dt || dt->kind != Json::Str || !sh || sh->kind != Json::Arr || !of ||
+            of->kind != Json::Arr || of->arr.size() != 2)
+            return false;
+        StTensor st;
+        st.dtype = dt->s;
+        const size_t es = stDtypeSize(st.dtype);
+        if (!es) return false;
+        uint64_t numel = 1;
+        for (const Json &d : sh->arr) {
+            if (d.kind != Json::Int || d.i < 0 || d.i > (1LL << 40)) return false;
+            st.shape.push_back(d.i);
+            numel *= (uint64_t) d.i;
+            if (numel > (1ULL << 42)) return false;
+        }
+        if (of->arr[0].kind != Json::Int || of->arr[1].kind != Json::Int) return false;
+        const long long b = of->arr[0].i, e = of->arr[1].i;
+        if (b < 0 || e < b || (uint64_t) e > dataSize || (uint64_t) (e - b) != numel * es) return false;
+        st.bytes.resize((size_t) (e - b));
+        if (e > b) {
+            if (std::fseek(f, (long) (8 + n + (uint64_t) b), SEEK_SET) != 0) return false;
+            if (std::fread(st.bytes.data(), 1, st.bytes.size(), f) != st.bytes.size()) return false;
+        }
+        if (!out.emplace(kv.first, std::move(st)).second) return false;  // duplicate name
+    }
+    return true;
+}
+
+// ------------------------------------------------------------------ device <-> host
+
+// Rows [r0, r0 + n) of every head of a [kvHeads, cap, headDim] buffer -> host [kvHeads, n, headDim].
+StTensor download(const Tensor &buf, int r0, int n) {
+    StTensor t;
+    t.dtype = buf.dtype == Dtype::bf16 ? "BF16" : buf.dtype == Dtype::f32 ? "F32" : "U8";
+    t.shape = {buf.shape[0], n, buf.shape[2]};
+    const size_t es = dtypeSize(buf.dtype);
+    const size_t rowBytes = (size_t) buf.shape[2] * es;
+    t.bytes.resize((size_t) buf.shape[0] * n * rowBytes);
+    if (n > 0)
+        hipOk(hipMemcpy2D(t.bytes.data(), (size_t) n * rowBytes,
+                          static_cast<const char *>(buf.data) + (size_t) r0 * buf.strides[1] * es,
+                          (size_t) buf.strides[0] * es, (size_t) n * rowBytes, (size_t) buf.shape[0],
+                          hipMemcpyDeviceToHost),
+              "ESKVCache snapshot download");
+    return t;
+}
+
+// A fresh zeroed [kvHeads, cap, headDim] bf16 buffer holding `rows` rows of host data
+// [kvHeads, rowsStored, headDim] (rows <= rowsStored; the rest of the buffer is zero).
+Tensor upload(const std::vector<uint8_t> &src, int64_t kvH, int64_t rowsStored, int64_t hd, int rows, int cap) {
+    Tensor t = Tensor::empty({kvH, cap, hd}, Dtype::bf16);
+    hipOk(hipMemset(t.data, 0, t.nbytes()), "ESKVCache snapshot clear");
+    const size_t rowBytes = (size_t) hd * 2;
+    if (rows > 0)
+        hipOk(hipMemcpy2D(t.data, (size_t) cap * rowBytes, src.data(), (size_t) rowsStored * rowBytes,
+                          (size_t) rows * rowBytes, (size_t) kvH, hipMemcpyHostToDevice),
+              "ESKVCache snapshot upload");
+    return t;
+}
+
+// A device copy of rows [r0, r0 + n) of every head (the marker / rewind window copies).
+Tensor copyWindow(const Tensor &buf, int r0, int n) {
+    Tensor t = Tensor::empty({buf.shape[0], n, buf.shape[2]}, Dtype::bf16);
+    const size_t rowBytes = (size_t) buf.shape[2] * 2;
+    if (n > 0)
+        hipOk(hipMemcpy2D(t.data, (size_t) n * rowBytes,
+                          static_cast<const char *>(buf.data) + (size_t) r0 * buf.strides[1] * 2,
+                          (size_t) buf.strides[0] * 2, (size_t) n * rowBytes, (size_t) buf.shape[0],
+                          hipMemcpyDeviceToDevice),
+              "ESKVCache window copy");
+    return t;
+}
+
+// A fresh chunk-aligned buffer with `src`'s rows at the front (the compaction layout).
+Tensor rehomeDevice(const Tensor &src, int cap) {
+    const int64_t kvH = src.shape[0], n = src.shape[1], hd = src.shape[2];
+    Tensor t = Tensor::empty({kvH, cap, hd}, Dtype::bf16);
+    hipOk(hipMemset(t.data, 0, t.nbytes()), "ESKVCache rewind clear");
+    if (n > 0)
+        hipOk(hipMemcpy2D(t.data, (size_t) cap * hd * 2, src.data, (size_t) src.strides[0] * 2,
+                          (size_t) n * hd * 2, (size_t) kvH, hipMemcpyDeviceToDevice),
+              "ESKVCache rewind install");
+    return t;
+}
+
+uint16_t bf16Rne(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return (uint16_t) ((u >> 16) | 0x40);  // NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t) (u >> 16);
+}
+
+bool isKvTensor(const StTensor &t) {
+    return t.dtype == "BF16" && t.shape.size() == 3 && t.shape[0] > 0 && t.shape[2] > 0 && t.shape[2] % 8 == 0 &&
+           t.shape[1] < (1LL << 30);
+}
+
+int parseInt(const std::map<std::string, std::string> &meta, const std::string &key, bool &ok) {
+    auto it = meta.find(key);
+    if (it == meta.end()) {
+        ok = false;
+        return 0;
+    }
+    try {
+        size_t used = 0;
+        const long long v = std::stoll(it->second, &used);
+        if (used != it->second.size() || v < INT32_MIN || v > INT32_MAX) ok = false;
+        return (int) v;
+    } catch (const std::exception &) {
+        ok = false;
+        return 0;
+    }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ markers and rewind
+
+ESKVCache::Marker ESKVCache::takeMarker(int pos, bool copyLost, hipStream_t) const {
+    hipOk(hipDeviceSynchronize(), "ESKVCache mark");
+    Marker m;
+    m.pos = pos;
+    for (size_t i = 0; i < slots_.size(); ++i) {
+        const Slot &s = slots_[i];
+        if (!s.k || !s.v) continue;  // raw layers never evict: prefix-sliceable
+        const int live = s.len - s.start;
+        if (live >= pos && !(copyLost && s.lost)) continue;  // the full prefix is still there
+        // Deep copy now: later appends overwrite these rows in place.
+        Tensor k = copyWindow(*s.k, s.start, live);
+        Tensor v = s.shared ? k : copyWindow(*s.v, s.start, live);
+        m.slidingKV.push_back({(int) i, {k, v}});
+    }
+    return m;
+}
+
+void ESKVCache::markPrefix(int pos, const std::string &fingerprint) {
+    // Below the sliding window plus a prefill chunk an evicting layer cannot be told from
+    // a never-evicting one (ESKVCache.mm:121-146).
+    if (pos < 4096)
+        throw std::invalid_argument("ESKVCache::markPrefix: marker positions below 4096 unsupported");
+    Marker m = takeMarker(pos, /*copyLost=*/false, nullptr);
+    m.fp = fingerprint;
+    markers_.push_back(std::move(m));
+}
+
+bool ESKVCache::markRewindPoint(int pos) {
+    // ESKVCache.mm:148-179: layers whose buffer still holds the whole prefix are rewound by
+    // truncation later (guarded by `lost`); evicting or already-compacted layers are copied.
+    if (pos <= 0) return false;
+    for (const auto &a : k_)
+        if (a) return false;  // legacy storage: no rewind
+    bool prealloc = false;
+    for (const Slot &s : slots_) prealloc = prealloc || s.k.has_value();
+    if (!prealloc) return false;
+    rewindMark_ = takeMarker(pos, /*copyLost=*/true, nullptr);
+    return true;
+}
+
+int ESKVCache::rewindToMark() {
+    // ESKVCache.mm:181-222: validate every layer before mutating any.
+    if (!rewindMark_) return -1;
+    const int P = rewindMark_->pos;
+    std::vector<const std::pair<Tensor, Tensor> *> copyFor(slots_.size(), nullptr);
+    for (const auto &lkv : rewindMark_->slidingKV) copyFor[lkv.first] = &lkv.second;
+    for (size_t i = 0; i < slots_.size(); ++i) {
+        const Slot &s = slots_[i];
+        if (s.k && !copyFor[i] && (s.lost || s.len < P)) {
+            rewindMark_.reset();
+            return -1;
+        }
+    }
+    // Build the new slots first (allocation may throw), then commit.
+    std::vector<Slot> next = slots_;
+    for (size_t i = 0; i < slots_.size(); ++i) {
+        Slot &s = next[i];
+        if (copyFor[i]) {
+            // the mark's window, content at the front (eviction re-applies on the next append)
+            const Tensor &k = copyFor[i]->first;
+            const int content = (int) k.shape[1];
+            const int cap = chunkUp(content + kGrowChunk);
+            s.k = rehomeDevice(k, cap);
+            s.v = s.shared ? *s.k : rehomeDevice(copyFor[i]->second, cap);
+            s.len = content;
+            s.start = 0;
+            s.lost = content < P;
+        } else if (s.k) {
+            s.len = P;  // full-prefix buffer: cursor truncation
+            s.start = 0;
+        }
+    }
+    hipOk(hipDeviceSynchronize(), "ESKVCache rewind");
+    slots_ = std::move(next);
+    rewindMark_.reset();
+    return P;
+}
+
+// ------------------------------------------------------------------ save / restore
+
+bool ESKVCache::saveSnapshot(const std::string &path, const std::string &fingerprint, int pos) const {
+    try {
+        hipOk(hipDeviceSynchronize(), "ESKVCache snapshot");
+        std::vector<std::pair<std::string, StTensor>> ts;
+        std::map<std::string, std::string> meta;
+        for (size_t i = 0; i < slots_.size(); ++i) {
+            const Slot &s = slots_[i];
+            if (!s.k) return false;  // a snapshot needs every layer primed
+            const std::string id = std::to_string(i);
+            StTensor k = download(*s.k, s.start, s.len - s.start);
+            if (s.v) {
+                StTensor v = s.shared ? k : download(*s.v, s.start, s.len - s.start);
+                if (s.shared) meta["shared_" + id] = "1";
+                ts.emplace_back("k_" + id, std::move(k));
+                ts.emplace_back("v_" + id, std::move(v));
+            } else {
+                ts.emplace_back("k_" + id, std::move(k));  // raw-K: one pre-norm stream
+            }
+        }
+        meta["fingerprint"] = fingerprint;
+        meta["pos"] = std::to_string(pos);
+        meta["layers"] = std::to_string(slots_.size());
+        meta["marker_count"] = std::to_string(markers_.size());
+        for (size_t mi = 0; mi < markers_.size(); ++mi) {
+            const Marker &m = markers_[mi];
+            const std::string tag = "marker_" + std::to_string(mi);
+            meta[tag + "_pos"] = std::to_string(m.pos);
+            meta[tag + "_fp"] = m.fp;
+            for (const auto &lkv : m.slidingKV) {
+                const std::string sfx = "_" + std::to_string(lkv.first);
+                const Tensor &k = lkv.second.first;
+                ts.emplace_back("m" + std::to_string(mi) + "_k" + sfx, download(k, 0, (int) k.shape[1]));
+                ts.emplace_back("m" + std::to_string(mi) + "_v" + sfx,
+                                download(lkv.second.second, 0, (int) k.shape[1]));
+            }
+        }
+        return writeSafetensors(path, ts, meta);
+    } catch (const std::exception &) {
+        return false;
+    }
+}
+
+int ESKVCache::restoreSnapshot(const std::string &path, const std::string &fingerprint, RawMode mode,
+                               const std::function<std::string(int)> &prefixFp) {
+    try {
+        std::map<std::string, StTensor> T;
+        std::map<std::string, std::string> meta;
+        if (!readSafetensors(path, T, meta)) return -1;
+        bool ok = true;
+        const int fullPos = parseInt(meta, "pos", ok);
+        const int layers = parseInt(meta, "layers", ok);
+        if (!ok || !meta.count("fingerprint") || layers != (int) slots_.size() || fullPos < 0) return -1;
+        auto has = [&](const std::string &n) { return T.count(n) != 0; };
+
+        // A full-fingerprint match restores everything; otherwise the longest marker whose
+        // fingerprint the caller reproduces (ESKVCache.mm:287-310).
+        int targetPos = fullPos, markerIdx = -1;
+        if (meta.at("fingerprint") != fingerprint) {
+            bool okc = true;
+            const int nMark = meta.count("marker_count") ? parseInt(meta, "marker_count", okc) : 0;
+            if (!okc || !prefixFp || nMark <= 0) return -1;
+            int bestPos = -1;
+            for (int mi = 0; mi < nMark; ++mi) {
+                const std::string tag = "marker_" + std::to_string(mi);
+                if (!meta.count(tag + "_pos") || !meta.count(tag + "_fp")) continue;
+                bool okp = true;
+                const int mpos = parseInt(meta, tag + "_pos", okp);
+                if (!okp || mpos <= bestPos) continue;
+                const std::string cand = prefixFp(mpos);
+                if (!cand.empty() && cand == meta.at(tag + "_fp")) {
+                    bestPos = mpos;
+                    markerIdx = mi;
+                }
+            }
+            if (markerIdx < 0) return -1;
+            targetPos = bestPos;
+        }
+
+        // Classify and validate every layer before touching the cache.
+        enum Kind { Composite, RawK, RawQ8 };
+        std::vector<Kind> kind(slots_.size());
+        bool anyRaw = false;
+        for (size_t i = 0; i < slots_.size(); ++i) {
+            const std::string id = std::to_string(i);
+            const std::string mk = "m" + std::to_string(markerIdx) + "_k_" + id;
+            const std::string mv = "m" + std::to_string(markerIdx) + "_v_" + id;
+            if (markerIdx >= 0 && has(mk)) {
+                if (!has(mv) || !isKvTensor(T.at(mk)) || T.at(mv).shape != T.at(mk).shape ||
+                    T.at(mv).dtype != "BF16")
+                    return -1;
+            }
+            if (has("k_" + id) && has("v_" + id)) {
+                const StTensor &k = T.at("k_" + id), &v = T.at("v_" + id);
+                if (!isKvTensor(k) || v.dtype != "BF16" || v.shape != k.shape) return -1;
+                kind[i] = Composite;
+            } else if (has("k_" + id)) {
+                if (!isKvTensor(T.at("k_" + id))) return -1;
+                kind[i] = RawK;
+                anyRaw = true;
+            } else if (has("rq_" + id)) {
+                if (!has("rs_" + id) || !has("rb_" + id)) return -1;
+                const StTensor &q = T.at("rq_" + id), &sc = T.at("rs_" + id), &bs = T.at("rb_" + id);
+                if (q.dtype != "U8" || q.shape.size() != 3 || q.shape[0] <= 0 || q.shape[2] <= 0 ||
+                    q.shape[2] % 8 != 0 || sc.dtype != "F32" || bs.dtype != "F32" ||
+                    sc.shape != std::vector<int64_t>{q.shape[0], q.shape[1], 1} || bs.shape != sc.shape)
+                    return -1;
+                kind[i] = RawQ8;
+                anyRaw = true;
+            } else {
+                return -1;  // unprimed layer, or quantized-KV tensors (no quantized storage here)
+            }
+        }
+        // Storage-mode gate (ESKVCache.mm:333-343): composite <-> raw is not derivable.  This
+        // cache holds no q8 rows, so q8 layers restore only as bf16 raw rows (mode raw).
+        if (mode == RawMode::rawQ8) return -1;
+        if (mode != RawMode::asStored) {
+            if (anyRaw && mode == RawMode::composite) return -1;
+            if (!anyRaw && mode != RawMode::composite) return -1;
+        }
+        for (size_t i = 0; i < slots_.size(); ++i)
+            if (kind[i] == RawQ8 && mode != RawMode::raw) return -1;
+
+        // Build every layer's new slot (allocations may throw: nothing is committed yet).
+        std::vector<Slot> next(slots_.size());
+        for (size_t i = 0; i < slots_.size(); ++i) {
+            const std::string id = std::to_string(i);
+            Slot &s = next[i];
+            const std::string mk = "m" + std::to_string(markerIdx) + "_k_" + id;
+            if (markerIdx >= 0 && T.count(mk)) {
+                // an evicting layer takes the marker's window verbatim
+                const StTensor &k = T.at(mk), &v = T.at("m" + std::to_string(markerIdx) + "_v_" + id);
+                const int content = (int) k.shape[1];
+                const int cap = chunkUp(content + kGrowChunk);
+                s.k = upload(k.bytes, k.shape[0], content, k.shape[2], content, cap);
+                const bool shared = meta.count("shared_" + id) && meta.at("shared_" + id) == "1" &&
+                                    v.bytes == k.bytes;
+                s.v = shared ? *s.k : upload(v.bytes, v.shape[0], content, v.shape[2], content, cap);
+                s.shared = shared;
+                s.len = content;
+                s.lost = content < targetPos;
+                continue;
+            }
+            if (kind[i] == RawQ8) {
+                // Rehydration (ESKVCache.mm:366-383): bf16(float(q) * scale + bias), the values
+                // the q8 decode path computes on.
+                const StTensor &q = T.at("rq_" + id), &sc = T.at("rs_" + id), &bs = T.at("rb_" + id);
+                const int64_t kvH = q.shape[0], rows = q.shape[1], hd = q.shape[2];
+                const int content = (int) std::min<int64_t>(rows, targetPos);
+                std::vector<uint8_t> dq((size_t) kvH * rows * hd * 2);
+                for (int64_t h = 0; h < kvH; ++h)
+                    for (int64_t r = 0; r < rows; ++r) {
+                        float scale, bias;
+                        std::memcpy(&scale, &sc.bytes[(size_t) (h * rows + r) * 4], 4);
+                        std::memcpy(&bias, &bs.bytes[(size_t) (h * rows + r) * 4], 4);
+                        for (int64_t d = 0; d < hd; ++d) {
+                            const size_t e = (size_t) ((h * rows + r) * hd + d);
+                            const float prod = (float) q.bytes[e] * scale;
+                            const uint16_t b = bf16Rne(prod + bias);
+                            std::memcpy(&dq[e * 2], &b, 2);
+                        }
+                    }
+                s.k = upload(dq, kvH, rows, hd, content, chunkUp(content + kGrowChunk));
+                s.len = content;
+                s.lost = content < targetPos;
+                continue;
+            }
+            const StTensor &k = T.at("k_" + id);
+            const int content = (int) std::min<int64_t>(k.shape[1], targetPos);
+            const int cap = chunkUp(content + kGrowChunk);
+            s.k = upload(k.bytes, k.shape[0], k.shape[1], k.shape[2], content, cap);
+            if (kind[i] == Composite) {
+                const StTensor &v = T.at("v_" + id);
+                const bool shared = meta.count("shared_" + id) && meta.at("shared_" + id) == "1" &&
+                                    v.bytes == k.bytes;
+                s.v = shared ? *s.k : upload(v.bytes, v.shape[0], v.shape[1], v.shape[2], content, cap);
+                s.shared = shared;
+            }
+            s.len = content;
+            s.lost = content < targetPos;  // a stored sliding window is not a full prefix
+        }
+        hipOk(hipDeviceSynchronize(), "ESKVCache restore");
+        slots_ = std::move(next);
+        return targetPos;
+    } catch (const std::exception &) {
+        return -1;
+    }
+}
+
+}  // namespace es

@@ -1,6 +1,7 @@
 // es_capi.cpp -- the C ABI of include/esda_cache.h over es::ESKVCache and
 // es::esDecodeAttnGlobal.  Exceptions are caught here and turned into status codes.
 #include <exception>
+#include <functional>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -91,6 +92,16 @@ int esda_cache_update_raw(esda_cache *cache, int32_t layer, const void *k_new, i
     });
 }
 
+int esda_cache_current_raw(esda_cache *cache, int32_t layer, esda_view *view, int32_t *len, int32_t *pitch) {
+    return guarded([&] {
+        needCache(cache);
+        auto r = cache->impl.currentRaw(layer);
+        toView(r.view, view);
+        if (len) *len = r.len;
+        if (pitch) *pitch = r.pitch;
+    });
+}
+
 int esda_cache_current(esda_cache *cache, int32_t layer, int32_t prealloc, esda_view *k_out, esda_view *v_out) {
     return guarded([&] {
         needCache(cache);
@@ -163,6 +174,29 @@ int esda_cache_save_snapshot(const esda_cache *cache, const char *path, const ch
 int esda_cache_restore_snapshot(esda_cache *cache, const char *path, const char *fingerprint) {
     if (!cache || !path || !fingerprint) return -1;
     return cache->impl.restoreSnapshot(path, fingerprint);
+}
+
+int esda_cache_restore_snapshot_ex(esda_cache *cache, const char *path, const char *fingerprint, int32_t mode,
+                                   esda_prefix_fp_fn prefix_fp, void *user) {
+    if (!cache || !path || !fingerprint || mode < 0 || mode > 3) return -1;
+    std::function<std::string(int)> fn;
+    if (prefix_fp)
+        fn = [prefix_fp, user](int pos) {
+            const char *s = prefix_fp(pos, user);
+            return std::string(s ? s : "");
+        };
+    return cache->impl.restoreSnapshot(path, fingerprint, static_cast<es::ESKVCache::RawMode>(mode), fn);
+}
+
+int esda_cache_mark_prefix(esda_cache *cache, int32_t pos, const char *fingerprint) {
+    return guarded([&] {
+        if (!cache || !fingerprint) throw std::invalid_argument("esda_cache_mark_prefix: null pointer");
+        cache->impl.markPrefix(pos, fingerprint);
+    });
+}
+
+void esda_cache_clear_rewind_mark(esda_cache *cache) {
+    if (cache) cache->impl.clearRewindMark();
 }
 
 int esda_cache_mark_rewind_point(esda_cache *cache, int32_t pos) {

@@ -10,9 +10,10 @@
 //  decode() is the fused decode step of this library: the prealloc append and the
 //  attention of the new token in one GPU pass (esda_decode), replacing update()
 //  followed by SDPA at ESAttention.mm:105 and :188.
-//  KV snapshots, prefix markers, turn rewind, quantized / q8 storage and the compiled
-//  step mode are not implemented: their members keep the reference's signatures and
-//  return its failure values (-1 / false).
+//  KV snapshots (the reference's safetensors layout), prefix markers and turn rewind
+//  follow ESKVCache.mm:121-456.  Quantized / q8 storage and the compiled step mode are
+//  not implemented: a snapshot holding q8 rows restores only as bf16 raw rows (the
+//  reference's "rehydration"), and quantized-KV snapshots are refused (-1).
 //
 //  Every call takes a HIP stream (nullptr = the default stream).  Buffer growth and
 //  compaction synchronise that stream before the old buffer is released.  An instance
@@ -52,6 +53,9 @@ public:
         int len, pitch;
     };
     Raw updateRaw(int layer, const Tensor &kNew, bool prealloc, hipStream_t stream = nullptr);
+    // The Raw record of a prealloc raw-K slot without appending (the reference hands it out
+    // only from updateRaw).  Throws std::runtime_error for a non-raw slot.
+    Raw currentRaw(int layer) const;
 
     // Fused decode step for `layer` (prealloc storage): appends the single new row of
     // kNew/vNew ([kvHeads, 1, headDim]) and returns softmax(scale q K^T) V over the rows
@@ -70,17 +74,30 @@ public:
     // The cached {K, V} without appending (ESKVCache.mm:112-119).
     std::pair<Tensor, Tensor> current(int layer, bool prealloc) const;
 
-    // Not implemented (persistence, rewind, quantized storage): the reference's
-    // signatures (ESKVCache.h:102-174) with its failure results.
+    // Persistence and rewind (ESKVCache.h:102-174, ESKVCache.mm:121-456).
+    // markPrefix: remember position `pos` (>= 4096, else std::invalid_argument) with the
+    // prompt-prefix fingerprint; layers whose live window no longer starts at row 0 of the
+    // prefix (they evicted) have that window copied now.
     void markPrefix(int pos, const std::string &fingerprint);
+    // saveSnapshot: safetensors file of every layer's live rows (k_<i>/v_<i>; raw layers
+    // k_<i> only), metadata {fingerprint, pos, layers, marker_*} and the markers' windows
+    // (m<j>_k_<i>/m<j>_v_<i>).  false if a layer is unprimed or the file cannot be written.
     bool saveSnapshot(const std::string &path, const std::string &fingerprint, int pos) const;
     enum class RawMode { composite, raw, rawQ8, asStored };
+    // restoreSnapshot: -1 (cache untouched) on a missing or malformed file, a layer-count
+    // or fingerprint mismatch with no usable marker, or a storage-mode mismatch; otherwise
+    // re-homes every layer into fresh chunk-aligned buffers and returns the restored
+    // position (the snapshot's, or the longest marker whose fingerprint prefixFp(pos)
+    // reproduces).  RawMode::rawQ8 is refused (no q8 storage here).
     int restoreSnapshot(const std::string &path, const std::string &fingerprint,
                         RawMode mode = RawMode::asStored,
                         const std::function<std::string(int)> &prefixFp = nullptr);
+    // One in-memory rewind mark: markRewindPoint(pos) (false for legacy storage, pos <= 0
+    // or an unprimed cache), rewindToMark() -> pos, or -1 when a layer can no longer be
+    // rebuilt at pos (the mark is consumed either way).
     bool markRewindPoint(int pos);
     int rewindToMark();
-    void clearRewindMark() {}
+    void clearRewindMark() { rewindMark_.reset(); }
 
     int seqLen() const { return seqLen_; }
     void markStep(int nNew) { seqLen_ += nNew; }
@@ -104,6 +121,16 @@ private:
     };
     std::vector<std::optional<Tensor>> k_, v_;  // legacy storage
     std::vector<Slot> slots_;                   // prealloc storage
+    // A position, its prefix fingerprint, and copies of the evicting layers' live windows
+    // taken at that moment (layer index, {k, v}; v is k for a shared slot).
+    struct Marker {
+        int pos = 0;
+        std::string fp;
+        std::vector<std::pair<int, std::pair<Tensor, Tensor>>> slidingKV;
+    };
+    std::vector<Marker> markers_;
+    std::optional<Marker> rewindMark_;
+    Marker takeMarker(int pos, bool copyLost, hipStream_t stream) const;
     int seqLen_ = 0;
     std::optional<Tensor> posDev_;     // per-layer position words for decode()
     std::optional<Tensor> workspace_;  // esda_decode / esda_decode_raw workspace

@@ -17,9 +17,12 @@
  *   esda_cache_decode_raw          updateRaw + esDecodeAttnGlobal      ESAttention.mm:291-300
  *   esda_cache_seq_len / mark_step ESKVCache::seqLen / markStep        ESKVCache.h:176-177
  *   esda_cache_reset               ESKVCache::reset                    ESKVCache.h:178, ESKVCache.mm:622-638
- *   esda_cache_save_snapshot, restore_snapshot, mark_rewind_point, rewind_to_mark:
- *                                  ESKVCache.h:102-174; not implemented, they return the
- *                                  reference's failure values (0 = false, -1)
+ *   esda_cache_save_snapshot       ESKVCache::saveSnapshot             ESKVCache.h:129, ESKVCache.mm:224-278
+ *   esda_cache_restore_snapshot(_ex) ESKVCache::restoreSnapshot        ESKVCache.h:138-146, ESKVCache.mm:280-456
+ *   esda_cache_mark_prefix         ESKVCache::markPrefix               ESKVCache.h:127, ESKVCache.mm:121-146
+ *   esda_cache_mark_rewind_point, rewind_to_mark, clear_rewind_mark:
+ *                                  ESKVCache::markRewindPoint / rewindToMark / clearRewindMark
+ *                                  ESKVCache.h:160-163, ESKVCache.mm:148-222
  *   esda_cache_slot                slot bookkeeping (len, start, capacity) for callers
  *                                  and tests; the reference keeps it private (ESKVCache.h:183-192)
  *   esda_decode_attn_global        esDecodeAttnGlobal                  ESDecodeAttn.h:27-28
@@ -61,6 +64,11 @@ int esda_cache_update_raw(esda_cache *cache, int32_t layer, const void *k_new, i
 
 int esda_cache_current(esda_cache *cache, int32_t layer, int32_t prealloc, esda_view *k_out,
                        esda_view *v_out);
+/* A prealloc raw-K slot's live rows without appending: no counterpart in the reference,
+ * whose callers see the raw view only from updateRaw; for callers and tests that inspect
+ * a raw slot (e.g. after a snapshot restore or a rewind). */
+int esda_cache_current_raw(esda_cache *cache, int32_t layer, esda_view *view, int32_t *len,
+                           int32_t *pitch);
 
 /* Fused decode step: append one row (v_new == k_new: one shared K=V buffer) and attend.
  * q: [num_q_heads, head_dim] bf16; out: [num_q_heads, head_dim] bf16. */
@@ -83,11 +91,25 @@ int esda_cache_seq_len(const esda_cache *cache);
 void esda_cache_mark_step(esda_cache *cache, int32_t n_new);
 void esda_cache_reset(esda_cache *cache);
 
+/* Snapshots (safetensors, the reference's layout): save returns 1 on success, 0 when a
+ * layer is unprimed or the file cannot be written.  Restore returns the restored position,
+ * or -1 with the cache untouched (missing / malformed file, layer-count or fingerprint
+ * mismatch without a usable marker, storage-mode mismatch). */
 int esda_cache_save_snapshot(const esda_cache *cache, const char *path, const char *fingerprint,
                              int32_t pos);
 int esda_cache_restore_snapshot(esda_cache *cache, const char *path, const char *fingerprint);
+/* The caller's prompt-prefix fingerprint at a marker position ("" or NULL: none). */
+typedef const char *(*esda_prefix_fp_fn)(int32_t pos, void *user);
+/* mode: 0 composite, 1 raw, 2 raw q8 (refused: no q8 storage), 3 as stored
+ * (ESKVCache::RawMode); prefix_fp may be NULL. */
+int esda_cache_restore_snapshot_ex(esda_cache *cache, const char *path, const char *fingerprint,
+                                   int32_t mode, esda_prefix_fp_fn prefix_fp, void *user);
+/* Marks position pos (>= 4096, else ESDA_ERR_INVALID_ARGUMENT) for the next snapshot. */
+int esda_cache_mark_prefix(esda_cache *cache, int32_t pos, const char *fingerprint);
+/* One in-memory rewind mark: 1 / 0; rewind returns the position or -1. */
 int esda_cache_mark_rewind_point(esda_cache *cache, int32_t pos);
 int esda_cache_rewind_to_mark(esda_cache *cache);
+void esda_cache_clear_rewind_mark(esda_cache *cache);
 
 /* esDecodeAttnGlobal: q [num_q_heads, 512], raw_buf the unsliced [num_kv_heads, pitch,
  * 512] buffer, rows 0 .. len-1 attended (already appended); out [num_q_heads, 512]. */

@@ -204,7 +204,9 @@ def test_decode_raw_through_the_cache_matches_oracle():
     assert ln == 271 and np.array_equal(_view(view)[:, :270], model)
 
 
-def test_not_implemented_members_return_reference_failure_values(tmp_path):
+def test_unprimed_cache_failure_values_and_step_counter(tmp_path):
+    """An unprimed cache: nothing to snapshot or rewind (the reference's false / -1);
+    seqLen counts markStep calls until reset."""
     from apertura_amd.cache import ESKVCache
     cache = ESKVCache(3)
     assert cache.save_snapshot(str(tmp_path / "kv.safetensors"), "fp", 10) is False
