@@ -368,7 +368,26 @@ typedef struct {
     int32_t Hkv, len, pitch;
     float eps, scale;
     double *out;
+    /* q8 raw stream (raw == NULL): u8 rows and per-row scale / bias [Hkv, pitch] */
+    const uint8_t *q8;
+    const float *sc, *bs;
 } raw_job_t;
+
+/* Row t of kv head kvh as fp32: the bf16 raw row, or the q8 row dequantised as
+ * float(q) * scale + bias with two roundings (ESKVCache.mm:366-383; the values the q8
+ * decode kernel computes on, ESDecodeAttn.mm:316-319). */
+static void raw_row(const raw_job_t *j, int32_t kvh, int32_t t, float *x) {
+    const size_t r = (size_t) kvh * j->pitch + t;
+    if (j->raw) {
+        for (int32_t i = 0; i < 512; ++i) x[i] = orc_bf16_to_f32(j->raw[r * 512 + i]);
+    } else {
+        const float sc = j->sc[r], bs = j->bs[r];
+        for (int32_t i = 0; i < 512; ++i) {
+            const float prod = (float) j->q8[r * 512 + i] * sc;
+            x[i] = prod + bs;
+        }
+    }
+}
 
 /* One query head over all len rows of its kv head.  Reconstruction follows
  * ESDecodeAttn.mm:51-93: rinv = rsqrt(mean(kraw^2) + eps); cos/sin of the fp32
@@ -382,22 +401,23 @@ static void item_raw(void *ctx, int64_t it) {
     double *s = (double *) malloc(sizeof(double) * j->len);
     double *rv = (double *) malloc(sizeof(double) * j->len);
     double mx = -INFINITY;
+    float xr[512];
     for (int32_t t = 0; t < j->len; ++t) {
-        const uint16_t *xr = j->raw + ((size_t) kvh * j->pitch + t) * D;
+        raw_row(j, kvh, t, xr);
         double ss = 0.0;
-        for (int32_t i = 0; i < D; ++i) { double v = orc_bf16_to_f32(xr[i]); ss += v * v; }
+        for (int32_t i = 0; i < D; ++i) { double v = xr[i]; ss += v * v; }
         const float rinv = 1.0f / sqrtf((float) (ss / 512.0) + j->eps);
         rv[t] = rinv;
         double dot = 0.0;
         for (int32_t dd = 0; dd < D; ++dd) {
-            const float kn = orc_bf16_to_f32(xr[dd]) * rinv * orc_bf16_to_f32(j->kw[dd]);
+            const float kn = xr[dd] * rinv * orc_bf16_to_f32(j->kw[dd]);
             float kd = kn;
             const int32_t f = dd & 255;
             if (f < 64) {
                 const float a = (float) t * j->inv_freq[f];
                 const float c = bf(cosf(a)), sn = bf(sinf(a));
                 const int32_t pd = dd < 256 ? dd + 256 : dd - 256;
-                const float kn2 = orc_bf16_to_f32(xr[pd]) * rinv * orc_bf16_to_f32(j->kw[pd]);
+                const float kn2 = xr[pd] * rinv * orc_bf16_to_f32(j->kw[pd]);
                 const float sgn = (g_fault == 5) ? -1.0f : 1.0f;
                 kd = dd < 256 ? kn * c - sgn * kn2 * sn : kn * c + sgn * kn2 * sn;
             }
@@ -409,9 +429,9 @@ static void item_raw(void *ctx, int64_t it) {
     double den = 0.0;
     for (int32_t t = 0; t < j->len; ++t) { s[t] = exp(s[t] - mx); den += s[t]; }
     for (int32_t t = 0; t < j->len; ++t) {
-        const uint16_t *xr = j->raw + ((size_t) kvh * j->pitch + t) * D;
+        raw_row(j, kvh, t, xr);
         const double w = s[t] / den * rv[t];
-        for (int32_t i = 0; i < D; ++i) acc[i] += w * (double) orc_bf16_to_f32(xr[i]);
+        for (int32_t i = 0; i < D; ++i) acc[i] += w * (double) xr[i];
     }
     for (int32_t i = 0; i < D; ++i) j->out[(size_t) h * D + i] = acc[i];
     free(s); free(rv);
@@ -421,7 +441,42 @@ int32_t orc_decode_raw_f64(const uint16_t *q, const uint16_t *raw, int32_t Hkv, 
                            int32_t pitch, const uint16_t *kw, float eps, const float *inv_freq,
                            float scale, double *out, int32_t nthreads) {
     if (Hkv <= 0 || len <= 0 || pitch < len) return -1;
-    raw_job_t j = {q, raw, kw, inv_freq, Hkv, len, pitch, eps, scale, out};
+    raw_job_t j = {q, raw, kw, inv_freq, Hkv, len, pitch, eps, scale, out, NULL, NULL, NULL};
     run_items(item_raw, &j, (int64_t) Hkv * 8, nthreads);
     return 0;
+}
+
+int32_t orc_decode_raw_q8_f64(const uint16_t *q, const uint8_t *qraw, const float *sc, const float *bs,
+                              int32_t Hkv, int32_t len, int32_t pitch, const uint16_t *kw, float eps,
+                              const float *inv_freq, float scale, double *out, int32_t nthreads) {
+    if (Hkv <= 0 || len <= 0 || pitch < len) return -1;
+    raw_job_t j = {q, NULL, kw, inv_freq, Hkv, len, pitch, eps, scale, out, qraw, sc, bs};
+    run_items(item_raw, &j, (int64_t) Hkv * 8, nthreads);
+    return 0;
+}
+
+/* Per-row affine u8 (ESDecodeAttn.mm:491-509, ESKVCache.mm:506-511): over the row's n
+ * values (bf16 -> fp32), mn = min, mx = max; scale = max((mx - mn) / 255, 1e-8);
+ * q = min(round((x - mn) / scale), 255) with round half away from zero; bias = mn.
+ * IEEE fp32 subtraction and division. */
+void orc_quantize_rows(const uint16_t *x, int64_t rows, int32_t n, uint8_t *q, float *scale,
+                       float *bias) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint16_t *xr = x + r * n;
+        float mn = INFINITY, mx = -INFINITY;
+        for (int32_t i = 0; i < n; ++i) {
+            const float v = orc_bf16_to_f32(xr[i]);
+            if (v < mn) mn = v;
+            if (v > mx) mx = v;
+        }
+        float sc = (mx - mn) / 255.0f;
+        if (!(sc > 1e-8f)) sc = 1e-8f;
+        if (g_fault == 6) sc = (mx - mn) / 256.0f;
+        for (int32_t i = 0; i < n; ++i) {
+            const float t = roundf((orc_bf16_to_f32(xr[i]) - mn) / sc);
+            q[r * n + i] = (uint8_t) (t < 255.0f ? t : 255.0f);
+        }
+        scale[r] = sc;
+        bias[r] = mn;
+    }
 }

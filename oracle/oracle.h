@@ -20,6 +20,8 @@
  *                        of ESDecodeAttn.mm:253-273, applied to plain bf16 K/V
  *   orc_rope_inv_freq    ESRotaryEmbedding.mm:8-23
  *   orc_rms_norm_rows    ESRMSNorm.mm:20-27 (manual f32 path)
+ *   orc_quantize_rows    ESDecodeAttn.mm:491-539 (esQuantizeRawRows: per-row affine u8)
+ *   orc_decode_raw_q8_f64 ESDecodeAttn.mm:275-369 (q8 rows dequantised, then as below)
  *   orc_decode_raw_f64   ESDecodeAttn.mm:17-117 reconstruction (rinv, kw, p-RoPE pairs
  *                        (d, d+256) for d < 64, bf16 cos/sin, bf16 K, V = kraw*rinv)
  *                        + merge, evaluated in fp64 after the kernel's rounding points
@@ -106,6 +108,18 @@ void orc_rms_norm_rows(const uint16_t *x, const uint16_t *w, int64_t rows, int32
 int32_t orc_decode_raw_f64(const uint16_t *q, const uint16_t *raw, int32_t Hkv, int32_t len,
                            int32_t pitch, const uint16_t *kw, float eps, const float *inv_freq,
                            float scale, double *out, int32_t nthreads);
+
+/* Raw-K decode over a q8 raw stream: u8 rows qraw [Hkv, pitch, 512] with per-row scale and
+ * bias [Hkv, pitch] f32, dequantised as float(q) * scale + bias; otherwise as
+ * orc_decode_raw_f64 (esDecodeAttnGlobalQ8, ESDecodeAttn.mm:275-369, 455-489). */
+int32_t orc_decode_raw_q8_f64(const uint16_t *q, const uint8_t *qraw, const float *sc, const float *bs,
+                              int32_t Hkv, int32_t len, int32_t pitch, const uint16_t *kw, float eps,
+                              const float *inv_freq, float scale, double *out, int32_t nthreads);
+
+/* Per-row affine u8 quantisation of bf16 rows [rows, n] (esQuantizeRawRows,
+ * ESDecodeAttn.mm:491-539): q [rows, n] u8, scale / bias [rows] f32. */
+void orc_quantize_rows(const uint16_t *x, int64_t rows, int32_t n, uint8_t *q, float *scale,
+                       float *bias);
 
 /* Planted-mistake switch for the oracle's own self-tests (0 = none).  Used only by
  * tests that show a plausible mistake is caught by the pins. */

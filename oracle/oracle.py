@@ -69,6 +69,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_decode_raw_f64.argtypes = [_P, _P, i32, i32, i32, _P, ctypes.c_float, _P,
                                      ctypes.c_float, _P, i32]
     L.orc_decode_raw_f64.restype = i32
+    L.orc_decode_raw_q8_f64.argtypes = [_P, _P, _P, _P, i32, i32, i32, _P, ctypes.c_float, _P,
+                                        ctypes.c_float, _P, i32]
+    L.orc_decode_raw_q8_f64.restype = i32
+    L.orc_quantize_rows.argtypes = [_P, ctypes.c_int64, i32, _P, _P, _P]
     L.orc_set_fault.argtypes = [i32]
 
 
@@ -211,6 +215,36 @@ def decode_raw_f64(q, raw, len_: int, kw, eps: float, inv_freq, scale: float = 1
     if rc != 0:
         raise ValueError("orc_decode_raw_f64 rejected the shapes")
     return out
+
+
+def decode_raw_q8_f64(q, qraw, sc, bs, len_: int, kw, eps: float, inv_freq, scale: float = 1.0,
+                      threads=None) -> np.ndarray:
+    """q8 raw stream: qraw [Hkv, pitch, 512] u8, sc / bs [Hkv, pitch] (or [Hkv, pitch, 1]) f32."""
+    Hkv, pitch, D = qraw.shape
+    assert D == 512 and q.shape == (Hkv * 8, 512)
+    qraw = np.ascontiguousarray(qraw, dtype=np.uint8)
+    sc = np.ascontiguousarray(sc, dtype=np.float32).reshape(Hkv, pitch)
+    bs = np.ascontiguousarray(bs, dtype=np.float32).reshape(Hkv, pitch)
+    out = np.empty((Hkv * 8, 512), dtype=np.float64)
+    inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    rc = lib().orc_decode_raw_q8_f64(_ptr(q), _ptr(qraw), _ptr(sc), _ptr(bs), Hkv, int(len_), pitch,
+                                     _ptr(kw), ctypes.c_float(eps), _ptr(inv), ctypes.c_float(scale),
+                                     _ptr(out), _threads(threads))
+    if rc != 0:
+        raise ValueError("orc_decode_raw_q8_f64 rejected the shapes")
+    return out
+
+
+def quantize_rows(x: np.ndarray):
+    """Per-row affine u8 of bf16 rows x [..., n] -> (q u8 [..., n], scale f32 [...], bias f32 [...])."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    n = x.shape[-1]
+    rows = x.size // n
+    q = np.empty(x.shape, dtype=np.uint8)
+    sc = np.empty(x.shape[:-1], dtype=np.float32)
+    bs = np.empty(x.shape[:-1], dtype=np.float32)
+    lib().orc_quantize_rows(_ptr(x), rows, n, _ptr(q), _ptr(sc), _ptr(bs))
+    return q, sc, bs
 
 
 class planted_fault:

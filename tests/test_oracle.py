@@ -419,6 +419,59 @@ def test_raw_decode_matches_hf_rope_composition():
     assert np.abs(ours - ref).max() < 2e-3
 
 
+# ------------------------------------------------------------ q8 raw stream
+
+def test_quantize_rows_properties():
+    """Per-row affine u8 (ESDecodeAttn.mm:491-509): the row's min maps to 0 and its max
+    to 255, every value dequantises to within half a step, scale = (max - min) / 255 in
+    fp32 and bias = min."""
+    rng = np.random.default_rng(31)
+    x = orc.to_bf16((rng.standard_normal((40, 512)) * rng.uniform(0.01, 5, (40, 1))).astype(np.float32))
+    q, sc, bs = orc.quantize_rows(x)
+    xf = orc.from_bf16(x).astype(np.float32)
+    mn, mx = xf.min(axis=1), xf.max(axis=1)
+    assert np.array_equal(bs, mn)
+    assert np.array_equal(sc, np.maximum((mx - mn) / np.float32(255), np.float32(1e-8)))
+    assert (q[np.arange(40), xf.argmin(axis=1)] == 0).all() and (q[np.arange(40), xf.argmax(axis=1)] == 255).all()
+    deq = q.astype(np.float64) * sc[:, None] + bs[:, None]
+    assert (np.abs(deq - xf) <= sc[:, None] * 0.5 * (1 + 1e-5) + np.abs(xf) * 1e-6).all()
+
+
+def test_quantize_rows_rounds_ties_away_from_zero():
+    # range 255/16 gives scale 1/16 exactly; 2.5/16 sits on a tie (round-half-even would give 2)
+    row = np.zeros(512, np.float32)
+    row[1], row[2], row[3] = 255 / 16, 2.5 / 16, 7.5 / 16
+    q, sc, bs = orc.quantize_rows(orc.to_bf16(row)[None])
+    assert sc[0] == np.float32(1 / 16) and bs[0] == 0
+    assert q[0, 1] == 255 and q[0, 2] == 3 and q[0, 3] == 8 and q[0, 0] == 0
+
+
+def test_quantize_rows_constant_row_keeps_a_finite_scale():
+    x = orc.to_bf16(np.full((2, 512), [[0.75], [-3.0]], np.float32))
+    q, sc, bs = orc.quantize_rows(x)
+    assert (q == 0).all() and (sc == np.float32(1e-8)).all() and list(bs) == [0.75, -3.0]
+
+
+def test_q8_decode_equals_raw_decode_on_exactly_representable_rows():
+    """With power-of-two scales and integer biases every dequantised value q * scale + bias
+    is exact in fp32 and in bf16, so the q8 decode must reproduce the (pinned) raw-K decode
+    of those bf16 rows bit for bit."""
+    rng = np.random.default_rng(37)
+    Hkv, pitch, L = 2, 60, 53
+    qraw = rng.integers(0, 256, size=(Hkv, pitch, 512), dtype=np.uint8)
+    sc = (2.0 ** -rng.integers(4, 7, size=(Hkv, pitch))).astype(np.float32)
+    bs = -rng.integers(1, 5, size=(Hkv, pitch)).astype(np.float32)
+    deq = qraw.astype(np.float32) * sc[..., None] + bs[..., None]
+    raw = orc.to_bf16(deq)
+    assert np.array_equal(orc.from_bf16(raw), deq)
+    q = rms_rows(rng, (Hkv * 8, 512))
+    kw = orc.to_bf16((1.0 + 0.1 * rng.standard_normal(512)).astype(np.float32))
+    inv = orc.rope_inv_freq(512, 1.0e6, 0.25)
+    a = orc.decode_raw_q8_f64(q, qraw, sc, bs, L, kw, 1e-6, inv, scale=512 ** -0.5)
+    b = orc.decode_raw_f64(q, raw, L, kw, 1e-6, inv, scale=512 ** -0.5)
+    assert np.array_equal(a, b)
+
+
 # ------------------------------------------------------------ planted faults
 
 def _pins_fail(fn) -> bool:
@@ -440,6 +493,7 @@ def _pins_fail(fn) -> bool:
                                                          shared=False))),
     (4, lambda: test_append_writes_exactly_one_row(False, False)),
     (5, lambda: test_raw_decode_matches_hf_rope_composition()),
+    (6, lambda: test_quantize_rows_properties()),
 ])
 def test_planted_fault_is_caught(fault, pin):
     with orc.planted_fault(fault):
