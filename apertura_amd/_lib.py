@@ -22,7 +22,8 @@ EXPORTS = (
     # include/esda.h
     "esda_decode_workspace_size", "esda_decode", "esda_decode_stages", "esda_decode_status",
     "esda_kv_append", "esda_decode_raw_workspace_size", "esda_decode_raw",
-    "esda_decode_raw_stages", "esda_fill_i32", "esda_last_error", "esda_version",
+    "esda_decode_raw_stages", "esda_decode_raw_q8", "esda_decode_raw_q8_stages", "esda_quantize_raw_rows",
+    "esda_fill_i32", "esda_last_error", "esda_version",
     # include/esda_cache.h
     "esda_cache_create", "esda_cache_destroy", "esda_cache_update", "esda_cache_update_raw",
     "esda_cache_current", "esda_cache_current_raw", "esda_cache_decode", "esda_cache_decode_raw", "esda_cache_slot",
@@ -83,6 +84,17 @@ class RawArgs(ctypes.Structure):
     ]
 
 
+class RawQ8Args(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k_new", ctypes.c_void_p), ("q8_cache", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+        ("sb_seq_stride", ctypes.c_int64), ("sb_head_stride", ctypes.c_int64),
+        ("pos", ctypes.c_void_p), ("kw", ctypes.c_void_p), ("inv_freq", ctypes.c_void_p),
+        ("out", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class View(ctypes.Structure):
     """esda_view: element (h, r, d) at data[h*head_stride + r*head_dim + d]."""
     _fields_ = [
@@ -114,6 +126,10 @@ def lib() -> ctypes.CDLL:
         L.esda_decode_raw.argtypes = [ctypes.POINTER(RawDesc), ctypes.POINTER(RawArgs), P]
         L.esda_decode_raw_stages.argtypes = [ctypes.POINTER(RawDesc), ctypes.POINTER(RawArgs),
                                              ctypes.c_int, P]
+        L.esda_decode_raw_q8.argtypes = [ctypes.POINTER(RawDesc), ctypes.POINTER(RawQ8Args), P]
+        L.esda_decode_raw_q8_stages.argtypes = [ctypes.POINTER(RawDesc), ctypes.POINTER(RawQ8Args),
+                                                ctypes.c_int, P]
+        L.esda_quantize_raw_rows.argtypes = [P, i32, i32, P, i64, P, P, i64, i32, P]
         L.esda_fill_i32.argtypes = [P, i32, i32, P]
         L.esda_last_error.restype = ctypes.c_char_p
         L.esda_last_error.argtypes = []

@@ -27,6 +27,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <utility>
 
 #include "esda.h"
@@ -100,6 +101,11 @@ struct AttendParams {
     const uint16_t *kw;
     const float *inv_freq;
     float eps;
+    // q8 raw-K mode: u8 rows at q8 (strides as for k_cache, in bytes) and per-row scale /
+    // bias at qsc / qbs[b * sb_seq_stride + kv head * sb_head_stride + row]
+    unsigned char *q8;
+    float *qsc, *qbs;
+    long long sb_seq_stride, sb_head_stride;
 };
 
 // Max over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48) without
@@ -207,6 +213,15 @@ __device__ __forceinline__ void lds_dma16_s(const void *sbase, unsigned voff, un
 #endif
 }
 
+// One 4-byte LDS DMA per active lane (global_load_lds_dword): active lane l's 4 bytes land
+// at LDS byte address lds + 4*l.  Counted by the ring like lds_dma16.
+__device__ __forceinline__ void lds_dma4(const void *src, unsigned lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const unsigned base = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(base) : "memory");
+#endif
+}
+
 // a / b for non-negative a, b > 0: 32-bit division when both fit (the common case),
 // which is far shorter than the 64-bit sequence.
 __device__ __forceinline__ long long udiv64(long long a, long long b) {
@@ -243,8 +258,20 @@ constexpr int kRawDim = 512;
 constexpr int kRopePairs = 64;
 constexpr int kTabStride = 68;  // words per cos/sin table row: 64 + 4 (conflict-free 128-bit reads)
 // LDS of the raw-mode exchanges for NW waves: row sums of squares [3][16][NW], the
-// cos/sin tables [2][16][kTabStride], the row norm factors [2][2][16].
-constexpr int raw_extra_lds(int nw) { return 3 * 16 * nw * 4 + 2 * 16 * kTabStride * 4 + 2 * 2 * 16 * 4; }
+// cos/sin tables [2][16][kTabStride], the row factors [2][3][16]; q8 mode adds the row
+// sums [3][16][NW].
+constexpr int raw_extra_lds(int nw, bool q8 = false) {
+    return 3 * 16 * nw * 4 + 2 * 16 * kTabStride * 4 + 2 * 3 * 16 * 4 + (q8 ? 3 * 16 * nw * 4 : 0);
+}
+// q8 raw-K mode: u8 stages are widened into bf16 staging slots laid out as the D = 512
+// ring (16 rows of 1056-byte blocks), four deep; per-row scale / bias ride beside each
+// u8 stage.
+constexpr int kQ8Stage = 16 * 1056;
+constexpr int kQ8Slots = 4;
+constexpr int kQ8SbStages = 16;
+constexpr int q8_extra_lds(int nw) {
+    return raw_extra_lds(nw, true) + kQ8Slots * kQ8Stage + kQ8SbStages * 2 * 16 * 4;
+}
 
 // Cody-Waite split of pi/2 (hi + mid + lo, each the nearest fp32 to what remains).
 constexpr float kTwoOverPi = 0.636619746685028076171875f;     // fp32(2/pi)
@@ -311,7 +338,15 @@ __device__ __forceinline__ float bf16_hi(unsigned w) { return __builtin_bit_cast
 // RPK (raw mode): kv heads per workgroup, 1 or 2 (the host's pk).  With 2, a stage holds 8
 // rows of each of two kv heads of one sequence at the same 8 positions, so the cos/sin
 // table of a stage has 8 rows instead of 16: half the table work per stage.
-template <int D, bool SHARED, int NW, bool RAW, int RPK = 1>
+//
+// Q8 (raw mode over a q8 raw stream, esDecodeAttnGlobalQ8, ESDecodeAttn.mm:275-369): rows
+// are u8 with a per-row scale and bias, x = q * scale + bias.  The u8 ring (512-byte rows)
+// is widened into bf16 staging slots three stages ahead, where q is exact, so the raw
+// pipeline runs on q itself: the Gram diagonal and a row sum give sum(q^2) and sum(q)
+// exactly, hence sum(x^2); K = bf16(rope(fma(q, scale*rinv, bias*rinv) * kw)); V enters
+// as q with the weight P = bf16(e * scale * rinv) and the bias as sum P * bias / scale.
+// The workgroup holding a sequence's new row quantizes it into the cache first.
+template <int D, bool SHARED, int NW, bool RAW, int RPK = 1, bool Q8 = false>
 // The LDS ring allows one workgroup per CU, i.e. NW/4 waves per SIMD: telling the
 // compiler so lifts the register limit it would otherwise keep for higher occupancy,
 // which it meets by serialising LDS reads behind their uses.
@@ -319,16 +354,22 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_
 void attend_kernel(AttendParams p) {
     static_assert(!RAW || (D == kRawDim && SHARED && (NW == 4 || NW == 8)), "raw mode: one 512-dim stream, 4 or 8 waves");
     static_assert(RPK == 1 || (RAW && RPK == 2), "kv-head packing is a runtime choice outside raw mode");
-    using R = Ring<D, SHARED, NW, RAW ? raw_extra_lds(NW) : 0>;
-    constexpr int NS = R::NS, DW = R::DW, KKW = R::KKW, DTW = R::DTW;
+    static_assert(!Q8 || (RAW && NW == 8), "q8 mode is raw mode with 8 waves");
+    // R: the compute layout of a stage (and, outside q8 mode, the DMA ring); RD: the DMA ring.
+    using R = Ring<D, SHARED, NW, RAW && !Q8 ? raw_extra_lds(NW) : 0>;
+    using RD = std::conditional_t<Q8, Ring<256, true, NW, q8_extra_lds(NW)>, R>;
+    constexpr int NS = RD::NS, DW = R::DW, KKW = R::KKW, DTW = R::DTW;
+    // DMA instructions per wave per stage (q8: the u8 rows plus one scale / bias piece)
+    constexpr int DPW = Q8 ? RD::DPT + 1 : RD::DPW;
     // Stages between the one being accumulated and the newest one that must have landed.
-    constexpr int AHEAD = RAW ? 2 : 1;
+    constexpr int AHEAD = Q8 ? 3 : RAW ? 2 : 1;
     static_assert(NS >= AHEAD + 3, "the ring must hold the look-ahead stages and one in flight");
+    static_assert(!Q8 || NS <= kQ8SbStages, "one scale / bias area per ring stage");
     // Distinct arrays per stage: the compiler tracks DMA completion per LDS object, so a
     // read of stage u only waits for stage u's DMA, never for the stages behind it.
-    __shared__ __attribute__((aligned(16))) unsigned char r0[R::SB], r1[R::SB], r2[R::SB], r3[R::SB],
-        r4[R::SB], r5[R::SB], r6[R::SB], r7[R::SB], r8[R::SB], r9[R::SB], r10[R::SB], r11[R::SB],
-        r12[R::SB], r13[R::SB], r14[R::SB], r15[R::SB];
+    __shared__ __attribute__((aligned(16))) unsigned char r0[RD::SB], r1[RD::SB], r2[RD::SB], r3[RD::SB],
+        r4[RD::SB], r5[RD::SB], r6[RD::SB], r7[RD::SB], r8[RD::SB], r9[RD::SB], r10[RD::SB], r11[RD::SB],
+        r12[RD::SB], r13[RD::SB], r14[RD::SB], r15[RD::SB];
     // Stage buffer u (a compile-time index).
     auto ring = [&](auto uc) -> unsigned char * {
         constexpr int u = decltype(uc)::value % NS;
@@ -353,11 +394,18 @@ void attend_kernel(AttendParams p) {
     // Raw mode: per-row partial sums of squares xss[stage % 3][row][wave], the cos/sin
     // table xtab[stage % 2][row][pair] (bf16 cos in the low half, sin in the high half)
     // and the per-row norm factors xr.
-    __shared__ __attribute__((aligned(16))) unsigned char rawlds[RAW ? raw_extra_lds(NW) : 16];
+    __shared__ __attribute__((aligned(16))) unsigned char rawlds[RAW ? raw_extra_lds(NW, Q8) : 16];
     auto *xss = reinterpret_cast<float (*)[16][NW]>(rawlds);
     auto *xtab = reinterpret_cast<unsigned (*)[16][kTabStride]>(rawlds + 3 * 16 * NW * 4);
-    // xr[stage % 2][0][row] = rinv, xr[stage % 2][1][row] = 1 / rinv
-    auto *xr = reinterpret_cast<float (*)[2][16]>(rawlds + 3 * 16 * NW * 4 + 2 * 16 * kTabStride * 4);
+    // xr[stage % 2][0][row] = the weight factor (rinv; q8: scale * rinv), [1] its inverse,
+    // [2] (q8) bias / scale
+    auto *xr = reinterpret_cast<float (*)[3][16]>(rawlds + 3 * 16 * NW * 4 + 2 * 16 * kTabStride * 4);
+    // q8: row sums of q [stage % 3][row][wave]
+    auto *xsq = reinterpret_cast<float (*)[16][NW]>(rawlds + 3 * 16 * NW * 4 + 2 * 16 * kTabStride * 4 +
+                                                    2 * 3 * 16 * 4);
+    // q8: bf16 staging slots and the per-stage scale / bias rows
+    __shared__ __attribute__((aligned(16))) unsigned char q8stg[Q8 ? kQ8Slots * kQ8Stage : 16];
+    __shared__ __attribute__((aligned(16))) float q8sb[Q8 ? kQ8SbStages : 1][2][16];
     // cos/sin table of a stage: TR rows (one per position) x 64 pairs over 64*NW threads
     constexpr int TR = 16 / RPK;
     constexpr int EPT = TR * 64 / (64 * NW);
@@ -391,6 +439,9 @@ void attend_kernel(AttendParams p) {
     uint16_t *vbase = p.v_cache + head_off;
     const uint16_t *knew = append ? p.k_new + ((size_t) b * p.Hkv + kvh) * pk * D : nullptr;
     const uint16_t *vnew = SHARED ? knew : p.v_new + ((size_t) b * p.Hkv + kvh) * pk * D;
+    // q8: the u8 rows (same element strides, in bytes) and the scale / bias rows
+    unsigned char *q8base = Q8 ? p.q8 + head_off : nullptr;
+    const size_t sb_off = Q8 ? (size_t) b * p.sb_seq_stride + (size_t) kvh * pk * p.sb_head_stride : 0;
 
     // 32-dim chunk of the QK k-step kk of this wave.  Raw mode interleaves the waves so
     // that each rotary pair (d, d + 256), d < 64, sits in one lane of wave 0 or 1.
@@ -427,50 +478,144 @@ void attend_kernel(AttendParams p) {
 #pragma unroll
         for (int e = 0; e < EPT; ++e) invf[e] = p.inv_freq[EPT * (tid % TPR) + e];
     }
+    if constexpr (Q8) {
+        // The new row of each kv head of the group is quantized into the cache before the
+        // ring starts (wave pr: kv head pr), esQuantizeRawRows' arithmetic
+        // (ESDecodeAttn.mm:491-509): min / max over the row, scale = max((max - min) / 255,
+        // 1e-8), q = min(round((x - min) / scale), 255) rounding half away from zero, IEEE
+        // division.  The ring then reads it like every other row.
+        if (append && j1 == sv.nvis) {
+            for (int pr = wave; pr < pk; pr += NW) {
+                const u32x4 t = *reinterpret_cast<const u32x4 *>(knew + pr * D + lane * 8);
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x[2 * e] = bf16_lo(t[e]);
+                    x[2 * e + 1] = bf16_hi(t[e]);
+                }
+                float mn = x[0], mx = x[0];
+#pragma unroll
+                for (int e = 1; e < 8; ++e) {
+                    mn = fminf(mn, x[e]);
+                    mx = fmaxf(mx, x[e]);
+                }
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) {
+                    mn = fminf(mn, __shfl_xor(mn, o));
+                    mx = fmaxf(mx, __shfl_xor(mx, o));
+                }
+                float scl = (mx - mn) / 255.0f;
+                if (!(scl > 1e-8f)) scl = 1e-8f;
+                unsigned lo = 0u, hi = 0u;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const unsigned qi = (unsigned) fminf(roundf((x[e] - mn) / scl), 255.0f);
+                    if (e < 4) lo |= qi << (8 * e);
+                    else hi |= qi << (8 * (e - 4));
+                }
+                unsigned char *row = q8base + (size_t) pr * p.head_stride + (size_t) sv.newrow * kRawDim;
+                *reinterpret_cast<uint2 *>(row + lane * 8) = uint2{lo, hi};
+                if (lane == 0) {
+                    const size_t at = sb_off + (size_t) pr * p.sb_head_stride + (size_t) sv.newrow;
+                    p.qsc[at] = scl;
+                    p.qbs[at] = mn;
+                }
+            }
+        }
+    }
     ESDA_WAIT_VM(0);  // operands are in registers before the ring starts counting its own loads
+    if constexpr (Q8) lds_barrier();  // and the new row's stores are done before any wave's DMA
 
     // DMA source slot of this lane: sub-row dq, chunk dchunk of the row.
-    const int dq = lane / R::CPR, dchunk = lane % R::CPR;
+    const int dq = lane / RD::CPR, dchunk = lane % RD::CPR;
     const int nst = (j1 - j0 + RPP - 1) >> lrpp;
+    constexpr int EB = Q8 ? 1 : 2;                // bytes per cache element (strides count elements)
+    constexpr int ROWB = Q8 ? kRawDim : D * 2;    // bytes per cache row
     // Per-lane byte offsets of this wave's DMA slots inside a stage's row range (stage row
     // r: kv head r / RPP of the group, row r % RPP; below 2^31 bytes, checked by the host).
-    unsigned dvoff[R::DPT];
+    unsigned dvoff[RD::DPT];
 #pragma unroll
-    for (int t = 0; t < R::DPT; ++t) {
-        const int r = wave * R::DPT + t + dq * R::NI;
-        dvoff[t] = (unsigned) ((((size_t) (r >> lrpp) * p.head_stride) + (size_t) (r & (RPP - 1)) * D + dchunk * 8) * 2);
+    for (int t = 0; t < RD::DPT; ++t) {
+        const int r = wave * RD::DPT + t + dq * RD::NI;
+        dvoff[t] = (unsigned) ((size_t) (r >> lrpp) * p.head_stride * EB + (size_t) (r & (RPP - 1)) * ROWB + dchunk * 16);
     }
-    auto dma = [&](int st, unsigned char *buf) {
+    // DMA of stage st into ring buffer `buf` (ring slot `slot`).
+    auto dma = [&](int st, unsigned char *buf, int slot) {
         const int jst = j0 + st * RPP;
+        if constexpr (Q8) {
+            // scale / bias of the stage's rows: wave w loads the scales (w < 4) or biases of
+            // stage rows 4(w % 4) .. +3, one row per lane
+            if (lane < 4) {
+                const int sr = 4 * (wave & 3) + lane, pr = sr >> lrpp;
+                const int j = jst + (sr & (RPP - 1)), jj = j < j1 ? j : j1 - 1;
+                const float *src = (wave < 4 ? p.qsc : p.qbs) + sb_off + (size_t) pr * p.sb_head_stride +
+                                   (size_t) (sv.first + jj);
+                lds_dma4(src, lds_addr(&q8sb[slot][wave >> 2][4 * (wave & 3)]));
+            }
+        }
         if (jst + RPP < j1 && sv.first + jst + RPP <= p.cap) {
             // Interior stage: RPP consecutive cache rows per kv head, none clamped or new.
+            if constexpr (Q8) {
+                const unsigned char *qb = q8base + (size_t) (sv.first + jst) * kRawDim;
+#pragma unroll
+                for (int t = 0; t < RD::DPT; ++t) lds_dma16_s(qb, dvoff[t], lds_addr(buf) + (wave * RD::DPT + t) * RD::BLK);
+                return;
+            }
             const uint16_t *kb = kbase + (size_t) (sv.first + jst) * D;
             const uint16_t *vb = vbase + (size_t) (sv.first + jst) * D;
 #pragma unroll
-            for (int t = 0; t < R::DPT; ++t) {
-                const int i = wave * R::DPT + t;
-                lds_dma16_s(kb, dvoff[t], lds_addr(buf) + i * R::BLK);
-                if constexpr (!SHARED) lds_dma16_s(vb, dvoff[t], lds_addr(buf) + R::TB + i * R::BLK);
+            for (int t = 0; t < RD::DPT; ++t) {
+                const int i = wave * RD::DPT + t;
+                lds_dma16_s(kb, dvoff[t], lds_addr(buf) + i * RD::BLK);
+                if constexpr (!SHARED) lds_dma16_s(vb, dvoff[t], lds_addr(buf) + RD::TB + i * RD::BLK);
             }
             return;
         }
 #pragma unroll
-        for (int t = 0; t < R::DPT; ++t) {
-            const int i = wave * R::DPT + t;            // DMA block of this stage
-            const int sr = i + dq * R::NI;              // stage row this lane feeds
+        for (int t = 0; t < RD::DPT; ++t) {
+            const int i = wave * RD::DPT + t;           // DMA block of this stage
+            const int sr = i + dq * RD::NI;             // stage row this lane feeds
             const int pr = sr >> lrpp;                  // its kv head within the group
             const int j = jst + (sr & (RPP - 1));       // its logical row
             const int jj = j < j1 ? j : j1 - 1;          // clamp: masked rows read a visible row
             int r = sv.first + jj;
             if (r >= p.cap) r -= p.cap;
+            if constexpr (Q8) {
+                // the new row was quantized into the cache before the ring started
+                lds_dma16(q8base + (size_t) pr * p.head_stride + (size_t) r * kRawDim + dchunk * 16,
+                          lds_addr(buf) + i * RD::BLK);
+                continue;
+            }
             const bool from_new = append && (jj == sv.nvis - 1);
             const size_t hoff = (size_t) pr * p.head_stride + (size_t) r * D;
             const uint16_t *ks = (from_new ? knew + pr * D : kbase + hoff) + dchunk * 8;
-            lds_dma16(ks, lds_addr(buf) + i * R::BLK);
+            lds_dma16(ks, lds_addr(buf) + i * RD::BLK);
             if constexpr (!SHARED) {
                 const uint16_t *vs = (from_new ? vnew + pr * D : vbase + hoff) + dchunk * 8;
-                lds_dma16(vs, lds_addr(buf) + R::TB + i * R::BLK);
+                lds_dma16(vs, lds_addr(buf) + RD::TB + i * RD::BLK);
             }
+        }
+    };
+    // q8: bf16 staging slot of stage s, and the widening of u8 stage s (ring buffer u8buf)
+    // into it: thread t takes row t / 32, bytes 16 (t % 32) .. +16; a byte's bf16 is the
+    // upper half of its fp32 (exact for 0 .. 255).
+    auto stg = [&](int s) -> unsigned char * { return q8stg + (s & (kQ8Slots - 1)) * kQ8Stage; };
+    auto convert = [&](int s, const unsigned char *u8buf) {
+        if constexpr (Q8) {
+            const int r = tid >> 5, c16 = tid & 31;
+            const u32x4 w = *reinterpret_cast<const u32x4 *>(u8buf + (r & 7) * RD::BLK + (r >> 3) * kRawDim + c16 * 16);
+            unsigned o[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const unsigned lo = __builtin_bit_cast(unsigned, (float) ((w[e] >> (16 * h)) & 255u));
+                    const unsigned hi = __builtin_bit_cast(unsigned, (float) ((w[e] >> (16 * h + 8)) & 255u));
+                    o[2 * e + h] = __builtin_amdgcn_perm(hi, lo, 0x07060302u);
+                }
+            unsigned char *dst = stg(s) + r * R::BLK + c16 * 32;
+            *reinterpret_cast<u32x4 *>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+            *reinterpret_cast<u32x4 *>(dst + 16) = u32x4{o[4], o[5], o[6], o[7]};
         }
     };
 
@@ -483,6 +628,7 @@ void attend_kernel(AttendParams p) {
     constexpr int VOFF = SHARED ? 0 : R::TB;
 
     float m = -INFINITY, l = 0.0f;
+    float bt = 0.0f;  // q8: sum of P * bias / scale of this lane's head (the bias part of PV)
     f32x4 acc[DTW];
 #pragma unroll
     for (int dt = 0; dt < DTW; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -509,18 +655,27 @@ void attend_kernel(AttendParams p) {
     // diagonal of the stage's 16x16 Gram matrix over those dims.  The A and B operands of
     // v_mfma_f32_16x16x32_bf16 take the same lane data (row li, dims 8lg..+8 of each
     // chunk), and products of bf16 values are exact in the fp32 accumulation.
+    // q8: the operand is q itself, so the diagonal is sum(q^2), and an MFMA against ones
+    // gives sum(q) -> xsq; both are exact integers (per wave at most 64 * 255^2 < 2^24).
     auto publish_ss = [&](int buf) {
         if constexpr (RAW) {
-            f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f};
+            f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f}, g1 = {0.0f, 0.0f, 0.0f, 0.0f};
+            bf16x8 ones;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ones[e] = (__bf16) 1.0f;
 #pragma unroll
             for (int kk = 0; kk < KKW; ++kk) {
                 const bf16x8 a = __builtin_bit_cast(bf16x8, araw[kk]);
                 g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, a, g, 0, 0, 0);
+                if constexpr (Q8) g1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, g1, 0, 0, 0);
             }
             // C layout: lane (li, lg) holds C[4lg + i][li]; row li's diagonal entry is
             // register li - 4lg of the lanes with lg == li / 4.
             const int i = li - 4 * lg;
-            if (i >= 0 && i < 4) xss[buf][li][wave] = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
+            if (i >= 0 && i < 4) {
+                xss[buf][li][wave] = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
+                if constexpr (Q8) xsq[buf][li][wave] = i == 0 ? g1[0] : i == 1 ? g1[1] : i == 2 ? g1[2] : g1[3];
+            }
         }
     };
     // cos/sin table of stage st: this thread's row tid / TPR, pairs EPT*(tid % TPR) .. +EPT.
@@ -556,24 +711,59 @@ void attend_kernel(AttendParams p) {
         }
         return sum * (1.0f / kRawDim) + p.eps;
     };
-    // Scores of the stage held in araw: rebuild K in registers, then MFMA.
-    auto qk_raw = [&](int ssbuf, int tabbuf, int par) {
+    // q8: mean(x^2) + eps of a row from its exact integer sums, x = q * scale + bias:
+    // mean(x^2) = scale^2 var(q) + mean(x)^2 with 512^2 var(q) = 512 sum(q^2) - sum(q)^2, an
+    // exact integer (no cancellation in fp32).
+    auto q8_ms = [&](int buf, int row, float scl, float bias) {
+        int s2 = 0, s1 = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            s2 += (int) xss[buf][row][w];
+            s1 += (int) xsq[buf][row][w];
+        }
+        const float var = (float) (512LL * s2 - (long long) s1 * s1);
+        const float mean = scl * ((float) s1 * (1.0f / kRawDim)) + bias;
+        return scl * scl * var * (1.0f / (kRawDim * kRawDim)) + mean * mean + p.eps;
+    };
+    // Scores of the stage held in araw: rebuild K in registers, then MFMA.  sbslot: the
+    // ring slot of the stage (q8: its scale / bias rows).
+    auto qk_raw = [&](int ssbuf, int tabbuf, int par, int sbslot) {
         if constexpr (RAW) {
-            const float ms = row_ms(ssbuf, li);
-            const float rinv = __builtin_amdgcn_rsqf(ms);
-            // rinv and 1/rinv (= ms * rinv) of the row, for the stage's softmax weights.
-            if (wave == 0 && lg == 0) {
-                xr[par][0][li] = rinv;
-                xr[par][1][li] = ms * rinv;
-            }
             float kn[KKW][8];
-    #pragma unroll
-            for (int kk = 0; kk < KKW; ++kk)
-    #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    kn[kk][2 * e] = bf16_lo(araw[kk][e]) * rinv * kwf[kk][2 * e];
-                    kn[kk][2 * e + 1] = bf16_hi(araw[kk][e]) * rinv * kwf[kk][2 * e + 1];
+            if constexpr (Q8) {
+                const float scl = q8sb[sbslot][0][li], bias = q8sb[sbslot][1][li];
+                const float rinv = __builtin_amdgcn_rsqf(q8_ms(ssbuf, li, scl, bias));
+                const float alpha = scl * rinv, beta = bias * rinv;
+                // the weight factor scale * rinv, its inverse, and bias / scale
+                if (wave == 0 && lg == 0) {
+                    xr[par][0][li] = alpha;
+                    xr[par][1][li] = 1.0f / alpha;
+                    xr[par][2][li] = bias / scl;
                 }
+    #pragma unroll
+                for (int kk = 0; kk < KKW; ++kk)
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kn[kk][2 * e] = __builtin_fmaf(bf16_lo(araw[kk][e]), alpha, beta) * kwf[kk][2 * e];
+                        kn[kk][2 * e + 1] = __builtin_fmaf(bf16_hi(araw[kk][e]), alpha, beta) * kwf[kk][2 * e + 1];
+                    }
+            } else {
+                (void) sbslot;
+                const float ms = row_ms(ssbuf, li);
+                const float rinv = __builtin_amdgcn_rsqf(ms);
+                // rinv and 1/rinv (= ms * rinv) of the row, for the stage's softmax weights.
+                if (wave == 0 && lg == 0) {
+                    xr[par][0][li] = rinv;
+                    xr[par][1][li] = ms * rinv;
+                }
+    #pragma unroll
+                for (int kk = 0; kk < KKW; ++kk)
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kn[kk][2 * e] = bf16_lo(araw[kk][e]) * rinv * kwf[kk][2 * e];
+                        kn[kk][2 * e + 1] = bf16_hi(araw[kk][e]) * rinv * kwf[kk][2 * e + 1];
+                    }
+            }
             if (wave < 2) {
                 // chunk `wave` (k-step 0) holds dims d = 32*wave + 8lg + e < 64; chunk wave + 8
                 // (k-step KP) their rotary partners.
@@ -601,24 +791,37 @@ void attend_kernel(AttendParams p) {
         }
     };
 
+    // The buffer the compute reads for stage s held in ring slot uc: the ring itself, or
+    // (q8) the stage's bf16 staging slot.
+    auto cbuf = [&](int s, auto uc) -> unsigned char * {
+        if constexpr (Q8) return stg(s);
+        else return ring(uc);
+    };
     // Prologue: fill NS-1 stages; publish what iteration 0 needs.
     unroll<NS - 1>([&](auto uc) {
         constexpr int u = decltype(uc)::value;
-        if (u < nst) dma(u, ring(uc));
+        if (u < nst) dma(u, ring(uc), u);
     });
     if constexpr (RAW) {
-        // stages 0..2 landed (stage 2 for the first iteration's sums of squares)
+        // stages 0..2 landed (stage 2 for the first iteration's sums of squares; q8: the
+        // stages widened here)
         if (nst - 1 >= NS - 2) {
-            ESDA_WAIT_VM((NS - 4) * R::DPW);
+            ESDA_WAIT_VM((NS - 4) * DPW);
         } else {
             ESDA_WAIT_VM(0);
         }
         lds_barrier();
-        load_raw(ring(std::integral_constant<int, 0>{}));
+        if constexpr (Q8) {
+            convert(0, ring(std::integral_constant<int, 0>{}));
+            if (nst > 1) convert(1, ring(std::integral_constant<int, 1>{}));
+            if (nst > 2) convert(2, ring(std::integral_constant<int, 2>{}));
+            lds_barrier();
+        }
+        load_raw(cbuf(0, std::integral_constant<int, 0>{}));
         publish_ss(0);
         publish_tab(0, 0);
         if (nst > 1) {
-            load_raw(ring(std::integral_constant<int, 1>{}));
+            load_raw(cbuf(1, std::integral_constant<int, 1>{}));
             publish_ss(1);
             publish_tab(1, 1);
         }
@@ -628,14 +831,14 @@ void attend_kernel(AttendParams p) {
             u32x4 keep[KKW];
 #pragma unroll
             for (int kk = 0; kk < KKW; ++kk) keep[kk] = araw[kk];
-            load_raw(ring(std::integral_constant<int, 0>{}));
-            qk_raw(0, 0, 0);
+            load_raw(cbuf(0, std::integral_constant<int, 0>{}));
+            qk_raw(0, 0, 0, 0);
 #pragma unroll
             for (int kk = 0; kk < KKW; ++kk) araw[kk] = keep[kk];
         }
     } else {
         if (nst - 1 >= NS - 2) {
-            ESDA_WAIT_VM((NS - 2) * R::DPW);
+            ESDA_WAIT_VM((NS - 2) * DPW);
         } else {
             ESDA_WAIT_VM(0);
         }
@@ -654,13 +857,17 @@ void attend_kernel(AttendParams p) {
         if (st + AHEAD < nst) {
             // own DMA for stage st+AHEAD done; the stages behind it may stay in flight
             if (nst - st - AHEAD - 1 >= NS - 2 - AHEAD) {
-                ESDA_WAIT_VM((NS - 2 - AHEAD) * R::DPW);
+                ESDA_WAIT_VM((NS - 2 - AHEAD) * DPW);
             } else {
                 ESDA_WAIT_VM(0);
             }
         }
         lds_barrier();
-        if (st + NS - 1 < nst) dma(st + NS - 1, ring(std::integral_constant<int, (u + NS - 1) % NS>{}));
+        if (st + NS - 1 < nst) dma(st + NS - 1, ring(std::integral_constant<int, (u + NS - 1) % NS>{}), (u + NS - 1) % NS);
+        // q8: widen stage st+3 (landed: this iteration's wait) for the next iterations
+        if constexpr (Q8) {
+            if (st + 3 < nst) convert(st + 3, ring(std::integral_constant<int, (u + 3) % NS>{}));
+        }
         f32x4 sc = xch[st & 1][0][lane];
 #pragma unroll
         for (int w = 1; w < NW; ++w) sc += xch[st & 1][w][lane];
@@ -668,8 +875,8 @@ void attend_kernel(AttendParams p) {
         // the two interleave): past the last stage it reads stale but in-bounds LDS and
         // writes exchange slots that are never read again.
         if constexpr (RAW) {
-            qk_raw((st + 1) % 3, (st + 1) & 1, (st + 1) & 1);
-            load_raw(ring(std::integral_constant<int, (u + 2) % NS>{}));
+            qk_raw((st + 1) % 3, (st + 1) & 1, (st + 1) & 1, (u + 1) % NS);
+            load_raw(cbuf(st + 2, std::integral_constant<int, (u + 2) % NS>{}));
             publish_ss((st + 2) % 3);
             publish_tab(st + 2, st & 1);
         } else {
@@ -685,6 +892,7 @@ void attend_kernel(AttendParams p) {
             const float mnew = fmaxf(m, tmax);
             const float corr = __builtin_amdgcn_exp2f(m - mnew);
             l *= corr;
+            if constexpr (Q8) bt *= corr;
 #pragma unroll
             for (int dt = 0; dt < DTW; ++dt) acc[dt] *= corr;
             m = mnew;
@@ -694,13 +902,17 @@ void attend_kernel(AttendParams p) {
             // V = kraw * rinv enters through the weight: P = bf16(e * rinv).  l adds the
             // same rounded weight divided by rinv (ms * rinv = 1 / rinv), so numerator and
             // denominator carry identical rounding and a dominant row is reproduced exactly.
+            // q8: the factor is scale * rinv (V enters as q) and the bias adds P * bias / scale.
             const f32x4 ri = *reinterpret_cast<const f32x4 *>(&xr[st & 1][0][4 * lg]);
             const f32x4 rn = *reinterpret_cast<const f32x4 *>(&xr[st & 1][1][4 * lg]);
+            f32x4 gm = {0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (Q8) gm = *reinterpret_cast<const f32x4 *>(&xr[st & 1][2][4 * lg]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float e = __builtin_amdgcn_exp2f(sc[r] - m);
                 const __bf16 pw = (__bf16) (e * ri[r]);
                 l += (float) pw * rn[r];
+                if constexpr (Q8) bt += (float) pw * gm[r];
                 pbs[r] = __builtin_bit_cast(short, pw);
             }
         } else {
@@ -712,7 +924,7 @@ void attend_kernel(AttendParams p) {
             }
         }
         // O^T (this wave's dims) += V^T . P^T
-        const unsigned char *vb = ring(uc) + VOFF;
+        const unsigned char *vb = cbuf(st, uc) + VOFF;
 #pragma unroll
         for (int dt = 0; dt < DTW; ++dt) {
             const short4v a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -726,7 +938,7 @@ void attend_kernel(AttendParams p) {
     // into its cache row (bit-exact).  Its own DMA reads that row from k_new / v_new and
     // no other workgroup reads it; the copy runs after this workgroup's ring has
     // drained, so no outstanding load is counted against the ring's waits.
-    if (append && j1 == sv.nvis) {
+    if (!Q8 && append && j1 == sv.nvis) {
         for (int pr = wave; pr < pk; pr += NW) {  // wave pr copies kv head pr of the group
             const size_t row = (size_t) pr * p.head_stride + (size_t) sv.newrow * D;
             for (int c = lane; c < D / 8; c += 64) {
@@ -742,6 +954,13 @@ void attend_kernel(AttendParams p) {
     // Partial of this split: every wave holds the same (m, l) and its own dim slice.
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
+    if constexpr (Q8) {
+        // the bias part of PV is the same for every dim of a head
+        bt += __shfl_xor(bt, 16);
+        bt += __shfl_xor(bt, 32);
+#pragma unroll
+        for (int dt = 0; dt < DTW; ++dt) acc[dt] += bt;
+    }
     if (direct) {
         // The only segment of this (sequence, kv head): normalise here, with the merge's
         // arithmetic (acc * (1 / l), then bf16); the merge skips this pair.
@@ -1106,6 +1325,52 @@ __global__ __launch_bounds__(kMergeRowsThreads) void merge_rows_kernel(MergePara
     *reinterpret_cast<uint2 *>(p.out + ((size_t) b * p.Hq + h) * p.D + d4 * 4) = __builtin_bit_cast(uint2, r);
 }
 
+// Per-row affine u8 of raw rows (esQuantizeRawRows, ESDecodeAttn.mm:491-539): one wave
+// per row of src [kv heads, n, 512] bf16; row (h, i) -> q8[h * q_head_stride + (row0 + i)
+// * 512 ..], scale / bias at [h * sb_head_stride + row0 + i].  The attend kernel's q8 mode
+// quantizes the decode step's new row with the same arithmetic.
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t *src, int n, long long rows,
+                                                            unsigned char *q8, long long q_head_stride,
+                                                            float *scale, float *bias, long long sb_head_stride,
+                                                            int row0) {
+    const long long r = (long long) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const long long h = r / n, i = r - (r / n) * n;
+    const u32x4 t = *reinterpret_cast<const u32x4 *>(src + r * kRawDim + lane * 8);
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        x[2 * e] = bf16_lo(t[e]);
+        x[2 * e + 1] = bf16_hi(t[e]);
+    }
+    float mn = x[0], mx = x[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) {
+        mn = fminf(mn, x[e]);
+        mx = fmaxf(mx, x[e]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        mn = fminf(mn, __shfl_xor(mn, o));
+        mx = fmaxf(mx, __shfl_xor(mx, o));
+    }
+    float scl = (mx - mn) / 255.0f;
+    if (!(scl > 1e-8f)) scl = 1e-8f;
+    unsigned lo = 0u, hi = 0u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const unsigned qi = (unsigned) fminf(roundf((x[e] - mn) / scl), 255.0f);
+        if (e < 4) lo |= qi << (8 * e);
+        else hi |= qi << (8 * (e - 4));
+    }
+    *reinterpret_cast<uint2 *>(q8 + h * q_head_stride + (row0 + i) * kRawDim + lane * 8) = uint2{lo, hi};
+    if (lane == 0) {
+        scale[h * sb_head_stride + row0 + i] = scl;
+        bias[h * sb_head_stride + row0 + i] = mn;
+    }
+}
+
 __global__ void fill_i32_kernel(int *dst, int value, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) dst[i] = value;
@@ -1287,10 +1552,10 @@ constexpr int ring_waves() { return D == 256 ? 8 : 4; }
 // reconstruction work.
 constexpr int kRawWaves = 8;
 
-template <int D, bool SHARED, bool RAW = false, int RPK = 1>
+template <int D, bool SHARED, bool RAW = false, int RPK = 1, bool Q8 = false>
 hipError_t launch_attend(const AttendParams &ap, dim3 grid, hipStream_t st) {
     constexpr int NW = RAW ? kRawWaves : ring_waves<D>();
-    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW, RPK>), grid, dim3(64 * NW), 0, st, ap);
+    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW, RPK, Q8>), grid, dim3(64 * NW), 0, st, ap);
     return hipGetLastError();
 }
 
@@ -1326,8 +1591,9 @@ int raw_as_decode(const esda_raw_desc *r, esda_decode_desc *d) {
 }
 
 // Launches the requested stages of one decode step (raw: the raw-K attend kernel).
+// mode: 0 composite, 1 raw-K, 2 q8 raw-K.
 int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap_in, uint16_t *out,
-               void *workspace, int stages, bool raw, hipStream_t st) {
+               void *workspace, int stages, int mode, hipStream_t st) {
     unsigned char *ws = static_cast<unsigned char *>(workspace);
     long long *table = reinterpret_cast<long long *>(ws + pl.off_table);
     float *part_ml = reinterpret_cast<float *>(ws + pl.off_ml);
@@ -1356,9 +1622,12 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         ap.scale_log2e = d->scale * kLog2e;
         ap.out = out;
         const dim3 grid = pl.balanced ? dim3(pl.W) : dim3(pl.S, d->num_kv_heads / pl.pk, d->batch);
-        hipError_t e = !raw            ? dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st)
-                       : pl.pk == 2    ? launch_attend<kRawDim, true, true, 2>(ap, grid, st)
-                                       : launch_attend<kRawDim, true, true, 1>(ap, grid, st);
+        hipError_t e;
+        if (mode == 0) e = dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
+        else if (mode == 1) e = pl.pk == 2 ? launch_attend<kRawDim, true, true, 2>(ap, grid, st)
+                                           : launch_attend<kRawDim, true, true, 1>(ap, grid, st);
+        else e = pl.pk == 2 ? launch_attend<kRawDim, true, true, 2, true>(ap, grid, st)
+                            : launch_attend<kRawDim, true, true, 1, true>(ap, grid, st);
         if (e != hipSuccess) return hip_fail(e, "attend_kernel launch");
     }
     // One split per pair: the attend workgroups wrote every output themselves.
@@ -1452,7 +1721,7 @@ int esda_decode_stages(const esda_decode_desc *d, const esda_decode_args *a, int
     ap.v_cache = static_cast<uint16_t *>(a->v_cache);
     ap.pos = a->pos;
     ap.row_base = a->row_base;
-    return run_stages(d, pl, ap, static_cast<uint16_t *>(a->out), a->workspace, stages, false,
+    return run_stages(d, pl, ap, static_cast<uint16_t *>(a->out), a->workspace, stages, 0,
                       reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -1502,12 +1771,82 @@ int esda_decode_raw_stages(const esda_raw_desc *desc, const esda_raw_args *a, in
     ap.kw = static_cast<const uint16_t *>(a->kw);
     ap.inv_freq = a->inv_freq;
     ap.eps = desc->eps;
-    return run_stages(&d, pl, ap, static_cast<uint16_t *>(a->out), a->workspace, stages, true,
+    return run_stages(&d, pl, ap, static_cast<uint16_t *>(a->out), a->workspace, stages, 1,
                       reinterpret_cast<hipStream_t>(stream));
 }
 
 int esda_decode_raw(const esda_raw_desc *desc, const esda_raw_args *args, void *stream) {
     return esda_decode_raw_stages(desc, args, ESDA_STAGE_ATTEND | ESDA_STAGE_MERGE, stream);
+}
+
+int esda_decode_raw_q8_stages(const esda_raw_desc *desc, const esda_raw_q8_args *a, int stages, void *stream) {
+    esda_decode_desc d;
+    int rc = raw_as_decode(desc, &d);
+    if (rc) return rc;
+    if ((d.head_stride % 16) || (d.seq_stride % 16))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_q8: u8 strides must be multiples of 16 bytes");
+    Plan pl;
+    rc = make_plan(&d, &pl, /*raw=*/true);
+    if (rc) return rc;
+    if (!a) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_q8: null arguments");
+    if (!a->q || !a->q8_cache || !a->scale || !a->bias || !a->pos || !a->kw || !a->inv_freq || !a->out)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_q8: null device pointer");
+    if (!aligned16(a->q) || (a->k_new && !aligned16(a->k_new)) || !aligned16(a->q8_cache) ||
+        !aligned16(a->kw) || !aligned16(a->inv_freq) || !aligned16(a->out) ||
+        (reinterpret_cast<uintptr_t>(a->scale) & 3u) || (reinterpret_cast<uintptr_t>(a->bias) & 3u))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_q8: tensors must be 16-byte aligned (scale / bias 4)");
+    if (a->sb_head_stride < d.cap || a->sb_seq_stride < (int64_t) d.num_kv_heads * a->sb_head_stride)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_q8: scale / bias strides smaller than the cache");
+    if (!a->workspace || a->workspace_bytes < pl.bytes || !aligned16(a->workspace))
+        return fail(ESDA_ERR_WORKSPACE, "esda_decode_raw_q8: workspace missing or smaller than esda_decode_raw_workspace_size");
+    if ((stages & (ESDA_STAGE_ATTEND | ESDA_STAGE_MERGE)) == 0 || (stages & ~3))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_q8_stages: bad stage mask");
+    rc = check_device();
+    if (rc) return rc;
+    AttendParams ap{};
+    ap.q = static_cast<const uint16_t *>(a->q);
+    ap.k_new = static_cast<const uint16_t *>(a->k_new);
+    ap.v_new = ap.k_new;
+    ap.k_cache = static_cast<uint16_t *>(a->q8_cache);  // not read in q8 mode
+    ap.v_cache = ap.k_cache;
+    ap.q8 = static_cast<unsigned char *>(a->q8_cache);
+    ap.qsc = a->scale;
+    ap.qbs = a->bias;
+    ap.sb_seq_stride = a->sb_seq_stride;
+    ap.sb_head_stride = a->sb_head_stride;
+    ap.pos = a->pos;
+    ap.row_base = nullptr;
+    ap.kw = static_cast<const uint16_t *>(a->kw);
+    ap.inv_freq = a->inv_freq;
+    ap.eps = desc->eps;
+    return run_stages(&d, pl, ap, static_cast<uint16_t *>(a->out), a->workspace, stages, 2,
+                      reinterpret_cast<hipStream_t>(stream));
+}
+
+int esda_decode_raw_q8(const esda_raw_desc *desc, const esda_raw_q8_args *args, void *stream) {
+    return esda_decode_raw_q8_stages(desc, args, ESDA_STAGE_ATTEND | ESDA_STAGE_MERGE, stream);
+}
+
+int esda_quantize_raw_rows(const void *src, int32_t kv_heads, int32_t n_rows, void *q8, int64_t q_head_stride,
+                           float *scale, float *bias, int64_t sb_head_stride, int32_t row0, void *stream) {
+    if (!src || !q8 || !scale || !bias)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_quantize_raw_rows: null pointer");
+    if (kv_heads <= 0 || n_rows < 0 || row0 < 0)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_quantize_raw_rows: bad sizes");
+    if (!aligned16(src) || (reinterpret_cast<uintptr_t>(q8) & 7u) || (q_head_stride % 8))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_quantize_raw_rows: src 16-byte, q8 rows 8-byte aligned");
+    if (q_head_stride < (int64_t) (row0 + n_rows) * kRawDim || sb_head_stride < row0 + n_rows)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_quantize_raw_rows: head strides smaller than the rows written");
+    if (n_rows == 0) return ESDA_OK;
+    int rc = check_device();
+    if (rc) return rc;
+    const long long rows = (long long) kv_heads * n_rows;
+    const unsigned blocks = (unsigned) ((rows + 3) / 4);
+    hipLaunchKernelGGL(quantize_rows_kernel, dim3(blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t *>(src), n_rows, rows, static_cast<unsigned char *>(q8),
+                       q_head_stride, scale, bias, sb_head_stride, row0);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? ESDA_OK : hip_fail(e, "quantize_rows_kernel launch");
 }
 
 int esda_decode_status(const esda_decode_desc *desc, void *workspace, int32_t *bad_sequences,

@@ -11,7 +11,7 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import DecodeArgs, DecodeDesc, RawArgs, RawDesc, check, lib
+from ._lib import DecodeArgs, DecodeDesc, RawArgs, RawDesc, RawQ8Args, check, lib
 
 STAGE_ATTEND = 1
 STAGE_MERGE = 2
@@ -257,6 +257,91 @@ class RawCall:
                              _dev_ptr(kw, bf), _dev_ptr(inv_freq), _dev_ptr(out, bf), _dev_ptr(workspace),
                              workspace.numel() * workspace.element_size())
         self._fn = lib().esda_decode_raw_stages
+        self._pd, self._pa = ctypes.byref(self._desc), ctypes.byref(self._args)
+
+    def __call__(self, stream=None, stages: int | None = None) -> torch.Tensor:
+        rc = self._fn(self._pd, self._pa, self.stages if stages is None else stages, _stream_ptr(stream))
+        if rc:
+            check(rc)
+        return self.out
+
+
+# ----------------------------------------------------------------- q8 raw-K mode
+
+def quantize_raw_rows(src: torch.Tensor, q8: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor,
+                      row0: int = 0, stream=None) -> None:
+    """Quantize src [Hkv, n, 512] bf16 into rows row0 .. row0+n-1 of a q8 cache for one
+    sequence: q8 [Hkv, cap, 512] u8, scale / bias [Hkv, cap] f32 (esQuantizeRawRows)."""
+    Hkv, n, D = src.shape
+    if D != 512 or not src.is_contiguous() or src.dtype != torch.bfloat16:
+        raise ValueError("src must be contiguous bf16 [Hkv, n, 512]")
+    if q8.dtype != torch.uint8 or q8.dim() != 3 or q8.shape[0] != Hkv or q8.stride(2) != 1 or q8.stride(1) != 512:
+        raise ValueError("q8 must be u8 [Hkv, cap, 512] with dense rows")
+    if scale.shape != q8.shape[:2] or bias.shape != q8.shape[:2] or scale.stride(1) != 1 or bias.stride() != scale.stride():
+        raise ValueError("scale / bias must be f32 [Hkv, cap]")
+    check(lib().esda_quantize_raw_rows(_dev_ptr(src, torch.bfloat16), Hkv, n, _dev_ptr(q8), q8.stride(0),
+                                       _dev_ptr(scale), _dev_ptr(bias), scale.stride(0), row0,
+                                       _stream_ptr(stream)))
+
+
+def _q8_args(step: RawStep, q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace) -> RawQ8Args:
+    bf = torch.bfloat16
+    if q.shape != (step.batch, step.num_q_heads, 512) or not q.is_contiguous():
+        raise ValueError("q must be contiguous [B, Hq, 512]")
+    if k_new is not None and (k_new.shape != (step.batch, step.num_kv_heads, 512) or not k_new.is_contiguous()):
+        raise ValueError("k_new must be contiguous [B, Hkv, 512]")
+    if q8.dtype != torch.uint8 or q8.shape != (step.batch, step.num_kv_heads, step.cap, 512):
+        raise ValueError("q8 cache must be u8 [B, Hkv, cap, 512]")
+    if scale.dtype != torch.float32 or scale.shape != (step.batch, step.num_kv_heads, step.cap) or \
+            bias.shape != scale.shape or bias.stride() != scale.stride() or scale.stride(2) != 1:
+        raise ValueError("scale / bias must be f32 [B, Hkv, cap] with the same strides")
+    if pos.dtype != torch.int32 or pos.shape != (step.batch,):
+        raise ValueError("pos must be int32 [B]")
+    return RawQ8Args(_dev_ptr(q, bf), _dev_ptr(k_new, bf), _dev_ptr(q8), _dev_ptr(scale), _dev_ptr(bias),
+                     scale.stride(0), scale.stride(1), _dev_ptr(pos), _dev_ptr(kw, bf), _dev_ptr(inv_freq),
+                     _dev_ptr(out, bf), _dev_ptr(workspace), workspace.numel() * workspace.element_size())
+
+
+def q8_step_for(q8: torch.Tensor, num_q_heads: int, **kw) -> RawStep:
+    """RawStep of a q8 cache [B, Hkv, cap, 512] u8 (strides in bytes)."""
+    B, Hkv, cap, D = q8.shape
+    if D != 512 or q8.stride(3) != 1 or q8.stride(2) != D:
+        raise ValueError("q8 cache rows must be dense [B, Hkv, cap, 512]")
+    return RawStep(batch=B, num_q_heads=num_q_heads, num_kv_heads=Hkv, cap=cap,
+                   seq_stride=q8.stride(0), head_stride=q8.stride(1), **kw)
+
+
+def decode_raw_q8(step: RawStep, q: torch.Tensor, k_new: torch.Tensor | None, q8: torch.Tensor,
+                  scale: torch.Tensor, bias: torch.Tensor, pos: torch.Tensor, kw: torch.Tensor,
+                  inv_freq: torch.Tensor, out: torch.Tensor | None = None,
+                  workspace: torch.Tensor | None = None, stream=None,
+                  stages: int = STAGE_ATTEND | STAGE_MERGE) -> torch.Tensor:
+    """q8 raw-K decode step: quantize k_new (or None) into row pos[b], then attend rows
+    0 .. pos[b] of the q8 stream; returns out [B, Hq, 512] bf16."""
+    if out is None:
+        out = torch.empty_like(q)
+    if workspace is None:
+        workspace = new_raw_workspace(step, q.device)
+    args = _q8_args(step, q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace)
+    d = step.desc()
+    check(lib().esda_decode_raw_q8_stages(ctypes.byref(d), ctypes.byref(args), stages, _stream_ptr(stream)))
+    return out
+
+
+class RawQ8Call:
+    """decode_raw_q8 with its arguments marshalled once (see DecodeCall)."""
+
+    def __init__(self, step: RawStep, q, k_new, q8, scale, bias, pos, kw, inv_freq, out=None, workspace=None,
+                 stages: int = STAGE_ATTEND | STAGE_MERGE):
+        if out is None:
+            out = torch.empty_like(q)
+        if workspace is None:
+            workspace = new_raw_workspace(step, q.device)
+        self._keep = (q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace)
+        self.step, self.out, self.workspace, self.stages = step, out, workspace, stages
+        self._desc = step.desc()
+        self._args = _q8_args(step, q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace)
+        self._fn = lib().esda_decode_raw_q8_stages
         self._pd, self._pa = ctypes.byref(self._desc), ctypes.byref(self._args)
 
     def __call__(self, stream=None, stages: int | None = None) -> torch.Tensor:

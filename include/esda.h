@@ -158,6 +158,46 @@ int esda_decode_raw(const esda_raw_desc *desc, const esda_raw_args *args, void *
 int esda_decode_raw_stages(const esda_raw_desc *desc, const esda_raw_args *args, int stages,
                            void *stream);
 
+/* ------------------------------------------------------------- q8 raw-K mode
+ *
+ * The raw stream stored as per-row affine u8 (rawKVQ8): row x = q * scale + bias with
+ * q u8 [512], scale and bias f32 (ESKVCache.h:81-91, ESKVCache.mm:506-566).  The kernel
+ * widens q exactly, rebuilds K / V as in raw-K mode from x, and quantizes the new row
+ * (k_new, bf16) into row pos[b] before attending (esQuantizeRawRows' arithmetic).
+ * Description: esda_raw_desc, with seq_stride / head_stride counting u8 elements (bytes;
+ * multiples of 16).  Workspace: esda_decode_raw_workspace_size. */
+typedef struct esda_raw_q8_args {
+    const void *q;             /* [B, Hq, 512] bf16 (post q-norm + RoPE)                   */
+    const void *k_new;         /* [B, Hkv, 512] bf16 raw rows to quantize into row pos[b], or
+                                  NULL when the rows are already cached                   */
+    void *q8_cache;            /* u8 rows: (b, kvh, row, d) at b*seq_stride + kvh*head_stride
+                                  + row*512 + d                                           */
+    float *scale;              /* per row: (b, kvh, row) at b*sb_seq_stride + kvh*sb_head_stride + row */
+    float *bias;
+    int64_t sb_seq_stride;     /* elements; >= num_kv_heads * sb_head_stride              */
+    int64_t sb_head_stride;    /* elements; >= cap                                        */
+    const int32_t *pos;        /* [B] int32, device memory: row of the newest token       */
+    const void *kw;            /* [512] bf16 k-norm weights                               */
+    const float *inv_freq;     /* [64] f32 rotary inverse frequencies                     */
+    void *out;                 /* [B, Hq, 512] bf16                                       */
+    void *workspace;           /* esda_decode_raw_workspace_size bytes; first 256 zeroed once */
+    size_t workspace_bytes;
+} esda_raw_q8_args;
+
+/* Fused q8 raw-K decode step (quantize-append + rebuild + attend + merge): replaces
+ * ESKVCache::updateRawQ8 (ESKVCache.mm:513-556) followed by esDecodeAttnGlobalQ8
+ * (ESDecodeAttn.mm:455-489) as called at ESAttention.mm:270-279. */
+int esda_decode_raw_q8(const esda_raw_desc *desc, const esda_raw_q8_args *args, void *stream);
+int esda_decode_raw_q8_stages(const esda_raw_desc *desc, const esda_raw_q8_args *args, int stages,
+                              void *stream);
+
+/* Quantize src [kv_heads, n_rows, 512] bf16 (contiguous) into rows row0 .. row0+n_rows-1 of
+ * a q8 cache: q8 + h*q_head_stride + row*512, scale / bias + h*sb_head_stride + row
+ * (esQuantizeRawRows, ESDecodeAttn.mm:491-539; ESKVCache::quantizeRawRows). */
+int esda_quantize_raw_rows(const void *src, int32_t kv_heads, int32_t n_rows, void *q8,
+                           int64_t q_head_stride, float *scale, float *bias, int64_t sb_head_stride,
+                           int32_t row0, void *stream);
+
 /* dst[0 .. n-1] = value on `stream` (a kernel, so it may be captured in a graph): sets
  * the per-sequence position words that replace the host-built additive mask upload of
  * ESGemma4TextModel.mm:68-83 / ESAttention.mm:17-22. */

@@ -1,0 +1,137 @@
+"""GPU parity of the q8 raw-K decode (esda_decode_raw_q8) and the row quantizer
+(esda_quantize_raw_rows) against the CPU oracle, through the C ABI.
+
+The quantizer and the decode step's in-kernel quantization of the appended row must give
+the oracle's u8 rows, scales and biases bit for bit (IEEE fp32 subtract / divide, round
+half away from zero: ESDecodeAttn.mm:491-509); every byte of the q8 cache and every
+scale and bias is compared after the append.  Outputs are held to max-abs <= 2e-2 and
+mean-abs <= 2e-3 against the fp64 q8 oracle (orc_decode_raw_q8_f64: rows dequantised as
+float(q) * scale + bias, then the raw-K reconstruction of ESDecodeAttn.mm:275-369).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL_MAX, TOL_MEAN = 2e-2, 2e-3
+EPS = 1e-6
+
+
+def _dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def _host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _raw_rows(rng, shape, row_scale=2.0):
+    return orc.to_bf16((rng.standard_normal(shape, dtype=np.float32) * row_scale).astype(np.float32))
+
+
+def test_quantize_raw_rows_matches_the_oracle_bit_for_bit():
+    from apertura_amd.decode import quantize_raw_rows
+    rng = np.random.default_rng(41)
+    Hkv, n, cap = 3, 700, 800
+    x = _raw_rows(rng, (Hkv, n, 512)) * 1  # bf16 bits
+    xf = orc.from_bf16(x).astype(np.float32)
+    xf[0, 0] = 0.25                                 # a constant row
+    xf[1, 1] = 0.0
+    xf[1, 1, 1], xf[1, 1, 2] = 255 / 16, 2.5 / 16   # a tie at 2.5 steps
+    xf[2, 2] *= 1e-3                                # a tiny range
+    x = orc.to_bf16(xf)
+    q8 = torch.full((Hkv, cap, 512), 7, dtype=torch.uint8, device="cuda")
+    sc = torch.full((Hkv, cap), -1.0, dtype=torch.float32, device="cuda")
+    bs = torch.full((Hkv, cap), -1.0, dtype=torch.float32, device="cuda")
+    quantize_raw_rows(_dev(x), q8, sc, bs, row0=50)
+    torch.cuda.synchronize()
+    eq, esc, ebs = orc.quantize_rows(x)
+    gq, gsc, gbs = q8.cpu().numpy(), sc.cpu().numpy(), bs.cpu().numpy()
+    assert np.array_equal(gq[:, 50:50 + n], eq)
+    assert np.array_equal(gsc[:, 50:50 + n].view(np.uint32), esc.view(np.uint32))
+    assert np.array_equal(gbs[:, 50:50 + n].view(np.uint32), ebs.view(np.uint32))
+    # rows outside row0 .. row0 + n - 1 untouched
+    assert (gq[:, :50] == 7).all() and (gq[:, 50 + n:] == 7).all() and (gsc[:, :50] == -1).all()
+    assert eq[1, 1, 2] == 3  # the tie rounded away from zero
+
+
+def run_q8(name, *, B=1, Hq=32, Hkv=4, cap, pos, scale=1.0, seed=0, split_rows=0, append=True,
+           partial=0.25, fault=0):
+    from apertura_amd.decode import decode_raw_q8, new_raw_workspace, q8_step_for
+    print(f"\n[q8] {name}: B={B} Hq={Hq} Hkv={Hkv} cap={cap} pos={list(pos)[:4]} scale={scale} "
+          f"append={append} split_rows={split_rows}", flush=True)
+    rng = np.random.default_rng(seed)
+    raw = _raw_rows(rng, (B, Hkv, cap, 512))
+    qc, sc, bs = orc.quantize_rows(raw)
+    q = orc.to_bf16(rng.standard_normal((B, Hq, 512), dtype=np.float32))
+    q = orc.rms_norm_rows(q, None, 1e-6)
+    kn = _raw_rows(rng, (B, Hkv, 512))
+    kw = orc.to_bf16((1.0 + 0.25 * rng.standard_normal(512)).astype(np.float32))
+    inv = orc.rope_inv_freq(512, 1.0e6, partial)
+    q8_d = torch.from_numpy(qc).cuda()
+    sc_d, bs_d = torch.from_numpy(sc).cuda(), torch.from_numpy(bs).cuda()
+    step = q8_step_for(q8_d, Hq, eps=EPS, scale=scale, split_rows=split_rows)
+    out = decode_raw_q8(step, _dev(q), _dev(kn) if append else None, q8_d, sc_d, bs_d,
+                        torch.tensor(list(pos), dtype=torch.int32, device="cuda"), _dev(kw),
+                        torch.from_numpy(inv).cuda(), workspace=new_raw_workspace(step, "cuda"))
+    torch.cuda.synchronize()
+    if append:
+        nq, nsc, nbs = orc.quantize_rows(kn)
+        for b in range(B):
+            qc[b, :, pos[b]], sc[b, :, pos[b]], bs[b, :, pos[b]] = nq[b], nsc[b], nbs[b]
+    assert np.array_equal(q8_d.cpu().numpy(), qc), "q8 rows differ after the append"
+    assert np.array_equal(sc_d.cpu().numpy().view(np.uint32), sc.view(np.uint32)), "scales differ"
+    assert np.array_equal(bs_d.cpu().numpy().view(np.uint32), bs.view(np.uint32)), "biases differ"
+    o = orc.from_bf16(_host(out)).reshape(B, Hq, 512).astype(np.float64)
+    errs = []
+    for b in range(B):
+        with orc.planted_fault(fault):
+            ref = orc.decode_raw_q8_f64(q[b], qc[b], sc[b], bs[b], pos[b] + 1, kw, EPS, inv, scale)
+        err = np.abs(o[b] - ref)
+        errs.append(err)
+        if not fault:
+            print(f"[q8] {name} b={b}: max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
+            assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN, name
+    return o, errs
+
+
+def test_q8_small_with_append():
+    run_q8("small", cap=512, pos=[299], scale=512 ** -0.5)
+
+
+def test_q8_in_model_scale_one():
+    run_q8("scale1", cap=1024, pos=[1000], scale=1.0, seed=3)
+
+
+def test_q8_long_context_131072():
+    """The C4 shape over a q8 raw stream: 131072 rows, two kv heads per workgroup."""
+    run_q8("c4-q8", cap=131072, pos=[131071], scale=512 ** -0.5, seed=5)
+
+
+def test_q8_batched_ragged_positions():
+    run_q8("batched", B=3, cap=4096, pos=[17, 2500, 4095], scale=512 ** -0.5, seed=7)
+
+
+def test_q8_no_append_reads_cached_rows():
+    run_q8("no-append", cap=2048, pos=[1500], append=False, seed=9)
+
+
+@pytest.mark.parametrize("split_rows", [16, 48, 512])
+def test_q8_split_sizes(split_rows):
+    run_q8(f"split{split_rows}", cap=1024, pos=[777], split_rows=split_rows, seed=11)
+
+
+def test_q8_unpacked_odd_kv_heads():
+    run_q8("unpacked-hkv3", B=2, Hq=24, Hkv=3, cap=1024, pos=[1000, 333], scale=512 ** -0.5, seed=19)
+
+
+def test_q8_single_row():
+    run_q8("one-row", cap=64, pos=[0], seed=15)
+
+
+def test_q8_rope_sign_fault_is_detected():
+    _, errs = run_q8("rope-fault", cap=2048, pos=[2047], scale=1.0, seed=17, fault=5)
+    assert max(e.max() for e in errs) > 10 * TOL_MAX
