@@ -711,19 +711,22 @@ void attend_kernel(AttendParams p) {
         }
         return sum * (1.0f / kRawDim) + p.eps;
     };
-    // q8: mean(x^2) + eps of a row from its exact integer sums, x = q * scale + bias:
-    // mean(x^2) = scale^2 var(q) + mean(x)^2 with 512^2 var(q) = 512 sum(q^2) - sum(q)^2, an
-    // exact integer (no cancellation in fp32).
+    // q8: mean(x^2) + eps of a row from its sums, x = q * scale + bias: mean(x^2) =
+    // scale^2 var(q) + mean(x)^2, 512^2 var(q) = 512 sum(q^2) - sum(q)^2.  sum(q) < 2^24 is
+    // exact in fp32; sum(q^2) may round by a few units in 3.3e7, which moves var(q) by
+    // ~1e-5 of its size at most and mean(x^2) far less (the mean term carries no such error).
     auto q8_ms = [&](int buf, int row, float scl, float bias) {
-        int s2 = 0, s1 = 0;
+        float s2 = 0.0f, s1 = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            s2 += (int) xss[buf][row][w];
-            s1 += (int) xsq[buf][row][w];
+        for (int q4 = 0; q4 < NW; q4 += 4) {
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(&xss[buf][row][q4]);
+            const f32x4 c = *reinterpret_cast<const f32x4 *>(&xsq[buf][row][q4]);
+            s2 += (a[0] + a[1]) + (a[2] + a[3]);
+            s1 += (c[0] + c[1]) + (c[2] + c[3]);
         }
-        const float var = (float) (512LL * s2 - (long long) s1 * s1);
-        const float mean = scl * ((float) s1 * (1.0f / kRawDim)) + bias;
-        return scl * scl * var * (1.0f / (kRawDim * kRawDim)) + mean * mean + p.eps;
+        const float var = fmaxf(__builtin_fmaf(512.0f, s2, -s1 * s1), 0.0f);
+        const float mean = __builtin_fmaf(scl, s1 * (1.0f / kRawDim), bias);
+        return scl * scl * var * (1.0f / (kRawDim * kRawDim)) + __builtin_fmaf(mean, mean, p.eps);
     };
     // Scores of the stage held in araw: rebuild K in registers, then MFMA.  sbslot: the
     // ring slot of the stage (q8: its scale / bias rows).

@@ -50,6 +50,9 @@ WORKLOADS = {
                pos=lambda rng, B: [131071], scale=512 ** -0.5),
     # C4's shape in raw-K mode (the reference's esDecodeAttnGlobal path): the cache holds
     # pre-norm k_proj rows; K and V are rebuilt in the kernel; in-model scale 1.0.
+    # The same over a q8 raw stream (rawKVQ8: u8 rows + per-row scale / bias, 520 B a row).
+    "c4q8": dict(B=1, Hq=32, Hkv=4, D=512, cap=131072, window=0, ring=False, shared=True, raw=True, q8=True,
+                 pos=lambda rng, B: [131071], scale=1.0),
     "c4raw": dict(B=1, Hq=32, Hkv=4, D=512, cap=131072, window=0, ring=False, shared=True, raw=True,
                   pos=lambda rng, B: [131071], scale=1.0),
 }
@@ -94,11 +97,15 @@ def visible_rows(w, pos):
     return out
 
 
+Q8_ROW_BYTES = 512 + 8  # u8 row + f32 scale and bias
+
+
 def algorithmic_bytes(w, pos) -> int:
-    row = w["D"] * 2 * (1 if w["shared"] else 2)
+    row = Q8_ROW_BYTES if w.get("q8") else w["D"] * 2 * (1 if w["shared"] else 2)
     kv = sum(visible_rows(w, pos)) * w["Hkv"] * row
     q_o = 2 * w["B"] * w["Hq"] * w["D"] * 2
-    append = 2 * w["B"] * w["Hkv"] * row  # new-row read + cache write
+    # new-row read + cache write (q8: the bf16 row read, its quantized row written)
+    append = w["B"] * w["Hkv"] * ((w["D"] * 2 + row) if w.get("q8") else 2 * row)
     return kv + q_o + append
 
 
@@ -122,8 +129,8 @@ def main() -> int:
     import numpy as np
     import torch
 
-    from apertura_amd.decode import (DecodeCall, DecodeStep, RawCall, RawStep, STAGE_ATTEND,
-                                     new_raw_workspace, new_workspace)
+    from apertura_amd.decode import (DecodeCall, DecodeStep, RawCall, RawQ8Call, RawStep, STAGE_ATTEND,
+                                     new_raw_workspace, new_workspace, q8_step_for, quantize_raw_rows)
 
     if args.calibrate_copy:
         return calibrate_copy(args)
@@ -158,10 +165,22 @@ def main() -> int:
         kw = (1.0 + 0.25 * torch.randn(D, device=dev, generator=gen)).to(torch.bfloat16)
         inv_freq = torch.zeros(D // 2, dtype=torch.float32, device=dev)
         inv_freq[:64] = 1.0 / (1.0e6 ** (torch.arange(64, dtype=torch.float64, device=dev) * 2 / D)).float()
-        step = RawStep.for_cache(k_cache, Hq, eps=1e-6, scale=w["scale"], split_rows=args.split_rows)
-        ws = new_raw_workspace(step, dev)
-        call = RawCall(step, q, k_new, k_cache, pos_d, kw, inv_freq, out=out, workspace=ws)
-        raw = (kw, inv_freq)
+        if w.get("q8"):
+            # the same raw rows quantized into a q8 stream on the GPU (esda_quantize_raw_rows)
+            q8 = torch.empty((B, Hkv, cap, D), dtype=torch.uint8, device=dev)
+            sc = torch.empty((B, Hkv, cap), dtype=torch.float32, device=dev)
+            bs = torch.empty_like(sc)
+            for b in range(B):
+                quantize_raw_rows(k_cache[b], q8[b], sc[b], bs[b])
+            step = q8_step_for(q8, Hq, eps=1e-6, scale=w["scale"], split_rows=args.split_rows)
+            ws = new_raw_workspace(step, dev)
+            call = RawQ8Call(step, q, k_new, q8, sc, bs, pos_d, kw, inv_freq, out=out, workspace=ws)
+            raw = (kw, inv_freq, q8, sc, bs)
+        else:
+            step = RawStep.for_cache(k_cache, Hq, eps=1e-6, scale=w["scale"], split_rows=args.split_rows)
+            ws = new_raw_workspace(step, dev)
+            call = RawCall(step, q, k_new, k_cache, pos_d, kw, inv_freq, out=out, workspace=ws)
+            raw = (kw, inv_freq)
     else:
         step = DecodeStep.for_cache(k_cache, Hq, window=w["window"], ring=w["ring"],
                                     kv_shared=w["shared"], scale=w["scale"], split_rows=args.split_rows)
@@ -229,7 +248,9 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        if raw is not None:
+        if raw is not None and w.get("q8"):
+            cpu = cpu_baseline_q8(w, pos, q, raw, args.cpu_threads)
+        elif raw is not None:
             cpu = cpu_baseline_raw(w, pos, q, k_cache, raw[0], raw[1], args.cpu_threads)
         else:
             cpu = cpu_baseline(w, pos, q, k_cache, v_cache, k_new, v_new, args.cpu_threads)
@@ -257,7 +278,9 @@ def main() -> int:
         "config": {
             "workload": {"c4": "C4 global k_eq_v decode, L=131072", "c2": "C2 global k_eq_v decode, L=8193",
                          "c1": "C1 local decode, L=1024", "c3": "C3 local ring decode, B=8",
-                         "c4raw": "C4 shape, raw-K mode (K/V rebuilt in-kernel), L=131072"}[args.workload],
+                         "c4raw": "C4 shape, raw-K mode (K/V rebuilt in-kernel), L=131072",
+                         "c4q8": "C4 shape, q8 raw-K stream (u8 rows + scale/bias, K/V rebuilt in-kernel), "
+                                 "L=131072"}[args.workload],
             "batch": B, "num_q_heads": Hq, "num_kv_heads": Hkv, "head_dim": D,
             "visible_rows": visible_rows(w, pos), "kv_shared": w["shared"],
             "window": w["window"], "ring": w["ring"], "split_rows": step.split_rows or "auto",
@@ -265,7 +288,9 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": ("attend_kernel<512,shared,raw> (raw-K rebuild + split-K + fused append)" if raw is not None
+            "kernel": ("attend_kernel<512,shared,raw,q8> (u8 widening + raw-K rebuild + split-K + fused quantize-append)"
+                       if w.get("q8") else
+                       "attend_kernel<512,shared,raw> (raw-K rebuild + split-K + fused append)" if raw is not None
                        else "attend_kernel<D,kv_shared> (split-K + fused append)"),
             "achieved": round(gbs_attend, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(gbs_attend / PEAK_HBM_GBS, 4), "traffic": profiled_traffic(args.workload),
@@ -491,6 +516,40 @@ def cpu_baseline_raw(w, pos, q, k_cache, kw, inv_freq, threads: int):
             "cores": threads, "kind": "port",
             "sample": f"{rows} of {visible_rows(w, pos)[0]} rows per kv head x{reps} repeats "
                       f"({t_total:.1f} s), fp64 raw-K oracle (MLX CPU path unavailable offline); "
+                      f"host {os.cpu_count()} cpus visible"}
+
+
+def cpu_baseline_q8(w, pos, q, raw, threads: int):
+    """CPU oracle of the q8 raw-K step (orc_decode_raw_q8_f64) on a bounded sample, as
+    cpu_baseline_raw; throughput in the q8 stream's bytes per row (520)."""
+    import numpy as np
+    import torch
+
+    root = os.path.dirname(os.path.abspath(__file__))
+    sys.path.insert(0, root)
+    from oracle import oracle as orc
+
+    kw, inv_freq, q8, sc, bs = raw
+    B, Hq, Hkv, D = w["B"], w["Hq"], w["Hkv"], w["D"]
+    rows = 16384
+    qh = q.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16).reshape(B, Hq, D)[0]
+    q8h = np.ascontiguousarray(q8[0, :, :rows].cpu().numpy())
+    sch = np.ascontiguousarray(sc[0, :, :rows].cpu().numpy())
+    bsh = np.ascontiguousarray(bs[0, :, :rows].cpu().numpy())
+    kwh = kw.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+    inv = inv_freq.detach().cpu().numpy()
+    reps, t_total = 0, 0.0
+    while t_total < 10.0 and reps < 50:
+        t0 = time.perf_counter()
+        orc.decode_raw_q8_f64(qh, q8h, sch, bsh, rows, kwh, 1e-6, inv, w["scale"], threads=threads)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    sec = t_total / reps
+    nbytes = rows * Hkv * Q8_ROW_BYTES
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "us_per_step": None,
+            "cores": threads, "kind": "port",
+            "sample": f"{rows} of {visible_rows(w, pos)[0]} rows per kv head x{reps} repeats "
+                      f"({t_total:.1f} s), fp64 q8 raw-K oracle (MLX CPU path unavailable offline); "
                       f"host {os.cpu_count()} cpus visible"}
 
 
