@@ -30,7 +30,8 @@ EXPORTS = (
     "esda_cache_seq_len", "esda_cache_mark_step", "esda_cache_reset", "esda_cache_save_snapshot",
     "esda_cache_restore_snapshot", "esda_cache_restore_snapshot_ex", "esda_cache_mark_prefix",
     "esda_cache_mark_rewind_point", "esda_cache_rewind_to_mark", "esda_cache_clear_rewind_mark",
-    "esda_decode_attn_global",
+    "esda_decode_attn_global", "esda_cache_update_raw_q8", "esda_cache_current_raw_q8",
+    "esda_cache_decode_raw_q8", "esda_decode_attn_global_q8",
 )
 _VOID = ("esda_cache_destroy", "esda_cache_mark_step", "esda_cache_reset", "esda_cache_clear_rewind_mark")
 
@@ -103,6 +104,14 @@ class View(ctypes.Structure):
     ]
 
 
+class Q8View(ctypes.Structure):
+    """esda_q8_view: u8 rows q [kv_heads, pitch, 512], f32 scale / bias [kv_heads, pitch]."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+        ("kv_heads", ctypes.c_int32), ("len", ctypes.c_int32), ("pitch", ctypes.c_int32),
+    ]
+
+
 def library_path() -> str:
     return _LIB_PATH
 
@@ -156,6 +165,11 @@ def lib() -> ctypes.CDLL:
         L.esda_cache_mark_rewind_point.argtypes = [P, i32]
         L.esda_cache_rewind_to_mark.argtypes = [P]
         L.esda_decode_attn_global.argtypes = [P, i32, P, i32, i32, i32, P, f32, P, i32, P, P]
+        QVP = ctypes.POINTER(Q8View)
+        L.esda_cache_update_raw_q8.argtypes = [P, i32, P, i32, i32, P, QVP]
+        L.esda_cache_current_raw_q8.argtypes = [P, i32, QVP]
+        L.esda_cache_decode_raw_q8.argtypes = [P, i32, P, i32, P, i32, P, f32, P, i32, P, P]
+        L.esda_decode_attn_global_q8.argtypes = [P, i32, P, P, P, i32, i32, i32, P, f32, P, i32, P, P]
         for name in EXPORTS:
             if name in _VOID:
                 getattr(L, name).restype = None

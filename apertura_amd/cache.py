@@ -14,7 +14,7 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import View, check, lib
+from ._lib import Q8View, View, check, lib
 from .decode import _dev_ptr, _stream_ptr
 
 
@@ -53,6 +53,34 @@ def _hip_copy_2d(dst: int, dpitch: int, src: int, spitch: int, width: int, heigh
     rc = _hip.hipMemcpy2D(dst, dpitch, src, spitch, width, height, 3)  # hipMemcpyDeviceToDevice
     if rc != 0:
         raise RuntimeError(f"hipMemcpy2D failed ({rc})")
+
+
+@dataclass
+class RawQ8View:
+    """A q8 raw slot (ESKVCache::RawQ8): u8 rows [kv_heads, pitch, 512] and f32 scale /
+    bias [kv_heads, pitch] at device addresses q / scale / bias; rows 0 .. len-1 live."""
+    q: int
+    scale: int
+    bias: int
+    kv_heads: int
+    len: int
+    pitch: int
+
+    @classmethod
+    def of(cls, v: Q8View) -> "RawQ8View":
+        return cls(int(v.q or 0), int(v.scale or 0), int(v.bias or 0), v.kv_heads, v.len, v.pitch)
+
+    def torch(self, device="cuda") -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """Copies of the live rows: (q u8 [kv_heads, len, 512], scale, bias f32 [kv_heads, len])."""
+        h, n, p = self.kv_heads, self.len, self.pitch
+        q = torch.empty((h, n, 512), dtype=torch.uint8, device=device)
+        sc = torch.empty((h, n), dtype=torch.float32, device=device)
+        bs = torch.empty((h, n), dtype=torch.float32, device=device)
+        if n:
+            _hip_copy_2d(q.data_ptr(), n * 512, self.q, p * 512, n * 512, h)
+            _hip_copy_2d(sc.data_ptr(), n * 4, self.scale, p * 4, n * 4, h)
+            _hip_copy_2d(bs.data_ptr(), n * 4, self.bias, p * 4, n * 4, h)
+        return q, sc, bs
 
 
 def _rows(t: torch.Tensor, what: str):
@@ -144,13 +172,45 @@ class ESKVCache:
                                           _dev_ptr(out, torch.bfloat16), _stream_ptr(stream)))
         return out
 
+    def update_raw_q8(self, layer: int, k_new: torch.Tensor, stream=None) -> RawQ8View:
+        """ESKVCache::updateRawQ8: quantize k_new [kvHeads, n, 512] bf16 raw rows into the
+        layer's q8 slot (a bf16 raw slot migrates first)."""
+        kvh, n, hd = _rows(k_new, "k_new")
+        if hd != 512:
+            raise ValueError("q8 raw rows are 512 wide")
+        v = Q8View()
+        check(lib().esda_cache_update_raw_q8(self._h, layer, _dev_ptr(k_new), kvh, n, _stream_ptr(stream),
+                                             ctypes.byref(v)))
+        return RawQ8View.of(v)
+
+    def current_raw_q8(self, layer: int) -> RawQ8View:
+        v = Q8View()
+        check(lib().esda_cache_current_raw_q8(self._h, layer, ctypes.byref(v)))
+        return RawQ8View.of(v)
+
+    def decode_raw_q8(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, kw: torch.Tensor, eps: float,
+                      inv_freq, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """Fused updateRawQ8 + esDecodeAttnGlobalQ8 of one decode step (the new row is
+        quantized inside the kernel)."""
+        kvh, n, hd = _rows(k_new, "k_new")
+        if n != 1 or hd != 512:
+            raise ValueError("decode_raw_q8 appends one 512-dim row per kv head")
+        hq = q.numel() // 512
+        if out is None:
+            out = torch.empty((hq, 512), dtype=torch.bfloat16, device=q.device)
+        f = (ctypes.c_float * len(inv_freq))(*[float(x) for x in inv_freq])
+        check(lib().esda_cache_decode_raw_q8(self._h, layer, _dev_ptr(q, torch.bfloat16), hq, _dev_ptr(k_new),
+                                             kvh, _dev_ptr(kw, torch.bfloat16), eps, f, len(inv_freq),
+                                             _dev_ptr(out, torch.bfloat16), _stream_ptr(stream)))
+        return out
+
     def slot(self, layer: int) -> dict:
         ln, st, cap, fl = (ctypes.c_int32() for _ in range(4))
         check(lib().esda_cache_slot(self._h, layer, ctypes.byref(ln), ctypes.byref(st), ctypes.byref(cap),
                                     ctypes.byref(fl)))
         f = int(fl.value)
         return {"len": int(ln.value), "start": int(st.value), "capacity": int(cap.value),
-                "lost": bool(f & 1), "shared": bool(f & 2), "raw": bool(f & 4)}
+                "lost": bool(f & 1), "shared": bool(f & 2), "raw": bool(f & 4), "q8": bool(f & 8)}
 
     def seq_len(self) -> int:
         return lib().esda_cache_seq_len(self._h)
@@ -208,4 +268,25 @@ def es_decode_attn_global(q: torch.Tensor, raw_buf: torch.Tensor, length: int, p
     check(lib().esda_decode_attn_global(_dev_ptr(q, torch.bfloat16), hq, _dev_ptr(raw_buf, torch.bfloat16),
                                         raw_buf.shape[0], length, pitch, _dev_ptr(kw, torch.bfloat16), eps, f,
                                         len(inv_freq), _dev_ptr(out, torch.bfloat16), _stream_ptr(stream)))
+    return out
+
+
+def es_decode_attn_global_q8(q: torch.Tensor, q8_buf: torch.Tensor, scale_buf: torch.Tensor,
+                             bias_buf: torch.Tensor, length: int, pitch: int, kw: torch.Tensor, eps: float,
+                             inv_freq, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """esDecodeAttnGlobalQ8: q [numQ, 512]; q8_buf the unsliced u8 [numKV, pitch, 512]
+    buffer, scale_buf / bias_buf f32 [numKV, pitch(, 1)]; rows 0 .. length-1 attended."""
+    if q8_buf.dim() != 3 or q8_buf.dtype != torch.uint8 or not q8_buf.is_contiguous():
+        raise ValueError("q8_buf must be a contiguous uint8 [numKV, pitch, 512] tensor")
+    for t in (scale_buf, bias_buf):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != q8_buf.shape[0] * q8_buf.shape[1]:
+            raise ValueError("scale_buf / bias_buf must be contiguous float32 [numKV, pitch]")
+    hq = q.numel() // 512
+    if out is None:
+        out = torch.empty((hq, 512), dtype=torch.bfloat16, device=q.device)
+    f = (ctypes.c_float * len(inv_freq))(*[float(x) for x in inv_freq])
+    check(lib().esda_decode_attn_global_q8(_dev_ptr(q, torch.bfloat16), hq, _dev_ptr(q8_buf),
+                                           _dev_ptr(scale_buf), _dev_ptr(bias_buf), q8_buf.shape[0], length,
+                                           pitch, _dev_ptr(kw, torch.bfloat16), eps, f, len(inv_freq),
+                                           _dev_ptr(out, torch.bfloat16), _stream_ptr(stream)))
     return out

@@ -80,7 +80,8 @@ Tensor liveView(const Tensor &buf, int start, int len) {
 
 }  // namespace
 
-ESKVCache::ESKVCache(int numLayers) : k_(numLayers), v_(numLayers), slots_(numLayers) {
+ESKVCache::ESKVCache(int numLayers)
+    : k_(numLayers), v_(numLayers), slots_(numLayers), rq8slots_(numLayers) {
     if (numLayers <= 0) throw std::invalid_argument("ESKVCache: numLayers must be positive");
 }
 
@@ -95,6 +96,7 @@ const ESKVCache::Slot &ESKVCache::slotAt(int layer) const {
 
 int ESKVCache::slotCapacity(int layer) const {
     const Slot &s = slotAt(layer);
+    if (rq8slots_[layer].q) return (int) rq8slots_[layer].q->shape[1];
     return s.k ? (int) s.k->shape[1] : 0;
 }
 
@@ -157,8 +159,8 @@ std::pair<Tensor, Tensor> ESKVCache::update(int layer, const Tensor &kNew, const
     }
 
     Slot &s = slots_[layer];
-    // Mode-mismatch guard (ESKVCache.mm:59-62): raw rows are pre-norm, not K/V.
-    if (s.k && !s.v)
+    // Mode-mismatch guard (ESKVCache.mm:59-62): raw rows (bf16 or q8) are pre-norm, not K/V.
+    if ((s.k && !s.v) || rq8slots_[layer].q)
         throw std::runtime_error("ESKVCache::update: slot holds raw-K content — not usable "
                                  "by the composite path; re-prime the cache");
     const bool aliased = kNew.data == vNew.data;
@@ -220,6 +222,9 @@ ESKVCache::Raw ESKVCache::updateRaw(int layer, const Tensor &kNew, bool prealloc
     if (s.k && s.v)
         throw std::runtime_error("ESKVCache::updateRaw: slot holds composite K/V content "
                                  "(post-norm) — not derivable as raw; re-prime the cache");
+    // a bf16 slot beside the q8 rows would split the stream in two
+    if (rq8slots_[layer].q)
+        throw std::runtime_error("ESKVCache::updateRaw: slot holds q8 raw rows; use updateRawQ8");
     if (!s.k) {
         s.k = clone(kNew, st);
         s.len = nNew;
@@ -264,7 +269,7 @@ Tensor ESKVCache::decode(int layer, const Tensor &q, const Tensor &kNew, const T
         throw std::invalid_argument("ESKVCache::decode: q must be contiguous bf16 [numQHeads, headDim]");
     const int Hq = (int) (q.numel() / hd);
     Slot &s = slots_[layer];
-    if (s.k && !s.v)
+    if ((s.k && !s.v) || rq8slots_[layer].q)
         throw std::runtime_error("ESKVCache::decode: slot holds raw-K content — not usable "
                                  "by the composite path; re-prime the cache");
     const bool aliased = kNew.data == vNew.data;
@@ -342,6 +347,8 @@ Tensor ESKVCache::decodeRaw(int layer, const Tensor &q, const Tensor &kNew, cons
     if (s.k && s.v)
         throw std::runtime_error("ESKVCache::decodeRaw: slot holds composite K/V content "
                                  "(post-norm) — not derivable as raw; re-prime the cache");
+    if (rq8slots_[layer].q)
+        throw std::runtime_error("ESKVCache::decodeRaw: slot holds q8 raw rows; use decodeRawQ8");
     if (!s.k) {
         s.k = Tensor::empty({kvH, 1, 512}, Dtype::bf16);
         s.len = 0;
@@ -405,10 +412,209 @@ Tensor ESKVCache::decodeRaw(int layer, const Tensor &q, const Tensor &kNew, cons
     return o;
 }
 
+// ------------------------------------------------------------------ q8 raw-K storage
+
+std::array<Tensor, 3> ESKVCache::quantizeRawRows(const Tensor &kNew, hipStream_t st) {
+    checkRows(kNew, "ESKVCache::quantizeRawRows kNew");
+    if (kNew.shape[2] != 512) throw std::invalid_argument("esQuantizeRawRows: expects headDim 512");
+    const int64_t kvH = kNew.shape[0], n = kNew.shape[1];
+    // packed rows (the reference copies a transposed view packed first, ESDecodeAttn.mm:519)
+    const Tensor src = kNew.contiguous() ? kNew : clone(kNew, st);
+    Tensor q = Tensor::empty({kvH, n, 512}, Dtype::u8);
+    Tensor sc = Tensor::empty({kvH, n, 1}, Dtype::f32);
+    Tensor bs = Tensor::empty({kvH, n, 1}, Dtype::f32);
+    esdaCheck(esda_quantize_raw_rows(src.data, (int32_t) kvH, (int32_t) n, q.data, n * 512,
+                                     static_cast<float *>(sc.data), static_cast<float *>(bs.data), n, 0, st));
+    if (!kNew.contiguous()) hipCheck(hipStreamSynchronize(st), "esQuantizeRawRows");  // src copy released
+    return {q, sc, bs};
+}
+
+namespace {
+// A [kvH, cap, w] tensor of `dtype`, zero-filled.
+Tensor zerosOf(const std::vector<int64_t> &shape, Dtype dt, hipStream_t st) {
+    Tensor t = Tensor::empty(shape, dt);
+    hipCheck(hipMemsetAsync(t.data, 0, t.nbytes(), st), "ESKVCache zero fill");
+    return t;
+}
+// dst[h, 0 .. n) = src[h, 0 .. n) for every head h of [kvH, rows, w] tensors of one dtype.
+void copyHeads(const Tensor &dst, const Tensor &src, int n, hipStream_t st) {
+    if (n <= 0) return;
+    const size_t es = dtypeSize(src.dtype), row = (size_t) src.shape[2] * es;
+    hipCheck(hipMemcpy2DAsync(dst.data, (size_t) dst.strides[0] * es, src.data, (size_t) src.strides[0] * es,
+                              (size_t) n * row, (size_t) src.shape[0], hipMemcpyDeviceToDevice, st),
+             "ESKVCache q8 copy");
+}
+}  // namespace
+
+void ESKVCache::growQ8(RQ8Slot &s, int nNew, hipStream_t st) {
+    const int cap = (int) s.q->shape[1];
+    if (s.len + nNew <= cap) return;
+    const int newCap = roundUpChunk(s.len + nNew + kGrowChunk);
+    const int64_t kvH = s.q->shape[0];
+    Tensor nq = zerosOf({kvH, newCap, 512}, Dtype::u8, st);
+    Tensor nsc = zerosOf({kvH, newCap, 1}, Dtype::f32, st);
+    Tensor nbs = zerosOf({kvH, newCap, 1}, Dtype::f32, st);
+    copyHeads(nq, *s.q, s.len, st);
+    copyHeads(nsc, *s.sc, s.len, st);
+    copyHeads(nbs, *s.bs, s.len, st);
+    hipCheck(hipStreamSynchronize(st), "ESKVCache q8 growth");  // queued reads of the old buffers
+    s.q = nq;
+    s.sc = nsc;
+    s.bs = nbs;
+}
+
+void ESKVCache::migrateToQ8(int layer, hipStream_t st) {
+    // ESKVCache.mm:522-536: a bf16 raw slot (a restored snapshot) is quantized once into a
+    // q8 slot of capacity roundUp(len + kGrowChunk) and retired.
+    Slot &b = slots_[layer];
+    RQ8Slot &s = rq8slots_[layer];
+    if (s.q || !b.k || b.v) return;
+    const int live = b.len - b.start;
+    const int64_t kvH = b.k->shape[0];
+    const int cap = roundUpChunk(b.len + kGrowChunk);
+    Tensor q = zerosOf({kvH, cap, 512}, Dtype::u8, st);
+    Tensor sc = zerosOf({kvH, cap, 1}, Dtype::f32, st);
+    Tensor bs = zerosOf({kvH, cap, 1}, Dtype::f32, st);
+    if (live > 0) {
+        const Tensor rows = clone(liveView(*b.k, b.start, b.len), st);
+        esdaCheck(esda_quantize_raw_rows(rows.data, (int32_t) kvH, live, q.data, (int64_t) cap * 512,
+                                         static_cast<float *>(sc.data), static_cast<float *>(bs.data), cap, 0, st));
+        hipCheck(hipStreamSynchronize(st), "ESKVCache q8 migration");
+    }
+    s.q = q;
+    s.sc = sc;
+    s.bs = bs;
+    s.len = live;
+    b = Slot{};
+}
+
+ESKVCache::RawQ8 ESKVCache::currentRawQ8(int layer) const {
+    checkLayer(layer);
+    const RQ8Slot &s = rq8slots_[layer];
+    if (!s.q) throw std::runtime_error("ESKVCache::currentRawQ8: layer holds no q8 rows");
+    const int pitch = (int) s.q->shape[1];
+    auto view = [&](const Tensor &t) { return s.len == pitch ? t : t.slice(1, 0, s.len); };
+    return {view(*s.q), view(*s.sc), view(*s.bs), *s.q, *s.sc, *s.bs, s.len, pitch};
+}
+
+ESKVCache::RawQ8 ESKVCache::updateRawQ8(int layer, const Tensor &kNew, hipStream_t st) {
+    // ESKVCache.mm:513-556.
+    checkLayer(layer);
+    checkRows(kNew, "ESKVCache::updateRawQ8 kNew");
+    if (kNew.shape[2] != 512) throw std::invalid_argument("ESKVCache::updateRawQ8: expects headDim 512");
+    if (slots_[layer].k && slots_[layer].v)
+        throw std::runtime_error("ESKVCache::updateRawQ8: slot holds composite K/V content "
+                                 "(post-norm) — not derivable as raw; re-prime the cache");
+    migrateToQ8(layer, st);
+    RQ8Slot &s = rq8slots_[layer];
+    const int nNew = (int) kNew.shape[1];
+    const Tensor src = kNew.contiguous() ? kNew : clone(kNew, st);
+    if (!s.q) {
+        // first store: capacity == content, as for the reference's first q8 store
+        auto qsb = quantizeRawRows(src, st);
+        s.q = qsb[0];
+        s.sc = qsb[1];
+        s.bs = qsb[2];
+        s.len = nNew;
+    } else {
+        if (kNew.shape[0] != s.q->shape[0])
+            throw std::invalid_argument("ESKVCache::updateRawQ8: kv heads differ from the slot");
+        growQ8(s, nNew, st);
+        const int cap = (int) s.q->shape[1];
+        esdaCheck(esda_quantize_raw_rows(src.data, (int32_t) kNew.shape[0], nNew, s.q->data, (int64_t) cap * 512,
+                                         static_cast<float *>(s.sc->data), static_cast<float *>(s.bs->data), cap,
+                                         s.len, st));
+        s.len += nNew;
+    }
+    if (!kNew.contiguous()) hipCheck(hipStreamSynchronize(st), "ESKVCache::updateRawQ8");
+    return currentRawQ8(layer);
+}
+
+Tensor ESKVCache::decodeRawQ8(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
+                              const std::vector<float> &invFreq, hipStream_t st, Tensor *out) {
+    checkLayer(layer);
+    checkRows(kNew, "ESKVCache::decodeRawQ8 kNew");
+    if (kNew.shape[1] != 1 || kNew.shape[2] != 512)
+        throw std::invalid_argument("ESKVCache::decodeRawQ8: kNew must be [kvHeads, 1, 512]");
+    if (invFreq.size() < 64)
+        throw std::invalid_argument("ESKVCache::decodeRawQ8: invFreq needs at least 64 entries");
+    if (slots_[layer].k && slots_[layer].v)
+        throw std::runtime_error("ESKVCache::decodeRawQ8: slot holds composite K/V content "
+                                 "(post-norm) — not derivable as raw; re-prime the cache");
+    migrateToQ8(layer, st);
+    const int kvH = (int) kNew.shape[0];
+    RQ8Slot &s = rq8slots_[layer];
+    if (!s.q) {
+        s.q = Tensor::empty({kvH, 1, 512}, Dtype::u8);
+        s.sc = Tensor::empty({kvH, 1, 1}, Dtype::f32);
+        s.bs = Tensor::empty({kvH, 1, 1}, Dtype::f32);
+        s.len = 0;
+    } else {
+        if (kvH != s.q->shape[0]) throw std::invalid_argument("ESKVCache::decodeRawQ8: kv heads differ from the slot");
+        growQ8(s, 1, st);
+    }
+    if (!invFreqDev_ || !std::equal(invFreqHost_.begin(), invFreqHost_.end(), invFreq.begin()) ||
+        invFreqHost_.size() != 64) {
+        if (invFreqDev_) hipCheck(hipStreamSynchronize(st), "ESKVCache rotary table");
+        invFreqHost_.assign(invFreq.begin(), invFreq.begin() + 64);
+        invFreqDev_ = Tensor::empty({64}, Dtype::f32);
+        hipCheck(hipMemcpyAsync(invFreqDev_->data, invFreqHost_.data(), 64 * sizeof(float),
+                                hipMemcpyHostToDevice, st),
+                 "ESKVCache rotary table upload");
+        hipCheck(hipStreamSynchronize(st), "ESKVCache rotary table upload");
+    }
+    if (!q.defined() || q.dtype != Dtype::bf16 || !q.contiguous() || q.numel() % 512)
+        throw std::invalid_argument("ESKVCache::decodeRawQ8: q must be contiguous bf16 [numQHeads, 512]");
+    if (!kw.defined() || kw.dtype != Dtype::bf16 || kw.numel() != 512 || !kw.contiguous())
+        throw std::invalid_argument("ESKVCache::decodeRawQ8: kw must be contiguous bf16 [512]");
+    const int Hq = (int) (q.numel() / 512);
+    const int cap = (int) s.q->shape[1];
+    esda_raw_desc d{};
+    d.batch = 1;
+    d.num_q_heads = Hq;
+    d.num_kv_heads = kvH;
+    d.head_dim = 512;
+    d.cap = cap;
+    d.head_stride = (int64_t) cap * 512;
+    d.seq_stride = (int64_t) kvH * cap * 512;
+    d.max_visible = s.len + 1;
+    d.split_rows = 0;
+    d.scale = 1.0f;
+    d.eps = eps;
+    size_t wsBytes = 0;
+    esdaCheck(esda_decode_raw_workspace_size(&d, &wsBytes));
+    Tensor o;
+    if (out) {
+        if (out->dtype != Dtype::bf16 || !out->contiguous() || out->numel() != (int64_t) Hq * 512)
+            throw std::invalid_argument("ESKVCache::decodeRawQ8: out must be contiguous bf16 [numQHeads, 512]");
+        o = *out;
+    } else {
+        o = Tensor::empty({Hq, 512}, Dtype::bf16);
+    }
+    esda_raw_q8_args a{};
+    a.q = q.data;
+    a.k_new = kNew.data;
+    a.q8_cache = s.q->data;
+    a.scale = static_cast<float *>(s.sc->data);
+    a.bias = static_cast<float *>(s.bs->data);
+    a.sb_head_stride = cap;
+    a.sb_seq_stride = (int64_t) kvH * cap;
+    a.pos = positionWord(layer, s.len, st);
+    a.kw = kw.data;
+    a.inv_freq = static_cast<const float *>(invFreqDev_->data);
+    a.out = o.data;
+    a.workspace = workspace(wsBytes, st);
+    a.workspace_bytes = workspace_->nbytes();
+    esdaCheck(esda_decode_raw_q8(&d, &a, st));
+    s.len += 1;
+    return o;
+}
+
 void ESKVCache::reset() {
     for (auto &a : k_) a.reset();
     for (auto &a : v_) a.reset();
     for (auto &s : slots_) s = Slot{};
+    for (auto &s : rq8slots_) s = RQ8Slot{};
     markers_.clear();
     rewindMark_.reset();
     seqLen_ = 0;

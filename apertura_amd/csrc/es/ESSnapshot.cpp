@@ -27,6 +27,8 @@
 #include <utility>
 #include <vector>
 
+#include "esda.h"
+
 namespace es {
 namespace {
 
@@ -366,12 +368,13 @@ StTensor download(const Tensor &buf, int r0, int n) {
     return t;
 }
 
-// A fresh zeroed [kvHeads, cap, headDim] bf16 buffer holding `rows` rows of host data
-// [kvHeads, rowsStored, headDim] (rows <= rowsStored; the rest of the buffer is zero).
-Tensor upload(const std::vector<uint8_t> &src, int64_t kvH, int64_t rowsStored, int64_t hd, int rows, int cap) {
-    Tensor t = Tensor::empty({kvH, cap, hd}, Dtype::bf16);
+// A fresh zeroed [kvHeads, cap, w] buffer of `dt` holding `rows` rows of host data
+// [kvHeads, rowsStored, w] (rows <= rowsStored; the rest of the buffer is zero).
+Tensor upload(const std::vector<uint8_t> &src, int64_t kvH, int64_t rowsStored, int64_t hd, int rows, int cap,
+              Dtype dt = Dtype::bf16) {
+    Tensor t = Tensor::empty({kvH, cap, hd}, dt);
     hipOk(hipMemset(t.data, 0, t.nbytes()), "ESKVCache snapshot clear");
-    const size_t rowBytes = (size_t) hd * 2;
+    const size_t rowBytes = (size_t) hd * dtypeSize(dt);
     if (rows > 0)
         hipOk(hipMemcpy2D(t.data, (size_t) cap * rowBytes, src.data(), (size_t) rowsStored * rowBytes,
                           (size_t) rows * rowBytes, (size_t) kvH, hipMemcpyHostToDevice),
@@ -473,6 +476,7 @@ bool ESKVCache::markRewindPoint(int pos) {
         if (a) return false;  // legacy storage: no rewind
     bool prealloc = false;
     for (const Slot &s : slots_) prealloc = prealloc || s.k.has_value();
+    for (const RQ8Slot &s : rq8slots_) prealloc = prealloc || s.q.has_value();
     if (!prealloc) return false;
     rewindMark_ = takeMarker(pos, /*copyLost=*/true, nullptr);
     return true;
@@ -486,7 +490,7 @@ int ESKVCache::rewindToMark() {
     for (const auto &lkv : rewindMark_->slidingKV) copyFor[lkv.first] = &lkv.second;
     for (size_t i = 0; i < slots_.size(); ++i) {
         const Slot &s = slots_[i];
-        if (s.k && !copyFor[i] && (s.lost || s.len < P)) {
+        if ((s.k && !copyFor[i] && (s.lost || s.len < P)) || (rq8slots_[i].q && rq8slots_[i].len < P)) {
             rewindMark_.reset();
             return -1;
         }
@@ -512,6 +516,8 @@ int ESKVCache::rewindToMark() {
     }
     hipOk(hipDeviceSynchronize(), "ESKVCache rewind");
     slots_ = std::move(next);
+    for (RQ8Slot &s : rq8slots_)
+        if (s.q) s.len = P;  // q8 rows never evict: cursor truncation
     rewindMark_.reset();
     return P;
 }
@@ -525,8 +531,15 @@ bool ESKVCache::saveSnapshot(const std::string &path, const std::string &fingerp
         std::map<std::string, std::string> meta;
         for (size_t i = 0; i < slots_.size(); ++i) {
             const Slot &s = slots_[i];
-            if (!s.k) return false;  // a snapshot needs every layer primed
             const std::string id = std::to_string(i);
+            if (const RQ8Slot &r = rq8slots_[i]; r.q) {
+                // q8 raw layer: packed rows and the per-row scale / bias, live [0, len)
+                ts.emplace_back("rq_" + id, download(*r.q, 0, r.len));
+                ts.emplace_back("rs_" + id, download(*r.sc, 0, r.len));
+                ts.emplace_back("rb_" + id, download(*r.bs, 0, r.len));
+                continue;
+            }
+            if (!s.k) return false;  // a snapshot needs every layer primed
             StTensor k = download(*s.k, s.start, s.len - s.start);
             if (s.v) {
                 StTensor v = s.shared ? k : download(*s.v, s.start, s.len - s.start);
@@ -630,18 +643,25 @@ int ESKVCache::restoreSnapshot(const std::string &path, const std::string &finge
                 return -1;  // unprimed layer, or quantized-KV tensors (no quantized storage here)
             }
         }
-        // Storage-mode gate (ESKVCache.mm:333-343): composite <-> raw is not derivable.  This
-        // cache holds no q8 rows, so q8 layers restore only as bf16 raw rows (mode raw).
-        if (mode == RawMode::rawQ8) return -1;
+        // Storage-mode gate (ESKVCache.mm:333-343): composite <-> raw is not derivable; the
+        // two raw forms convert (q8 -> bf16 dequantizes, bf16 -> q8 quantizes).
         if (mode != RawMode::asStored) {
             if (anyRaw && mode == RawMode::composite) return -1;
             if (!anyRaw && mode != RawMode::composite) return -1;
         }
-        for (size_t i = 0; i < slots_.size(); ++i)
-            if (kind[i] == RawQ8 && mode != RawMode::raw) return -1;
+        // Layers that end as q8 rows: stored q8 kept (asStored / rawQ8) and bf16 raw
+        // quantized (rawQ8).  The q8 format is defined for 512-wide rows only.
+        std::vector<bool> toQ8(slots_.size(), false);
+        for (size_t i = 0; i < slots_.size(); ++i) {
+            const std::string id = std::to_string(i);
+            if (kind[i] == RawQ8 && mode != RawMode::raw) toQ8[i] = true;
+            if (kind[i] == RawK && mode == RawMode::rawQ8) toQ8[i] = true;
+            if (toQ8[i] && T.at(kind[i] == RawQ8 ? "rq_" + id : "k_" + id).shape[2] != 512) return -1;
+        }
 
         // Build every layer's new slot (allocations may throw: nothing is committed yet).
         std::vector<Slot> next(slots_.size());
+        std::vector<RQ8Slot> nextQ8(slots_.size());
         for (size_t i = 0; i < slots_.size(); ++i) {
             const std::string id = std::to_string(i);
             Slot &s = next[i];
@@ -658,6 +678,40 @@ int ESKVCache::restoreSnapshot(const std::string &path, const std::string &finge
                 s.shared = shared;
                 s.len = content;
                 s.lost = content < targetPos;
+                continue;
+            }
+            if (kind[i] == RawQ8 && toQ8[i]) {
+                // q8 rows kept as stored (ESKVCache.mm:384-392), cut at the target position
+                const StTensor &q = T.at("rq_" + id), &sc = T.at("rs_" + id), &bs = T.at("rb_" + id);
+                const int64_t kvH = q.shape[0], rows = q.shape[1];
+                const int content = (int) std::min<int64_t>(rows, targetPos);
+                const int cap = chunkUp(content + kGrowChunk);
+                RQ8Slot &r = nextQ8[i];
+                r.q = upload(q.bytes, kvH, rows, 512, content, cap, Dtype::u8);
+                r.sc = upload(sc.bytes, kvH, rows, 1, content, cap, Dtype::f32);
+                r.bs = upload(bs.bytes, kvH, rows, 1, content, cap, Dtype::f32);
+                r.len = content;
+                continue;
+            }
+            if (kind[i] == RawK && toQ8[i]) {
+                // bf16 raw rows quantized during restore (ESKVCache.mm:394-408)
+                const StTensor &k = T.at("k_" + id);
+                const int64_t kvH = k.shape[0], rows = k.shape[1];
+                const int content = (int) std::min<int64_t>(rows, targetPos);
+                const int cap = chunkUp(content + kGrowChunk);
+                RQ8Slot &r = nextQ8[i];
+                r.q = upload({}, kvH, 0, 512, 0, cap, Dtype::u8);
+                r.sc = upload({}, kvH, 0, 1, 0, cap, Dtype::f32);
+                r.bs = upload({}, kvH, 0, 1, 0, cap, Dtype::f32);
+                r.len = content;
+                if (content > 0) {
+                    const Tensor rowsDev = upload(k.bytes, kvH, rows, 512, content, content);
+                    const int rc = esda_quantize_raw_rows(rowsDev.data, (int32_t) kvH, content, r.q->data,
+                                                          (int64_t) cap * 512, static_cast<float *>(r.sc->data),
+                                                          static_cast<float *>(r.bs->data), cap, 0, nullptr);
+                    if (rc != 0) throw std::runtime_error("ESKVCache restore: row quantization failed");
+                    hipOk(hipDeviceSynchronize(), "ESKVCache restore quantize");
+                }
                 continue;
             }
             if (kind[i] == RawQ8) {
@@ -700,6 +754,7 @@ int ESKVCache::restoreSnapshot(const std::string &path, const std::string &finge
         }
         hipOk(hipDeviceSynchronize(), "ESKVCache restore");
         slots_ = std::move(next);
+        rq8slots_ = std::move(nextQ8);
         return targetPos;
     } catch (const std::exception &) {
         return -1;

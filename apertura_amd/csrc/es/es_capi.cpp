@@ -139,6 +139,48 @@ int esda_cache_decode_raw(esda_cache *cache, int32_t layer, const void *q, int32
     });
 }
 
+namespace {
+void toQ8View(const es::ESKVCache::RawQ8 &r, esda_q8_view *v) {
+    if (!v) return;
+    v->q = r.qbuf.data;
+    v->scale = static_cast<float *>(r.scbuf.data);
+    v->bias = static_cast<float *>(r.bsbuf.data);
+    v->kv_heads = (int32_t) r.qbuf.shape[0];
+    v->len = r.len;
+    v->pitch = r.pitch;
+}
+}  // namespace
+
+int esda_cache_update_raw_q8(esda_cache *cache, int32_t layer, const void *k_new, int32_t kv_heads, int32_t n_new,
+                             void *stream, esda_q8_view *view) {
+    return guarded([&] {
+        needCache(cache);
+        toQ8View(cache->impl.updateRawQ8(layer, rows(k_new, kv_heads, n_new, 512), asStream(stream)), view);
+    });
+}
+
+int esda_cache_current_raw_q8(esda_cache *cache, int32_t layer, esda_q8_view *view) {
+    return guarded([&] {
+        needCache(cache);
+        toQ8View(cache->impl.currentRawQ8(layer), view);
+    });
+}
+
+int esda_cache_decode_raw_q8(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads,
+                             const void *k_new, int32_t kv_heads, const void *kw, float eps, const float *inv_freq,
+                             int32_t n_freq, void *out, void *stream) {
+    return guarded([&] {
+        needCache(cache);
+        if (!q || !out || !kw || !inv_freq || num_q_heads <= 0 || n_freq < 0)
+            throw std::invalid_argument("esda_cache_decode_raw_q8: null pointer");
+        es::Tensor qt = es::Tensor::wrap(const_cast<void *>(q), {num_q_heads, 512}, es::Dtype::bf16);
+        es::Tensor ot = es::Tensor::wrap(out, {num_q_heads, 512}, es::Dtype::bf16);
+        es::Tensor kwt = es::Tensor::wrap(const_cast<void *>(kw), {512}, es::Dtype::bf16);
+        std::vector<float> f(inv_freq, inv_freq + n_freq);
+        cache->impl.decodeRawQ8(layer, qt, rows(k_new, kv_heads, 1, 512), kwt, eps, f, asStream(stream), &ot);
+    });
+}
+
 int esda_cache_slot(esda_cache *cache, int32_t layer, int32_t *len, int32_t *start, int32_t *capacity,
                     int32_t *flags) {
     return guarded([&] {
@@ -151,6 +193,7 @@ int esda_cache_slot(esda_cache *cache, int32_t layer, int32_t *len, int32_t *sta
             if (cache->impl.slotLost(layer)) f |= 1;
             if (cache->impl.slotShared(layer)) f |= 2;
             if (cache->impl.slotRaw(layer)) f |= 4;
+            if (cache->impl.slotQ8(layer)) f |= 8;
             *flags = f;
         }
     });
@@ -219,6 +262,26 @@ int esda_decode_attn_global(const void *q, int32_t num_q_heads, const void *raw_
         es::Tensor ot = es::Tensor::wrap(out, {num_q_heads, 512}, es::Dtype::bf16);
         std::vector<float> f(inv_freq, inv_freq + n_freq);
         es::esDecodeAttnGlobal(qt, rb, len, pitch, kwt, eps, f, asStream(stream), &ot);
+    });
+}
+
+int esda_decode_attn_global_q8(const void *q, int32_t num_q_heads, const void *q8_buf, const float *scale_buf,
+                               const float *bias_buf, int32_t num_kv_heads, int32_t len, int32_t pitch,
+                               const void *kw, float eps, const float *inv_freq, int32_t n_freq, void *out,
+                               void *stream) {
+    return guarded([&] {
+        if (!q || !q8_buf || !scale_buf || !bias_buf || !kw || !inv_freq || !out || n_freq < 0)
+            throw std::invalid_argument("esda_decode_attn_global_q8: null pointer");
+        if (num_q_heads <= 0 || num_kv_heads <= 0 || pitch <= 0)
+            throw std::invalid_argument("esda_decode_attn_global_q8: sizes must be positive");
+        es::Tensor qt = es::Tensor::wrap(const_cast<void *>(q), {num_q_heads, 512}, es::Dtype::bf16);
+        es::Tensor qb = es::Tensor::wrap(const_cast<void *>(q8_buf), {num_kv_heads, pitch, 512}, es::Dtype::u8);
+        es::Tensor sb = es::Tensor::wrap(const_cast<float *>(scale_buf), {num_kv_heads, pitch, 1}, es::Dtype::f32);
+        es::Tensor bb = es::Tensor::wrap(const_cast<float *>(bias_buf), {num_kv_heads, pitch, 1}, es::Dtype::f32);
+        es::Tensor kwt = es::Tensor::wrap(const_cast<void *>(kw), {512}, es::Dtype::bf16);
+        es::Tensor ot = es::Tensor::wrap(out, {num_q_heads, 512}, es::Dtype::bf16);
+        std::vector<float> f(inv_freq, inv_freq + n_freq);
+        es::esDecodeAttnGlobalQ8(qt, qb, sb, bb, len, pitch, kwt, eps, f, asStream(stream), &ot);
     });
 }
 

@@ -23,4 +23,11 @@ Tensor esDecodeAttnGlobal(const Tensor &q, const Tensor &rawBuf, int len, int pi
                           float eps, const std::vector<float> &invFreq, hipStream_t stream = nullptr,
                           Tensor *out = nullptr);
 
+// The same over a q8 raw stream (esDecodeAttnGlobalQ8, ESDecodeAttn.h:30-35,
+// ESDecodeAttn.mm:455-489): qBuf [numKV, pitch, 512] u8 and scBuf / bsBuf [numKV, pitch, 1]
+// f32, the unsliced buffers of ESKVCache::updateRawQ8; rows x = q * scale + bias.
+Tensor esDecodeAttnGlobalQ8(const Tensor &q, const Tensor &qBuf, const Tensor &scBuf, const Tensor &bsBuf,
+                            int len, int pitch, const Tensor &kw, float eps, const std::vector<float> &invFreq,
+                            hipStream_t stream = nullptr, Tensor *out = nullptr);
+
 }  // namespace es

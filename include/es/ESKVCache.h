@@ -10,16 +10,18 @@
 //  decode() is the fused decode step of this library: the prealloc append and the
 //  attention of the new token in one GPU pass (esda_decode), replacing update()
 //  followed by SDPA at ESAttention.mm:105 and :188.
-//  KV snapshots (the reference's safetensors layout), prefix markers and turn rewind
-//  follow ESKVCache.mm:121-456.  Quantized / q8 storage and the compiled step mode are
-//  not implemented: a snapshot holding q8 rows restores only as bf16 raw rows (the
-//  reference's "rehydration"), and quantized-KV snapshots are refused (-1).
+//  q8 raw-K storage (rawKVQ8: per-row affine u8 rows with an f32 scale and bias,
+//  ESKVCache.mm:506-566), KV snapshots (the reference's safetensors layout), prefix
+//  markers and turn rewind follow the reference (ESKVCache.mm:121-456).  Quantized-KV
+//  storage (quantized_matmul groups) and the compiled step mode are not implemented:
+//  quantized-KV snapshots are refused (-1).
 //
 //  Every call takes a HIP stream (nullptr = the default stream).  Buffer growth and
 //  compaction synchronise that stream before the old buffer is released.  An instance
 //  is used from one thread at a time (the reference runs its engine on one thread).
 #include "ESTensor.h"
 
+#include <array>
 #include <functional>
 #include <optional>
 #include <string>
@@ -57,6 +59,27 @@ public:
     // only from updateRaw).  Throws std::runtime_error for a non-raw slot.
     Raw currentRaw(int layer) const;
 
+    // q8 raw-K storage (ESKVCache.h:81-91): kNew [kvHeads, nNew, 512] bf16 raw rows are
+    // quantized per row (u8 q, f32 scale and bias: x = q * scale + bias) and appended; the
+    // three buffers share one cursor.  A slot holding bf16 raw rows (a restored snapshot)
+    // is migrated on the first call: its live rows are quantized once and the bf16
+    // buffer retired.  Throws std::runtime_error for a composite slot.  Views: q
+    // [kvHeads, len, 512] u8, sc / bs [kvHeads, len, 1] f32; buffers of `pitch` rows.
+    struct RawQ8 {
+        Tensor qview, sc, bs, qbuf, scbuf, bsbuf;
+        int len, pitch;
+    };
+    RawQ8 updateRawQ8(int layer, const Tensor &kNew, hipStream_t stream = nullptr);
+    // The row quantizer behind updateRawQ8: {q u8 [kvH, n, 512], scale f32 [kvH, n, 1],
+    // bias f32 [kvH, n, 1]} (ESKVCache.mm:506-511, esQuantizeRawRows).
+    static std::array<Tensor, 3> quantizeRawRows(const Tensor &kNew, hipStream_t stream = nullptr);
+    // Fused q8 decode step: updateRawQ8(layer, kNew) and esDecodeAttnGlobalQ8 over the slot
+    // in one GPU pass (the kernel quantizes the new row itself).  kNew: [kvHeads, 1, 512].
+    Tensor decodeRawQ8(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
+                       const std::vector<float> &invFreq, hipStream_t stream = nullptr, Tensor *out = nullptr);
+    // The RawQ8 record of a q8 slot without appending (throws std::runtime_error otherwise).
+    RawQ8 currentRawQ8(int layer) const;
+
     // Fused decode step for `layer` (prealloc storage): appends the single new row of
     // kNew/vNew ([kvHeads, 1, headDim]) and returns softmax(scale q K^T) V over the rows
     // the reference would attend after update(maxKeep): [numQHeads, headDim] bf16 in
@@ -80,7 +103,7 @@ public:
     // prefix (they evicted) have that window copied now.
     void markPrefix(int pos, const std::string &fingerprint);
     // saveSnapshot: safetensors file of every layer's live rows (k_<i>/v_<i>; raw layers
-    // k_<i> only), metadata {fingerprint, pos, layers, marker_*} and the markers' windows
+    // k_<i> only; q8 raw layers rq_<i> u8 + rs_<i> / rb_<i> f32 scale and bias), metadata {fingerprint, pos, layers, marker_*} and the markers' windows
     // (m<j>_k_<i>/m<j>_v_<i>).  false if a layer is unprimed or the file cannot be written.
     bool saveSnapshot(const std::string &path, const std::string &fingerprint, int pos) const;
     enum class RawMode { composite, raw, rawQ8, asStored };
@@ -88,7 +111,10 @@ public:
     // or fingerprint mismatch with no usable marker, or a storage-mode mismatch; otherwise
     // re-homes every layer into fresh chunk-aligned buffers and returns the restored
     // position (the snapshot's, or the longest marker whose fingerprint prefixFp(pos)
-    // reproduces).  RawMode::rawQ8 is refused (no q8 storage here).
+    // reproduces).  Raw streams convert to the requested mode: RawMode::raw dequantizes
+    // stored q8 rows to bf16 (bf16(float(q) * scale + bias)), RawMode::rawQ8 quantizes
+    // stored bf16 raw rows; asStored keeps each layer's stored form.  Composite <-> raw is
+    // a mismatch.  Every layer's storage is replaced.
     int restoreSnapshot(const std::string &path, const std::string &fingerprint,
                         RawMode mode = RawMode::asStored,
                         const std::function<std::string(int)> &prefixFp = nullptr);
@@ -105,12 +131,13 @@ public:
 
     int numLayers() const { return (int) slots_.size(); }
     // Prealloc slot bookkeeping (read-only).
-    int slotLen(int layer) const { return slotAt(layer).len; }
+    int slotLen(int layer) const { return slotQ8(layer) ? rq8slots_[layer].len : slotAt(layer).len; }
     int slotStart(int layer) const { return slotAt(layer).start; }
     int slotCapacity(int layer) const;
     bool slotLost(int layer) const { return slotAt(layer).lost; }
     bool slotShared(int layer) const { return slotAt(layer).shared; }
     bool slotRaw(int layer) const { return slotAt(layer).k.has_value() && !slotAt(layer).v.has_value(); }
+    bool slotQ8(int layer) const { slotAt(layer); return rq8slots_[layer].q.has_value(); }
 
 private:
     struct Slot {
@@ -130,6 +157,14 @@ private:
     };
     std::vector<Marker> markers_;
     std::optional<Marker> rewindMark_;
+    // q8 raw storage: u8 rows [kvH, cap, 512] and scale / bias [kvH, cap, 1], live [0, len).
+    struct RQ8Slot {
+        std::optional<Tensor> q, sc, bs;
+        int len = 0;
+    };
+    std::vector<RQ8Slot> rq8slots_;
+    void growQ8(RQ8Slot &s, int nNew, hipStream_t stream);
+    void migrateToQ8(int layer, hipStream_t stream);
     Marker takeMarker(int pos, bool copyLost, hipStream_t stream) const;
     int seqLen_ = 0;
     std::optional<Tensor> posDev_;     // per-layer position words for decode()

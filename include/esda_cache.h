@@ -15,6 +15,9 @@
  *   esda_cache_current             ESKVCache::current                  ESKVCache.h:117, ESKVCache.mm:112-119
  *   esda_cache_decode              ESKVCache::update + SDPA decode     ESAttention.mm:105, :188
  *   esda_cache_decode_raw          updateRaw + esDecodeAttnGlobal      ESAttention.mm:291-300
+ *   esda_cache_update_raw_q8       ESKVCache::updateRawQ8              ESKVCache.h:81-88, ESKVCache.mm:513-556
+ *   esda_cache_decode_raw_q8       updateRawQ8 + esDecodeAttnGlobalQ8  ESAttention.mm:270-277
+ *   esda_cache_current_raw_q8      a q8 slot's RawQ8 record without appending (no counterpart)
  *   esda_cache_seq_len / mark_step ESKVCache::seqLen / markStep        ESKVCache.h:176-177
  *   esda_cache_reset               ESKVCache::reset                    ESKVCache.h:178, ESKVCache.mm:622-638
  *   esda_cache_save_snapshot       ESKVCache::saveSnapshot             ESKVCache.h:129, ESKVCache.mm:224-278
@@ -26,6 +29,7 @@
  *   esda_cache_slot                slot bookkeeping (len, start, capacity) for callers
  *                                  and tests; the reference keeps it private (ESKVCache.h:183-192)
  *   esda_decode_attn_global        esDecodeAttnGlobal                  ESDecodeAttn.h:27-28
+ *   esda_decode_attn_global_q8     esDecodeAttnGlobalQ8                ESDecodeAttn.h:30-36
  */
 #ifndef APERTURA_ESDA_CACHE_H
 #define APERTURA_ESDA_CACHE_H
@@ -82,8 +86,32 @@ int esda_cache_decode_raw(esda_cache *cache, int32_t layer, const void *q, int32
                           const void *k_new, int32_t kv_heads, const void *kw, float eps,
                           const float *inv_freq, int32_t n_freq, void *out, void *stream);
 
+/* A q8 raw slot (ESKVCache::RawQ8): u8 rows q [kv_heads, pitch, 512] and f32 scale / bias
+ * [kv_heads, pitch] (element (h, r) at h*pitch + r); rows 0 .. len-1 are live and each
+ * dequantizes to x = float(q) * scale + bias.  Non-owning: valid until the slot grows. */
+typedef struct esda_q8_view {
+    void *q;
+    float *scale;
+    float *bias;
+    int32_t kv_heads;
+    int32_t len;
+    int32_t pitch;
+} esda_q8_view;
+
+/* Quantize n_new bf16 raw rows k_new [kv_heads, n_new, 512] and append them to the layer's
+ * q8 slot (a bf16 raw slot migrates first: its live rows are quantized once and retired). */
+int esda_cache_update_raw_q8(esda_cache *cache, int32_t layer, const void *k_new, int32_t kv_heads,
+                             int32_t n_new, void *stream, esda_q8_view *view);
+int esda_cache_current_raw_q8(esda_cache *cache, int32_t layer, esda_q8_view *view);
+/* Fused q8 decode step: the new raw row is quantized in the kernel into row len of the slot,
+ * then rows 0 .. len are attended.  Arguments as esda_cache_decode_raw. */
+int esda_cache_decode_raw_q8(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads,
+                             const void *k_new, int32_t kv_heads, const void *kw, float eps,
+                             const float *inv_freq, int32_t n_freq, void *out, void *stream);
+
 /* flags: bit 0 = rows before start were discarded by a compaction, bit 1 = shared K=V
- * buffer, bit 2 = raw-K content. */
+ * buffer, bit 2 = raw-K content, bit 3 = q8 raw-K content (len and capacity are then the
+ * q8 slot's). */
 int esda_cache_slot(esda_cache *cache, int32_t layer, int32_t *len, int32_t *start,
                     int32_t *capacity, int32_t *flags);
 
@@ -100,8 +128,8 @@ int esda_cache_save_snapshot(const esda_cache *cache, const char *path, const ch
 int esda_cache_restore_snapshot(esda_cache *cache, const char *path, const char *fingerprint);
 /* The caller's prompt-prefix fingerprint at a marker position ("" or NULL: none). */
 typedef const char *(*esda_prefix_fp_fn)(int32_t pos, void *user);
-/* mode: 0 composite, 1 raw, 2 raw q8 (refused: no q8 storage), 3 as stored
- * (ESKVCache::RawMode); prefix_fp may be NULL. */
+/* mode: 0 composite, 1 raw (q8 layers dequantize to bf16), 2 raw q8 (bf16 raw layers
+ * quantize), 3 as stored (ESKVCache::RawMode); prefix_fp may be NULL. */
 int esda_cache_restore_snapshot_ex(esda_cache *cache, const char *path, const char *fingerprint,
                                    int32_t mode, esda_prefix_fp_fn prefix_fp, void *user);
 /* Marks position pos (>= 4096, else ESDA_ERR_INVALID_ARGUMENT) for the next snapshot. */
@@ -117,6 +145,14 @@ int esda_decode_attn_global(const void *q, int32_t num_q_heads, const void *raw_
                             int32_t num_kv_heads, int32_t len, int32_t pitch, const void *kw,
                             float eps, const float *inv_freq, int32_t n_freq, void *out,
                             void *stream);
+
+/* esDecodeAttnGlobalQ8: as esda_decode_attn_global over a q8 raw stream, q8_buf the
+ * unsliced u8 [num_kv_heads, pitch, 512] buffer and scale_buf / bias_buf its f32
+ * [num_kv_heads, pitch] per-row scale and bias. */
+int esda_decode_attn_global_q8(const void *q, int32_t num_q_heads, const void *q8_buf,
+                               const float *scale_buf, const float *bias_buf, int32_t num_kv_heads,
+                               int32_t len, int32_t pitch, const void *kw, float eps,
+                               const float *inv_freq, int32_t n_freq, void *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -94,7 +94,8 @@ def test_es_cache_handle_host_side_behaviour(tmp_path):
     assert c.save_snapshot(str(tmp_path / "s"), "fp", 1) is False
     assert c.restore_snapshot(str(tmp_path / "s"), "fp") == -1
     assert c.mark_rewind_point(1) is False and c.rewind_to_mark() == -1
-    assert c.slot(2) == {"len": 0, "start": 0, "capacity": 0, "lost": False, "shared": False, "raw": False}
+    assert c.slot(2) == {"len": 0, "start": 0, "capacity": 0, "lost": False, "shared": False, "raw": False,
+                         "q8": False}
     with pytest.raises(_lib.EsdaError) as ei:
         c.slot(4)
     assert ei.value.code == 1
@@ -104,6 +105,14 @@ def test_es_cache_handle_host_side_behaviour(tmp_path):
     assert rc == 1 and b"null" in _lib.lib().esda_last_error()
     rc = _lib.lib().esda_cache_current(c._h, 1, 1, ctypes.byref(view), ctypes.byref(view))
     assert rc == 2  # no rows yet: std::runtime_error
+    q8v = _lib.Q8View()
+    assert _lib.lib().esda_cache_current_raw_q8(c._h, 1, ctypes.byref(q8v)) == 2  # no q8 rows
+    rc = _lib.lib().esda_cache_update_raw_q8(c._h, 0, None, 2, 1, None, ctypes.byref(q8v))
+    assert rc == 1 and b"null" in _lib.lib().esda_last_error()
+    rc = _lib.lib().esda_cache_decode_raw_q8(c._h, 0, None, 16, None, 2, None, 1e-6, None, 0, None, None)
+    assert rc == 1
+    rc = _lib.lib().esda_decode_attn_global_q8(None, 16, None, None, None, 2, 1, 1, None, 1e-6, None, 0, None, None)
+    assert rc == 1
     with pytest.raises(_lib.EsdaError):
         ESKVCache(0)
 

@@ -155,7 +155,10 @@ def test_refused_restores_leave_the_cache_untouched(tmp_path):
     assert target.restore_snapshot(str(tmp_path / "missing.safetensors"), "fp") == -1
     assert target.restore_snapshot(good, "other-fp") == -1                 # fingerprint miss, no markers
     assert target.restore_snapshot(good, "fp", mode="composite") == -1    # the file holds a raw layer
-    assert target.restore_snapshot(good, "fp", mode="rawQ8") == -1        # no q8 storage here
+    comp_only = str(tmp_path / "composite.safetensors")
+    _save_composite_only(comp_only, 4)
+    assert target.restore_snapshot(comp_only, "fp", mode="rawQ8") == -1   # composite -> raw q8
+    assert target.restore_snapshot(comp_only, "fp", mode="raw") == -1     # composite -> raw
     assert ESKVCache(3).restore_snapshot(good, "fp") == -1                 # layer count
     after = _snapshot_state(target, 4)
     for (s0, l0), (s1, l1) in zip(before, after):
@@ -166,10 +169,21 @@ def test_refused_restores_leave_the_cache_untouched(tmp_path):
     assert not ESKVCache(2).save_snapshot(str(tmp_path / "x.safetensors"), "fp", 0)
 
 
+def _save_composite_only(path, layers):
+    from safetensors.torch import save_file
+    rng = np.random.default_rng(40)
+    t = {}
+    for i in range(layers):
+        for n in ("k_", "v_"):
+            t[n + str(i)] = torch.from_numpy(rms_rows(rng, (1, 20, 128)).view(np.int16)).view(torch.bfloat16)
+    save_file(t, path, metadata={"fingerprint": "fp", "pos": "20", "layers": str(layers)})
+
+
 def test_reference_layout_files_restore(tmp_path):
     """Files written by the safetensors package in the reference's layout: a composite
-    layer (k_0/v_0), a raw-K layer (k_1), and a q8 raw layer (rq_2/rs_2/rb_2) that restores
-    only as bf16 raw rows, bf16(float(q) * scale + bias) (ESKVCache.mm:366-383)."""
+    layer (k_0/v_0), a raw-K layer (k_1), and a q8 raw layer (rq_2/rs_2/rb_2).  As stored
+    the q8 layer keeps its bytes; mode raw rehydrates it to bf16(float(q) * scale + bias)
+    (ESKVCache.mm:366-383); mode rawQ8 quantizes the bf16 raw layer (ESKVCache.mm:394-408)."""
     from apertura_amd.cache import ESKVCache
     from safetensors.torch import save_file
     rng = np.random.default_rng(4)
@@ -185,14 +199,25 @@ def test_reference_layout_files_restore(tmp_path):
     path = str(tmp_path / "ref.safetensors")
     save_file(tensors, path, metadata={"fingerprint": "ref", "pos": "90", "layers": "3"})
     c = ESKVCache(3)
-    assert c.restore_snapshot(path, "ref") == -1                  # as stored: q8 rows cannot be held
     assert c.restore_snapshot(path, "ref", mode="composite") == -1
+    assert c.restore_snapshot(path, "ref") == 90                  # as stored
+    assert c.slot(1)["raw"] and not c.slot(1)["q8"] and np.array_equal(_live(c, 1)[0], k1)
+    s2 = c.slot(2)
+    assert s2["q8"] and not s2["raw"] and s2["len"] == 90 and s2["capacity"] == 512  # roundUp(90 + 256)
+    gq, gsc, gbs = (t.cpu().numpy() for t in c.current_raw_q8(2).torch())
+    assert np.array_equal(gq, q2) and np.array_equal(gsc, sc2[..., 0]) and np.array_equal(gbs, bs2[..., 0])
+    assert c.restore_snapshot(path, "ref", mode="rawQ8") == 90    # bf16 raw layer quantized
+    eq, esc, ebs = orc.quantize_rows(k1)
+    gq, gsc, gbs = (t.cpu().numpy() for t in c.current_raw_q8(1).torch())
+    assert c.slot(1)["q8"] and np.array_equal(gq, eq)
+    assert np.array_equal(gsc.view(np.uint32), esc.view(np.uint32)) and np.array_equal(gbs.view(np.uint32), ebs.view(np.uint32))
     assert c.restore_snapshot(path, "ref", mode="raw") == 90
     assert np.array_equal(_live(c, 0)[0], k0) and np.array_equal(_live(c, 0)[1], v0)
     assert c.slot(0)["lost"] and c.slot(0)["len"] == 77           # 77 rows of a 90-position prefix
     assert c.slot(1)["raw"] and np.array_equal(_live(c, 1)[0], k1)
     expect = orc.to_bf16((q2.astype(np.float32) * sc2) + bs2)
-    assert c.slot(2)["raw"] and np.array_equal(_live(c, 2)[0], expect)
+    assert c.slot(2)["raw"] and not c.slot(2)["q8"] and np.array_equal(_live(c, 2)[0], expect)
+    assert not c.slot(1)["q8"] and np.array_equal(_live(c, 1)[0], k1)
 
 
 def test_prefix_marker_restores_the_longest_reproducible_prefix(tmp_path):
