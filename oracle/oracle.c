@@ -480,3 +480,109 @@ void orc_quantize_rows(const uint16_t *x, int64_t rows, int32_t n, uint8_t *q, f
         bias[r] = mn;
     }
 }
+
+/* ------------------------------------------------------------ prefill */
+
+typedef struct {
+    const uint16_t *q, *k, *v;
+    int64_t q_head_stride, q_row_stride, kv_head_stride;
+    int32_t Hq, Hkv, D, Sq, Sk, q_pos0, k_pos0, window;
+    float scale;
+    double *out;
+    int32_t status;
+} prefill_job_t;
+
+/* Key j (absolute k_pos0 + j) is visible to query i (absolute q_pos0 + i) under the
+ * additive mask of buildMask (ESGemma4TextModel.mm:68-83: kAbs <= qAbs, and on sliding
+ * layers kAbs > qAbs - window) aligned to the retained keys by alignMask
+ * (ESAttention.mm:17-22: the last Sk columns). */
+static int prefill_visible(const prefill_job_t *j, int32_t i, int32_t kj) {
+    const int64_t qa = (int64_t) j->q_pos0 + i, ka = (int64_t) j->k_pos0 + kj;
+    if (g_fault == 7 ? ka >= qa : ka > qa) return 0; /* planted: the diagonal masked */
+    if (j->window > 0 && ka <= qa - j->window) return 0;
+    return 1;
+}
+
+/* One (query row, query head): O = softmax(scale * q K^T + M) V over the visible keys,
+ * GQA kv-major (ESOps.h:64-68), fp64. */
+static void item_prefill(void *ctx, int64_t it) {
+    prefill_job_t *j = (prefill_job_t *) ctx;
+    const int32_t i = (int32_t) (it / j->Hq), h = (int32_t) (it % j->Hq), D = j->D;
+    const int32_t g = j->Hq / j->Hkv;
+    const int32_t kvh = g_fault == 1 ? h % j->Hkv : h / g;
+    const float scale = g_fault == 3 ? 1.0f : j->scale;
+    double *out = j->out + ((size_t) i * j->Hq + h) * D;
+    double *qd = (double *) malloc(sizeof(double) * D);
+    double *s = (double *) malloc(sizeof(double) * (j->Sk > 0 ? j->Sk : 1));
+    const uint16_t *qh = j->q + (size_t) h * j->q_head_stride + (size_t) i * j->q_row_stride;
+    for (int32_t d = 0; d < D; ++d) qd[d] = orc_bf16_to_f32(qh[d]);
+    const uint16_t *kb = j->k + (size_t) kvh * j->kv_head_stride, *vb = j->v + (size_t) kvh * j->kv_head_stride;
+    double mx = -INFINITY;
+    int32_t n = 0;
+    for (int32_t t = 0; t < j->Sk; ++t) {
+        if (!prefill_visible(j, i, t)) { s[t] = -INFINITY; continue; }
+        const uint16_t *kr = kb + (size_t) t * D;
+        double acc = 0.0;
+        for (int32_t d = 0; d < D; ++d) acc += qd[d] * (double) orc_bf16_to_f32(kr[d]);
+        s[t] = acc * (double) scale;
+        if (s[t] > mx) mx = s[t];
+        ++n;
+    }
+    for (int32_t d = 0; d < D; ++d) out[d] = 0.0;
+    if (n == 0) { j->status = -1; free(qd); free(s); return; }
+    double den = 0.0;
+    for (int32_t t = 0; t < j->Sk; ++t) { s[t] = s[t] == -INFINITY ? 0.0 : exp(s[t] - mx); den += s[t]; }
+    for (int32_t t = 0; t < j->Sk; ++t) {
+        if (s[t] == 0.0) continue;
+        const uint16_t *vr = vb + (size_t) t * D;
+        const double w = s[t] / den;
+        for (int32_t d = 0; d < D; ++d) out[d] += w * (double) orc_bf16_to_f32(vr[d]);
+    }
+    free(qd); free(s);
+}
+
+int32_t orc_prefill_f64(const uint16_t *q, int64_t q_head_stride, int64_t q_row_stride,
+                        const uint16_t *k, const uint16_t *v, int64_t kv_head_stride,
+                        int32_t Hq, int32_t Hkv, int32_t D, int32_t Sq, int32_t Sk,
+                        int32_t q_pos0, int32_t k_pos0, int32_t window, float scale,
+                        double *out, int32_t nthreads) {
+    if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || D <= 0 || Sq <= 0 || Sk <= 0 || window < 0) return -1;
+    prefill_job_t j = {q, k, v, q_head_stride, q_row_stride, kv_head_stride,
+                       Hq, Hkv, D, Sq, Sk, q_pos0, k_pos0, window, scale, out, 0};
+    run_items(item_prefill, &j, (int64_t) Sq * Hq, nthreads);
+    return j.status;
+}
+
+/* Raw-K prefill reconstruction, ESAttention.mm:306-326, per kv head h and row t (absolute
+ * position pos0 + t):
+ *   rinv = 1 / sqrt(mean(x^2) + eps) (ESRMSNorm, f32)
+ *   K0 = bf16(x * rinv * kw), V = bf16(x * rinv)           (kNorm_, vNorm_)
+ *   c, s = bf16(cos / sin(f32(pos * inv_freq[f]))), f = d mod D/2 (emb = [freqs, freqs])
+ *   K = bf16(bf16(K0 * c) + bf16(rotateHalf(K0) * s)), rotateHalf(K0)[d] = -K0[d + D/2]
+ *       for d < D/2 and K0[d - D/2] above (ESOps.h:58-62)
+ * raw, k, v: [Hkv, Sk, D] dense; inv_freq: D/2 entries. */
+void orc_raw_prefill_kv(const uint16_t *raw, int32_t Hkv, int32_t Sk, int32_t D, const uint16_t *kw,
+                        float eps, const float *inv_freq, int32_t pos0, uint16_t *k, uint16_t *v) {
+    const int32_t half = D / 2;
+    float *x = (float *) malloc(sizeof(float) * D);
+    float *k0 = (float *) malloc(sizeof(float) * D);
+    for (int64_t r = 0; r < (int64_t) Hkv * Sk; ++r) {
+        const int32_t t = (int32_t) (r % Sk);
+        const uint16_t *xr = raw + r * D;
+        float ss = 0.0f;
+        for (int32_t d = 0; d < D; ++d) { x[d] = orc_bf16_to_f32(xr[d]); ss += x[d] * x[d]; }
+        const float rinv = 1.0f / sqrtf(ss / (float) D + eps);
+        for (int32_t d = 0; d < D; ++d) {
+            k0[d] = bf(x[d] * rinv * orc_bf16_to_f32(kw[d]));
+            v[r * D + d] = orc_f32_to_bf16(x[d] * rinv);
+        }
+        for (int32_t d = 0; d < D; ++d) {
+            const float a = (float) (pos0 + t) * inv_freq[d % half];
+            const float c = bf(cosf(a)), sn = bf(sinf(a));
+            float rh = d < half ? -k0[d + half] : k0[d - half];
+            if (g_fault == 8) rh = -rh; /* planted: rotateHalf with the wrong sign */
+            k[r * D + d] = orc_f32_to_bf16(bf(k0[d] * c) + bf(rh * sn));
+        }
+    }
+    free(x); free(k0);
+}

@@ -22,6 +22,10 @@
  *   orc_rms_norm_rows    ESRMSNorm.mm:20-27 (manual f32 path)
  *   orc_quantize_rows    ESDecodeAttn.mm:491-539 (esQuantizeRawRows: per-row affine u8)
  *   orc_decode_raw_q8_f64 ESDecodeAttn.mm:275-369 (q8 rows dequantised, then as below)
+ *   orc_prefill_f64      ESAttention.mm:168-193 at seq > 1 (SDPA over a prefill chunk with
+ *                        the buildMask / alignMask additive mask), GQA kv-major
+ *   orc_raw_prefill_kv   ESAttention.mm:306-326 (raw-K prefill: kNorm / vNorm by ops, RoPE
+ *                        by ops with bf16 cos/sin and bf16 products and sum)
  *   orc_decode_raw_f64   ESDecodeAttn.mm:17-117 reconstruction (rinv, kw, p-RoPE pairs
  *                        (d, d+256) for d < 64, bf16 cos/sin, bf16 K, V = kraw*rinv)
  *                        + merge, evaluated in fp64 after the kernel's rounding points
@@ -124,6 +128,26 @@ void orc_quantize_rows(const uint16_t *x, int64_t rows, int32_t n, uint8_t *q, f
 /* Planted-mistake switch for the oracle's own self-tests (0 = none).  Used only by
  * tests that show a plausible mistake is caught by the pins. */
 void orc_set_fault(int32_t fault);
+
+/* Prefill attention (ESAttention.mm:168-193 at seq > 1: SDPA with the additive mask of
+ * ESGemma4TextModel.mm:68-83 aligned by ESAttention.mm:17-22), fp64.
+ *   q: element (h, i, d) at q[h*q_head_stride + i*q_row_stride + d], query row i < Sq at
+ *      absolute position q_pos0 + i
+ *   k, v: element (kvh, j, d) at k[kvh*kv_head_stride + j*D + d], key j < Sk at absolute
+ *      position k_pos0 + j
+ *   key j is visible to query i iff kAbs <= qAbs and (window == 0 or kAbs > qAbs - window)
+ *   out: (i, h, d) at out[(i*Hq + h)*D + d]
+ * Returns -1 for a query with no visible key. */
+int32_t orc_prefill_f64(const uint16_t *q, int64_t q_head_stride, int64_t q_row_stride,
+                        const uint16_t *k, const uint16_t *v, int64_t kv_head_stride,
+                        int32_t Hq, int32_t Hkv, int32_t D, int32_t Sq, int32_t Sk,
+                        int32_t q_pos0, int32_t k_pos0, int32_t window, float scale,
+                        double *out, int32_t nthreads);
+
+/* Raw-K prefill reconstruction of K and V by the reference's ops (ESAttention.mm:306-326):
+ * raw, k, v [Hkv, Sk, D] bf16; key row t at absolute position pos0 + t. */
+void orc_raw_prefill_kv(const uint16_t *raw, int32_t Hkv, int32_t Sk, int32_t D, const uint16_t *kw,
+                        float eps, const float *inv_freq, int32_t pos0, uint16_t *k, uint16_t *v);
 
 #ifdef __cplusplus
 }

@@ -73,6 +73,12 @@ def _declare(L: ctypes.CDLL) -> None:
                                         ctypes.c_float, _P, i32]
     L.orc_decode_raw_q8_f64.restype = i32
     L.orc_quantize_rows.argtypes = [_P, ctypes.c_int64, i32, _P, _P, _P]
+    i64 = ctypes.c_int64
+    L.orc_prefill_f64.argtypes = [_P, i64, i64, _P, _P, i64, i32, i32, i32, i32, i32, i32, i32, i32,
+                                  ctypes.c_float, _P, i32]
+    L.orc_prefill_f64.restype = i32
+    L.orc_raw_prefill_kv.argtypes = [_P, i32, i32, i32, _P, ctypes.c_float, _P, i32, _P, _P]
+    L.orc_raw_prefill_kv.restype = None
     L.orc_set_fault.argtypes = [i32]
 
 
@@ -245,6 +251,37 @@ def quantize_rows(x: np.ndarray):
     bs = np.empty(x.shape[:-1], dtype=np.float32)
     lib().orc_quantize_rows(_ptr(x), rows, n, _ptr(q), _ptr(sc), _ptr(bs))
     return q, sc, bs
+
+
+def prefill_f64(q, k, v, q_pos0: int, k_pos0: int, window: int, scale: float, threads=None) -> np.ndarray:
+    """Prefill attention: q [Hq, Sq, D], k / v [Hkv, Sk, D] bf16 bits; query i at absolute
+    position q_pos0 + i, key j at k_pos0 + j; returns out [Sq, Hq, D] fp64."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    Hq, Sq, D = q.shape
+    Hkv, Sk, _ = k.shape
+    assert v.shape == k.shape and k.shape[2] == D
+    out = np.empty((Sq, Hq, D), dtype=np.float64)
+    rc = lib().orc_prefill_f64(_ptr(q), Sq * D, D, _ptr(k), _ptr(v), Sk * D, Hq, Hkv, D, Sq, Sk,
+                               int(q_pos0), int(k_pos0), int(window), ctypes.c_float(scale), _ptr(out),
+                               _threads(threads))
+    if rc != 0:
+        raise ValueError("orc_prefill_f64: a query sees no key, or the shapes are invalid")
+    return out
+
+
+def raw_prefill_kv(raw, kw, eps: float, inv_freq, pos0: int = 0):
+    """Raw-K prefill reconstruction: raw [Hkv, Sk, D] bf16 bits -> (K, V) bf16 bits."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint16)
+    Hkv, Sk, D = raw.shape
+    inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    assert inv.shape == (D // 2,)
+    k = np.empty_like(raw)
+    v = np.empty_like(raw)
+    lib().orc_raw_prefill_kv(_ptr(raw), Hkv, Sk, D, _ptr(np.ascontiguousarray(kw, dtype=np.uint16)),
+                             ctypes.c_float(eps), _ptr(inv), int(pos0), _ptr(k), _ptr(v))
+    return k, v
 
 
 class planted_fault:

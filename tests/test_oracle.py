@@ -494,6 +494,9 @@ def _pins_fail(fn) -> bool:
     (4, lambda: test_append_writes_exactly_one_row(False, False)),
     (5, lambda: test_raw_decode_matches_hf_rope_composition()),
     (6, lambda: test_quantize_rows_properties()),
+    (7, lambda: test_prefill_matches_hf_eager_attention(dict(Hq=8, Hkv=1, D=64, Sq=12, Sk=40, q_pos0=28,
+                                                             k_pos0=0, window=0))),
+    (8, lambda: test_raw_prefill_kv_matches_torch_bf16_ops(512, 0.25)),
 ])
 def test_planted_fault_is_caught(fault, pin):
     with orc.planted_fault(fault):
@@ -524,3 +527,114 @@ def test_refround_coarse_at_in_model_scale():
     ref = orc.decode_f64(step, q, kc, kc, [511])
     rr = orc.from_bf16(orc.decode_refround(step, q, kc, kc, [511])).astype(np.float64)
     assert np.abs(rr - ref).max() > TOL_MAX
+
+
+# ---------------------------------------------------------------- prefill
+
+def _prefill_inputs(rng, Hq, Hkv, D, Sq, Sk):
+    q = rms_rows(rng, (Hq, Sq, D))
+    k = rms_rows(rng, (Hkv, Sk, D))
+    v = rms_rows(rng, (Hkv, Sk, D))
+    return q, k, v
+
+
+def _hf_prefill_f64(q, k, v, q_pos0, k_pos0, window, scale):
+    """transformers' gemma4 eager_attention_forward in fp64 over a query chunk, with the
+    HF-rule additive mask on absolute positions (query i at q_pos0 + i, key j at k_pos0 + j)."""
+    from transformers.models.gemma4.modeling_gemma4 import eager_attention_forward
+    Hq, Sq, D = q.shape
+    Hkv, Sk, _ = k.shape
+
+    class M(torch.nn.Module):
+        num_key_value_groups = Hq // Hkv
+        head_dim = D
+        training = False
+
+    rows = [_hf_allowed(window, q_pos0 + i, range(k_pos0, k_pos0 + Sk)) for i in range(Sq)]
+    mask = torch.tensor([[0.0 if a else -1e30 for a in r] for r in rows], dtype=torch.float64)
+    f = lambda a: torch.from_numpy(orc.from_bf16(a).astype(np.float64))[None]
+    o, _ = eager_attention_forward(M(), f(q), f(k), f(v), mask[None, None], scaling=scale)
+    return o[0].numpy()  # [Sq, Hq, D]
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(Hq=4, Hkv=2, D=32, Sq=24, Sk=24, q_pos0=0, k_pos0=0, window=0),     # fresh causal prefill
+    dict(Hq=8, Hkv=1, D=64, Sq=12, Sk=40, q_pos0=28, k_pos0=0, window=0),    # a chunk after 28 cached
+    dict(Hq=4, Hkv=2, D=32, Sq=12, Sk=27, q_pos0=20, k_pos0=5, window=8),    # sliding, evicted keys
+    dict(Hq=6, Hkv=3, D=16, Sq=30, Sk=30, q_pos0=0, k_pos0=0, window=4),     # sliding inside the chunk
+])
+def test_prefill_matches_hf_eager_attention(cfg):
+    rng = np.random.default_rng(31)
+    q, k, v = _prefill_inputs(rng, cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["Sq"], cfg["Sk"])
+    scale = cfg["D"] ** -0.5
+    ours = orc.prefill_f64(q, k, v, cfg["q_pos0"], cfg["k_pos0"], cfg["window"], scale)
+    ref = _hf_prefill_f64(q, k, v, cfg["q_pos0"], cfg["k_pos0"], cfg["window"], scale)
+    # HF's eager softmax runs in fp32 (dtype=torch.float32) even for fp64 inputs.
+    np.testing.assert_allclose(ours, ref, rtol=0, atol=2e-6)
+
+
+def test_prefill_rows_equal_decode_steps():
+    """Query row i of a prefill is the decode step at position q_pos0 + i over the same
+    cache rows (row_base = k_pos0), for causal and sliding layers."""
+    rng = np.random.default_rng(32)
+    Hq, Hkv, D, Sq, Sk, q_pos0, k_pos0 = 8, 2, 32, 10, 50, 45, 5
+    q, k, v = _prefill_inputs(rng, Hq, Hkv, D, Sq, Sk)
+    for window in (0, 7):
+        out = orc.prefill_f64(q, k, v, q_pos0, k_pos0, window, 0.3)
+        step = orc.Step(B=1, Hq=Hq, Hkv=Hkv, D=D, cap=Sk, window=window, scale=0.3)
+        for i in range(Sq):
+            dec = orc.decode_f64(step, np.ascontiguousarray(q[:, i])[None], k.reshape(-1), v.reshape(-1),
+                                 [q_pos0 + i], row_base=[k_pos0])
+            np.testing.assert_allclose(out[i], dec[0], rtol=0, atol=1e-12)
+
+
+def test_prefill_closed_forms():
+    rng = np.random.default_rng(33)
+    q, k, v = _prefill_inputs(rng, 4, 2, 16, 6, 1)
+    out = orc.prefill_f64(q, k, v, 0, 0, 0, 1.0)  # query 0 at position 0 sees only key 0
+    np.testing.assert_allclose(out[0], np.repeat(orc.from_bf16(v[:, 0]), 2, axis=0), rtol=0, atol=1e-12)
+    q, k, v = _prefill_inputs(rng, 4, 2, 16, 6, 9)
+    out = orc.prefill_f64(q, k, v, 3, 0, 1, 1.0)  # window 1: each query sees its own key only
+    for i in range(6):
+        np.testing.assert_allclose(out[i], np.repeat(orc.from_bf16(v[:, 3 + i]), 2, axis=0), rtol=0, atol=1e-12)
+    with pytest.raises(ValueError):  # keys all after the first query: nothing visible
+        orc.prefill_f64(q, k, v, 0, 2, 0, 1.0)
+
+
+def _torch_raw_prefill_kv(raw, kw, eps, inv):
+    """ESAttention.mm:306-326 in torch bf16 ops: kNorm / vNorm in fp32 then cast; cos / sin
+    of fp32 angles cast to bf16; K*c + rotate_half(K)*s with every product and the sum in
+    bf16 (HF's rotate_half)."""
+    from transformers.models.gemma4.modeling_gemma4 import rotate_half
+    Hkv, Sk, D = raw.shape
+    x = torch.from_numpy(orc.from_bf16(raw))
+    rinv = 1.0 / torch.sqrt((x * x).sum(-1, keepdim=True) / D + eps)
+    K = (x * rinv * torch.from_numpy(orc.from_bf16(kw))).to(torch.bfloat16)
+    V = (x * rinv).to(torch.bfloat16)
+    freqs = torch.arange(Sk, dtype=torch.float32)[:, None] * torch.from_numpy(inv)[None, :]
+    emb = torch.cat([freqs, freqs], -1)
+    c, s = torch.cos(emb).to(torch.bfloat16), torch.sin(emb).to(torch.bfloat16)
+    K = K * c + rotate_half(K) * s
+    f = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    return f(K), f(V)
+
+
+@pytest.mark.parametrize("D,partial", [(512, 0.25), (256, 1.0)])
+def test_raw_prefill_kv_matches_torch_bf16_ops(D, partial):
+    rng = np.random.default_rng(34)
+    raw = orc.to_bf16(rng.standard_normal((2, 300, D)).astype(np.float32) * 2)
+    kw = orc.to_bf16((1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32))
+    inv = orc.rope_inv_freq(D, 1.0e6 if D == 512 else 1.0e4, partial)
+    k, v = orc.raw_prefill_kv(raw, kw, 1e-6, inv)
+    tk, tv = _torch_raw_prefill_kv(raw, kw, 1e-6, inv)
+    # fp32 summation order (rinv) and cos / sin last-ulp differences move a value across a
+    # bf16 rounding boundary only rarely: a rotated element sums two bf16 products, so it
+    # can move by two bf16 steps, on a tiny fraction of elements.
+    for ours, ref in ((k, tk), (v, tv)):
+        a, b = orc.from_bf16(ours), orc.from_bf16(ref)
+        assert (np.abs(a - b) <= np.maximum(np.abs(a), np.abs(b)) * 2.0 ** -6).all()
+        assert np.mean(ours != ref) < 2e-3
+    # the rotated pairs really rotate: position 0 leaves K = kNorm(x); later positions do not
+    k0 = orc.to_bf16(orc.from_bf16(raw[:, 0]) / np.sqrt((orc.from_bf16(raw[:, 0]) ** 2).mean(-1, keepdims=True) + 1e-6)
+                     * orc.from_bf16(kw))
+    assert np.mean(k[:, 0] == k0) > 0.99 and np.mean(k[:, 100, :64] != k0[:, :64]) > 0.5
