@@ -1,5 +1,5 @@
-"""ctypes binding of libesda.so (the C ABI declared in include/esda.h and
-include/esda_cache.h).
+"""ctypes binding of libesda.so (the C ABI declared in include/esda.h,
+include/esda_cache.h and include/esda_prefill.h).
 
 The library is loaded from the package directory only (built in-tree by
 ``apertura_amd/build.py``); a missing library raises instead of falling back.
@@ -32,6 +32,8 @@ EXPORTS = (
     "esda_cache_mark_rewind_point", "esda_cache_rewind_to_mark", "esda_cache_clear_rewind_mark",
     "esda_decode_attn_global", "esda_cache_update_raw_q8", "esda_cache_current_raw_q8",
     "esda_cache_decode_raw_q8", "esda_decode_attn_global_q8",
+    # include/esda_prefill.h
+    "esda_prefill_workspace_size", "esda_prefill", "esda_raw_prefill_kv", "esda_raw_q8_prefill_kv",
 )
 _VOID = ("esda_cache_destroy", "esda_cache_mark_step", "esda_cache_reset", "esda_cache_clear_rewind_mark")
 
@@ -104,6 +106,24 @@ class View(ctypes.Structure):
     ]
 
 
+class PrefillDesc(ctypes.Structure):
+    _fields_ = [
+        ("num_q_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("seq_q", ctypes.c_int32), ("seq_k", ctypes.c_int32), ("q_pos0", ctypes.c_int32),
+        ("k_pos0", ctypes.c_int32), ("window", ctypes.c_int32),
+        ("q_head_stride", ctypes.c_int64), ("q_row_stride", ctypes.c_int64),
+        ("kv_head_stride", ctypes.c_int64), ("out_row_stride", ctypes.c_int64),
+        ("out_head_stride", ctypes.c_int64), ("split_keys", ctypes.c_int32), ("scale", ctypes.c_float),
+    ]
+
+
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("out", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class Q8View(ctypes.Structure):
     """esda_q8_view: u8 rows q [kv_heads, pitch, 512], f32 scale / bias [kv_heads, pitch]."""
     _fields_ = [
@@ -170,6 +190,11 @@ def lib() -> ctypes.CDLL:
         L.esda_cache_current_raw_q8.argtypes = [P, i32, QVP]
         L.esda_cache_decode_raw_q8.argtypes = [P, i32, P, i32, P, i32, P, f32, P, i32, P, P]
         L.esda_decode_attn_global_q8.argtypes = [P, i32, P, P, P, i32, i32, i32, P, f32, P, i32, P, P]
+        PD = ctypes.POINTER(PrefillDesc)
+        L.esda_prefill_workspace_size.argtypes = [PD, ctypes.POINTER(sz)]
+        L.esda_prefill.argtypes = [PD, ctypes.POINTER(PrefillArgs), P]
+        L.esda_raw_prefill_kv.argtypes = [P, i64, i32, i32, i32, P, f32, P, i32, P, P, i64, P]
+        L.esda_raw_q8_prefill_kv.argtypes = [P, i64, P, P, i64, i32, i32, P, f32, P, i32, P, P, i64, P]
         for name in EXPORTS:
             if name in _VOID:
                 getattr(L, name).restype = None

@@ -21,6 +21,7 @@ CXX = os.environ.get("CXX", "g++")
 
 SOURCES = [
     "esda_decode.hip",
+    "esda_prefill.hip",
     "es/ESKVCache.cpp",
     "es/ESDecodeAttn.cpp",
     "es/ESSnapshot.cpp",

@@ -1,0 +1,633 @@
+// esda_prefill.hip -- Gemma-4 prefill attention for MI355X (gfx950, CDNA4).
+//
+// Reference behaviour (Apertura tree): a chunk of seq > 1 new tokens attends the cache
+// through mx::fast::scaled_dot_product_attention (ESAttention.mm:188; raw-K layers
+// :328 after the op-level reconstruction :306-326) with the additive mask of
+// ESGemma4TextModel.mm:68-83 aligned by ESAttention.mm:17-22; the op-level tiled core
+// (ESAttention.mm:195-251) computes the same quantity by online softmax.
+//
+// Kernels
+//   prefill_kernel<D>   grid (query tiles, kv heads, key splits), 8 waves (two per
+//                       SIMD), one workgroup per CU.  A query tile is 128 * QB query
+//                       rows (QB = 1 at D = 512, 2 at D = 256 and 128: qb_of) of one kv
+//                       head's GQA group, ordered position-major (row r: position
+//                       r / G, group head r % G); wave w owns rows 16 QB w .. as QB
+//                       blocks of 16 -- the MFMA N dimension.  The
+//                       tile's visible keys (or one split of them) stream through an
+//                       LDS ring of 32-key stages filled by LDS DMA.  Per stage each
+//                       wave forms S^T[32 keys x its queries] over the whole head dim
+//                       with v_mfma_f32_16x16x32_bf16 (K rows from LDS, Q^T held in
+//                       registers), masks boundary stages by position, runs an fp32
+//                       online softmax per query column, and accumulates O^T[D x its
+//                       queries] += V^T . P^T, V^T by transpose reads from LDS and P^T
+//                       straight from the score registers (the 32 keys are ordered so
+//                       that the score layout is the B-operand layout).  O^T stays in
+//                       registers (D/16 x QB tiles: QB * D / 16 accumulators per lane).
+//   prefill_merge_kernel  reduces split partials (m, l, acc) per (query row, head).
+//   raw_prefill_kv_kernel rebuilds K and V of a raw-K (or q8 raw-K) stream by the
+//                       reference's op-level rounding points.
+// The C ABI (include/esda_prefill.h) is at the end of the file.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdint>
+#include <string>
+
+#include "esda.h"
+#include "esda_device.h"
+#include "esda_internal.h"
+#include "esda_prefill.h"
+
+namespace {
+
+constexpr int kWaves = 8;
+constexpr int kStageKeys = 32;
+constexpr int kBlk = 1056;                 // LDS bytes per DMA block: 1 KB + 32 B pad
+constexpr int kRingBudget = 136 * 1024;    // LDS bytes for the K / V ring
+constexpr int kTargetGroups = 256;         // one workgroup per CU
+
+struct PrefillParams {
+    const uint16_t *q, *k, *v;
+    uint16_t *out;
+    float *part_acc;   // [splits][Sq * Hq][D]
+    float *part_ml;    // [splits][Sq * Hq][2]
+    long long q_hs, q_rs, kv_hs, o_rs, o_hs;
+    int Hq, Hkv, G, Sq, Sk, q_pos0, k_pos0, window;
+    int tiles, splits, kps;  // query tiles per kv head, key splits, keys per split
+    float scale_log2e;
+};
+
+// Keys [j0, j1) that some row of query tile `tile` (QT rows) can see.
+__host__ __device__ inline void tile_keys(const PrefillParams &p, int tile, int QT, int &j0, int &j1) {
+    const long long rows = (long long) p.Sq * p.G;
+    const long long r0 = (long long) tile * QT;
+    const long long r1 = (r0 + QT < rows ? r0 + QT : rows) - 1;
+    const long long qa0 = p.q_pos0 + r0 / p.G, qa1 = p.q_pos0 + r1 / p.G;
+    long long lo = p.window > 0 ? qa0 - p.window + 1 - p.k_pos0 : 0;
+    long long hi = qa1 - p.k_pos0 + 1;
+    if (lo < 0) lo = 0;
+    if (hi > p.Sk) hi = p.Sk;
+    if (hi < lo) hi = lo;
+    j0 = (int) lo;
+    j1 = (int) hi;
+}
+
+// LDS ring geometry for head dim D: a 16-key half stage is NI DMA blocks of kBlk bytes,
+// block b holding keys b + NI*q (q < 512/D) at +2D*q; a stage is the K halves then the V
+// halves.  Both the 128-bit row reads (QK A operand) and the transpose reads (PV A
+// operand) are bank-conflict-free in this layout (the decode kernel's measured layout).
+// 16-query blocks per wave: O^T takes QB * D / 16 accumulator registers per lane (128
+// at D = 512 and 256) beside Q^T's QB * D / 8 (64), within two waves per SIMD.
+__host__ __device__ constexpr int qb_of(int D) { return D == 128 ? 2 : 512 / D; }
+
+template <int D>
+struct PRing {
+    static constexpr int NI = D / 32;                 // DMA blocks per 16-key half
+    static constexpr int HB = NI * kBlk;              // one half stage of one tensor
+    static constexpr int SB = 4 * HB;                 // stage: K halves, V halves
+    static constexpr int NS = kRingBudget / SB > 8 ? 8 : kRingBudget / SB;
+    static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+    static constexpr int DPW = 4 * NI / kWaves;       // DMA instructions per wave per stage
+    static_assert(NS >= 2, "the ring needs two stages");
+    static_assert((NS - 2) * DPW <= 60, "vmcnt holds at most 63 outstanding loads");
+    __host__ __device__ static constexpr int off(int r) { return (r % NI) * kBlk + (r / NI) * 2 * D; }
+};
+
+template <int D>
+__global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p) {
+    using R = PRing<D>;
+    constexpr int QB = qb_of(D);        // 16-query blocks per wave
+    constexpr int QT = 16 * QB * kWaves;  // query rows per tile
+    constexpr int KS = D / 32;          // QK k-steps
+    constexpr int DT = D / 16;          // PV dim tiles
+    __shared__ __attribute__((aligned(16))) unsigned char ring[R::NS * R::SB];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int tile = p.tiles - 1 - (int) blockIdx.x;  // heaviest (latest) tiles first
+    const int kvh = blockIdx.y, split = blockIdx.z;
+    const long long nrows = (long long) p.Sq * p.Hq;
+
+    int tj0, tj1;
+    tile_keys(p, tile, QT, tj0, tj1);
+    const int j0 = min(tj1, tj0 + split * p.kps);
+    const int j1 = min(tj1, j0 + p.kps);
+
+    // This lane's query row in block qb: tile row wave*16*QB + 16qb + li, global row gr
+    // (position gr / G, head kvh*G + gr % G); rows past the end repeat the last row and
+    // are not written.
+    const long long nq = (long long) p.Sq * p.G;
+    auto qrow = [&](int qb) -> long long {
+        const long long gr = (long long) tile * QT + wave * 16 * QB + qb * 16 + li;
+        return gr < nq ? gr : nq - 1;
+    };
+    auto qvalid = [&](int qb) { return (long long) tile * QT + wave * 16 * QB + qb * 16 + li < nq; };
+
+    if (j0 >= j1) {  // an empty split: no keys for this tile; the merge skips it
+        if (p.splits > 1 && lg == 0) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+                if (qvalid(qb)) {
+                    const long long gr = qrow(qb);
+                    const long long row = (gr / p.G) * p.Hq + kvh * p.G + gr % p.G;
+                    *reinterpret_cast<f32x2 *>(p.part_ml + 2 * ((long long) split * nrows + row)) =
+                        f32x2{-INFINITY, 0.0f};
+                }
+        }
+        return;
+    }
+
+    // Q^T B operands: lane (li, lg) holds dims 32ks + 8lg .. +8 of its query row.
+    bf16x8 qreg[QB][KS];
+    int qabs[QB];  // absolute position of this lane's query in block qb
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const long long gr = qrow(qb);
+        const uint16_t *qr = p.q + (size_t) (kvh * p.G + gr % p.G) * p.q_hs + (size_t) (gr / p.G) * p.q_rs + lg * 8;
+        qabs[qb] = p.q_pos0 + (int) (gr / p.G);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            u32x4 w = qvalid(qb) ? *reinterpret_cast<const u32x4 *>(qr + ks * 32) : u32x4{0u, 0u, 0u, 0u};
+            qreg[qb][ks] = __builtin_bit_cast(bf16x8, w);
+        }
+    }
+
+    // DMA: instruction t of this wave (index ii = wave*DPW + t of the stage) fills block
+    // b = ii % NI of half hh = (ii / NI) % 2 of tensor ii / (2 NI); lane l reads chunk
+    // l % CPR of key row 16hh + b + NI*(l / CPR).
+    const uint16_t *kvb = p.k + (size_t) kvh * p.kv_hs;
+    const uint16_t *vvb = p.v + (size_t) kvh * p.kv_hs;
+    const int nst = (j1 - j0 + kStageKeys - 1) / kStageKeys;
+    auto issue = [&](int s) {
+        if (s >= nst) return;
+        unsigned char *buf = ring + (s % R::NS) * R::SB;
+        const int jb = j0 + s * kStageKeys;
+#pragma unroll
+        for (int t = 0; t < R::DPW; ++t) {
+            const int ii = wave * R::DPW + t;
+            const int tensor = ii / (2 * R::NI), hh = (ii / R::NI) % 2, b = ii % R::NI;
+            int j = jb + 16 * hh + b + R::NI * (lane / R::CPR);
+            j = j < j1 ? j : j1 - 1;  // rows past the range repeat the last key (masked)
+            const uint16_t *src = (tensor ? vvb : kvb) + (size_t) j * D + (lane % R::CPR) * 8;
+            lds_dma16(src, lds_addr(buf) + (tensor * 2 + hh) * R::HB + b * kBlk);
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < R::NS - 1; ++s) issue(s);
+
+    const int qk_off = R::off(li) + lg * 16;                    // + 64 ks (+ HB: keys 16..31)
+    const int tr_off = R::off(4 * lg + li / 4) + (li % 4) * 8;  // + 32 dt (+ HB)
+
+    float m[QB], l[QB];
+    f32x4 acc[QB][DT];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        m[qb] = -INFINITY;
+        l[qb] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[qb][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    // Positions of the tile's first and last rows (the host keeps positions below 2^31).
+    const int qa_min = p.q_pos0 + (int) ((long long) tile * QT / p.G);
+    const int qa_max = p.q_pos0 + (int) (((long long) tile * QT + QT < nq ? (long long) tile * QT + QT : nq) - 1) / p.G;
+
+    for (int s = 0; s < nst; ++s) {
+        // stage s landed (this wave's loads; the barrier covers the other waves') and
+        // every wave is done with stage s-1, whose buffer stage s+NS-1 reuses
+        if constexpr (R::NS > 2) {
+            if (s + R::NS - 2 < nst) ESDA_WAIT_VM((R::NS - 2) * R::DPW);
+            else ESDA_WAIT_VM(0);
+        } else {
+            ESDA_WAIT_VM(0);
+        }
+        lds_barrier();
+        issue(s + R::NS - 1);
+        const unsigned char *kb = ring + (s % R::NS) * R::SB;
+        const unsigned char *vb = kb + 2 * R::HB;
+        const int jb = j0 + s * kStageKeys;
+
+        // S^T[keys x queries]: sacc[h][qb] covers keys 16h + 4lg + r of query column li.
+        f32x4 sacc[2][QB];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) sacc[h][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const bf16x8 ka0 = *reinterpret_cast<const bf16x8 *>(kb + qk_off + 64 * ks);
+            const bf16x8 ka1 = *reinterpret_cast<const bf16x8 *>(kb + R::HB + qk_off + 64 * ks);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                sacc[0][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, qreg[qb][ks], sacc[0][qb], 0, 0, 0);
+                sacc[1][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, qreg[qb][ks], sacc[1][qb], 0, 0, 0);
+            }
+        }
+
+        // Visibility: a stage is fully visible to every row of the tile when its last key
+        // is at or before the tile's first position, its first key is inside the window
+        // of the tile's last position, and it lies inside the split.
+        const int ka_first = p.k_pos0 + jb, ka_last = ka_first + kStageKeys - 1;
+        const bool full = jb + kStageKeys <= j1 && ka_last <= qa_min &&
+                          (p.window == 0 || ka_first > qa_max - p.window);
+
+        bf16x8 pb[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            float sv[8];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sv[4 * h + r] = sacc[h][qb][r] * p.scale_log2e;
+            if (!full) {
+                const int qa = qabs[qb];
+                const int lo = p.window > 0 ? qa - p.window : INT_MIN;  // visible: lo < ka <= qa
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int j = jb + 16 * h + 4 * lg + r;
+                        const int ka = p.k_pos0 + j;
+                        if (!(j < j1 && ka <= qa && ka > lo)) sv[4 * h + r] = -INFINITY;
+                    }
+            }
+            float mt = sv[0];
+#pragma unroll
+            for (int e = 1; e < 8; ++e) mt = fmaxf(mt, sv[e]);
+            mt = wave_max_across_groups(mt);
+            if (mt > m[qb] + kRescaleSlack) {
+                const float corr = __builtin_amdgcn_exp2f(m[qb] - mt);  // 0 while m is -inf
+                l[qb] *= corr;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) acc[qb][dt] *= corr;
+                m[qb] = mt;
+            }
+            const float mu = m[qb] == -INFINITY ? 0.0f : m[qb];  // all keys so far masked
+            short8v pv;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const __bf16 pr = (__bf16) __builtin_amdgcn_exp2f(sv[e] - mu);
+                l[qb] += (float) pr;
+                pv[e] = __builtin_bit_cast(short, pr);
+            }
+            pb[qb] = __builtin_bit_cast(bf16x8, pv);
+        }
+
+        // O^T += V^T . P^T: lane (li, lg) gets dim 16dt + li of keys 4lg .. 4lg+3 (first
+        // half) and 16 + 4lg .. (second half): the k order of the P^T registers.
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const short4v a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4v *) (vb + tr_off + 32 * dt));
+            const short4v a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4v *) (vb + R::HB + tr_off + 32 * dt));
+            const short8v a8 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+            const bf16x8 a = __builtin_bit_cast(bf16x8, a8);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+                acc[qb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qb], acc[qb][dt], 0, 0, 0);
+        }
+    }
+
+    // Row totals over the four lane groups; then the output (one split) or the partial.
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        l[qb] += __shfl_xor(l[qb], 16);
+        l[qb] += __shfl_xor(l[qb], 32);
+        if (!qvalid(qb)) continue;
+        const long long gr = qrow(qb);
+        const int qi = (int) (gr / p.G), qh = kvh * p.G + (int) (gr % p.G);
+        const long long row = (long long) qi * p.Hq + qh;
+        if (p.splits == 1) {
+            const float inv = 1.0f / l[qb];
+            uint16_t *o = p.out + (size_t) qi * p.o_rs + (size_t) qh * p.o_hs + 4 * lg;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const f32x4 v4 = acc[qb][dt] * inv;
+                bf16x4 b4 = {(__bf16) v4[0], (__bf16) v4[1], (__bf16) v4[2], (__bf16) v4[3]};
+                *reinterpret_cast<bf16x4 *>(o + 16 * dt) = b4;
+            }
+        } else {
+            float *pa = p.part_acc + ((long long) split * nrows + row) * D + 4 * lg;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4 *>(pa + 16 * dt) = acc[qb][dt];
+            if (lg == 0)
+                *reinterpret_cast<f32x2 *>(p.part_ml + 2 * ((long long) split * nrows + row)) = f32x2{m[qb], l[qb]};
+        }
+    }
+}
+
+// out(i, h, 4 dims) = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) over the splits
+// with l_s > 0 (one thread per (row, 4 dims)).
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
+    const long long nrows = (long long) p.Sq * p.Hq;
+    const long long t = (long long) blockIdx.x * 256 + threadIdx.x;
+    if (t >= nrows * (D / 4)) return;
+    const long long row = t / (D / 4);
+    const int d4 = (int) (t % (D / 4));
+    float M = -INFINITY;
+    for (int s = 0; s < p.splits; ++s) {
+        const f32x2 ml = *reinterpret_cast<const f32x2 *>(p.part_ml + 2 * ((long long) s * nrows + row));
+        if (ml[1] > 0.0f) M = fmaxf(M, ml[0]);
+    }
+    float den = 0.0f;
+    f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < p.splits; ++s) {
+        const f32x2 ml = *reinterpret_cast<const f32x2 *>(p.part_ml + 2 * ((long long) s * nrows + row));
+        if (!(ml[1] > 0.0f)) continue;
+        const float w = __builtin_amdgcn_exp2f(ml[0] - M);
+        den += ml[1] * w;
+        num += w * *reinterpret_cast<const f32x4 *>(p.part_acc + ((long long) s * nrows + row) * D + 4 * d4);
+    }
+    const f32x4 v4 = num * (1.0f / den);
+    const int i = (int) (row / p.Hq), h = (int) (row % p.Hq);
+    bf16x4 b4 = {(__bf16) v4[0], (__bf16) v4[1], (__bf16) v4[2], (__bf16) v4[3]};
+    *reinterpret_cast<bf16x4 *>(p.out + (size_t) i * p.o_rs + (size_t) h * p.o_hs + 4 * d4) = b4;
+}
+
+// ------------------------------------------------------------ raw-K reconstruction
+//
+// One wave per key row.  Lane l holds dims HP*l .. +HP of each half (HP = D/128), so each
+// rotary pair (d, d + D/2) sits in one lane.  The sum of squares is an fp32 wave
+// reduction; rinv = 1 / sqrt(mean + eps) with IEEE division and square root.
+struct RawKvParams {
+    const uint16_t *raw;        // bf16 rows, or NULL with q8 / scale / bias
+    const unsigned char *q8;
+    const float *sc, *bs;
+    long long raw_hs, sb_hs, out_hs;
+    const uint16_t *kw;
+    const float *inv_freq;
+    float eps;
+    int Hkv, rows, pos0;
+    uint16_t *k, *v;
+};
+
+__device__ __forceinline__ float bf16r(float x) { return (float) (__bf16) x; }
+
+template <int D, bool Q8>
+__global__ __launch_bounds__(256) void raw_prefill_kv_kernel(RawKvParams p) {
+#pragma clang fp contract(off)  // every rounding point as written (no fused multiply-add)
+    constexpr int HP = D / 128, HALF = D / 2;
+    const int lane = threadIdx.x & 63;
+    const long long gw = (long long) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= (long long) p.Hkv * p.rows) return;
+    const int h = (int) (gw / p.rows), t = (int) (gw % p.rows);
+    float x[2][HP];
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int e = 0; e < HP; ++e) {
+            const int d = half * HALF + HP * lane + e;
+            if constexpr (Q8) {
+                const size_t r = (size_t) h * p.sb_hs + t;
+                const float prod = (float) p.q8[(size_t) h * p.raw_hs + (size_t) t * D + d] * p.sc[r];
+                x[half][e] = bf16r(prod + p.bs[r]);  // the bf16 raw view of the q8 row
+            } else {
+                x[half][e] = __builtin_bit_cast(float, (unsigned) p.raw[(size_t) h * p.raw_hs + (size_t) t * D + d] << 16);
+            }
+        }
+    float ss = 0.0f;
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int e = 0; e < HP; ++e) ss += x[half][e] * x[half][e];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    const float rinv = 1.0f / sqrtf(ss / (float) D + p.eps);
+    uint16_t *ko = p.k + (size_t) h * p.out_hs + (size_t) t * D;
+    uint16_t *vo = p.v + (size_t) h * p.out_hs + (size_t) t * D;
+    const float pos = (float) (p.pos0 + t);
+#pragma unroll
+    for (int e = 0; e < HP; ++e) {
+        const int d = HP * lane + e;
+        const float k0a = bf16r(x[0][e] * rinv * __builtin_bit_cast(float, (unsigned) p.kw[d] << 16));
+        const float k0b = bf16r(x[1][e] * rinv * __builtin_bit_cast(float, (unsigned) p.kw[d + HALF] << 16));
+        float sn, cs;
+        sincos_f32(pos * p.inv_freq[d], sn, cs);
+        const float c = bf16r(cs), s = bf16r(sn);
+        ko[d] = __builtin_bit_cast(uint16_t, (__bf16) (bf16r(k0a * c) + bf16r(-k0b * s)));
+        ko[d + HALF] = __builtin_bit_cast(uint16_t, (__bf16) (bf16r(k0b * c) + bf16r(k0a * s)));
+        vo[d] = __builtin_bit_cast(uint16_t, (__bf16) (x[0][e] * rinv));
+        vo[d + HALF] = __builtin_bit_cast(uint16_t, (__bf16) (x[1][e] * rinv));
+    }
+}
+
+// ------------------------------------------------------------ host side
+
+int fail(int code, const std::string &msg) {
+    esda_detail::set_error(msg);
+    return code;
+}
+
+bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+int qt_of(int D) { return 16 * qb_of(D) * kWaves; }
+
+// Validates a description and fills the kernel parameters' shape fields and plan.
+int plan_prefill(const esda_prefill_desc *d, PrefillParams *p) {
+    if (!d) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: null description");
+    const int D = d->head_dim;
+    if (D != 128 && D != 256 && D != 512)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: head_dim must be 128, 256 or 512");
+    if (d->num_q_heads <= 0 || d->num_kv_heads <= 0 || d->num_q_heads % d->num_kv_heads)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: num_q_heads must be a multiple of num_kv_heads");
+    if (d->seq_q <= 0 || d->seq_k <= 0 || d->window < 0 || d->q_pos0 < 0 || d->k_pos0 < 0)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: sizes, positions and window must be non-negative");
+    if ((long long) d->q_pos0 + d->seq_q > INT_MAX || (long long) d->k_pos0 + d->seq_k > INT_MAX)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: positions must stay below 2^31");
+    if (d->k_pos0 > d->q_pos0 || (long long) d->k_pos0 + d->seq_k < (long long) d->q_pos0 + d->seq_q)
+        return fail(ESDA_ERR_INVALID_ARGUMENT,
+                    "esda_prefill: the keys must hold every query's own position (k_pos0 <= q_pos0, "
+                    "k_pos0 + seq_k >= q_pos0 + seq_q)");
+    for (long long st : {d->q_head_stride, d->q_row_stride, d->kv_head_stride, d->out_row_stride, d->out_head_stride})
+        if (st < 0 || st % 8)
+            return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: strides must be non-negative multiples of 8");
+    if (d->kv_head_stride < (long long) d->seq_k * D && d->num_kv_heads > 1)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: kv_head_stride smaller than a head's rows");
+    if (d->split_keys < 0 || d->split_keys % kStageKeys)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: split_keys must be a multiple of 32");
+    if (!(d->scale > 0.0f) || !std::isfinite(d->scale))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: scale must be positive and finite");
+    *p = PrefillParams{};
+    p->Hq = d->num_q_heads;
+    p->Hkv = d->num_kv_heads;
+    p->G = d->num_q_heads / d->num_kv_heads;
+    p->Sq = d->seq_q;
+    p->Sk = d->seq_k;
+    p->q_pos0 = d->q_pos0;
+    p->k_pos0 = d->k_pos0;
+    p->window = d->window;
+    p->q_hs = d->q_head_stride;
+    p->q_rs = d->q_row_stride;
+    p->kv_hs = d->kv_head_stride;
+    p->o_rs = d->out_row_stride;
+    p->o_hs = d->out_head_stride;
+    p->scale_log2e = d->scale * 1.4426950408889634f;
+    const int QT = qt_of(D);
+    const long long tiles = ((long long) d->seq_q * p->G + QT - 1) / QT;
+    if (tiles * d->num_kv_heads > 65535LL * 64)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: too many query tiles");
+    p->tiles = (int) tiles;
+    // The widest key range of any tile (the last one under a causal mask).
+    int maxn = 0;
+    for (int t = 0; t < p->tiles; ++t) {
+        int a, b;
+        tile_keys(*p, t, QT, a, b);
+        maxn = std::max(maxn, b - a);
+    }
+    int kps;
+    if (d->split_keys > 0) {
+        kps = d->split_keys;
+    } else {
+        // enough workgroups to cover the CUs, each with at least 8 stages
+        const long long groups = tiles * d->num_kv_heads;
+        long long s = (kTargetGroups + groups - 1) / groups;
+        const long long smax = std::max<long long>(1, maxn / (8 * kStageKeys));
+        s = std::min(s, smax);
+        kps = (int) (((maxn + s - 1) / s + kStageKeys - 1) / kStageKeys * kStageKeys);
+    }
+    if (kps <= 0) kps = kStageKeys;
+    const long long splits = (maxn + kps - 1) / kps;
+    if (splits > 65535) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: too many key splits");
+    p->kps = kps;
+    p->splits = (int) std::max<long long>(1, splits);
+    return ESDA_OK;
+}
+
+size_t workspace_of(const PrefillParams &p, int D) {
+    if (p.splits <= 1) return 0;
+    const size_t rows = (size_t) p.Sq * p.Hq;
+    return (size_t) p.splits * rows * ((size_t) D * 4 + 8) + 256;
+}
+
+template <int D>
+void launch_prefill(const PrefillParams &p, hipStream_t st) {
+    hipLaunchKernelGGL((prefill_kernel<D>), dim3(p.tiles, p.Hkv, p.splits), dim3(64 * kWaves), 0, st, p);
+    if (p.splits > 1) {
+        const long long n = (long long) p.Sq * p.Hq * (D / 4);
+        hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, p);
+    }
+}
+
+int run_raw_kv(const RawKvParams &p, int D, bool q8, hipStream_t st) {
+    int rc = esda_detail::check_device();
+    if (rc != ESDA_OK) return rc;
+    const long long waves = (long long) p.Hkv * p.rows;
+    if (waves == 0) return ESDA_OK;
+    const dim3 grid((unsigned) ((waves + 3) / 4)), block(256);
+    if (q8) {
+        hipLaunchKernelGGL((raw_prefill_kv_kernel<512, true>), grid, block, 0, st, p);
+    } else if (D == 512) {
+        hipLaunchKernelGGL((raw_prefill_kv_kernel<512, false>), grid, block, 0, st, p);
+    } else if (D == 256) {
+        hipLaunchKernelGGL((raw_prefill_kv_kernel<256, false>), grid, block, 0, st, p);
+    } else {
+        hipLaunchKernelGGL((raw_prefill_kv_kernel<128, false>), grid, block, 0, st, p);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(ESDA_ERR_HIP, std::string("raw_prefill_kv launch: ") + hipGetErrorString(e));
+    return ESDA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int esda_prefill_workspace_size(const esda_prefill_desc *desc, size_t *bytes) {
+    if (!bytes) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill_workspace_size: null output");
+    PrefillParams p;
+    const int rc = plan_prefill(desc, &p);
+    if (rc != ESDA_OK) return rc;
+    *bytes = workspace_of(p, desc->head_dim);
+    return ESDA_OK;
+}
+
+int esda_prefill(const esda_prefill_desc *desc, const esda_prefill_args *a, void *stream) {
+    PrefillParams p;
+    int rc = plan_prefill(desc, &p);
+    if (rc != ESDA_OK) return rc;
+    if (!a || !a->q || !a->k || !a->v || !a->out) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: null pointer");
+    if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->out))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: tensors must be 16-byte aligned");
+    const int D = desc->head_dim;
+    const size_t need = workspace_of(p, D);
+    if (need) {
+        if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
+            return fail(ESDA_ERR_WORKSPACE, "esda_prefill: workspace missing or smaller than "
+                                            "esda_prefill_workspace_size");
+        const size_t rows = (size_t) p.Sq * p.Hq;
+        p.part_acc = static_cast<float *>(a->workspace);
+        p.part_ml = reinterpret_cast<float *>(static_cast<char *>(a->workspace) + (size_t) p.splits * rows * D * 4);
+    }
+    rc = esda_detail::check_device();
+    if (rc != ESDA_OK) return rc;
+    p.q = static_cast<const uint16_t *>(a->q);
+    p.k = static_cast<const uint16_t *>(a->k);
+    p.v = static_cast<const uint16_t *>(a->v);
+    p.out = static_cast<uint16_t *>(a->out);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (D == 512) launch_prefill<512>(p, st);
+    else if (D == 256) launch_prefill<256>(p, st);
+    else launch_prefill<128>(p, st);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(ESDA_ERR_HIP, std::string("esda_prefill launch: ") + hipGetErrorString(e));
+    return ESDA_OK;
+}
+
+int esda_raw_prefill_kv(const void *raw, int64_t raw_head_stride, int32_t kv_heads, int32_t rows, int32_t head_dim,
+                        const void *kw, float eps, const float *inv_freq, int32_t pos0, void *k_out, void *v_out,
+                        int64_t out_head_stride, void *stream) {
+    if (head_dim != 128 && head_dim != 256 && head_dim != 512)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_raw_prefill_kv: head_dim must be 128, 256 or 512");
+    if (!raw || !kw || !inv_freq || !k_out || !v_out)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_raw_prefill_kv: null pointer");
+    if (kv_heads <= 0 || rows < 0 || pos0 < 0 || !(eps >= 0.0f) ||
+        (kv_heads > 1 && (raw_head_stride < (int64_t) rows * head_dim || out_head_stride < (int64_t) rows * head_dim)))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_raw_prefill_kv: invalid sizes or strides");
+    RawKvParams p{};
+    p.raw = static_cast<const uint16_t *>(raw);
+    p.raw_hs = raw_head_stride;
+    p.out_hs = out_head_stride;
+    p.kw = static_cast<const uint16_t *>(kw);
+    p.inv_freq = inv_freq;
+    p.eps = eps;
+    p.Hkv = kv_heads;
+    p.rows = rows;
+    p.pos0 = pos0;
+    p.k = static_cast<uint16_t *>(k_out);
+    p.v = static_cast<uint16_t *>(v_out);
+    return run_raw_kv(p, head_dim, false, static_cast<hipStream_t>(stream));
+}
+
+int esda_raw_q8_prefill_kv(const void *q8, int64_t q_head_stride, const float *scale, const float *bias,
+                           int64_t sb_head_stride, int32_t kv_heads, int32_t rows, const void *kw, float eps,
+                           const float *inv_freq, int32_t pos0, void *k_out, void *v_out, int64_t out_head_stride,
+                           void *stream) {
+    if (!q8 || !scale || !bias || !kw || !inv_freq || !k_out || !v_out)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_raw_q8_prefill_kv: null pointer");
+    if (kv_heads <= 0 || rows < 0 || pos0 < 0 || !(eps >= 0.0f) ||
+        (kv_heads > 1 && (q_head_stride < (int64_t) rows * 512 || sb_head_stride < rows ||
+                          out_head_stride < (int64_t) rows * 512)))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_raw_q8_prefill_kv: invalid sizes or strides");
+    RawKvParams p{};
+    p.q8 = static_cast<const unsigned char *>(q8);
+    p.sc = scale;
+    p.bs = bias;
+    p.raw_hs = q_head_stride;
+    p.sb_hs = sb_head_stride;
+    p.out_hs = out_head_stride;
+    p.kw = static_cast<const uint16_t *>(kw);
+    p.inv_freq = inv_freq;
+    p.eps = eps;
+    p.Hkv = kv_heads;
+    p.rows = rows;
+    p.pos0 = pos0;
+    p.k = static_cast<uint16_t *>(k_out);
+    p.v = static_cast<uint16_t *>(v_out);
+    return run_raw_kv(p, 512, true, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -127,3 +127,22 @@ def test_raw_descriptions_are_validated_without_device():
         with pytest.raises(_lib.EsdaError) as ei:
             raw_workspace_bytes(RawStep(**kw))
         assert ei.value.code == 1
+
+
+def test_prefill_descriptions_are_validated_without_device():
+    """esda_prefill's plan is host-side: malformed descriptions fail with
+    ESDA_ERR_INVALID_ARGUMENT before any device call; splits size the workspace."""
+    from apertura_amd._lib import EsdaError
+    from apertura_amd.prefill import PrefillStep, prefill_workspace_bytes
+    good = dict(num_q_heads=32, num_kv_heads=4, head_dim=512, seq_q=512, seq_k=16384, q_pos0=15872, k_pos0=0)
+    n = prefill_workspace_bytes(PrefillStep(**good))
+    assert n > 0  # 16 query tiles per kv head: the keys are split to cover the CUs
+    assert prefill_workspace_bytes(PrefillStep(**{**good, "seq_q": 16384, "q_pos0": 0})) == 0  # enough tiles
+    for bad in (dict(head_dim=64), dict(num_q_heads=30), dict(seq_q=0), dict(window=-1),
+                dict(k_pos0=15873),                              # the first query's own key missing
+                dict(seq_k=100),                                 # the last queries' keys missing
+                dict(split_keys=48), dict(scale=0.0), dict(q_head_stride=12),
+                dict(q_pos0=2 ** 31 - 100)):
+        with pytest.raises(EsdaError) as ei:
+            prefill_workspace_bytes(PrefillStep(**{**good, **bad}))
+        assert ei.value.code == 1, bad

@@ -1,0 +1,205 @@
+"""GPU parity of the prefill side (esda_prefill, esda_raw_prefill_kv,
+esda_raw_q8_prefill_kv) against the CPU oracle, through the C ABI.
+
+Prefill attention is held to max-abs <= 2e-2 and mean-abs <= 2e-3 against the fp64 oracle
+(orc_prefill_f64: SDPA over the chunk with the buildMask / alignMask visibility,
+ESAttention.mm:188, ESGemma4TextModel.mm:68-83, ESAttention.mm:17-22).  Shapes cover
+Gemma-4's global (D=512, 8 query heads per kv head) and local (D=256, 2 per kv head,
+sliding window with evicted keys) layers, fresh causal prefill and chunks after a cached
+past, tiles padded past the last query, key splits (automatic, forced, empty), strided
+query / cache / output layouts and a shared K = V buffer.  At the chunked-prefill
+benchmark shape (512 queries over 16384 keys) sampled query rows are checked (query rows
+are independent).  The raw-K reconstruction is compared with the oracle's op-level
+restatement element by element (at most two bf16 steps apart, on a tiny fraction).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from _synth import rms_rows
+
+pytestmark = pytest.mark.gpu
+
+TOL_MAX, TOL_MEAN = 2e-2, 2e-3
+
+
+def _dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def _host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def run_prefill(name, *, Hq, Hkv, D, Sq, Sk, q_pos0, k_pos0, window=0, split_keys=0, seed=0,
+                layout="dense", shared=False, rows=None, fault=0):
+    from apertura_amd.prefill import PrefillStep, prefill
+    print(f"\n[prefill] {name}: Hq={Hq} Hkv={Hkv} D={D} Sq={Sq} Sk={Sk} q_pos0={q_pos0} k_pos0={k_pos0} "
+          f"window={window} split_keys={split_keys} layout={layout} shared={shared}", flush=True)
+    rng = np.random.default_rng(seed)
+    q = rms_rows(rng, (Hq, Sq, D))
+    k = rms_rows(rng, (Hkv, Sk, D))
+    v = k if shared else rms_rows(rng, (Hkv, Sk, D))
+    scale = D ** -0.5
+    if layout == "dense":
+        qd, kd = _dev(q), _dev(k)
+        vd = kd if shared else _dev(v)
+        out = torch.empty((Sq, Hq, D), dtype=torch.bfloat16, device="cuda")
+    else:
+        # q as the projection's [Sq, Hq, D], the cache as an unsliced [Hkv, cap, D] buffer,
+        # out as [Hq, Sq, D]: all passed as strided views
+        qd = _dev(np.ascontiguousarray(q.transpose(1, 0, 2))).transpose(0, 1)
+        cap = Sk + 40
+        kb = torch.zeros((Hkv, cap, D), dtype=torch.bfloat16, device="cuda")
+        kb[:, :Sk] = _dev(k)
+        kd = kb[:, :Sk]
+        if shared:
+            vd = kd
+        else:
+            vb = torch.zeros_like(kb)
+            vb[:, :Sk] = _dev(v)
+            vd = vb[:, :Sk]
+        out = torch.empty((Hq, Sq, D), dtype=torch.bfloat16, device="cuda").transpose(0, 1)
+    step = PrefillStep.for_tensors(qd, kd, out, q_pos0=q_pos0, k_pos0=k_pos0, window=window, scale=scale,
+                                   split_keys=split_keys)
+    prefill(step, qd, kd, vd, out)
+    torch.cuda.synchronize()
+    o = orc.from_bf16(_host(out)).astype(np.float64)  # [Sq, Hq, D]
+    sel = list(range(Sq)) if rows is None else rows
+    errs = []
+    with orc.planted_fault(fault):
+        for r0 in ([0] if rows is None else sel):
+            qs = q if rows is None else q[:, r0:r0 + 1]
+            ref = orc.prefill_f64(qs, k, v, q_pos0 + (0 if rows is None else r0), k_pos0, window, scale)
+            got = o if rows is None else o[r0:r0 + 1]
+            errs.append(np.abs(got - ref))
+    err = np.concatenate([e.reshape(-1) for e in errs])
+    print(f"[prefill] {name}: max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
+    if not fault:
+        assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN, name
+    return err
+
+
+def test_global_fresh_causal_prefill_with_padded_tile():
+    run_prefill("global-fresh", Hq=32, Hkv=4, D=512, Sq=300, Sk=300, q_pos0=0, k_pos0=0, seed=1)
+
+
+def test_global_chunk_after_cached_past_auto_splits():
+    run_prefill("global-chunk", Hq=32, Hkv=4, D=512, Sq=64, Sk=1000, q_pos0=936, k_pos0=0, seed=2)
+
+
+def test_local_sliding_window_with_evicted_keys():
+    # chunked prefill keeps window + seq keys (ESAttention.mm:99-103): pastLen 500
+    run_prefill("local-window", Hq=8, Hkv=4, D=256, Sq=200, Sk=264, q_pos0=500, k_pos0=436, window=64, seed=3)
+
+
+def test_local_fresh_prefill_window_inside_the_chunk():
+    run_prefill("local-fresh", Hq=16, Hkv=8, D=256, Sq=700, Sk=700, q_pos0=0, k_pos0=0, window=128, seed=4)
+
+
+@pytest.mark.parametrize("split_keys", [32, 96, 4096])
+def test_forced_split_sizes_including_empty_splits(split_keys):
+    run_prefill(f"split{split_keys}", Hq=8, Hkv=2, D=128, Sq=150, Sk=400, q_pos0=250, k_pos0=0,
+                split_keys=split_keys, seed=5)
+
+
+@pytest.mark.parametrize("D", [512, 256, 128])
+def test_strided_layouts(D):
+    run_prefill(f"strided-d{D}", Hq=8, Hkv=2, D=D, Sq=77, Sk=190, q_pos0=113, k_pos0=0, seed=6,
+                layout="strided")
+
+
+def test_shared_k_equals_v_buffer():
+    run_prefill("shared", Hq=16, Hkv=2, D=512, Sq=90, Sk=90, q_pos0=0, k_pos0=0, seed=7, shared=True,
+                layout="strided")
+
+
+def test_single_query_and_single_key():
+    run_prefill("one-by-one", Hq=4, Hkv=1, D=256, Sq=1, Sk=1, q_pos0=0, k_pos0=0, seed=8)
+    run_prefill("one-query", Hq=32, Hkv=4, D=512, Sq=1, Sk=513, q_pos0=512, k_pos0=0, seed=9)
+
+
+def test_chunked_prefill_benchmark_shape_sampled_rows():
+    """512 queries over a 16384-key global cache (the chunked-prefill benchmark shape)."""
+    run_prefill("bench-global", Hq=32, Hkv=4, D=512, Sq=512, Sk=16384, q_pos0=15872, k_pos0=0, seed=10,
+                rows=[0, 1, 200, 511])
+
+
+def test_diagonal_fault_in_the_oracle_is_detected():
+    err = run_prefill("fault7", Hq=8, Hkv=2, D=128, Sq=40, Sk=40, q_pos0=0, k_pos0=0, seed=11, fault=7,
+                      rows=[5, 17, 39])
+    assert err.max() > 10 * TOL_MAX
+
+
+def _raw_inputs(rng, Hkv, Sk, D):
+    raw = orc.to_bf16((rng.standard_normal((Hkv, Sk, D), dtype=np.float32) * 2.0).astype(np.float32))
+    kw = orc.to_bf16((1.0 + 0.2 * rng.standard_normal(D)).astype(np.float32))
+    return raw, kw
+
+
+def _close_bf16(ours, ref, what):
+    """Equal but for rare bf16 rounding-boundary cases: a rotated element is the bf16 sum of
+    two bf16 products, so it may differ by two bf16 steps of its own size, or, where the
+    products nearly cancel, by one step of the row's largest element."""
+    a, b = orc.from_bf16(ours), orc.from_bf16(ref)
+    floor = np.abs(b).max(axis=-1, keepdims=True) * 2.0 ** -8
+    bad = np.abs(a - b) > np.maximum(np.abs(a), np.abs(b)) * 2.0 ** -6 + floor
+    frac = np.mean(ours != ref)
+    print(f"[raw-kv] {what}: differing {frac:.2e}, beyond two bf16 steps {bad.sum()}", flush=True)
+    assert not bad.any() and frac < 1e-2, what
+
+
+@pytest.mark.parametrize("D,theta,partial", [(512, 1.0e6, 0.25), (256, 1.0e4, 1.0), (128, 1.0e4, 1.0)])
+def test_raw_prefill_kv_matches_the_oracle(D, theta, partial):
+    from apertura_amd.prefill import raw_prefill_kv
+    rng = np.random.default_rng(20 + D)
+    Hkv, Sk, pos0 = 2, 777, 5
+    raw, kw = _raw_inputs(rng, Hkv, Sk, D)
+    inv = orc.rope_inv_freq(D, theta, partial)
+    k, v = raw_prefill_kv(_dev(raw), _dev(kw), 1e-6, torch.from_numpy(inv).cuda(), pos0)
+    torch.cuda.synchronize()
+    ek, ev = orc.raw_prefill_kv(raw, kw, 1e-6, inv, pos0)
+    _close_bf16(_host(k), ek, f"K d{D}")
+    _close_bf16(_host(v), ev, f"V d{D}")
+
+
+def test_raw_q8_prefill_kv_matches_the_oracle():
+    from apertura_amd.prefill import raw_q8_prefill_kv
+    rng = np.random.default_rng(30)
+    Hkv, Sk, cap = 2, 500, 640
+    raw, kw = _raw_inputs(rng, Hkv, Sk, 512)
+    qc, sc, bs = orc.quantize_rows(raw)
+    inv = orc.rope_inv_freq(512, 1.0e6, 0.25)
+    qb = torch.zeros((Hkv, cap, 512), dtype=torch.uint8, device="cuda")
+    sb = torch.zeros((Hkv, cap), dtype=torch.float32, device="cuda")
+    bb = torch.zeros((Hkv, cap), dtype=torch.float32, device="cuda")
+    qb[:, :Sk], sb[:, :Sk], bb[:, :Sk] = torch.from_numpy(qc).cuda(), torch.from_numpy(sc).cuda(), torch.from_numpy(bs).cuda()
+    k, v = raw_q8_prefill_kv(qb[:, :Sk], sb[:, :Sk], bb[:, :Sk], _dev(kw), 1e-6, torch.from_numpy(inv).cuda())
+    torch.cuda.synchronize()
+    # the reference's bf16 raw view of the q8 rows: bf16(float(q) * scale + bias), two roundings
+    view = orc.to_bf16((qc.astype(np.float32) * sc[..., None]).astype(np.float32) + bs[..., None])
+    ek, ev = orc.raw_prefill_kv(view, kw, 1e-6, inv, 0)
+    _close_bf16(_host(k), ek, "q8 K")
+    _close_bf16(_host(v), ev, "q8 V")
+
+
+def test_raw_prefill_end_to_end():
+    """ESAttention.mm:306-332: reconstruct K / V from the raw stream (keys at positions
+    0 .. seqK-1), then prefill attention of the chunk at pastLen."""
+    from apertura_amd.prefill import PrefillStep, prefill, raw_prefill_kv
+    rng = np.random.default_rng(40)
+    Hq, Hkv, Sk, Sq = 16, 2, 600, 100
+    raw, kw = _raw_inputs(rng, Hkv, Sk, 512)
+    inv = orc.rope_inv_freq(512, 1.0e6, 0.25)
+    q = rms_rows(rng, (Hq, Sq, 512))
+    k, v = raw_prefill_kv(_dev(raw), _dev(kw), 1e-6, torch.from_numpy(inv).cuda())
+    step = PrefillStep(num_q_heads=Hq, num_kv_heads=Hkv, head_dim=512, seq_q=Sq, seq_k=Sk, q_pos0=Sk - Sq,
+                       k_pos0=0, scale=1.0)
+    out = prefill(step, _dev(q), k, v)
+    torch.cuda.synchronize()
+    ek, ev = orc.raw_prefill_kv(raw, kw, 1e-6, inv, 0)
+    ref = orc.prefill_f64(q, ek, ev, Sk - Sq, 0, 0, 1.0)
+    err = np.abs(orc.from_bf16(_host(out)).astype(np.float64) - ref)
+    print(f"[raw-prefill] max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
+    assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN
