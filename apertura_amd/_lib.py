@@ -33,7 +33,8 @@ EXPORTS = (
     "esda_decode_attn_global", "esda_cache_update_raw_q8", "esda_cache_current_raw_q8",
     "esda_cache_decode_raw_q8", "esda_decode_attn_global_q8",
     # include/esda_prefill.h
-    "esda_prefill_workspace_size", "esda_prefill", "esda_raw_prefill_kv", "esda_raw_q8_prefill_kv",
+    "esda_prefill_workspace_size", "esda_prefill", "esda_prefill_stages", "esda_raw_prefill_kv",
+    "esda_raw_q8_prefill_kv", "esda_cache_prefill", "esda_cache_prefill_raw",
 )
 _VOID = ("esda_cache_destroy", "esda_cache_mark_step", "esda_cache_reset", "esda_cache_clear_rewind_mark")
 
@@ -193,6 +194,9 @@ def lib() -> ctypes.CDLL:
         PD = ctypes.POINTER(PrefillDesc)
         L.esda_prefill_workspace_size.argtypes = [PD, ctypes.POINTER(sz)]
         L.esda_prefill.argtypes = [PD, ctypes.POINTER(PrefillArgs), P]
+        L.esda_prefill_stages.argtypes = [PD, ctypes.POINTER(PrefillArgs), ctypes.c_int, P]
+        L.esda_cache_prefill.argtypes = [P, i32, P, i32, i32, P, P, i32, i32, i32, i32, f32, i32, i32, P, P]
+        L.esda_cache_prefill_raw.argtypes = [P, i32, P, i32, i32, P, i32, P, f32, P, i32, i32, f32, i32, P, P]
         L.esda_raw_prefill_kv.argtypes = [P, i64, i32, i32, i32, P, f32, P, i32, P, P, i64, P]
         L.esda_raw_q8_prefill_kv.argtypes = [P, i64, P, P, i64, i32, i32, P, f32, P, i32, P, P, i64, P]
         for name in EXPORTS:

@@ -204,6 +204,41 @@ class ESKVCache:
                                              _dev_ptr(out, torch.bfloat16), _stream_ptr(stream)))
         return out
 
+    def prefill(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, max_keep: int,
+                window: int, scale: float, past_len: int, prealloc: bool = True, out: torch.Tensor | None = None,
+                stream=None) -> torch.Tensor:
+        """ESKVCache::prefill: append a chunk (k_new / v_new [kvHeads, seq, headDim]; v_new may
+        be k_new itself) and attend q [numQHeads, seq, headDim] over the live rows with the
+        reference's mask.  Returns [seq, numQHeads * headDim] bf16."""
+        kvh, n, hd = _rows(k_new, "k_new")
+        _rows(v_new, "v_new")
+        if q.dim() != 3 or q.shape[1] != n or q.shape[2] != hd or not q.is_contiguous():
+            raise ValueError("q must be contiguous [numQHeads, seq, headDim] with seq = k_new rows")
+        hq = q.shape[0]
+        if out is None:
+            out = torch.empty((n, hq * hd), dtype=torch.bfloat16, device=q.device)
+        check(lib().esda_cache_prefill(self._h, layer, _dev_ptr(q, torch.bfloat16), hq, n, _dev_ptr(k_new),
+                                       _dev_ptr(v_new), kvh, hd, max_keep, window, scale, past_len,
+                                       1 if prealloc else 0, _dev_ptr(out, torch.bfloat16), _stream_ptr(stream)))
+        return out
+
+    def prefill_raw(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, kw: torch.Tensor, eps: float, inv_freq,
+                    past_len: int, scale: float, q8: bool = False, out: torch.Tensor | None = None,
+                    stream=None) -> torch.Tensor:
+        """ESKVCache::prefillRaw: append the chunk's raw rows (into the q8 stream when q8)
+        and attend over the whole raw stream (head dim 512)."""
+        kvh, n, hd = _rows(k_new, "k_new")
+        if hd != 512 or q.dim() != 3 or q.shape[1:] != (n, 512) or not q.is_contiguous():
+            raise ValueError("raw prefill: q [numQHeads, seq, 512] contiguous, k_new [kvHeads, seq, 512]")
+        hq = q.shape[0]
+        if out is None:
+            out = torch.empty((n, hq * 512), dtype=torch.bfloat16, device=q.device)
+        f = (ctypes.c_float * len(inv_freq))(*[float(x) for x in inv_freq])
+        check(lib().esda_cache_prefill_raw(self._h, layer, _dev_ptr(q, torch.bfloat16), hq, n, _dev_ptr(k_new), kvh,
+                                           _dev_ptr(kw, torch.bfloat16), eps, f, len(inv_freq), past_len, scale,
+                                           1 if q8 else 0, _dev_ptr(out, torch.bfloat16), _stream_ptr(stream)))
+        return out
+
     def slot(self, layer: int) -> dict:
         ln, st, cap, fl = (ctypes.c_int32() for _ in range(4))
         check(lib().esda_cache_slot(self._h, layer, ctypes.byref(ln), ctypes.byref(st), ctypes.byref(cap),

@@ -181,6 +181,36 @@ int esda_cache_decode_raw_q8(esda_cache *cache, int32_t layer, const void *q, in
     });
 }
 
+int esda_cache_prefill(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads, int32_t seq,
+                       const void *k_new, const void *v_new, int32_t kv_heads, int32_t head_dim, int32_t max_keep,
+                       int32_t window, float scale, int32_t past_len, int32_t prealloc, void *out, void *stream) {
+    return guarded([&] {
+        needCache(cache);
+        if (!q || !out || num_q_heads <= 0 || seq <= 0 || head_dim <= 0)
+            throw std::invalid_argument("esda_cache_prefill: null q / out or empty shape");
+        es::Tensor qt = es::Tensor::wrap(const_cast<void *>(q), {num_q_heads, seq, head_dim}, es::Dtype::bf16);
+        es::Tensor ot = es::Tensor::wrap(out, {seq, (int64_t) num_q_heads * head_dim}, es::Dtype::bf16);
+        cache->impl.prefill(layer, qt, rows(k_new, kv_heads, seq, head_dim), rows(v_new, kv_heads, seq, head_dim),
+                            max_keep, window, scale, past_len, prealloc != 0, asStream(stream), &ot);
+    });
+}
+
+int esda_cache_prefill_raw(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads, int32_t seq,
+                           const void *k_new, int32_t kv_heads, const void *kw, float eps, const float *inv_freq,
+                           int32_t n_freq, int32_t past_len, float scale, int32_t q8, void *out, void *stream) {
+    return guarded([&] {
+        needCache(cache);
+        if (!q || !out || !kw || !inv_freq || num_q_heads <= 0 || seq <= 0 || n_freq < 0)
+            throw std::invalid_argument("esda_cache_prefill_raw: null pointer or empty shape");
+        es::Tensor qt = es::Tensor::wrap(const_cast<void *>(q), {num_q_heads, seq, 512}, es::Dtype::bf16);
+        es::Tensor ot = es::Tensor::wrap(out, {seq, (int64_t) num_q_heads * 512}, es::Dtype::bf16);
+        es::Tensor kwt = es::Tensor::wrap(const_cast<void *>(kw), {512}, es::Dtype::bf16);
+        std::vector<float> f(inv_freq, inv_freq + n_freq);
+        cache->impl.prefillRaw(layer, qt, rows(k_new, kv_heads, seq, 512), kwt, eps, f, past_len, scale, q8 != 0,
+                               asStream(stream), &ot);
+    });
+}
+
 int esda_cache_slot(esda_cache *cache, int32_t layer, int32_t *len, int32_t *start, int32_t *capacity,
                     int32_t *flags) {
     return guarded([&] {

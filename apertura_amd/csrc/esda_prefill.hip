@@ -504,9 +504,10 @@ size_t workspace_of(const PrefillParams &p, int D) {
 }
 
 template <int D>
-void launch_prefill(const PrefillParams &p, hipStream_t st) {
-    hipLaunchKernelGGL((prefill_kernel<D>), dim3(p.tiles, p.Hkv, p.splits), dim3(64 * kWaves), 0, st, p);
-    if (p.splits > 1) {
+void launch_prefill(const PrefillParams &p, int stages, hipStream_t st) {
+    if (stages & 1)
+        hipLaunchKernelGGL((prefill_kernel<D>), dim3(p.tiles, p.Hkv, p.splits), dim3(64 * kWaves), 0, st, p);
+    if ((stages & 2) && p.splits > 1) {
         const long long n = (long long) p.Sq * p.Hq * (D / 4);
         hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, p);
     }
@@ -545,7 +546,7 @@ int esda_prefill_workspace_size(const esda_prefill_desc *desc, size_t *bytes) {
     return ESDA_OK;
 }
 
-int esda_prefill(const esda_prefill_desc *desc, const esda_prefill_args *a, void *stream) {
+int esda_prefill_stages(const esda_prefill_desc *desc, const esda_prefill_args *a, int stages, void *stream) {
     PrefillParams p;
     int rc = plan_prefill(desc, &p);
     if (rc != ESDA_OK) return rc;
@@ -569,12 +570,16 @@ int esda_prefill(const esda_prefill_desc *desc, const esda_prefill_args *a, void
     p.v = static_cast<const uint16_t *>(a->v);
     p.out = static_cast<uint16_t *>(a->out);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (D == 512) launch_prefill<512>(p, st);
-    else if (D == 256) launch_prefill<256>(p, st);
-    else launch_prefill<128>(p, st);
+    if (D == 512) launch_prefill<512>(p, stages, st);
+    else if (D == 256) launch_prefill<256>(p, stages, st);
+    else launch_prefill<128>(p, stages, st);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(ESDA_ERR_HIP, std::string("esda_prefill launch: ") + hipGetErrorString(e));
     return ESDA_OK;
+}
+
+int esda_prefill(const esda_prefill_desc *desc, const esda_prefill_args *a, void *stream) {
+    return esda_prefill_stages(desc, a, 3, stream);
 }
 
 int esda_raw_prefill_kv(const void *raw, int64_t raw_head_stride, int32_t kv_heads, int32_t rows, int32_t head_dim,

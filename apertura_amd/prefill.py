@@ -74,10 +74,15 @@ def prefill_workspace_bytes(step: PrefillStep) -> int:
     return int(n.value)
 
 
+STAGE_ATTEND = 1
+STAGE_MERGE = 2
+
+
 def prefill(step: PrefillStep, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None,
-            workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+            workspace: torch.Tensor | None = None, stream=None, stages: int = STAGE_ATTEND | STAGE_MERGE) -> torch.Tensor:
     """O [Sq, Hq, D] bf16 of ``step`` (strides as in ``step``; defaults: q [Hq, Sq, D],
-    k / v [Hkv, Sk, D], out [Sq, Hq, D], all dense)."""
+    k / v [Hkv, Sk, D], out [Sq, Hq, D], all dense).  ``stages`` selects the launches
+    (timing only: the output is complete only with both)."""
     bf = torch.bfloat16
     D = step.head_dim
     if out is None:
@@ -100,7 +105,7 @@ def prefill(step: PrefillStep, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
     a = PrefillArgs(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(out),
                     _dev_ptr(workspace) if nbytes else None, nbytes)
-    check(lib().esda_prefill(ctypes.byref(d), ctypes.byref(a), _stream_ptr(stream)))
+    check(lib().esda_prefill_stages(ctypes.byref(d), ctypes.byref(a), int(stages), _stream_ptr(stream)))
     return out
 
 

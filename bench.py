@@ -13,13 +13,20 @@ write + new-row read and write.  `roofline` prices the dominant kernel (the spli
 attend kernel, timed alone with HIP events on the launch stream); `cpu_baseline` times
 the CPU oracle's reference-rounding restatement on the same inputs.
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c2|c1|c3|c5] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c2|c1|c3|c5|p512g|p4kg|p512l] [--no-cpu]
 
 Workload c5 is the full Gemma-4-31B-shaped attention step: 60 layers (every 6th
 global: D=512, Hkv=4, k_eq_v, linear caches; the rest local: D=256, Hkv=16, window
 1024 over a 1024-row ring), B=32, lengths ~ U[1024, 32768]; each layer appends and
 attends in order (one esda_decode per layer, 120 kernels per step, replayed from a HIP
 graph).  It reports total attention us per token step.
+
+Workloads p512g / p4kg / p512l are the prefill side (esda_prefill): a 512-token chunk
+over a 16384-token global cache (the reference's own prefill decomposition shape: d512,
+nKV 4, groups 8, seqQ 512 at 16K, WIDE_HEAD_ATTENTION.md), a fresh 4096-token global
+prefill, and a 512-token chunk of a local layer (D=256, Hkv=16, window 1024 over
+window + chunk keys).  They report TFLOP/s of algorithmic attention FLOPs (4 * D per
+visible (query head, key) pair) against the bf16 MFMA peak.
 """
 from __future__ import annotations
 
@@ -30,6 +37,7 @@ import sys
 import time
 
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 
 def _die_multi_gpu(n: int) -> None:
@@ -55,6 +63,16 @@ WORKLOADS = {
                  pos=lambda rng, B: [131071], scale=1.0),
     "c4raw": dict(B=1, Hq=32, Hkv=4, D=512, cap=131072, window=0, ring=False, shared=True, raw=True,
                   pos=lambda rng, B: [131071], scale=1.0),
+}
+
+PREFILL_WORKLOADS = {
+    "p512g": dict(Hq=32, Hkv=4, D=512, Sq=512, Sk=16384, q_pos0=15872, k_pos0=0, window=0, scale=512 ** -0.5,
+                  name="global-layer prefill chunk: 512 queries over 16384 keys (causal), D=512, GQA 32/4"),
+    "p4kg": dict(Hq=32, Hkv=4, D=512, Sq=4096, Sk=4096, q_pos0=0, k_pos0=0, window=0, scale=512 ** -0.5,
+                 name="global-layer fresh prefill: 4096 tokens (causal), D=512, GQA 32/4"),
+    "p512l": dict(Hq=32, Hkv=16, D=256, Sq=512, Sk=1536, q_pos0=15872, k_pos0=15872 + 512 - 1536, window=1024,
+                  scale=1 / 16, name="local-layer prefill chunk: 512 queries over window + chunk = 1536 keys, "
+                                     "window 1024, D=256, GQA 32/16"),
 }
 
 # C5 layer types (ESModelConfig.mm:82-86: every 6th layer is global, the last one too).
@@ -114,7 +132,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c4", choices=sorted(WORKLOADS) + ["c5"])
+    ap.add_argument("--workload", default="c4", choices=sorted(WORKLOADS) + ["c5"] + sorted(PREFILL_WORKLOADS))
     ap.add_argument("--split-rows", type=int, default=0)
     ap.add_argument("--local-split-rows", type=int, default=0, help="c5: split rows of local layers")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -136,6 +154,8 @@ def main() -> int:
         return calibrate_copy(args)
     if args.workload == "c5":
         return bench_c5(args)
+    if args.workload in PREFILL_WORKLOADS:
+        return bench_prefill(args)
     w = WORKLOADS[args.workload]
     rng = np.random.default_rng(1234)
     pos = w["pos"](rng, w["B"])
@@ -338,6 +358,129 @@ def calibrate_copy(args) -> int:
     print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n,
                       "us": round(ms * 1e3, 3), "GB/s": round(2 * n / (ms * 1e-3) / 1e9, 2)}), flush=True)
     return 0
+
+
+def prefill_visible_pairs(w) -> int:
+    """Sum over query rows of the keys each sees (per query head)."""
+    import numpy as np
+    qa = w["q_pos0"] + np.arange(w["Sq"], dtype=np.int64)
+    lo = np.full_like(qa, w["k_pos0"]) if not w["window"] else np.maximum(w["k_pos0"], qa - w["window"] + 1)
+    hi = np.minimum(qa, w["k_pos0"] + w["Sk"] - 1)
+    return int(np.maximum(hi - lo + 1, 0).sum())
+
+
+def bench_prefill(args) -> int:
+    """One prefill attention call per step (esda_prefill: attention kernel + split merge)."""
+    import numpy as np
+    import torch
+
+    from apertura_amd.prefill import STAGE_ATTEND, PrefillStep, prefill, prefill_workspace_bytes
+
+    w = PREFILL_WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+
+    def rms_bf16(shape):
+        x = torch.randn(shape, device=dev, dtype=torch.float32, generator=gen)
+        x = x * torch.rsqrt(x.square().mean(-1, keepdim=True) + 1e-6)
+        return x.to(torch.bfloat16)
+
+    Hq, Hkv, D, Sq, Sk = w["Hq"], w["Hkv"], w["D"], w["Sq"], w["Sk"]
+    q, k, v = rms_bf16((Hq, Sq, D)), rms_bf16((Hkv, Sk, D)), rms_bf16((Hkv, Sk, D))
+    out = torch.empty((Sq, Hq, D), dtype=torch.bfloat16, device=dev)
+    step = PrefillStep(num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D, seq_q=Sq, seq_k=Sk, q_pos0=w["q_pos0"],
+                       k_pos0=w["k_pos0"], window=w["window"], scale=w["scale"])
+    ws = torch.empty(max(1, prefill_workspace_bytes(step)), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.Stream()
+
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    with torch.cuda.stream(stream):
+        call = lambda: prefill(step, q, k, v, out, ws, stream)
+        attend = lambda: prefill(step, q, k, v, out, ws, stream, stages=STAGE_ATTEND)
+        warm_steps = warm_up(call, args.warmup)
+        ms_step = timed(call, args.steps)
+        ms_attend = timed(attend, args.steps)
+        call()
+    torch.cuda.synchronize()
+
+    pairs = prefill_visible_pairs(w)
+    flops = 4 * D * Hq * pairs
+    tf = flops / (ms_step * 1e-3) / 1e12
+    tf_attend = flops / (ms_attend * 1e-3) / 1e12
+    cpu = None if args.no_cpu else cpu_baseline_prefill(w, q, k, v, args.cpu_threads)
+    line = {
+        "metric": "prefill-attn TFLOP/s at Gemma-4-31B shapes, 1 GPU",
+        "value": round(tf, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "warmup_steps_run": warm_steps,
+        "ms_per_step": round(ms_step, 6),
+        "us_per_step": round(ms_step * 1e3, 3),
+        "timing": "eager (one esda_prefill per step)",
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) rows, unit-RMS, bf16)",
+        "config": {"workload": w["name"], "num_q_heads": Hq, "num_kv_heads": Hkv, "head_dim": D, "seq_q": Sq,
+                   "seq_k": Sk, "q_pos0": w["q_pos0"], "k_pos0": w["k_pos0"], "window": w["window"],
+                   "visible_pairs_per_head": pairs, "algorithmic_flops_per_step": flops,
+                   "key_splits": (prefill_workspace_bytes(step) > 0)},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": f"prefill_kernel<{D}> (QK and PV on v_mfma_f32_16x16x32_bf16, online softmax)",
+            "achieved": round(tf_attend, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf_attend / PEAK_BF16_TFLOPS, 4), "traffic": profiled_traffic(args.workload),
+            "traffic_source": f"profiles/attend_{args.workload}.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+            "kernel_us": round(ms_attend * 1e3, 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline_prefill(w, q, k, v, threads: int):
+    """The fp64 prefill oracle on the host over a sample of query rows (rows are
+    independent; every row sees its full visible key range), doubled until >= 10 s."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as orc
+
+    qh = q.cpu().view(torch.int16).numpy().view(np.uint16)
+    kh = k.cpu().view(torch.int16).numpy().view(np.uint16)
+    vh = v.cpu().view(torch.int16).numpy().view(np.uint16)
+    Sq = w["Sq"]
+    n, secs, pairs = 1, 0.0, 0
+    while True:
+        rows = np.linspace(0, Sq - 1, num=min(n, Sq)).astype(int)
+        t0 = time.perf_counter()
+        for r in rows:
+            orc.prefill_f64(qh[:, r:r + 1], kh, vh, w["q_pos0"] + int(r), w["k_pos0"], w["window"], w["scale"],
+                            threads=threads)
+        secs = time.perf_counter() - t0
+        sub = dict(w, Sq=1)
+        pairs = sum(prefill_visible_pairs(dict(sub, q_pos0=w["q_pos0"] + int(r))) for r in rows)
+        if secs >= 10.0 or len(rows) >= Sq:
+            break
+        n *= 2
+    flops = 4 * w["D"] * w["Hq"] * pairs
+    return {"value": round(flops / secs / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{len(rows)} of {Sq} query rows (all heads, full visible key ranges), fp64 prefill oracle, "
+                      f"{secs:.1f} s"}
 
 
 def bench_c5(args) -> int:

@@ -94,6 +94,20 @@ public:
     Tensor decodeRaw(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
                      const std::vector<float> &invFreq, hipStream_t stream = nullptr, Tensor *out = nullptr);
 
+    // Prefill chunk (ESAttention::keyValue then SDPA at seq > 1, ESAttention.mm:77-108,
+    // 168-193): append kNew / vNew (seq rows; maxKeep as update, e.g. window + seq for a
+    // chunked sliding layer), then attend q [numQ, seq, hd] over the live rows with the
+    // reference's mask (pastLen = positions cached before the chunk; window 0 on global
+    // layers).  Returns O [seq, numQ * hd] bf16 (esPrefillAttention).
+    Tensor prefill(int layer, const Tensor &q, const Tensor &kNew, const Tensor &vNew, int maxKeep, int window,
+                   float scale, int pastLen, bool prealloc = true, hipStream_t stream = nullptr, Tensor *out = nullptr);
+    // Raw-K (q8 = false: updateRaw, prealloc) or q8 raw-K (updateRawQ8) prefill chunk,
+    // ESAttention.mm:253-332: append the chunk's raw rows, then esPrefillAttnRaw(Q8) over
+    // the whole stream.
+    Tensor prefillRaw(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
+                      const std::vector<float> &invFreq, int pastLen, float scale, bool q8 = false,
+                      hipStream_t stream = nullptr, Tensor *out = nullptr);
+
     // The cached {K, V} without appending (ESKVCache.mm:112-119).
     std::pair<Tensor, Tensor> current(int layer, bool prealloc) const;
 

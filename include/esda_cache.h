@@ -30,6 +30,8 @@
  *                                  and tests; the reference keeps it private (ESKVCache.h:183-192)
  *   esda_decode_attn_global        esDecodeAttnGlobal                  ESDecodeAttn.h:27-28
  *   esda_decode_attn_global_q8     esDecodeAttnGlobalQ8                ESDecodeAttn.h:30-36
+ *   esda_cache_prefill             update + SDPA at seq > 1            ESAttention.mm:77-108, :168-193
+ *   esda_cache_prefill_raw         updateRaw(Q8) + the raw-K prefill   ESAttention.mm:253-332
  */
 #ifndef APERTURA_ESDA_CACHE_H
 #define APERTURA_ESDA_CACHE_H
@@ -108,6 +110,22 @@ int esda_cache_current_raw_q8(esda_cache *cache, int32_t layer, esda_q8_view *vi
 int esda_cache_decode_raw_q8(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads,
                              const void *k_new, int32_t kv_heads, const void *kw, float eps,
                              const float *inv_freq, int32_t n_freq, void *out, void *stream);
+
+/* Prefill chunk: append seq rows k_new / v_new [kv_heads, seq, head_dim] (v_new == k_new:
+ * one shared K=V buffer; max_keep as esda_cache_update) and attend q [num_q_heads, seq,
+ * head_dim] over the live rows with the reference's mask: past_len positions cached before
+ * the chunk, window 0 (global) or the sliding window.  out [seq, num_q_heads * head_dim].
+ * prealloc as esda_cache_update. */
+int esda_cache_prefill(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads, int32_t seq,
+                       const void *k_new, const void *v_new, int32_t kv_heads, int32_t head_dim,
+                       int32_t max_keep, int32_t window, float scale, int32_t past_len, int32_t prealloc,
+                       void *out, void *stream);
+/* Raw-K prefill chunk (head_dim 512): append the chunk's raw rows (q8 != 0: into the q8
+ * stream) and attend over the whole stream, K / V rebuilt by the reference's prefill ops.
+ * inv_freq: host array of n_freq floats (zero-extended to 256). */
+int esda_cache_prefill_raw(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads, int32_t seq,
+                           const void *k_new, int32_t kv_heads, const void *kw, float eps, const float *inv_freq,
+                           int32_t n_freq, int32_t past_len, float scale, int32_t q8, void *out, void *stream);
 
 /* flags: bit 0 = rows before start were discarded by a compaction, bit 1 = shared K=V
  * buffer, bit 2 = raw-K content, bit 3 = q8 raw-K content (len and capacity are then the

@@ -69,6 +69,10 @@ typedef struct esda_prefill_args {
 
 int esda_prefill_workspace_size(const esda_prefill_desc *desc, size_t *bytes);
 int esda_prefill(const esda_prefill_desc *desc, const esda_prefill_args *args, void *stream);
+/* esda_prefill's launches one at a time (for timing): stages bit 0 = the attention kernel,
+ * bit 1 = the split merge (launched only when the plan splits the keys). */
+int esda_prefill_stages(const esda_prefill_desc *desc, const esda_prefill_args *args, int stages,
+                        void *stream);
 
 /* Raw-K prefill reconstruction (ESAttention.mm:306-326), for kv head h and key row t at
  * absolute position pos0 + t:
