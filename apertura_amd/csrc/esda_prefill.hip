@@ -8,11 +8,12 @@
 //
 // Kernels
 //   prefill_kernel<D>   grid (query tiles, kv heads, key splits), 8 waves (two per
-//                       SIMD), one workgroup per CU.  A query tile is 128 * QB query
-//                       rows (QB = 1 at D = 512, 2 at D = 256 and 128: qb_of) of one kv
-//                       head's GQA group, ordered position-major (row r: position
-//                       r / G, group head r % G); wave w owns rows 16 QB w .. as QB
-//                       blocks of 16 -- the MFMA N dimension.  The
+//                       SIMD), one workgroup per CU; one 16-query block per wave at
+//                       D = 512 and 256, two at D = 128 (nw_of, qb_of).  A
+//                       query tile is 16 * QB * NW query rows of one kv head's GQA group,
+//                       ordered position-major (row r: position r / G, group head r % G);
+//                       wave w owns rows 16 QB w .. as QB blocks of 16 -- the MFMA N
+//                       dimension.  The
 //                       tile's visible keys (or one split of them) stream through an
 //                       LDS ring of 32-key stages filled by LDS DMA.  Per stage each
 //                       wave forms S^T[32 keys x its queries] over the whole head dim
@@ -43,7 +44,6 @@
 
 namespace {
 
-constexpr int kWaves = 8;
 constexpr int kStageKeys = 32;
 constexpr int kBlk = 1056;                 // LDS bytes per DMA block: 1 KB + 32 B pad
 constexpr int kRingBudget = 136 * 1024;    // LDS bytes for the K / V ring
@@ -79,31 +79,33 @@ __host__ __device__ inline void tile_keys(const PrefillParams &p, int tile, int 
 // block b holding keys b + NI*q (q < 512/D) at +2D*q; a stage is the K halves then the V
 // halves.  Both the 128-bit row reads (QK A operand) and the transpose reads (PV A
 // operand) are bank-conflict-free in this layout (the decode kernel's measured layout).
-// 16-query blocks per wave: O^T takes QB * D / 16 accumulator registers per lane (128
-// at D = 512 and 256) beside Q^T's QB * D / 8 (64), within two waves per SIMD.
-__host__ __device__ constexpr int qb_of(int D) { return D == 128 ? 2 : 512 / D; }
+// Waves per workgroup and 16-query blocks per wave.  O^T takes QB * D / 16 accumulator
+// registers per lane beside Q^T's QB * D / 8 and two stages of scores (16 QB), within
+// the 256 registers of two waves per SIMD.  (Measured: at D = 256, four waves of two
+// blocks -- half the LDS reads per MFMA, one wave per SIMD -- ran 6% slower than eight
+// waves of one block; at D = 512 two blocks per wave do not fit without spills.)
+__host__ __device__ constexpr int nw_of(int) { return 8; }
+__host__ __device__ constexpr int qb_of(int D) { return D == 128 ? 2 : 1; }
 
 template <int D>
 struct PRing {
     static constexpr int NI = D / 32;                 // DMA blocks per 16-key half
     static constexpr int HB = NI * kBlk;              // one half stage of one tensor
-    static constexpr int SB = 4 * HB;                 // stage: K halves, V halves
-    static constexpr int NS = kRingBudget / SB > 8 ? 8 : kRingBudget / SB;
+    static constexpr int BYTES = 8 * HB;              // two K and two V stages
     static constexpr int CPR = D / 8;                 // 16-byte chunks per row
-    static constexpr int DPW = 4 * NI / kWaves;       // DMA instructions per wave per stage
-    static_assert(NS >= 2, "the ring needs two stages");
-    static_assert((NS - 2) * DPW <= 60, "vmcnt holds at most 63 outstanding loads");
+    static_assert(BYTES <= kRingBudget, "the K / V slots must fit the LDS budget");
     __host__ __device__ static constexpr int off(int r) { return (r % NI) * kBlk + (r / NI) * 2 * D; }
 };
 
 template <int D>
-__global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(64 * nw_of(D), 1) void prefill_kernel(PrefillParams p) {
     using R = PRing<D>;
+    constexpr int kWaves = nw_of(D);
     constexpr int QB = qb_of(D);        // 16-query blocks per wave
     constexpr int QT = 16 * QB * kWaves;  // query rows per tile
     constexpr int KS = D / 32;          // QK k-steps
     constexpr int DT = D / 16;          // PV dim tiles
-    __shared__ __attribute__((aligned(16))) unsigned char ring[R::NS * R::SB];
+    __shared__ __attribute__((aligned(16))) unsigned char ring[R::BYTES];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int li = lane & 15, lg = lane >> 4;
@@ -155,28 +157,46 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
         }
     }
 
-    // DMA: instruction t of this wave (index ii = wave*DPW + t of the stage) fills block
-    // b = ii % NI of half hh = (ii / NI) % 2 of tensor ii / (2 NI); lane l reads chunk
-    // l % CPR of key row 16hh + b + NI*(l / CPR).
+    // LDS: two K slots then two V slots, each a 32-key stage (two 16-key halves).  Stage
+    // s's K sits in K slot s % 2 and its V in V slot s % 2.  Iteration s forms the scores
+    // of stage s+1 while it runs the softmax and PV of stage s, so K runs one stage ahead
+    // of V: after iteration s's barrier, K(s+2) replaces K(s) (read by iteration s-1) and
+    // V(s+1) replaces V(s-1) (read by iteration s-1); both land during iteration s.
+    //
+    // DMA: K instruction t of this wave (ii = wave*KPW + t of the stage's 2 NI) fills block
+    // b = ii % NI of half hh = ii / NI; lane l reads chunk l % CPR of stage row
+    // r = 16hh + b + NI*(l / CPR).  V likewise.  Interior stages add the lane's byte offset
+    // to a wave-uniform base; the last, partial stage clamps each row to the range.
+    constexpr int KPW = 2 * R::NI / kWaves;  // DMA instructions per wave per tensor per stage
+    static_assert(KPW * kWaves == 2 * R::NI, "whole DMA blocks per wave");
     const uint16_t *kvb = p.k + (size_t) kvh * p.kv_hs;
     const uint16_t *vvb = p.v + (size_t) kvh * p.kv_hs;
     const int nst = (j1 - j0 + kStageKeys - 1) / kStageKeys;
-    auto issue = [&](int s) {
-        if (s >= nst) return;
-        unsigned char *buf = ring + (s % R::NS) * R::SB;
-        const int jb = j0 + s * kStageKeys;
+    unsigned voff[KPW];
+    int vrow[KPW], ldso[KPW];
 #pragma unroll
-        for (int t = 0; t < R::DPW; ++t) {
-            const int ii = wave * R::DPW + t;
-            const int tensor = ii / (2 * R::NI), hh = (ii / R::NI) % 2, b = ii % R::NI;
-            int j = jb + 16 * hh + b + R::NI * (lane / R::CPR);
-            j = j < j1 ? j : j1 - 1;  // rows past the range repeat the last key (masked)
-            const uint16_t *src = (tensor ? vvb : kvb) + (size_t) j * D + (lane % R::CPR) * 8;
-            lds_dma16(src, lds_addr(buf) + (tensor * 2 + hh) * R::HB + b * kBlk);
+    for (int t = 0; t < KPW; ++t) {
+        const int ii = wave * KPW + t, hh = ii / R::NI, b = ii % R::NI;
+        vrow[t] = 16 * hh + b + R::NI * (lane / R::CPR);
+        voff[t] = (unsigned) ((vrow[t] * D + (lane % R::CPR) * 8) * 2);
+        ldso[t] = hh * R::HB + b * kBlk;
+    }
+    auto kslot = [&](int s) { return ring + (s & 1) * 2 * R::HB; };
+    auto vslot = [&](int s) { return ring + 4 * R::HB + (s & 1) * 2 * R::HB; };
+    auto issue = [&](const uint16_t *head, int s, unsigned char *slot) {
+        const int jb = j0 + s * kStageKeys;
+        if (jb + kStageKeys <= j1) {
+            const uint16_t *base = head + (size_t) jb * D;
+#pragma unroll
+            for (int t = 0; t < KPW; ++t) lds_dma16_s(base, voff[t], lds_addr(slot) + ldso[t]);
+        } else {
+#pragma unroll
+            for (int t = 0; t < KPW; ++t) {
+                const int j = min(jb + vrow[t], j1 - 1);  // rows past the range repeat the last key
+                lds_dma16(head + (size_t) j * D + (lane % R::CPR) * 8, lds_addr(slot) + ldso[t]);
+            }
         }
     };
-#pragma unroll
-    for (int s = 0; s < R::NS - 1; ++s) issue(s);
 
     const int qk_off = R::off(li) + lg * 16;                    // + 64 ks (+ HB: keys 16..31)
     const int tr_off = R::off(4 * lg + li / 4) + (li % 4) * 8;  // + 32 dt (+ HB)
@@ -194,54 +214,63 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
     const int qa_min = p.q_pos0 + (int) ((long long) tile * QT / p.G);
     const int qa_max = p.q_pos0 + (int) (((long long) tile * QT + QT < nq ? (long long) tile * QT + QT : nq) - 1) / p.G;
 
-    for (int s = 0; s < nst; ++s) {
-        // stage s landed (this wave's loads; the barrier covers the other waves') and
-        // every wave is done with stage s-1, whose buffer stage s+NS-1 reuses
-        if constexpr (R::NS > 2) {
-            if (s + R::NS - 2 < nst) ESDA_WAIT_VM((R::NS - 2) * R::DPW);
-            else ESDA_WAIT_VM(0);
-        } else {
-            ESDA_WAIT_VM(0);
-        }
-        lds_barrier();
-        issue(s + R::NS - 1);
-        const unsigned char *kb = ring + (s % R::NS) * R::SB;
-        const unsigned char *vb = kb + 2 * R::HB;
-        const int jb = j0 + s * kStageKeys;
-
-        // S^T[keys x queries]: sacc[h][qb] covers keys 16h + 4lg + r of query column li.
-        f32x4 sacc[2][QB];
+    // S^T[keys x queries] of a stage: s[h][qb] covers keys 16h + 4lg + r of query column li.
+    struct Scores {
+        f32x4 s[2][QB];
+    };
+    auto qk = [&](const unsigned char *kb) {
+        Scores sc;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb) sacc[h][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int qb = 0; qb < QB; ++qb) sc.s[h][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const bf16x8 ka0 = *reinterpret_cast<const bf16x8 *>(kb + qk_off + 64 * ks);
             const bf16x8 ka1 = *reinterpret_cast<const bf16x8 *>(kb + R::HB + qk_off + 64 * ks);
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
-                sacc[0][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, qreg[qb][ks], sacc[0][qb], 0, 0, 0);
-                sacc[1][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, qreg[qb][ks], sacc[1][qb], 0, 0, 0);
+                sc.s[0][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, qreg[qb][ks], sc.s[0][qb], 0, 0, 0);
+                sc.s[1][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, qreg[qb][ks], sc.s[1][qb], 0, 0, 0);
             }
         }
+        return sc;
+    };
 
-        // Visibility: a stage is fully visible to every row of the tile when its last key
-        // is at or before the tile's first position, its first key is inside the window
-        // of the tile's last position, and it lies inside the split.
-        const int ka_first = p.k_pos0 + jb, ka_last = ka_first + kStageKeys - 1;
-        const bool full = jb + kStageKeys <= j1 && ka_last <= qa_min &&
-                          (p.window == 0 || ka_first > qa_max - p.window);
+    issue(kvb, 0, kslot(0));
+    issue(vvb, 0, vslot(0));
+    if (nst > 1) issue(kvb, 1, kslot(1));
+    ESDA_WAIT_VM(0);
+    lds_barrier();
+    Scores cur = qk(kslot(0));
 
-        bf16x8 pb[QB];
+    for (int s = 0; s < nst; ++s) {
+        // K(s+1) and V(s) landed (this wave's loads; the barrier covers the other waves')
+        // and every wave is done with iteration s-1
+        ESDA_WAIT_VM(0);
+        lds_barrier();
+        if (s + 2 < nst) issue(kvb, s + 2, kslot(s));
+        if (s + 1 < nst) issue(vvb, s + 1, vslot(s + 1));
+        const unsigned char *vb = vslot(s);
+        const int jb = j0 + s * kStageKeys;
+
+        // Stage s's scores in log2 units; positions a boundary stage does not show to a
+        // row are -inf.  A stage is fully visible to every row of the tile when its last
+        // key is at or before the tile's first position, its first key is inside the
+        // window of the tile's last position, and it lies inside the split.
+        float sv[QB][8];
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            float sv[8];
+        for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sv[4 * h + r] = sacc[h][qb][r] * p.scale_log2e;
-            if (!full) {
+                for (int r = 0; r < 4; ++r) sv[qb][4 * h + r] = cur.s[h][qb][r] * p.scale_log2e;
+        const int ka_first = p.k_pos0 + jb, ka_last = ka_first + kStageKeys - 1;
+        const bool full = jb + kStageKeys <= j1 && ka_last <= qa_min &&
+                          (p.window == 0 || ka_first > qa_max - p.window);
+        if (!full) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
                 const int qa = qabs[qb];
                 const int lo = p.window > 0 ? qa - p.window : INT_MIN;  // visible: lo < ka <= qa
 #pragma unroll
@@ -250,25 +279,49 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
                     for (int r = 0; r < 4; ++r) {
                         const int j = jb + 16 * h + 4 * lg + r;
                         const int ka = p.k_pos0 + j;
-                        if (!(j < j1 && ka <= qa && ka > lo)) sv[4 * h + r] = -INFINITY;
+                        if (!(j < j1 && ka <= qa && ka > lo)) sv[qb][4 * h + r] = -INFINITY;
                     }
             }
-            float mt = sv[0];
+        }
+
+        // One block for the stage's row maxima and the next stage's scores, so that the
+        // QK MFMAs of stage s+1 overlap the cross-lane max of stage s.  (On the last stage
+        // the scores are formed from the idle K slot and discarded.)
+        float mt[QB];
+        bool need = false;
 #pragma unroll
-            for (int e = 1; e < 8; ++e) mt = fmaxf(mt, sv[e]);
-            mt = wave_max_across_groups(mt);
-            if (mt > m[qb] + kRescaleSlack) {
-                const float corr = __builtin_amdgcn_exp2f(m[qb] - mt);  // 0 while m is -inf
+        for (int qb = 0; qb < QB; ++qb) {
+            float x = sv[qb][0];
+#pragma unroll
+            for (int e = 1; e < 8; ++e) x = fmaxf(x, sv[qb][e]);
+            mt[qb] = wave_max_across_groups(x);
+            need = need || mt[qb] > m[qb] + kRescaleSlack;
+        }
+        const Scores nxt = qk(kslot(s + 1));
+
+        // Raise the running max where a score exceeds it by the slack (rare): one
+        // wave-uniform branch; lanes that do not need it scale by 1.
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(need) != 0, 0)) {
+            asm volatile("" ::: "memory");  // keeps the rare rescale a branch (no if-conversion)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                const bool up = mt[qb] > m[qb] + kRescaleSlack;
+                const float corr = up ? __builtin_amdgcn_exp2f(m[qb] - mt[qb]) : 1.0f;  // 0 while m is -inf
                 l[qb] *= corr;
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) acc[qb][dt] *= corr;
-                m[qb] = mt;
+                m[qb] = up ? mt[qb] : m[qb];
             }
+        }
+
+        bf16x8 pb[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
             const float mu = m[qb] == -INFINITY ? 0.0f : m[qb];  // all keys so far masked
             short8v pv;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const __bf16 pr = (__bf16) __builtin_amdgcn_exp2f(sv[e] - mu);
+                const __bf16 pr = (__bf16) __builtin_amdgcn_exp2f(sv[qb][e] - mu);
                 l[qb] += (float) pr;
                 pv[e] = __builtin_bit_cast(short, pr);
             }
@@ -289,6 +342,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
             for (int qb = 0; qb < QB; ++qb)
                 acc[qb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qb], acc[qb][dt], 0, 0, 0);
         }
+        cur = nxt;
     }
 
     // Row totals over the four lane groups; then the output (one split) or the partial.
@@ -424,7 +478,7 @@ int fail(int code, const std::string &msg) {
 
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-int qt_of(int D) { return 16 * qb_of(D) * kWaves; }
+int qt_of(int D) { return 16 * qb_of(D) * nw_of(D); }
 
 // Validates a description and fills the kernel parameters' shape fields and plan.
 int plan_prefill(const esda_prefill_desc *d, PrefillParams *p) {
@@ -506,7 +560,7 @@ size_t workspace_of(const PrefillParams &p, int D) {
 template <int D>
 void launch_prefill(const PrefillParams &p, int stages, hipStream_t st) {
     if (stages & 1)
-        hipLaunchKernelGGL((prefill_kernel<D>), dim3(p.tiles, p.Hkv, p.splits), dim3(64 * kWaves), 0, st, p);
+        hipLaunchKernelGGL((prefill_kernel<D>), dim3(p.tiles, p.Hkv, p.splits), dim3(64 * nw_of(D)), 0, st, p);
     if ((stages & 2) && p.splits > 1) {
         const long long n = (long long) p.Sq * p.Hq * (D / 4);
         hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, p);

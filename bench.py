@@ -323,11 +323,11 @@ def main() -> int:
     return 0
 
 
-def profiled_traffic(workload: str):
-    """HBM bytes per attend launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-    (calibrated against a plain copy), as recorded in profiles/attend_<workload>.md; None
-    when that workload has no profile."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"attend_{workload}.md")
+def profiled_traffic(workload: str, kind: str = "attend"):
+    """HBM bytes per launch of the dominant kernel measured by rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE (calibrated against a plain copy), as recorded in
+    profiles/<kind>_<workload>.md; None when that workload has no profile."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{kind}_{workload}.md")
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
@@ -442,8 +442,8 @@ def bench_prefill(args) -> int:
             "bound": "mfma",
             "kernel": f"prefill_kernel<{D}> (QK and PV on v_mfma_f32_16x16x32_bf16, online softmax)",
             "achieved": round(tf_attend, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tf_attend / PEAK_BF16_TFLOPS, 4), "traffic": profiled_traffic(args.workload),
-            "traffic_source": f"profiles/attend_{args.workload}.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+            "frac": round(tf_attend / PEAK_BF16_TFLOPS, 4), "traffic": profiled_traffic(args.workload, "prefill"),
+            "traffic_source": f"profiles/prefill_{args.workload}.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
             "kernel_us": round(ms_attend * 1e3, 3),
         },
         "cpu_baseline": cpu,
