@@ -7,7 +7,7 @@
 // (ESAttention.mm:195-251) computes the same quantity by online softmax.
 //
 // Kernels
-//   prefill_kernel<D>   grid (query tiles, kv heads, key splits), 8 waves (two per
+//   prefill_kernel<D>   one workgroup per (query tile, kv head, key split), 8 waves (two per
 //                       SIMD), one workgroup per CU; one 16-query block per wave at
 //                       D = 512 and 256, two at D = 128 (nw_of, qb_of).  A
 //                       query tile is 16 * QB * NW query rows of one kv head's GQA group,
@@ -109,8 +109,14 @@ __global__ __launch_bounds__(64 * nw_of(D), 1) void prefill_kernel(PrefillParams
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    const int tile = p.tiles - 1 - (int) blockIdx.x;  // heaviest (latest) tiles first
-    const int kvh = blockIdx.y, split = blockIdx.z;
+    // Workgroup -> (tile, kv head, split): consecutive workgroups go to consecutive XCDs
+    // (dispatch is round-robin over the 8), so the (kv head, split) pair is the fastest
+    // index and the workgroups on one XCD share one K / V stream in its L2; tiles run
+    // heaviest (latest) first.
+    const int combos = p.Hkv * p.splits;
+    const int wg = (int) blockIdx.x;
+    const int tile = p.tiles - 1 - wg / combos;
+    const int kvh = (wg % combos) % p.Hkv, split = (wg % combos) / p.Hkv;
     const long long nrows = (long long) p.Sq * p.Hq;
 
     int tj0, tj1;
@@ -522,7 +528,7 @@ int plan_prefill(const esda_prefill_desc *d, PrefillParams *p) {
     p->scale_log2e = d->scale * 1.4426950408889634f;
     const int QT = qt_of(D);
     const long long tiles = ((long long) d->seq_q * p->G + QT - 1) / QT;
-    if (tiles * d->num_kv_heads > 65535LL * 64)
+    if (tiles * d->num_kv_heads > (1LL << 24))
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: too many query tiles");
     p->tiles = (int) tiles;
     // The widest key range of any tile (the last one under a causal mask).
@@ -545,7 +551,8 @@ int plan_prefill(const esda_prefill_desc *d, PrefillParams *p) {
     }
     if (kps <= 0) kps = kStageKeys;
     const long long splits = (maxn + kps - 1) / kps;
-    if (splits > 65535) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: too many key splits");
+    if (splits > 65535 || tiles * d->num_kv_heads * splits > INT_MAX)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: too many key splits");
     p->kps = kps;
     p->splits = (int) std::max<long long>(1, splits);
     return ESDA_OK;
@@ -560,7 +567,7 @@ size_t workspace_of(const PrefillParams &p, int D) {
 template <int D>
 void launch_prefill(const PrefillParams &p, int stages, hipStream_t st) {
     if (stages & 1)
-        hipLaunchKernelGGL((prefill_kernel<D>), dim3(p.tiles, p.Hkv, p.splits), dim3(64 * nw_of(D)), 0, st, p);
+        hipLaunchKernelGGL((prefill_kernel<D>), dim3(p.tiles * p.Hkv * p.splits), dim3(64 * nw_of(D)), 0, st, p);
     if ((stages & 2) && p.splits > 1) {
         const long long n = (long long) p.Sq * p.Hq * (D / 4);
         hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, p);
