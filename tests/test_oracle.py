@@ -18,6 +18,13 @@ The reference holds no attention goldens (its fixtures are gitignored and need t
   rope inv_freq      ESPrimitivesTests.mm:130-139, 191-210 (zero tail, full rotation)
   rms norm           ESPrimitivesTests.mm:93-116 (unit weight, weightless [2,2,2,2])
   raw-K decode       HF apply_rotary_pos_emb + rms norm composition feeding decode_f64
+  quantize_rows      quantisation bounds, ties away from zero, constant rows, endpoints
+  raw q8 decode      equals the raw-K decode on rows q8 represents exactly
+  prefill_f64        HF eager_attention_forward with HF masks over a query chunk; every
+                     row equals decode_f64 at its position; closed forms
+  raw_prefill_kv     torch bf16 ops with HF rotate_half (two bf16 steps at most)
+  ES primitives      the reference's own ESPrimitivesTests.mm assertions, transcribed into
+                     tests/golden/es_primitives.json
 
 Planted-mistake tests (orc_set_fault) show that a plausible bug in the oracle is
 caught by at least one pin.
@@ -638,3 +645,45 @@ def test_raw_prefill_kv_matches_torch_bf16_ops(D, partial):
     k0 = orc.to_bf16(orc.from_bf16(raw[:, 0]) / np.sqrt((orc.from_bf16(raw[:, 0]) ** 2).mean(-1, keepdims=True) + 1e-6)
                      * orc.from_bf16(kw))
     assert np.mean(k[:, 0] == k0) > 0.99 and np.mean(k[:, 100, :64] != k0[:, :64]) > 0.5
+
+
+# ------------------------------------------- the reference's own primitive test cases
+
+def _golden():
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "es_primitives.json")) as f:
+        return json.load(f)["cases"]
+
+
+def test_golden_es_primitives():
+    """The assertions of the reference's ESPrimitivesTests.mm for the primitives on this path
+    (tests/golden/es_primitives.json), evaluated on the oracle."""
+    g = _golden()
+    c = g["rms_norm_weightless"]
+    y = orc.from_bf16(orc.rms_norm_rows(orc.to_bf16(np.array([c["x"]], np.float32)), None, c["eps"]))
+    assert np.abs(y[0] - np.array(c["expect"])).max() <= c["atol"]
+    c = g["rms_norm_unit_weight_mean_square"]
+    y = orc.from_bf16(orc.rms_norm_rows(orc.to_bf16(np.array([c["x"]], np.float32)),
+                                        orc.to_bf16(np.array(c["weight"], np.float32)), c["eps"]))
+    assert abs(float(np.mean(y.astype(np.float64) ** 2)) - c["expect_mean_square"]) <= c["atol"]
+    c = g["repeat_kv_order"]
+    # GQA kv-major: query head h reads kv head h // n_rep (the oracle's mapping, seen through
+    # decode_f64 with one visible row per kv head whose V row is the head's value)
+    n_rep, kv = c["n_rep"], c["kv_heads"]
+    step = orc.Step(B=1, Hq=len(kv) * n_rep, Hkv=len(kv), D=8, cap=1, scale=1.0)
+    v = orc.to_bf16(np.repeat(np.array(kv, np.float32)[:, None, None], 8, axis=2))
+    q = orc.to_bf16(np.zeros((1, step.Hq, 8), np.float32))
+    out = orc.decode_f64(step, q, v.reshape(-1), v.reshape(-1), [0])
+    assert list(out[0, :, 0]) == c["expect"]
+    for name in ("local_rope_full_rotation_position_0", "global_prope_zero_tail_position_1"):
+        c = g[name]
+        inv = orc.rope_inv_freq(c["head_dim"], c["theta"], c["partial"])
+        ang = np.concatenate([inv, inv]).astype(np.float64) * c["position"]
+        cos, sin = np.cos(ang), np.sin(ang)
+        lo, hi = c.get("tail_dims", [0, c["head_dim"] // 2])
+        for base in (0, c["head_dim"] // 2):
+            assert np.abs(cos[base + lo:base + hi] - c.get("expect_tail_cos", c.get("expect_cos"))).max() <= c["atol"]
+            assert np.abs(sin[base + lo:base + hi] - c.get("expect_tail_sin", c.get("expect_sin"))).max() <= c["atol"]
+        if "first_dim_min_abs_sin" in c:
+            assert abs(sin[0]) > c["first_dim_min_abs_sin"]
