@@ -9,7 +9,8 @@
 //      live range into a fresh buffer when the write cursor reaches capacity.
 //  decode() is the fused decode step of this library: the prealloc append and the
 //  attention of the new token in one GPU pass (esda_decode), replacing update()
-//  followed by SDPA at ESAttention.mm:105 and :188.
+//  followed by SDPA at ESAttention.mm:105 and :188; prefill() / prefillRaw() append a
+//  chunk and attend it (ESAttention.mm:168-193, 253-332 at seq > 1).
 //  q8 raw-K storage (rawKVQ8: per-row affine u8 rows with an f32 scale and bias,
 //  ESKVCache.mm:506-566), KV snapshots (the reference's safetensors layout), prefix
 //  markers and turn rewind follow the reference (ESKVCache.mm:121-456).  Quantized-KV
