@@ -42,7 +42,7 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 def _die_multi_gpu(n: int) -> None:
     print(json.dumps({"error": f"--gpus {n}: this build measures one GPU only; the decode "
-                      "path shards by sequence / kv head with no exchange (see DESIGN.md)"}))
+                      "path shards by sequence / kv head with no exchange"}))
     sys.exit(2)
 
 
