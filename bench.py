@@ -13,7 +13,7 @@ write + new-row read and write.  `roofline` prices the dominant kernel (the spli
 attend kernel, timed alone with HIP events on the launch stream); `cpu_baseline` times
 the CPU oracle's reference-rounding restatement on the same inputs.
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c2|c1|c3|c5|p512g|p4kg|p512l] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c2|c1|c3|c5|p512g|p4kg|p512l|p4kl] [--no-cpu]
 
 Workload c5 is the full Gemma-4-31B-shaped attention step: 60 layers (every 6th
 global: D=512, Hkv=4, k_eq_v, linear caches; the rest local: D=256, Hkv=16, window
@@ -21,11 +21,11 @@ global: D=512, Hkv=4, k_eq_v, linear caches; the rest local: D=256, Hkv=16, wind
 attends in order (one esda_decode per layer, 120 kernels per step, replayed from a HIP
 graph).  It reports total attention us per token step.
 
-Workloads p512g / p4kg / p512l are the prefill side (esda_prefill): a 512-token chunk
-over a 16384-token global cache (the reference's own prefill decomposition shape: d512,
-nKV 4, groups 8, seqQ 512 at 16K, WIDE_HEAD_ATTENTION.md), a fresh 4096-token global
-prefill, and a 512-token chunk of a local layer (D=256, Hkv=16, window 1024 over
-window + chunk keys).  They report TFLOP/s of algorithmic attention FLOPs (4 * D per
+Workloads p512g / p4kg / p512l / p4kl are the prefill side (esda_prefill): a 512-token
+chunk over a 16384-token global cache (the reference's own prefill decomposition shape:
+d512, nKV 4, groups 8, seqQ 512 at 16K, WIDE_HEAD_ATTENTION.md), a fresh 4096-token
+global prefill, a 512-token chunk of a local layer (D=256, Hkv=16, window 1024 over
+window + chunk keys) and a fresh 4096-token local prefill (window 1024).  They report TFLOP/s of algorithmic attention FLOPs (4 * D per
 visible (query head, key) pair) against the bf16 MFMA peak.
 """
 from __future__ import annotations
@@ -70,6 +70,8 @@ PREFILL_WORKLOADS = {
                   name="global-layer prefill chunk: 512 queries over 16384 keys (causal), D=512, GQA 32/4"),
     "p4kg": dict(Hq=32, Hkv=4, D=512, Sq=4096, Sk=4096, q_pos0=0, k_pos0=0, window=0, scale=512 ** -0.5,
                  name="global-layer fresh prefill: 4096 tokens (causal), D=512, GQA 32/4"),
+    "p4kl": dict(Hq=32, Hkv=16, D=256, Sq=4096, Sk=4096, q_pos0=0, k_pos0=0, window=1024, scale=1 / 16,
+                 name="local-layer fresh prefill: 4096 tokens, window 1024, D=256, GQA 32/16"),
     "p512l": dict(Hq=32, Hkv=16, D=256, Sq=512, Sk=1536, q_pos0=15872, k_pos0=15872 + 512 - 1536, window=1024,
                   scale=1 / 16, name="local-layer prefill chunk: 512 queries over window + chunk = 1536 keys, "
                                      "window 1024, D=256, GQA 32/16"),
