@@ -7,15 +7,15 @@
 // (ESAttention.mm:195-251) computes the same quantity by online softmax.
 //
 // Kernels
-//   prefill_kernel<D>   one workgroup per (query tile, kv head, key split), 8 waves (two per
-//                       SIMD), one workgroup per CU; one 16-query block per wave at
-//                       D = 512 and 256, two at D = 128 (nw_of, qb_of).  A
-//                       query tile is 16 * QB * NW query rows of one kv head's GQA group,
+//   prefill_kernel<D, QB>  one workgroup per (query tile, kv head, key split), 8 waves
+//                       (two per SIMD), one workgroup per CU; QB 16-query blocks per wave
+//                       (one at D = 512, one or two at D = 256, two at D = 128).  A
+//                       query tile is 128 QB query rows of one kv head's GQA group,
 //                       ordered position-major (row r: position r / G, group head r % G);
 //                       wave w owns rows 16 QB w .. as QB blocks of 16 -- the MFMA N
-//                       dimension.  The
-//                       tile's visible keys (or one split of them) stream through an
-//                       LDS ring of 32-key stages filled by LDS DMA.  Per stage each
+//                       dimension.  The tile's visible keys (or one split of them)
+//                       stream through an LDS ring of 32-key stages filled by LDS DMA,
+//                       the next stage landing during this one.  Per stage each
 //                       wave forms S^T[32 keys x its queries] over the whole head dim
 //                       with v_mfma_f32_16x16x32_bf16 (K rows from LDS, Q^T held in
 //                       registers), masks boundary stages by position, runs an fp32
@@ -56,6 +56,7 @@ struct PrefillParams {
     float *part_ml;    // [splits][Sq * Hq][2]
     long long q_hs, q_rs, kv_hs, o_rs, o_hs;
     int Hq, Hkv, G, Sq, Sk, q_pos0, k_pos0, window;
+    int qb;                  // 16-query blocks per wave (query tile: 128 qb rows)
     int tiles, splits, kps;  // query tiles per kv head, key splits, keys per split
     float scale_log2e;
 };
@@ -79,13 +80,14 @@ __host__ __device__ inline void tile_keys(const PrefillParams &p, int tile, int 
 // block b holding keys b + NI*q (q < 512/D) at +2D*q; a stage is the K halves then the V
 // halves.  Both the 128-bit row reads (QK A operand) and the transpose reads (PV A
 // operand) are bank-conflict-free in this layout (the decode kernel's measured layout).
-// Waves per workgroup and 16-query blocks per wave.  O^T takes QB * D / 16 accumulator
-// registers per lane beside Q^T's QB * D / 8 and two stages of scores (16 QB), within
-// the 256 registers of two waves per SIMD.  (Measured: at D = 256, four waves of two
-// blocks -- half the LDS reads per MFMA, one wave per SIMD -- ran 6% slower than eight
-// waves of one block; at D = 512 two blocks per wave do not fit without spills.)
-__host__ __device__ constexpr int nw_of(int) { return 8; }
-__host__ __device__ constexpr int qb_of(int D) { return D == 128 ? 2 : 1; }
+// Eight waves per workgroup (two per SIMD) and QB 16-query blocks per wave.  O^T takes
+// QB * D / 16 accumulator registers per lane beside Q^T's QB * D / 8 and 8 QB of scores,
+// within the 256 registers of two waves per SIMD: QB = 1 at D = 512 (two blocks do not
+// fit without spills), 1 or 2 at D = 256 (pick_qb), 2 at D = 128.  (Measured: at D = 256,
+// four waves of two blocks -- one wave per SIMD -- ran 6% slower than eight waves of one
+// block, and forming the next stage's scores during this stage's softmax -- a second set
+// of score registers, forcing one block per wave at D = 256 -- was 5-20% slower.)
+constexpr int kWaves = 8;
 
 template <int D>
 struct PRing {
@@ -97,11 +99,9 @@ struct PRing {
     __host__ __device__ static constexpr int off(int r) { return (r % NI) * kBlk + (r / NI) * 2 * D; }
 };
 
-template <int D>
-__global__ __launch_bounds__(64 * nw_of(D), 1) void prefill_kernel(PrefillParams p) {
+template <int D, int QB>
+__global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p) {
     using R = PRing<D>;
-    constexpr int kWaves = nw_of(D);
-    constexpr int QB = qb_of(D);        // 16-query blocks per wave
     constexpr int QT = 16 * QB * kWaves;  // query rows per tile
     constexpr int KS = D / 32;          // QK k-steps
     constexpr int DT = D / 16;          // PV dim tiles
@@ -164,10 +164,9 @@ __global__ __launch_bounds__(64 * nw_of(D), 1) void prefill_kernel(PrefillParams
     }
 
     // LDS: two K slots then two V slots, each a 32-key stage (two 16-key halves).  Stage
-    // s's K sits in K slot s % 2 and its V in V slot s % 2.  Iteration s forms the scores
-    // of stage s+1 while it runs the softmax and PV of stage s, so K runs one stage ahead
-    // of V: after iteration s's barrier, K(s+2) replaces K(s) (read by iteration s-1) and
-    // V(s+1) replaces V(s-1) (read by iteration s-1); both land during iteration s.
+    // s's K sits in K slot s % 2 and its V in V slot s % 2.  After iteration s's barrier,
+    // K(s+1) and V(s+1) replace the stage s-1 slots (every wave is done with them); they
+    // land while iteration s computes.
     //
     // DMA: K instruction t of this wave (ii = wave*KPW + t of the stage's 2 NI) fills block
     // b = ii % NI of half hh = ii / NI; lane l reads chunk l % CPR of stage row
@@ -245,18 +244,17 @@ __global__ __launch_bounds__(64 * nw_of(D), 1) void prefill_kernel(PrefillParams
 
     issue(kvb, 0, kslot(0));
     issue(vvb, 0, vslot(0));
-    if (nst > 1) issue(kvb, 1, kslot(1));
-    ESDA_WAIT_VM(0);
-    lds_barrier();
-    Scores cur = qk(kslot(0));
 
     for (int s = 0; s < nst; ++s) {
-        // K(s+1) and V(s) landed (this wave's loads; the barrier covers the other waves')
-        // and every wave is done with iteration s-1
+        // Stage s landed (this wave's loads; the barrier covers the other waves') and every
+        // wave is done with iteration s-1
         ESDA_WAIT_VM(0);
         lds_barrier();
-        if (s + 2 < nst) issue(kvb, s + 2, kslot(s));
-        if (s + 1 < nst) issue(vvb, s + 1, vslot(s + 1));
+        if (s + 1 < nst) {
+            issue(kvb, s + 1, kslot(s + 1));
+            issue(vvb, s + 1, vslot(s + 1));
+        }
+        const Scores cur = qk(kslot(s));
         const unsigned char *vb = vslot(s);
         const int jb = j0 + s * kStageKeys;
 
@@ -290,9 +288,7 @@ __global__ __launch_bounds__(64 * nw_of(D), 1) void prefill_kernel(PrefillParams
             }
         }
 
-        // One block for the stage's row maxima and the next stage's scores, so that the
-        // QK MFMAs of stage s+1 overlap the cross-lane max of stage s.  (On the last stage
-        // the scores are formed from the idle K slot and discarded.)
+        // Row maxima of the stage.
         float mt[QB];
         bool need = false;
 #pragma unroll
@@ -303,7 +299,6 @@ __global__ __launch_bounds__(64 * nw_of(D), 1) void prefill_kernel(PrefillParams
             mt[qb] = wave_max_across_groups(x);
             need = need || mt[qb] > m[qb] + kRescaleSlack;
         }
-        const Scores nxt = qk(kslot(s + 1));
 
         // Raise the running max where a score exceeds it by the slack (rare): one
         // wave-uniform branch; lanes that do not need it scale by 1.
@@ -348,7 +343,6 @@ __global__ __launch_bounds__(64 * nw_of(D), 1) void prefill_kernel(PrefillParams
             for (int qb = 0; qb < QB; ++qb)
                 acc[qb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qb], acc[qb][dt], 0, 0, 0);
         }
-        cur = nxt;
     }
 
     // Row totals over the four lane groups; then the output (one split) or the partial.
@@ -484,7 +478,15 @@ int fail(int code, const std::string &msg) {
 
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-int qt_of(int D) { return 16 * qb_of(D) * nw_of(D); }
+// 16-query blocks per wave: two where they fit the registers (D <= 256), except at
+// D = 256 when the two-block tiles would leave CUs idle without key splits -- a split's
+// partials cost 4 D bytes per query row written and read again.
+int pick_qb(int D, long long rows, int Hkv) {
+    if (D == 512) return 1;
+    if (D == 128) return 2;
+    const long long tiles2 = (rows + 16 * 2 * kWaves - 1) / (16 * 2 * kWaves);
+    return tiles2 * Hkv >= kTargetGroups ? 2 : 1;
+}
 
 // Validates a description and fills the kernel parameters' shape fields and plan.
 int plan_prefill(const esda_prefill_desc *d, PrefillParams *p) {
@@ -526,7 +528,8 @@ int plan_prefill(const esda_prefill_desc *d, PrefillParams *p) {
     p->o_rs = d->out_row_stride;
     p->o_hs = d->out_head_stride;
     p->scale_log2e = d->scale * 1.4426950408889634f;
-    const int QT = qt_of(D);
+    p->qb = pick_qb(D, (long long) d->seq_q * p->G, d->num_kv_heads);
+    const int QT = 16 * p->qb * kWaves;
     const long long tiles = ((long long) d->seq_q * p->G + QT - 1) / QT;
     if (tiles * d->num_kv_heads > (1LL << 24))
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: too many query tiles");
@@ -566,8 +569,17 @@ size_t workspace_of(const PrefillParams &p, int D) {
 
 template <int D>
 void launch_prefill(const PrefillParams &p, int stages, hipStream_t st) {
-    if (stages & 1)
-        hipLaunchKernelGGL((prefill_kernel<D>), dim3(p.tiles * p.Hkv * p.splits), dim3(64 * nw_of(D)), 0, st, p);
+    if (stages & 1) {
+        const dim3 grid(p.tiles * p.Hkv * p.splits), block(64 * kWaves);
+        if constexpr (D == 512)
+            hipLaunchKernelGGL((prefill_kernel<512, 1>), grid, block, 0, st, p);
+        else if constexpr (D == 128)
+            hipLaunchKernelGGL((prefill_kernel<128, 2>), grid, block, 0, st, p);
+        else if (p.qb == 2)
+            hipLaunchKernelGGL((prefill_kernel<256, 2>), grid, block, 0, st, p);
+        else
+            hipLaunchKernelGGL((prefill_kernel<256, 1>), grid, block, 0, st, p);
+    }
     if ((stages & 2) && p.splits > 1) {
         const long long n = (long long) p.Sq * p.Hq * (D / 4);
         hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, p);

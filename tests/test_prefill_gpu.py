@@ -7,9 +7,10 @@ ESAttention.mm:188, ESGemma4TextModel.mm:68-83, ESAttention.mm:17-22).  Shapes c
 Gemma-4's global (D=512, 8 query heads per kv head) and local (D=256, 2 per kv head,
 sliding window with evicted keys) layers, fresh causal prefill and chunks after a cached
 past, tiles padded past the last query, key splits (automatic, forced, empty), strided
-query / cache / output layouts and a shared K = V buffer.  At the chunked-prefill
-benchmark shape (512 queries over 16384 keys) sampled query rows are checked (query rows
-are independent).  The raw-K reconstruction is compared with the oracle's op-level
+query / cache / output layouts, a shared K = V buffer, and both query-block
+configurations of head dim 256 (one and two 16-query blocks per wave).  At the
+benchmark shapes (512 queries over 16384 keys; 4096 fresh tokens of a sliding layer)
+sampled query rows are checked (query rows are independent).  The raw-K reconstruction is compared with the oracle's op-level
 restatement element by element (at most two bf16 steps apart, on a tiny fraction).
 """
 import numpy as np
@@ -96,6 +97,19 @@ def test_local_sliding_window_with_evicted_keys():
 
 def test_local_fresh_prefill_window_inside_the_chunk():
     run_prefill("local-fresh", Hq=16, Hkv=8, D=256, Sq=700, Sk=700, q_pos0=0, k_pos0=0, window=128, seed=4)
+
+
+def test_local_two_query_blocks_per_wave_with_padded_tile():
+    # 128 kv heads x 2 tiles of 256 rows fill the CUs, so D = 256 runs two query blocks
+    # per wave; the second tile holds one row
+    run_prefill("local-qb2", Hq=128, Hkv=128, D=256, Sq=257, Sk=257, q_pos0=0, k_pos0=0, window=64, seed=12)
+
+
+def test_local_fresh_prefill_benchmark_shape_sampled_rows():
+    """4096 fresh tokens of a sliding layer (window 1024, GQA 32/16): two query blocks
+    per wave, no key splits; rows on tile edges and around the window's reach."""
+    run_prefill("bench-local", Hq=32, Hkv=16, D=256, Sq=4096, Sk=4096, q_pos0=0, k_pos0=0, window=1024, seed=13,
+                rows=[0, 1, 127, 128, 1023, 1024, 1025, 2047, 4095])
 
 
 @pytest.mark.parametrize("split_keys", [32, 96, 4096])
