@@ -62,21 +62,27 @@ __device__ __forceinline__ void lds_barrier() {
 #endif
 }
 
-// One 64-lane x 16-byte LDS DMA (global_load_lds_dwordx4, non-temporal): lane l's 16
-// bytes from `src` land at LDS byte address lds + 16*l.  Issued from inline assembly so
+// One 64-lane x 16-byte LDS DMA (global_load_lds_dwordx4; non-temporal unless NT is
+// false, for data other workgroups read again): lane l's 16 bytes from `src` land at LDS
+// byte address lds + 16*l.  Issued from inline assembly so
 // that the compiler does not track it: the ring accounts for these loads itself
 // (ESDA_WAIT_VM before each stage), and compiler-inserted waits would drain the ring.
 // M0 carries the LDS base; nothing else in these kernels uses M0.
 // (The guard keeps the gfx950 assembly out of hipcc's host pass.)
+template <bool NT = true>
 __device__ __forceinline__ void lds_dma16(const void *src, unsigned lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const unsigned base = __builtin_amdgcn_readfirstlane(lds);  // wave-uniform by construction
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(base) : "memory");
+    if constexpr (NT)
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(base) : "memory");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory");
 #endif
 }
 
 // Same DMA with a wave-uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset:
 // interior stages advance the base with scalar adds and reuse the lane offsets.
+template <bool NT = true>
 __device__ __forceinline__ void lds_dma16_s(const void *sbase, unsigned voff, unsigned lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const uintptr_t a = (uintptr_t) sbase;
@@ -84,7 +90,10 @@ __device__ __forceinline__ void lds_dma16_s(const void *sbase, unsigned voff, un
     const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned) (a >> 32));
     const uint64_t sb = ((uint64_t) hi << 32) | lo;
     const unsigned base = __builtin_amdgcn_readfirstlane(lds);
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sb), "s"(base) : "memory");
+    if constexpr (NT)
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sb), "s"(base) : "memory");
+    else
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb), "s"(base) : "memory");
 #endif
 }
 

@@ -48,6 +48,9 @@ constexpr int kStageKeys = 32;
 constexpr int kBlk = 1056;                 // LDS bytes per DMA block: 1 KB + 32 B pad
 constexpr int kRingBudget = 136 * 1024;    // LDS bytes for the K / V ring
 constexpr int kTargetGroups = 256;         // one workgroup per CU
+// K / V stream loads without the non-temporal hint: the tiles of one kv head read the
+// same keys, and the L2 keeping them for the next tile was measured 2-12% faster.
+constexpr bool kStreamNT = false;
 
 struct PrefillParams {
     const uint16_t *q, *k, *v;
@@ -193,12 +196,12 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
         if (jb + kStageKeys <= j1) {
             const uint16_t *base = head + (size_t) jb * D;
 #pragma unroll
-            for (int t = 0; t < KPW; ++t) lds_dma16_s(base, voff[t], lds_addr(slot) + ldso[t]);
+            for (int t = 0; t < KPW; ++t) lds_dma16_s<kStreamNT>(base, voff[t], lds_addr(slot) + ldso[t]);
         } else {
 #pragma unroll
             for (int t = 0; t < KPW; ++t) {
                 const int j = min(jb + vrow[t], j1 - 1);  // rows past the range repeat the last key
-                lds_dma16(head + (size_t) j * D + (lane % R::CPR) * 8, lds_addr(slot) + ldso[t]);
+                lds_dma16<kStreamNT>(head + (size_t) j * D + (lane % R::CPR) * 8, lds_addr(slot) + ldso[t]);
             }
         }
     };
