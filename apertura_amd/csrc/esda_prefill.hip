@@ -261,17 +261,19 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
         const unsigned char *vb = vslot(s);
         const int jb = j0 + s * kStageKeys;
 
-        // Stage s's scores in log2 units; positions a boundary stage does not show to a
-        // row are -inf.  A stage is fully visible to every row of the tile when its last
-        // key is at or before the tile's first position, its first key is inside the
-        // window of the tile's last position, and it lies inside the split.
+        // Stage s's raw scores q.k; positions a boundary stage does not show to a row are
+        // -inf.  A stage is fully visible to every row of the tile when its last key is at
+        // or before the tile's first position, its first key is inside the window of the
+        // tile's last position, and it lies inside the split.  The softmax scale (times
+        // log2 e, > 0) is applied to the row maxima and inside the exponent's fma.
+        const float c2 = p.scale_log2e;
         float sv[QB][8];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sv[qb][4 * h + r] = cur.s[h][qb][r] * p.scale_log2e;
+                for (int r = 0; r < 4; ++r) sv[qb][4 * h + r] = cur.s[h][qb][r];
         const int ka_first = p.k_pos0 + jb, ka_last = ka_first + kStageKeys - 1;
         const bool full = jb + kStageKeys <= j1 && ka_last <= qa_min &&
                           (p.window == 0 || ka_first > qa_max - p.window);
@@ -291,7 +293,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
             }
         }
 
-        // Row maxima of the stage.
+        // Row maxima of the stage in log2 units (scaling by c2 > 0 keeps the order).
         float mt[QB];
         bool need = false;
 #pragma unroll
@@ -299,7 +301,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
             float x = sv[qb][0];
 #pragma unroll
             for (int e = 1; e < 8; ++e) x = fmaxf(x, sv[qb][e]);
-            mt[qb] = wave_max_across_groups(x);
+            mt[qb] = wave_max_across_groups(x) * c2;
             need = need || mt[qb] > m[qb] + kRescaleSlack;
         }
 
@@ -322,14 +324,14 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
             const float mu = m[qb] == -INFINITY ? 0.0f : m[qb];  // all keys so far masked
-            short8v pv;
+            bf16x8 pv;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const __bf16 pr = (__bf16) __builtin_amdgcn_exp2f(sv[qb][e] - mu);
-                l[qb] += (float) pr;
-                pv[e] = __builtin_bit_cast(short, pr);
-            }
-            pb[qb] = __builtin_bit_cast(bf16x8, pv);
+            for (int e = 0; e < 8; ++e) pv[e] = (__bf16) __builtin_amdgcn_exp2f(__builtin_fmaf(sv[qb][e], c2, -mu));
+            // l += the eight bf16 weights, two per v_dot2_f32_bf16 against (1, 1)
+            const bf16x2 one2 = {(__bf16) 1.0f, (__bf16) 1.0f};
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) l[qb] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pv[e], pv[e + 1]}, one2, l[qb], false);
+            pb[qb] = pv;
         }
 
         // O^T += V^T . P^T: lane (li, lg) gets dim 16dt + li of keys 4lg .. 4lg+3 (first
