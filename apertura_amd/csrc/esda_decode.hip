@@ -998,8 +998,8 @@ struct MergeParams {
 };
 
 constexpr int kMergeThreads = 256;
-constexpr int kMergeDims = 128;     // output dims per merge workgroup (32 lanes x float4)
-constexpr int kMergeGroups = 8;     // split groups reduced in parallel
+constexpr int kMergeDims = 64;      // output dims per merge workgroup (16 lanes x float4)
+constexpr int kMergeGroups = kMergeThreads / (kMergeDims / 4);  // split groups reduced in parallel (16)
 
 __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) {
     for (int o = 32; o > 0; o >>= 1) {
@@ -1017,13 +1017,13 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
 
 // Cross-split merge (ESDecodeAttn.mm:253-273 restated in the log2 domain):
 // M = max_s m_s; O = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
-// One workgroup per (sequence, query head, 128 output dims); 8 split groups x 32 float4
+// One workgroup per (sequence, query head, 64 output dims); 16 split groups x 16 float4
 // lanes.  Each thread issues its partial loads together with the (m, l) loads, so the
 // whole merge is one memory round trip; the per-split weights are then formed from the
-// block-wide max.
-// REGS: splits per thread held in registers (S <= 8 * REGS in one pass): 8, or 16 for
-// the raw-K C4 shape, which packs two kv heads into 128 splits (the larger register set
-// costs the 64-split merges ~0.6 us).
+// block-wide max.  (Against 128 dims x 8 groups, the narrower workgroups and one 8-byte
+// (m, l) load per split took 1.8 us off the C4 step and 1.2 us off C2's.)
+// REGS: splits per thread held in registers (S <= 16 * REGS in one pass): 4, or 16 for
+// more splits (the raw-K C4 shape packs two kv heads into 128 splits).
 
 // The splits that hold partials of pair (b, kvh): their count ns (0 when the sequence
 // is skipped) and the slot of the first, as the attend kernel laid them out.
@@ -1067,7 +1067,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
     size_t pbase;
     const int ns = pair_splits(p, b, kvh, pbase);
     if (ns <= 1) return;  // one workgroup covered the pair and wrote the output itself
-    const int dq = tid & 31, sg = tid >> 5;
+    const int dq = tid % (kMergeDims / 4), sg = tid / (kMergeDims / 4);
     const int d0 = blockIdx.x * kMergeDims + dq * 4;
 
     float mloc = -INFINITY;
@@ -1082,8 +1082,9 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
             if (s < ns) {
                 const size_t ix = (pbase + s) * p.G + g;
                 av[u] = *reinterpret_cast<const f32x4 *>(p.part_acc + ix * p.D + d0);
-                ms[u] = p.part_ml[ix * 2];
-                ls[u] = p.part_ml[ix * 2 + 1];
+                const f32x2 ml = *reinterpret_cast<const f32x2 *>(p.part_ml + ix * 2);
+                ms[u] = ml[0];
+                ls[u] = ml[1];
             } else {
                 av[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 ms[u] = -INFINITY;
@@ -1531,8 +1532,8 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
             hipLaunchKernelGGL(merge_rows_kernel, grid, dim3(kMergeRowsThreads), 0, st, mp);
         } else {
             dim3 grid(d->head_dim / kMergeDims, d->num_q_heads, d->batch);
-            if (pl.S <= kMergeGroups * 8)
-                hipLaunchKernelGGL(merge_kernel<8>, grid, dim3(kMergeThreads), 0, st, mp);
+            if (pl.S <= kMergeGroups * 4)
+                hipLaunchKernelGGL(merge_kernel<4>, grid, dim3(kMergeThreads), 0, st, mp);
             else
                 hipLaunchKernelGGL(merge_kernel<16>, grid, dim3(kMergeThreads), 0, st, mp);
         }
