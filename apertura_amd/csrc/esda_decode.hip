@@ -598,8 +598,9 @@ void attend_kernel(AttendParams p) {
                 const float scl = q8sb[sbslot][0][li], bias = q8sb[sbslot][1][li];
                 const float rinv = __builtin_amdgcn_rsqf(q8_ms(ssbuf, li, scl, bias));
                 const float alpha = scl * rinv, beta = bias * rinv;
-                // the weight factor scale * rinv, its inverse, and bias / scale
-                if (wave == 0 && lg == 0) {
+                // the weight factor scale * rinv, its inverse, and bias / scale (two IEEE
+                // divisions: written by wave 2, whose SIMD has no rotary work)
+                if (wave == 2 && lg == 0) {
                     xr[par][0][li] = alpha;
                     xr[par][1][li] = 1.0f / alpha;
                     xr[par][2][li] = bias / scl;
