@@ -22,7 +22,7 @@ EXPORTS = (
     # include/esda.h
     "esda_decode_workspace_size", "esda_decode", "esda_decode_stages", "esda_decode_status",
     "esda_kv_append", "esda_decode_raw_workspace_size", "esda_decode_raw",
-    "esda_decode_raw_stages", "esda_decode_raw_q8", "esda_decode_raw_q8_stages", "esda_quantize_raw_rows",
+    "esda_decode_raw_stages", "esda_decode_raw_q8", "esda_decode_raw_q8_stages", "esda_quantize_raw_rows", "esda_rope_table",
     "esda_fill_i32", "esda_last_error", "esda_version",
     # include/esda_cache.h
     "esda_cache_create", "esda_cache_destroy", "esda_cache_update", "esda_cache_update_raw",
@@ -85,6 +85,7 @@ class RawArgs(ctypes.Structure):
         ("pos", ctypes.c_void_p), ("kw", ctypes.c_void_p), ("inv_freq", ctypes.c_void_p),
         ("out", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("rope_table", ctypes.c_void_p), ("rope_table_rows", ctypes.c_int32),
     ]
 
 
@@ -96,6 +97,7 @@ class RawQ8Args(ctypes.Structure):
         ("pos", ctypes.c_void_p), ("kw", ctypes.c_void_p), ("inv_freq", ctypes.c_void_p),
         ("out", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("rope_table", ctypes.c_void_p), ("rope_table_rows", ctypes.c_int32),
     ]
 
 
@@ -160,6 +162,7 @@ def lib() -> ctypes.CDLL:
         L.esda_decode_raw_q8_stages.argtypes = [ctypes.POINTER(RawDesc), ctypes.POINTER(RawQ8Args),
                                                 ctypes.c_int, P]
         L.esda_quantize_raw_rows.argtypes = [P, i32, i32, P, i64, P, P, i64, i32, P]
+        L.esda_rope_table.argtypes = [P, i32, P, P]
         L.esda_fill_i32.argtypes = [P, i32, i32, P]
         L.esda_last_error.restype = ctypes.c_char_p
         L.esda_last_error.argtypes = []

@@ -92,6 +92,7 @@ struct AttendParams {
     // raw-K mode only
     const uint16_t *kw;
     const float *inv_freq;
+    const unsigned *rope_tab;  // optional [rows][64] cos/sin pairs (esda_rope_table), row = cache row
     float eps;
     // q8 raw-K mode: u8 rows at q8 (strides as for k_cache, in bytes) and per-row scale /
     // bias at qsc / qbs[b * sb_seq_stride + kv head * sb_head_stride + row]
@@ -112,8 +113,9 @@ struct AttendParams {
 // 32 B pad), sub-row q at +2D*q bytes.  The 32-byte pad (a measured choice: 16 B leaves
 // both the 128-bit row reads and the transpose reads 2-way bank-conflicted on gfx950)
 // makes both read patterns conflict-free with every address a base plus an immediate.
-// EXTRA: LDS bytes the kernel variant needs beside the ring and the score exchange.
-template <int D, bool SHARED, int NW, int EXTRA = 0>
+// EXTRA: LDS bytes the kernel variant needs beside the ring and the score exchange; PSX:
+// LDS bytes it keeps per ring stage beside the rows.
+template <int D, bool SHARED, int NW, int EXTRA = 0, int PSX = 0>
 struct Ring {
     static constexpr int RPI = 512 / D;                     // rows per DMA instruction
     static constexpr int NI = 16 / RPI;                     // DMA instructions per stage
@@ -130,7 +132,7 @@ struct Ring {
     static constexpr int XB = 2 * NW * 64 * 16;             // score-exchange bytes
     // reserve: kernel arguments' spill room (256 B) and the batch prefix scan (int64 per
     // sequence + one per wave)
-    static constexpr int NS_ = (160 * 1024 - XB - 256 - ((kMaxBatch + 1) + NW) * 8 - EXTRA) / SB;
+    static constexpr int NS_ = (160 * 1024 - XB - 256 - ((kMaxBatch + 1) + NW) * 8 - EXTRA) / (SB + PSX);
     static constexpr int NS = NS_ > 16 ? 16 : NS_;          // stages in the ring
     static_assert(DW % 32 == 0 && NI % NW == 0, "wave slices must cover whole MFMA steps");
     static_assert(NS >= 4, "the ring needs at least 4 stages");
@@ -152,11 +154,12 @@ struct Ring {
 constexpr int kRawDim = 512;
 constexpr int kRopePairs = 64;
 constexpr int kTabStride = 68;  // words per cos/sin table row: 64 + 4 (conflict-free 128-bit reads)
-// LDS of the raw-mode exchanges for NW waves: row sums of squares [3][16][NW], the
-// cos/sin tables [2][16][kTabStride], the row factors [2][3][16]; q8 mode adds the row
-// sums [3][16][NW].
-constexpr int raw_extra_lds(int nw, bool q8 = false) {
-    return 3 * 16 * nw * 4 + 2 * 16 * kTabStride * 4 + 2 * 3 * 16 * 4 + (q8 ? 3 * 16 * nw * 4 : 0);
+// LDS of the raw-mode exchanges for NW waves, in this order: row sums of squares
+// [3][16][NW], the row factors [2][3][16], (q8) the row sums [3][16][NW], and the cos/sin
+// tables [2][16][kTabStride] computed in the kernel (absent when a precomputed table is
+// DMA'd per ring stage instead).
+constexpr int raw_extra_lds(int nw, bool q8 = false, bool tab = false) {
+    return 3 * 16 * nw * 4 + 2 * 3 * 16 * 4 + (q8 ? 3 * 16 * nw * 4 : 0) + (tab ? 0 : 2 * 16 * kTabStride * 4);
 }
 // q8 raw-K mode: u8 stages are widened into bf16 staging slots laid out as the D = 512
 // ring (16 rows of 1056-byte blocks), four deep; per-row scale / bias ride beside each
@@ -164,8 +167,8 @@ constexpr int raw_extra_lds(int nw, bool q8 = false) {
 constexpr int kQ8Stage = 16 * 1056;
 constexpr int kQ8Slots = 4;
 constexpr int kQ8SbStages = 16;
-constexpr int q8_extra_lds(int nw) {
-    return raw_extra_lds(nw, true) + kQ8Slots * kQ8Stage + kQ8SbStages * 2 * 16 * 4;
+constexpr int q8_extra_lds(int nw, bool tab = false) {
+    return raw_extra_lds(nw, true, tab) + kQ8Slots * kQ8Stage + kQ8SbStages * 2 * 16 * 4;
 }
 
 
@@ -207,7 +210,12 @@ constexpr int q8_extra_lds(int nw) {
 // exactly, hence sum(x^2); K = bf16(rope(fma(q, scale*rinv, bias*rinv) * kw)); V enters
 // as q with the weight P = bf16(e * scale * rinv) and the bias as sum P * bias / scale.
 // The workgroup holding a sequence's new row quantizes it into the cache first.
-template <int D, bool SHARED, int NW, bool RAW, int RPK = 1, bool Q8 = false>
+//
+// TAB (raw mode, two kv heads per workgroup): the cos/sin rows of a stage's positions come
+// from the caller's precomputed table (esda_rope_table: the same sincos_f32 and bf16
+// rounding as publish_tab) by one 256-byte LDS DMA per row beside the stage's rows, into a
+// table area per ring slot, instead of being computed in every step.
+template <int D, bool SHARED, int NW, bool RAW, int RPK = 1, bool Q8 = false, bool TAB = false>
 // The LDS ring allows one workgroup per CU, i.e. NW/4 waves per SIMD: telling the
 // compiler so lifts the register limit it would otherwise keep for higher occupancy,
 // which it meets by serialising LDS reads behind their uses.
@@ -216,12 +224,16 @@ void attend_kernel(AttendParams p) {
     static_assert(!RAW || (D == kRawDim && SHARED && (NW == 4 || NW == 8)), "raw mode: one 512-dim stream, 4 or 8 waves");
     static_assert(RPK == 1 || (RAW && RPK == 2), "kv-head packing is a runtime choice outside raw mode");
     static_assert(!Q8 || (RAW && NW == 8), "q8 mode is raw mode with 8 waves");
+    static_assert(!TAB || (RAW && RPK == 2 && (16 / RPK) % NW == 0), "table rows: raw mode, two kv heads");
+    // bytes of one ring slot's cos/sin rows (TAB)
+    constexpr int TABB = TAB ? (16 / RPK) * kTabStride * 4 : 0;
     // R: the compute layout of a stage (and, outside q8 mode, the DMA ring); RD: the DMA ring.
-    using R = Ring<D, SHARED, NW, RAW && !Q8 ? raw_extra_lds(NW) : 0>;
-    using RD = std::conditional_t<Q8, Ring<256, true, NW, q8_extra_lds(NW)>, R>;
+    using R = Ring<D, SHARED, NW, RAW && !Q8 ? raw_extra_lds(NW, false, TAB) : 0, RAW && !Q8 ? TABB : 0>;
+    using RD = std::conditional_t<Q8, Ring<256, true, NW, q8_extra_lds(NW, TAB), TABB>, R>;
     constexpr int NS = RD::NS, DW = R::DW, KKW = R::KKW, DTW = R::DTW;
-    // DMA instructions per wave per stage (q8: the u8 rows plus one scale / bias piece)
-    constexpr int DPW = Q8 ? RD::DPT + 1 : RD::DPW;
+    // DMA instructions per wave per stage (q8: the u8 rows plus one scale / bias piece;
+    // TAB: plus its share of the cos/sin rows)
+    constexpr int DPW = (Q8 ? RD::DPT + 1 : RD::DPW) + (TAB ? (16 / RPK) / NW : 0);
     // Stages between the one being accumulated and the newest one that must have landed.
     constexpr int AHEAD = Q8 ? 3 : RAW ? 2 : 1;
     static_assert(NS >= AHEAD + 3, "the ring must hold the look-ahead stages and one in flight");
@@ -252,18 +264,21 @@ void attend_kernel(AttendParams p) {
         else return r15;
     };
     __shared__ f32x4 xch[2][NW][64];  // partial scores, double-buffered by stage parity
-    // Raw mode: per-row partial sums of squares xss[stage % 3][row][wave], the cos/sin
-    // table xtab[stage % 2][row][pair] (bf16 cos in the low half, sin in the high half)
-    // and the per-row norm factors xr.
-    __shared__ __attribute__((aligned(16))) unsigned char rawlds[RAW ? raw_extra_lds(NW, Q8) : 16];
+    // Raw mode: per-row partial sums of squares xss[stage % 3][row][wave], the per-row
+    // norm factors xr, and the cos/sin table xtab[stage % 2][row][pair] (bf16 cos in the low
+    // half, sin in the high half) when the kernel computes it.
+    __shared__ __attribute__((aligned(16))) unsigned char rawlds[RAW ? raw_extra_lds(NW, Q8, TAB) : 16];
     auto *xss = reinterpret_cast<float (*)[16][NW]>(rawlds);
-    auto *xtab = reinterpret_cast<unsigned (*)[16][kTabStride]>(rawlds + 3 * 16 * NW * 4);
     // xr[stage % 2][0][row] = the weight factor (rinv; q8: scale * rinv), [1] its inverse,
     // [2] (q8) bias / scale
-    auto *xr = reinterpret_cast<float (*)[3][16]>(rawlds + 3 * 16 * NW * 4 + 2 * 16 * kTabStride * 4);
+    auto *xr = reinterpret_cast<float (*)[3][16]>(rawlds + 3 * 16 * NW * 4);
     // q8: row sums of q [stage % 3][row][wave]
-    auto *xsq = reinterpret_cast<float (*)[16][NW]>(rawlds + 3 * 16 * NW * 4 + 2 * 16 * kTabStride * 4 +
-                                                    2 * 3 * 16 * 4);
+    auto *xsq = reinterpret_cast<float (*)[16][NW]>(rawlds + 3 * 16 * NW * 4 + 2 * 3 * 16 * 4);
+    auto *xtab = reinterpret_cast<unsigned (*)[16][kTabStride]>(rawlds + 3 * 16 * NW * 4 + 2 * 3 * 16 * 4 +
+                                                                (Q8 ? 3 * 16 * NW * 4 : 0));
+    // TAB: the cos/sin rows of the stage in ring slot u, rtab[u][row][pair] (rows past 64
+    // pairs are padding for conflict-free reads)
+    __shared__ __attribute__((aligned(16))) unsigned rtab[TAB ? NS : 1][TAB ? 16 / RPK : 1][kTabStride];
     // q8: bf16 staging slots and the per-stage scale / bias rows
     __shared__ __attribute__((aligned(16))) unsigned char q8stg[Q8 ? kQ8Slots * kQ8Stage : 16];
     __shared__ __attribute__((aligned(16))) float q8sb[Q8 ? kQ8SbStages : 1][2][16];
@@ -403,6 +418,16 @@ void attend_kernel(AttendParams p) {
     // DMA of stage st into ring buffer `buf` (ring slot `slot`).
     auto dma = [&](int st, unsigned char *buf, int slot) {
         const int jst = j0 + st * RPP;
+        if constexpr (TAB) {
+            // cos/sin rows of the stage's positions (cache rows; rows past the range repeat
+            // the last one): wave w loads rows w, w + NW, .., 64 lanes x 4 bytes each
+#pragma unroll
+            for (int k = 0; k < (16 / RPK) / NW; ++k) {
+                const int row = wave + NW * k;
+                const int j = jst + row, jj = j < j1 ? j : j1 - 1;
+                lds_dma4(p.rope_tab + (size_t) (sv.first + jj) * 64 + lane, lds_addr(&rtab[slot][row][0]));
+            }
+        }
         if constexpr (Q8) {
             // scale / bias of the stage's rows: wave w loads the scales (w < 4) or biases of
             // stage rows 4(w % 4) .. +3, one row per lane
@@ -632,7 +657,9 @@ void attend_kernel(AttendParams p) {
             if (wave < 2) {
                 // chunk `wave` (k-step 0) holds dims d = 32*wave + 8lg + e < 64; chunk wave + 8
                 // (k-step KP) their rotary partners.
-                const unsigned *tb = &xtab[tabbuf][li & (TR - 1)][32 * wave + 8 * lg];
+                const unsigned *tb;
+                if constexpr (TAB) tb = &rtab[sbslot][li & (TR - 1)][32 * wave + 8 * lg];
+                else tb = &xtab[tabbuf][li & (TR - 1)][32 * wave + 8 * lg];
                 const u32x4 t0 = *reinterpret_cast<const u32x4 *>(tb);
                 const u32x4 t1 = *reinterpret_cast<const u32x4 *>(tb + 4);
     #pragma unroll
@@ -684,11 +711,11 @@ void attend_kernel(AttendParams p) {
         }
         load_raw(cbuf(0, std::integral_constant<int, 0>{}));
         publish_ss(0);
-        publish_tab(0, 0);
+        if constexpr (!TAB) publish_tab(0, 0);
         if (nst > 1) {
             load_raw(cbuf(1, std::integral_constant<int, 1>{}));
             publish_ss(1);
-            publish_tab(1, 1);
+            if constexpr (!TAB) publish_tab(1, 1);
         }
         lds_barrier();
         // scores of stage 0 (its raw operand is read again; araw keeps stage 1's)
@@ -743,7 +770,7 @@ void attend_kernel(AttendParams p) {
             qk_raw((st + 1) % 3, (st + 1) & 1, (st + 1) & 1, (u + 1) % NS);
             load_raw(cbuf(st + 2, std::integral_constant<int, (u + 2) % NS>{}));
             publish_ss((st + 2) % 3);
-            publish_tab(st + 2, st & 1);
+            if constexpr (!TAB) publish_tab(st + 2, st & 1);
         } else {
             qk_partial(ring(std::integral_constant<int, (u + 1) % NS>{}), (st + 1) & 1);
         }
@@ -1237,6 +1264,17 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t *src,
     }
 }
 
+// Rotary cos/sin table for raw-K decode: entry (t, f) = bf16 cos | bf16 sin << 16 of the
+// fp32 angle t * inv_freq[f], t < rows, f < 64 -- publish_tab's arithmetic.
+__global__ __launch_bounds__(256) void rope_table_kernel(const float *inv_freq, long long n, unsigned *tab) {
+    const long long i = (long long) blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int t = (int) (i / kRopePairs), f = (int) (i % kRopePairs);
+    float s, c;
+    sincos_f32((float) t * inv_freq[f], s, c);
+    tab[i] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{c, s}, bf16x2));
+}
+
 __global__ void fill_i32_kernel(int *dst, int value, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) dst[i] = value;
@@ -1424,10 +1462,10 @@ constexpr int ring_waves() { return D == 256 ? 8 : 4; }
 // reconstruction work.
 constexpr int kRawWaves = 8;
 
-template <int D, bool SHARED, bool RAW = false, int RPK = 1, bool Q8 = false>
+template <int D, bool SHARED, bool RAW = false, int RPK = 1, bool Q8 = false, bool TAB = false>
 hipError_t launch_attend(const AttendParams &ap, dim3 grid, hipStream_t st) {
     constexpr int NW = RAW ? kRawWaves : ring_waves<D>();
-    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW, RPK, Q8>), grid, dim3(64 * NW), 0, st, ap);
+    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW, RPK, Q8, TAB>), grid, dim3(64 * NW), 0, st, ap);
     return hipGetLastError();
 }
 
@@ -1496,9 +1534,13 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         const dim3 grid = pl.balanced ? dim3(pl.W) : dim3(pl.S, d->num_kv_heads / pl.pk, d->batch);
         hipError_t e;
         if (mode == 0) e = dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
-        else if (mode == 1) e = pl.pk == 2 ? launch_attend<kRawDim, true, true, 2>(ap, grid, st)
+        // a precomputed cos/sin table is read where two kv heads share a workgroup; the
+        // one-kv-head form computes its table (its 16-row stages would need twice the rows)
+        else if (mode == 1) e = pl.pk == 2 ? (ap.rope_tab ? launch_attend<kRawDim, true, true, 2, false, true>(ap, grid, st)
+                                                          : launch_attend<kRawDim, true, true, 2>(ap, grid, st))
                                            : launch_attend<kRawDim, true, true, 1>(ap, grid, st);
-        else e = pl.pk == 2 ? launch_attend<kRawDim, true, true, 2, true>(ap, grid, st)
+        else e = pl.pk == 2 ? (ap.rope_tab ? launch_attend<kRawDim, true, true, 2, true, true>(ap, grid, st)
+                                           : launch_attend<kRawDim, true, true, 2, true>(ap, grid, st))
                             : launch_attend<kRawDim, true, true, 1, true>(ap, grid, st);
         if (e != hipSuccess) return hip_fail(e, "attend_kernel launch");
     }
@@ -1626,6 +1668,8 @@ int esda_decode_raw_stages(const esda_raw_desc *desc, const esda_raw_args *a, in
     if (!aligned16(a->q) || (a->k_new && !aligned16(a->k_new)) || !aligned16(a->raw_cache) ||
         !aligned16(a->kw) || !aligned16(a->inv_freq) || !aligned16(a->out))
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw: tensors must be 16-byte aligned");
+    if (a->rope_table && (a->rope_table_rows < d.cap || !aligned16(a->rope_table)))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw: rope_table needs >= cap rows, 16-byte aligned");
     if (!a->workspace || a->workspace_bytes < pl.bytes || !aligned16(a->workspace))
         return fail(ESDA_ERR_WORKSPACE, "esda_decode_raw: workspace missing or smaller than esda_decode_raw_workspace_size");
     if ((stages & (ESDA_STAGE_ATTEND | ESDA_STAGE_MERGE)) == 0 || (stages & ~3))
@@ -1642,6 +1686,7 @@ int esda_decode_raw_stages(const esda_raw_desc *desc, const esda_raw_args *a, in
     ap.row_base = nullptr;
     ap.kw = static_cast<const uint16_t *>(a->kw);
     ap.inv_freq = a->inv_freq;
+    ap.rope_tab = static_cast<const unsigned *>(a->rope_table);
     ap.eps = desc->eps;
     return run_stages(&d, pl, ap, static_cast<uint16_t *>(a->out), a->workspace, stages, 1,
                       reinterpret_cast<hipStream_t>(stream));
@@ -1667,6 +1712,8 @@ int esda_decode_raw_q8_stages(const esda_raw_desc *desc, const esda_raw_q8_args 
         !aligned16(a->kw) || !aligned16(a->inv_freq) || !aligned16(a->out) ||
         (reinterpret_cast<uintptr_t>(a->scale) & 3u) || (reinterpret_cast<uintptr_t>(a->bias) & 3u))
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_q8: tensors must be 16-byte aligned (scale / bias 4)");
+    if (a->rope_table && (a->rope_table_rows < d.cap || !aligned16(a->rope_table)))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_q8: rope_table needs >= cap rows, 16-byte aligned");
     if (a->sb_head_stride < d.cap || a->sb_seq_stride < (int64_t) d.num_kv_heads * a->sb_head_stride)
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_raw_q8: scale / bias strides smaller than the cache");
     if (!a->workspace || a->workspace_bytes < pl.bytes || !aligned16(a->workspace))
@@ -1690,6 +1737,7 @@ int esda_decode_raw_q8_stages(const esda_raw_desc *desc, const esda_raw_q8_args 
     ap.row_base = nullptr;
     ap.kw = static_cast<const uint16_t *>(a->kw);
     ap.inv_freq = a->inv_freq;
+    ap.rope_tab = static_cast<const unsigned *>(a->rope_table);
     ap.eps = desc->eps;
     return run_stages(&d, pl, ap, static_cast<uint16_t *>(a->out), a->workspace, stages, 2,
                       reinterpret_cast<hipStream_t>(stream));
@@ -1697,6 +1745,21 @@ int esda_decode_raw_q8_stages(const esda_raw_desc *desc, const esda_raw_q8_args 
 
 int esda_decode_raw_q8(const esda_raw_desc *desc, const esda_raw_q8_args *args, void *stream) {
     return esda_decode_raw_q8_stages(desc, args, ESDA_STAGE_ATTEND | ESDA_STAGE_MERGE, stream);
+}
+
+int esda_rope_table(const float *inv_freq, int32_t rows, void *table, void *stream) {
+    if (!inv_freq || !table) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_rope_table: null pointer");
+    if (rows < 0) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_rope_table: rows must be >= 0");
+    if (!aligned16(table) || (reinterpret_cast<uintptr_t>(inv_freq) & 3u))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_rope_table: table 16-byte, inv_freq 4-byte aligned");
+    int rc = check_device();
+    if (rc) return rc;
+    const long long n = (long long) rows * kRopePairs;
+    if (n == 0) return ESDA_OK;
+    hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), inv_freq, n, static_cast<unsigned *>(table));
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? ESDA_OK : hip_fail(e, "rope_table_kernel launch");
 }
 
 int esda_quantize_raw_rows(const void *src, int32_t kv_heads, int32_t n_rows, void *q8, int64_t q_head_stride,

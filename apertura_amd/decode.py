@@ -213,12 +213,33 @@ def new_raw_workspace(step: RawStep, device) -> torch.Tensor:
     return torch.zeros(raw_workspace_bytes(step), dtype=torch.uint8, device=device)
 
 
+def rope_table(inv_freq: torch.Tensor, rows: int, stream=None) -> torch.Tensor:
+    """The raw-K rotary table (esda_rope_table): int32 [rows, 64], entry (t, d) = bf16
+    cos | bf16 sin << 16 of float(t) * inv_freq[d] -- what the raw-K kernels otherwise
+    compute per step."""
+    if inv_freq.dtype != torch.float32 or inv_freq.numel() < 64 or not inv_freq.is_contiguous():
+        raise ValueError("inv_freq must be contiguous f32 [>= 64]")
+    tab = torch.empty((rows, 64), dtype=torch.int32, device=inv_freq.device)
+    check(lib().esda_rope_table(_dev_ptr(inv_freq), rows, _dev_ptr(tab), _stream_ptr(stream)))
+    return tab
+
+
+def _table(tab: torch.Tensor | None):
+    """(pointer, rows) of an optional rope_table."""
+    if tab is None:
+        return None, 0
+    if tab.dtype != torch.int32 or tab.dim() != 2 or tab.shape[1] != 64 or not tab.is_contiguous():
+        raise ValueError("rope_table must be contiguous int32 [rows, 64] (rope_table())")
+    return _dev_ptr(tab), tab.shape[0]
+
+
 def decode_raw(step: RawStep, q: torch.Tensor, k_new: torch.Tensor | None, raw_cache: torch.Tensor,
                pos: torch.Tensor, kw: torch.Tensor, inv_freq: torch.Tensor,
                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None, stream=None,
-               stages: int = STAGE_ATTEND | STAGE_MERGE) -> torch.Tensor:
+               stages: int = STAGE_ATTEND | STAGE_MERGE, rope_table: torch.Tensor | None = None) -> torch.Tensor:
     """Raw-K decode step: write k_new (raw rows, or None) at row pos[b], then attend rows
-    0 .. pos[b]; returns out [B, Hq, 512] bf16."""
+    0 .. pos[b]; returns out [B, Hq, 512] bf16.  rope_table: an optional precomputed
+    rotary table (rope_table(), >= cap rows), bit-identical to the kernel's own."""
     bf = torch.bfloat16
     if q.shape != (step.batch, step.num_q_heads, 512) or not q.is_contiguous():
         raise ValueError("q must be contiguous [B, Hq, 512]")
@@ -234,7 +255,7 @@ def decode_raw(step: RawStep, q: torch.Tensor, k_new: torch.Tensor | None, raw_c
         workspace = new_raw_workspace(step, q.device)
     args = RawArgs(_dev_ptr(q, bf), _dev_ptr(k_new, bf), _dev_ptr(raw_cache, bf), _dev_ptr(pos),
                    _dev_ptr(kw, bf), _dev_ptr(inv_freq), _dev_ptr(out, bf), _dev_ptr(workspace),
-                   workspace.numel() * workspace.element_size())
+                   workspace.numel() * workspace.element_size(), *_table(rope_table))
     d = step.desc()
     check(lib().esda_decode_raw_stages(ctypes.byref(d), ctypes.byref(args), stages, _stream_ptr(stream)))
     return out
@@ -244,18 +265,18 @@ class RawCall:
     """decode_raw with its arguments marshalled once (see DecodeCall)."""
 
     def __init__(self, step: RawStep, q, k_new, raw_cache, pos, kw, inv_freq, out=None, workspace=None,
-                 stages: int = STAGE_ATTEND | STAGE_MERGE):
+                 stages: int = STAGE_ATTEND | STAGE_MERGE, rope_table=None):
         if out is None:
             out = torch.empty_like(q)
         if workspace is None:
             workspace = new_raw_workspace(step, q.device)
-        self._keep = (q, k_new, raw_cache, pos, kw, inv_freq, out, workspace)
+        self._keep = (q, k_new, raw_cache, pos, kw, inv_freq, out, workspace, rope_table)
         self.step, self.out, self.workspace, self.stages = step, out, workspace, stages
         bf = torch.bfloat16
         self._desc = step.desc()
         self._args = RawArgs(_dev_ptr(q, bf), _dev_ptr(k_new, bf), _dev_ptr(raw_cache, bf), _dev_ptr(pos),
                              _dev_ptr(kw, bf), _dev_ptr(inv_freq), _dev_ptr(out, bf), _dev_ptr(workspace),
-                             workspace.numel() * workspace.element_size())
+                             workspace.numel() * workspace.element_size(), *_table(rope_table))
         self._fn = lib().esda_decode_raw_stages
         self._pd, self._pa = ctypes.byref(self._desc), ctypes.byref(self._args)
 
@@ -284,7 +305,8 @@ def quantize_raw_rows(src: torch.Tensor, q8: torch.Tensor, scale: torch.Tensor, 
                                        _stream_ptr(stream)))
 
 
-def _q8_args(step: RawStep, q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace) -> RawQ8Args:
+def _q8_args(step: RawStep, q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace,
+             rope_table=None) -> RawQ8Args:
     bf = torch.bfloat16
     if q.shape != (step.batch, step.num_q_heads, 512) or not q.is_contiguous():
         raise ValueError("q must be contiguous [B, Hq, 512]")
@@ -299,7 +321,8 @@ def _q8_args(step: RawStep, q, k_new, q8, scale, bias, pos, kw, inv_freq, out, w
         raise ValueError("pos must be int32 [B]")
     return RawQ8Args(_dev_ptr(q, bf), _dev_ptr(k_new, bf), _dev_ptr(q8), _dev_ptr(scale), _dev_ptr(bias),
                      scale.stride(0), scale.stride(1), _dev_ptr(pos), _dev_ptr(kw, bf), _dev_ptr(inv_freq),
-                     _dev_ptr(out, bf), _dev_ptr(workspace), workspace.numel() * workspace.element_size())
+                     _dev_ptr(out, bf), _dev_ptr(workspace), workspace.numel() * workspace.element_size(),
+                     *_table(rope_table))
 
 
 def q8_step_for(q8: torch.Tensor, num_q_heads: int, **kw) -> RawStep:
@@ -315,14 +338,14 @@ def decode_raw_q8(step: RawStep, q: torch.Tensor, k_new: torch.Tensor | None, q8
                   scale: torch.Tensor, bias: torch.Tensor, pos: torch.Tensor, kw: torch.Tensor,
                   inv_freq: torch.Tensor, out: torch.Tensor | None = None,
                   workspace: torch.Tensor | None = None, stream=None,
-                  stages: int = STAGE_ATTEND | STAGE_MERGE) -> torch.Tensor:
+                  stages: int = STAGE_ATTEND | STAGE_MERGE, rope_table: torch.Tensor | None = None) -> torch.Tensor:
     """q8 raw-K decode step: quantize k_new (or None) into row pos[b], then attend rows
     0 .. pos[b] of the q8 stream; returns out [B, Hq, 512] bf16."""
     if out is None:
         out = torch.empty_like(q)
     if workspace is None:
         workspace = new_raw_workspace(step, q.device)
-    args = _q8_args(step, q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace)
+    args = _q8_args(step, q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace, rope_table)
     d = step.desc()
     check(lib().esda_decode_raw_q8_stages(ctypes.byref(d), ctypes.byref(args), stages, _stream_ptr(stream)))
     return out
@@ -332,15 +355,15 @@ class RawQ8Call:
     """decode_raw_q8 with its arguments marshalled once (see DecodeCall)."""
 
     def __init__(self, step: RawStep, q, k_new, q8, scale, bias, pos, kw, inv_freq, out=None, workspace=None,
-                 stages: int = STAGE_ATTEND | STAGE_MERGE):
+                 stages: int = STAGE_ATTEND | STAGE_MERGE, rope_table=None):
         if out is None:
             out = torch.empty_like(q)
         if workspace is None:
             workspace = new_raw_workspace(step, q.device)
-        self._keep = (q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace)
+        self._keep = (q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace, rope_table)
         self.step, self.out, self.workspace, self.stages = step, out, workspace, stages
         self._desc = step.desc()
-        self._args = _q8_args(step, q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace)
+        self._args = _q8_args(step, q, k_new, q8, scale, bias, pos, kw, inv_freq, out, workspace, rope_table)
         self._fn = lib().esda_decode_raw_q8_stages
         self._pd, self._pa = ctypes.byref(self._desc), ctypes.byref(self._args)
 

@@ -145,6 +145,10 @@ typedef struct esda_raw_args {
     void *out;               /* [B, Hq, 512] bf16                                      */
     void *workspace;         /* esda_decode_raw_workspace_size bytes; first 256 zeroed once */
     size_t workspace_bytes;
+    const void *rope_table;  /* optional, NULL: computed in the kernel.  [rope_table_rows][64]
+                                u32 from esda_rope_table (cos / sin of row*inv_freq[d]);
+                                read where two kv heads share a workgroup              */
+    int32_t rope_table_rows; /* >= cap when rope_table is set                          */
 } esda_raw_args;
 
 int esda_decode_raw_workspace_size(const esda_raw_desc *desc, size_t *bytes);
@@ -182,6 +186,8 @@ typedef struct esda_raw_q8_args {
     void *out;                 /* [B, Hq, 512] bf16                                       */
     void *workspace;           /* esda_decode_raw_workspace_size bytes; first 256 zeroed once */
     size_t workspace_bytes;
+    const void *rope_table;    /* optional; as in esda_raw_args                           */
+    int32_t rope_table_rows;
 } esda_raw_q8_args;
 
 /* Fused q8 raw-K decode step (quantize-append + rebuild + attend + merge): replaces
@@ -194,6 +200,13 @@ int esda_decode_raw_q8_stages(const esda_raw_desc *desc, const esda_raw_q8_args 
 /* Quantize src [kv_heads, n_rows, 512] bf16 (contiguous) into rows row0 .. row0+n_rows-1 of
  * a q8 cache: q8 + h*q_head_stride + row*512, scale / bias + h*sb_head_stride + row
  * (esQuantizeRawRows, ESDecodeAttn.mm:491-539; ESKVCache::quantizeRawRows). */
+/* Rotary table for raw-K decode: table[t*64 + d] = bf16(cos(a)) | bf16(sin(a)) << 16 with
+ * a = float(t) * inv_freq[d] in fp32, t < rows -- the values the raw-K kernels otherwise
+ * compute per step (the reference kernel's inline cos / sin, ESDecodeAttn.mm:51-106),
+ * bit for bit.  A per-model precompute: one table serves every raw-K layer with the same
+ * inv_freq.  table: rows * 256 bytes, 16-byte aligned; inv_freq: [64] f32 (device). */
+int esda_rope_table(const float *inv_freq, int32_t rows, void *table, void *stream);
+
 int esda_quantize_raw_rows(const void *src, int32_t kv_heads, int32_t n_rows, void *q8,
                            int64_t q_head_stride, float *scale, float *bias, int64_t sb_head_stride,
                            int32_t row0, void *stream);

@@ -50,19 +50,21 @@ def _check(name, o, ref):
 
 
 def run_raw(name, *, B=1, Hq=32, Hkv=4, cap, pos, scale=1.0, seed=0, split_rows=0, append=True,
-            theta=1.0e6, partial=0.25, fault=0):
-    from apertura_amd.decode import RawStep, decode_raw, new_raw_workspace
+            theta=1.0e6, partial=0.25, fault=0, table=False):
+    from apertura_amd.decode import RawStep, decode_raw, new_raw_workspace, rope_table
     print(f"\n[raw] {name}: B={B} Hq={Hq} Hkv={Hkv} cap={cap} pos={list(pos)[:4]} scale={scale} "
-          f"append={append} split_rows={split_rows}", flush=True)
+          f"append={append} split_rows={split_rows} table={table}", flush=True)
     rng = np.random.default_rng(seed)
     q, raw, kn, kw = _raw_inputs(rng, B, Hq, Hkv, cap)
     inv = orc.rope_inv_freq(512, theta, partial)
     step = RawStep(batch=B, num_q_heads=Hq, num_kv_heads=Hkv, cap=cap, eps=EPS, scale=scale,
                    split_rows=split_rows)
     raw_d = _dev(raw)
+    inv_d = torch.from_numpy(inv).cuda()
     out = decode_raw(step, _dev(q), _dev(kn) if append else None, raw_d,
                      torch.tensor(list(pos), dtype=torch.int32, device="cuda"), _dev(kw),
-                     torch.from_numpy(inv).cuda(), workspace=new_raw_workspace(step, "cuda"))
+                     inv_d, workspace=new_raw_workspace(step, "cuda"),
+                     rope_table=rope_table(inv_d, cap) if table else None)
     torch.cuda.synchronize()
     if append:
         for b in range(B):
@@ -91,6 +93,54 @@ def test_raw_in_model_scale_one():
 def test_raw_long_context_131072():
     """The C4 shape in raw mode: 131072 rows, all visible, 64 splits per kv head."""
     run_raw("c4-raw", cap=131072, pos=[131071], scale=512 ** -0.5, seed=5)
+
+
+def test_raw_long_context_131072_with_rope_table():
+    """The C4 shape with the precomputed rotary table (esda_rope_table) read per stage."""
+    run_raw("c4-raw-table", cap=131072, pos=[131071], scale=512 ** -0.5, seed=5, table=True)
+
+
+def test_rope_table_matches_the_kernel_table_bit_for_bit():
+    """Decode with the precomputed table equals decode with the kernel's own cos/sin, bit for
+    bit (same sincos and rounding), over ragged batched positions with an append; the table
+    entries equal bf16(cos / sin) of the fp32 angle but for rare rounding-boundary cases."""
+    from apertura_amd.decode import RawStep, decode_raw, new_raw_workspace, rope_table
+    rng = np.random.default_rng(23)
+    B, cap = 3, 4096
+    q, raw, kn, kw = _raw_inputs(rng, B, 32, 4, cap)
+    inv = orc.rope_inv_freq(512, 1e6, 0.25)
+    inv_d = torch.from_numpy(inv).cuda()
+    step = RawStep(batch=B, num_q_heads=32, num_kv_heads=4, cap=cap, eps=EPS, scale=1.0)
+    pos = torch.tensor([4095, 1000, 2777], dtype=torch.int32, device="cuda")
+    tab = rope_table(inv_d, cap)
+    outs = []
+    for t in (None, tab):
+        raw_d = _dev(raw)
+        outs.append(decode_raw(step, _dev(q), _dev(kn), raw_d, pos, _dev(kw), inv_d,
+                               workspace=new_raw_workspace(step, "cuda"), rope_table=t).clone())
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    # the table against float64 cos / sin of the fp32 angle, rounded to bf16
+    got = tab.cpu().numpy().view(np.uint32)
+    ang = (np.arange(cap, dtype=np.float32)[:, None] * inv[None, :64]).astype(np.float64)
+    for half, fn in ((0, np.cos), (16, np.sin)):
+        g = orc.from_bf16(((got >> half) & 0xFFFF).astype(np.uint16)).astype(np.float64)
+        r = orc.from_bf16(orc.to_bf16(fn(ang).astype(np.float32))).astype(np.float64)
+        ulp = np.maximum(np.abs(r), 2.0 ** -126) * 2.0 ** -7
+        assert np.all(np.abs(g - r) <= ulp), fn.__name__
+        assert np.mean(g != r) < 1e-4, fn.__name__
+
+
+def test_rope_table_shorter_than_the_cache_is_refused():
+    from apertura_amd._lib import EsdaError
+    from apertura_amd.decode import RawStep, decode_raw, new_raw_workspace, rope_table
+    rng = np.random.default_rng(24)
+    q, raw, kn, kw = _raw_inputs(rng, 1, 32, 4, 256)
+    inv_d = torch.from_numpy(orc.rope_inv_freq(512, 1e6, 0.25)).cuda()
+    step = RawStep(batch=1, num_q_heads=32, num_kv_heads=4, cap=256, eps=EPS)
+    with pytest.raises(EsdaError):
+        decode_raw(step, _dev(q), None, _dev(raw), torch.tensor([255], dtype=torch.int32, device="cuda"),
+                   _dev(kw), inv_d, workspace=new_raw_workspace(step, "cuda"), rope_table=rope_table(inv_d, 255))
 
 
 def test_raw_batched_ragged_positions():

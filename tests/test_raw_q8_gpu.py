@@ -59,10 +59,10 @@ def test_quantize_raw_rows_matches_the_oracle_bit_for_bit():
 
 
 def run_q8(name, *, B=1, Hq=32, Hkv=4, cap, pos, scale=1.0, seed=0, split_rows=0, append=True,
-           partial=0.25, fault=0):
-    from apertura_amd.decode import decode_raw_q8, new_raw_workspace, q8_step_for
+           partial=0.25, fault=0, table=False):
+    from apertura_amd.decode import decode_raw_q8, new_raw_workspace, q8_step_for, rope_table
     print(f"\n[q8] {name}: B={B} Hq={Hq} Hkv={Hkv} cap={cap} pos={list(pos)[:4]} scale={scale} "
-          f"append={append} split_rows={split_rows}", flush=True)
+          f"append={append} split_rows={split_rows} table={table}", flush=True)
     rng = np.random.default_rng(seed)
     raw = _raw_rows(rng, (B, Hkv, cap, 512))
     qc, sc, bs = orc.quantize_rows(raw)
@@ -74,9 +74,11 @@ def run_q8(name, *, B=1, Hq=32, Hkv=4, cap, pos, scale=1.0, seed=0, split_rows=0
     q8_d = torch.from_numpy(qc).cuda()
     sc_d, bs_d = torch.from_numpy(sc).cuda(), torch.from_numpy(bs).cuda()
     step = q8_step_for(q8_d, Hq, eps=EPS, scale=scale, split_rows=split_rows)
+    inv_d = torch.from_numpy(inv).cuda()
     out = decode_raw_q8(step, _dev(q), _dev(kn) if append else None, q8_d, sc_d, bs_d,
                         torch.tensor(list(pos), dtype=torch.int32, device="cuda"), _dev(kw),
-                        torch.from_numpy(inv).cuda(), workspace=new_raw_workspace(step, "cuda"))
+                        inv_d, workspace=new_raw_workspace(step, "cuda"),
+                        rope_table=rope_table(inv_d, cap) if table else None)
     torch.cuda.synchronize()
     if append:
         nq, nsc, nbs = orc.quantize_rows(kn)
@@ -135,3 +137,32 @@ def test_q8_single_row():
 def test_q8_rope_sign_fault_is_detected():
     _, errs = run_q8("rope-fault", cap=2048, pos=[2047], scale=1.0, seed=17, fault=5)
     assert max(e.max() for e in errs) > 10 * TOL_MAX
+
+
+def test_q8_long_context_131072_with_rope_table():
+    """The C4 shape over a q8 stream with the precomputed rotary table."""
+    run_q8("c4-q8-table", cap=131072, pos=[131071], scale=512 ** -0.5, seed=31, table=True)
+
+
+def test_q8_rope_table_matches_the_kernel_table_bit_for_bit():
+    """q8 decode with the precomputed table equals the kernel-computed table's result bit for
+    bit, over ragged batched positions with the new rows quantized in."""
+    from apertura_amd.decode import decode_raw_q8, new_raw_workspace, q8_step_for, rope_table
+    rng = np.random.default_rng(33)
+    B, cap = 2, 4096
+    raw = _raw_rows(rng, (B, 4, cap, 512))
+    qc, sc, bs = orc.quantize_rows(raw)
+    q = orc.rms_norm_rows(orc.to_bf16(rng.standard_normal((B, 32, 512), dtype=np.float32)), None, 1e-6)
+    kn = _raw_rows(rng, (B, 4, 512))
+    kw = orc.to_bf16((1.0 + 0.25 * rng.standard_normal(512)).astype(np.float32))
+    inv_d = torch.from_numpy(orc.rope_inv_freq(512, 1.0e6, 0.25)).cuda()
+    pos = torch.tensor([4095, 2500], dtype=torch.int32, device="cuda")
+    outs = []
+    for t in (None, rope_table(inv_d, cap)):
+        q8_d = torch.from_numpy(qc).cuda()
+        sc_d, bs_d = torch.from_numpy(sc).cuda(), torch.from_numpy(bs).cuda()
+        step = q8_step_for(q8_d, 32, eps=EPS, scale=1.0)
+        outs.append(decode_raw_q8(step, _dev(q), _dev(kn), q8_d, sc_d, bs_d, pos, _dev(kw), inv_d,
+                                  workspace=new_raw_workspace(step, "cuda"), rope_table=t).clone())
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
