@@ -25,12 +25,26 @@ void esdaCheck(int rc) {
     throw std::runtime_error(esda_last_error());
 }
 
-// Per-thread, per-device scratch: the split workspace, the position word and the last
-// rotary table uploaded (the reference passes the table by value on every call).
+// Per-thread, per-device scratch: the split workspace, the position word, the last
+// rotary frequencies uploaded (the reference passes them by value on every call) and
+// their cos/sin table (esda_rope_table, grown in 4096-row steps).
 struct Scratch {
-    std::optional<Tensor> workspace, pos, invFreq;
+    std::optional<Tensor> workspace, pos, invFreq, ropeTab;
     std::vector<float> invFreqHost;
+    int ropeRows = 0;
 };
+
+// The cos/sin table of s.invFreq covering `rows` cache rows.
+const void *ropeTable(Scratch &s, int rows, hipStream_t st) {
+    if (!s.ropeTab || s.ropeRows < rows) {
+        if (s.ropeTab) hipCheck(hipStreamSynchronize(st), "rope table growth");
+        const int n = (rows + 4095) / 4096 * 4096;
+        s.ropeTab = Tensor::empty({(int64_t) n * 256}, Dtype::u8);
+        esdaCheck(esda_rope_table(static_cast<const float *>(s.invFreq->data), n, s.ropeTab->data, st));
+        s.ropeRows = n;
+    }
+    return s.ropeTab->data;
+}
 
 Scratch &scratch() {
     thread_local std::unordered_map<int, Scratch> perDevice;
@@ -63,6 +77,8 @@ Tensor esDecodeAttnGlobal(const Tensor &q, const Tensor &rawBuf, int len, int pi
         if (s.invFreq) hipCheck(hipStreamSynchronize(st), "esDecodeAttnGlobal rotary table");
         s.invFreqHost.assign(invFreq.begin(), invFreq.begin() + 64);
         s.invFreq = Tensor::empty({64}, Dtype::f32);
+        s.ropeTab.reset();
+        s.ropeRows = 0;
         hipCheck(hipMemcpyAsync(s.invFreq->data, s.invFreqHost.data(), 64 * sizeof(float), hipMemcpyHostToDevice, st),
                  "esDecodeAttnGlobal rotary table upload");
         hipCheck(hipStreamSynchronize(st), "esDecodeAttnGlobal rotary table upload");
@@ -104,6 +120,8 @@ Tensor esDecodeAttnGlobal(const Tensor &q, const Tensor &rawBuf, int len, int pi
     a.pos = static_cast<const int32_t *>(s.pos->data);
     a.kw = kw.data;
     a.inv_freq = static_cast<const float *>(s.invFreq->data);
+    a.rope_table = ropeTable(s, pitch, st);
+    a.rope_table_rows = s.ropeRows;
     a.out = o.data;
     a.workspace = s.workspace->data;
     a.workspace_bytes = s.workspace->nbytes();
@@ -139,6 +157,8 @@ Tensor esDecodeAttnGlobalQ8(const Tensor &q, const Tensor &qBuf, const Tensor &s
         if (s.invFreq) hipCheck(hipStreamSynchronize(st), "esDecodeAttnGlobalQ8 rotary table");
         s.invFreqHost.assign(invFreq.begin(), invFreq.begin() + 64);
         s.invFreq = Tensor::empty({64}, Dtype::f32);
+        s.ropeTab.reset();
+        s.ropeRows = 0;
         hipCheck(hipMemcpyAsync(s.invFreq->data, s.invFreqHost.data(), 64 * sizeof(float), hipMemcpyHostToDevice, st),
                  "esDecodeAttnGlobalQ8 rotary table upload");
         hipCheck(hipStreamSynchronize(st), "esDecodeAttnGlobalQ8 rotary table upload");
@@ -184,6 +204,8 @@ Tensor esDecodeAttnGlobalQ8(const Tensor &q, const Tensor &qBuf, const Tensor &s
     a.pos = static_cast<const int32_t *>(s.pos->data);
     a.kw = kw.data;
     a.inv_freq = static_cast<const float *>(s.invFreq->data);
+    a.rope_table = ropeTable(s, pitch, st);
+    a.rope_table_rows = s.ropeRows;
     a.out = o.data;
     a.workspace = s.workspace->data;
     a.workspace_bytes = s.workspace->nbytes();

@@ -250,6 +250,17 @@ void *ESKVCache::workspace(size_t bytes, hipStream_t st) {
     return workspace_->data;
 }
 
+const void *ESKVCache::ropeTable(int rows, hipStream_t st) {
+    if (!ropeTab_ || ropeRows_ < rows) {
+        if (ropeTab_) hipCheck(hipStreamSynchronize(st), "ESKVCache rope table growth");
+        const int n = (rows + 4095) / 4096 * 4096;
+        ropeTab_ = Tensor::empty({(int64_t) n * 256}, Dtype::u8);
+        esdaCheck(esda_rope_table(static_cast<const float *>(invFreqDev_->data), n, ropeTab_->data, st));
+        ropeRows_ = n;
+    }
+    return ropeTab_->data;
+}
+
 int *ESKVCache::positionWord(int layer, int value, hipStream_t st) {
     if (!posDev_) posDev_ = Tensor::empty({(int64_t) slots_.size()}, Dtype::i32);
     int32_t *p = static_cast<int32_t *>(posDev_->data) + layer;
@@ -363,6 +374,8 @@ Tensor ESKVCache::decodeRaw(int layer, const Tensor &q, const Tensor &kNew, cons
         if (invFreqDev_) hipCheck(hipStreamSynchronize(st), "ESKVCache rotary table");
         invFreqHost_.assign(invFreq.begin(), invFreq.begin() + 64);
         invFreqDev_ = Tensor::empty({64}, Dtype::f32);
+        ropeTab_.reset();
+        ropeRows_ = 0;
         hipCheck(hipMemcpyAsync(invFreqDev_->data, invFreqHost_.data(), 64 * sizeof(float),
                                 hipMemcpyHostToDevice, st),
                  "ESKVCache rotary table upload");
@@ -404,6 +417,8 @@ Tensor ESKVCache::decodeRaw(int layer, const Tensor &q, const Tensor &kNew, cons
     a.pos = positionWord(layer, s.len, st);
     a.kw = kw.data;
     a.inv_freq = static_cast<const float *>(invFreqDev_->data);
+    a.rope_table = ropeTable(d.cap, st);
+    a.rope_table_rows = ropeRows_;
     a.out = o.data;
     a.workspace = workspace(wsBytes, st);
     a.workspace_bytes = workspace_->nbytes();
@@ -558,6 +573,8 @@ Tensor ESKVCache::decodeRawQ8(int layer, const Tensor &q, const Tensor &kNew, co
         if (invFreqDev_) hipCheck(hipStreamSynchronize(st), "ESKVCache rotary table");
         invFreqHost_.assign(invFreq.begin(), invFreq.begin() + 64);
         invFreqDev_ = Tensor::empty({64}, Dtype::f32);
+        ropeTab_.reset();
+        ropeRows_ = 0;
         hipCheck(hipMemcpyAsync(invFreqDev_->data, invFreqHost_.data(), 64 * sizeof(float),
                                 hipMemcpyHostToDevice, st),
                  "ESKVCache rotary table upload");
@@ -602,6 +619,8 @@ Tensor ESKVCache::decodeRawQ8(int layer, const Tensor &q, const Tensor &kNew, co
     a.pos = positionWord(layer, s.len, st);
     a.kw = kw.data;
     a.inv_freq = static_cast<const float *>(invFreqDev_->data);
+    a.rope_table = ropeTable(d.cap, st);
+    a.rope_table_rows = ropeRows_;
     a.out = o.data;
     a.workspace = workspace(wsBytes, st);
     a.workspace_bytes = workspace_->nbytes();

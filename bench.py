@@ -150,7 +150,8 @@ def main() -> int:
     import torch
 
     from apertura_amd.decode import (DecodeCall, DecodeStep, RawCall, RawQ8Call, RawStep, STAGE_ATTEND,
-                                     new_raw_workspace, new_workspace, q8_step_for, quantize_raw_rows)
+                                     new_raw_workspace, new_workspace, q8_step_for, quantize_raw_rows,
+                                     rope_table)
 
     if args.calibrate_copy:
         return calibrate_copy(args)
@@ -187,6 +188,8 @@ def main() -> int:
         kw = (1.0 + 0.25 * torch.randn(D, device=dev, generator=gen)).to(torch.bfloat16)
         inv_freq = torch.zeros(D // 2, dtype=torch.float32, device=dev)
         inv_freq[:64] = 1.0 / (1.0e6 ** (torch.arange(64, dtype=torch.float64, device=dev) * 2 / D)).float()
+        # the per-model rotary table (esda_rope_table), built once like the weights
+        tab = rope_table(inv_freq, cap)
         if w.get("q8"):
             # the same raw rows quantized into a q8 stream on the GPU (esda_quantize_raw_rows)
             q8 = torch.empty((B, Hkv, cap, D), dtype=torch.uint8, device=dev)
@@ -196,12 +199,12 @@ def main() -> int:
                 quantize_raw_rows(k_cache[b], q8[b], sc[b], bs[b])
             step = q8_step_for(q8, Hq, eps=1e-6, scale=w["scale"], split_rows=args.split_rows)
             ws = new_raw_workspace(step, dev)
-            call = RawQ8Call(step, q, k_new, q8, sc, bs, pos_d, kw, inv_freq, out=out, workspace=ws)
+            call = RawQ8Call(step, q, k_new, q8, sc, bs, pos_d, kw, inv_freq, out=out, workspace=ws, rope_table=tab)
             raw = (kw, inv_freq, q8, sc, bs)
         else:
             step = RawStep.for_cache(k_cache, Hq, eps=1e-6, scale=w["scale"], split_rows=args.split_rows)
             ws = new_raw_workspace(step, dev)
-            call = RawCall(step, q, k_new, k_cache, pos_d, kw, inv_freq, out=out, workspace=ws)
+            call = RawCall(step, q, k_new, k_cache, pos_d, kw, inv_freq, out=out, workspace=ws, rope_table=tab)
             raw = (kw, inv_freq)
     else:
         step = DecodeStep.for_cache(k_cache, Hq, window=w["window"], ring=w["ring"],
@@ -307,6 +310,8 @@ def main() -> int:
             "visible_rows": visible_rows(w, pos), "kv_shared": w["shared"],
             "window": w["window"], "ring": w["ring"], "split_rows": step.split_rows or "auto",
             "algorithmic_bytes_per_step": nbytes,
+            **({"rope_table": "precomputed per model (esda_rope_table): 256 B per cache row read per "
+                              "pair of kv heads, beside the algorithmic bytes"} if w.get("raw") else {}),
         },
         "roofline": {
             "bound": "hbm",

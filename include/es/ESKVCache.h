@@ -186,11 +186,16 @@ private:
     std::optional<Tensor> workspace_;  // esda_decode / esda_decode_raw workspace
     std::optional<Tensor> invFreqDev_; // rotary table of the last decodeRaw()
     std::vector<float> invFreqHost_;
+    std::optional<Tensor> ropeTab_;    // cos/sin rows of invFreqDev_ (esda_rope_table)
+    int ropeRows_ = 0;
 
     const Slot &slotAt(int layer) const;
     void checkLayer(int layer) const;
     void growSlot(Slot &s, int nNew, hipStream_t stream, bool compactStart);
     void *workspace(size_t bytes, hipStream_t stream);
+    // esda_rope_table of invFreqDev_ covering at least `rows` cache rows (grown in 4096-row
+    // steps; the stream is synchronised before an old table is released).
+    const void *ropeTable(int rows, hipStream_t stream);
     int *positionWord(int layer, int value, hipStream_t stream);
 };
 
