@@ -129,6 +129,17 @@ def test_raw_descriptions_are_validated_without_device():
         assert ei.value.code == 1
 
 
+def test_rope_table_arguments_are_validated_without_device():
+    import ctypes
+    L = _lib.lib()
+    buf = (ctypes.c_uint8 * 512)()
+    addr = (ctypes.addressof(buf) + 15) // 16 * 16
+    assert L.esda_rope_table(None, 4, addr, None) == 1          # null inv_freq
+    assert L.esda_rope_table(addr, 4, None, None) == 1          # null table
+    assert L.esda_rope_table(addr, -1, addr, None) == 1         # negative rows
+    assert L.esda_rope_table(addr, 4, addr + 4, None) == 1      # table not 16-byte aligned
+
+
 def test_prefill_descriptions_are_validated_without_device():
     """esda_prefill's plan is host-side: malformed descriptions fail with
     ESDA_ERR_INVALID_ARGUMENT before any device call; splits size the workspace."""
