@@ -169,6 +169,33 @@ def test_edge_case(case):
     run_case(**case)
 
 
+def _random_case(seed):
+    """A seeded random decode configuration inside the API's contract: head dim, GQA
+    group, batch, global / windowed / ring caches, shared or separate V, split sizes."""
+    r = np.random.default_rng(1000 + seed)
+    D = int(r.choice([128, 256, 512]))
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    Hq = Hkv * int(r.choice([1, 2, 4, 8, 16]))
+    B = int(r.integers(1, 6))
+    kind = ["global", "window", "ring"][int(r.integers(0, 3))]
+    case = dict(name=f"random-{seed}-{kind}", B=B, Hq=Hq, Hkv=Hkv, D=D, seed=2000 + seed,
+                shared=bool(r.integers(0, 2)), split_rows=int(r.choice([0, 0, 16, 64, 256])))
+    if kind == "ring":
+        cap = int(r.choice([64, 256, 1024]))
+        case.update(cap=cap, window=int(r.integers(1, cap + 1)), ring=True,
+                    pos=[int(x) for x in r.integers(0, 4 * cap, B)])
+    else:
+        cap = int(r.integers(16, 3000))
+        case.update(cap=cap, window=0 if kind == "global" else int(r.integers(1, cap + 1)),
+                    pos=[int(x) for x in r.integers(0, cap, B)])
+    return case
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_randomized_configurations(seed):
+    run_case(**_random_case(seed))
+
+
 @pytest.mark.parametrize("D", [256, 512])
 def test_huge_logit_gap_does_not_overflow(D):
     """Keys scoring ~200 (natural-log units) above the rest: the running max must see

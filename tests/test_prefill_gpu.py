@@ -140,6 +140,26 @@ def test_chunked_prefill_benchmark_shape_sampled_rows():
                 rows=[0, 1, 200, 511])
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_randomized_shapes_sampled_rows(seed):
+    """Seeded random prefill calls inside the API's contract: head dim, GQA group, chunk
+    length, cached past, window (with the evicted prefix a sliding layer drops), forced or
+    automatic key splits, dense or strided layouts; eight sampled query rows each."""
+    r = np.random.default_rng(3000 + seed)
+    D = int(r.choice([128, 256, 512]))
+    Hkv = int(r.choice([1, 2, 4]))
+    Hq = Hkv * int(r.choice([1, 2, 4, 8]))
+    Sq = int(r.integers(1, 300))
+    past = int(r.integers(0, 1200))
+    window = 0 if r.integers(0, 2) == 0 else int(r.integers(1, 700))
+    k_pos0 = max(0, past - window) if window else 0
+    Sk = past + Sq - k_pos0
+    rows = sorted({int(x) for x in r.integers(0, Sq, 8)} | {Sq - 1})
+    run_prefill(f"random-{seed}", Hq=Hq, Hkv=Hkv, D=D, Sq=Sq, Sk=Sk, q_pos0=past, k_pos0=k_pos0,
+                window=window, split_keys=int(r.choice([0, 0, 32, 96])), seed=4000 + seed,
+                layout="dense" if r.integers(0, 2) == 0 else "strided", rows=rows)
+
+
 def test_diagonal_fault_in_the_oracle_is_detected():
     err = run_prefill("fault7", Hq=8, Hkv=2, D=128, Sq=40, Sk=40, q_pos0=0, k_pos0=0, seed=11, fault=7,
                       rows=[5, 17, 39])
