@@ -143,6 +143,18 @@ def test_rope_table_shorter_than_the_cache_is_refused():
                    _dev(kw), inv_d, workspace=new_raw_workspace(step, "cuda"), rope_table=rope_table(inv_d, 255))
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_raw_randomized_configurations(seed):
+    """Seeded random raw-K steps: batch, kv heads (odd counts run unpacked), cache size,
+    ragged positions, split sizes, scale, append or not, with or without the rotary table."""
+    r = np.random.default_rng(5000 + seed)
+    B, Hkv = int(r.integers(1, 4)), int(r.choice([1, 2, 3, 4, 6]))
+    cap = int(r.integers(64, 4096))
+    run_raw(f"random-{seed}", B=B, Hq=8 * Hkv, Hkv=Hkv, cap=cap, pos=[int(x) for x in r.integers(0, cap, B)],
+            scale=float(r.choice([1.0, 512 ** -0.5])), seed=6000 + seed, split_rows=int(r.choice([0, 16, 64])),
+            append=bool(r.integers(0, 2)), table=bool(r.integers(0, 2)))
+
+
 def test_raw_batched_ragged_positions():
     run_raw("batched", B=3, cap=4096, pos=[17, 2500, 4095], scale=512 ** -0.5, seed=7)
 
