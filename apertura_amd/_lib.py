@@ -175,7 +175,7 @@ def lib() -> ctypes.CDLL:
         L.esda_cache_update_raw.argtypes = [P, i32, P, i32, i32, i32, i32, P, VP, pi32, pi32]
         L.esda_cache_current.argtypes = [P, i32, i32, VP, VP]
         L.esda_cache_current_raw.argtypes = [P, i32, VP, pi32, pi32]
-        L.esda_cache_decode.argtypes = [P, i32, P, i32, P, P, i32, i32, i32, f32, P, P]
+        L.esda_cache_decode.argtypes = [P, i32, P, i32, P, P, i32, i32, i32, i32, f32, P, P]
         L.esda_cache_decode_raw.argtypes = [P, i32, P, i32, P, i32, P, f32, P, i32, P, P]
         L.esda_cache_slot.argtypes = [P, i32, pi32, pi32, pi32, pi32]
         L.esda_cache_seq_len.argtypes = [P]

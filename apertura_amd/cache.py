@@ -142,9 +142,10 @@ class ESKVCache:
         return CacheView.of(v), int(ln.value), int(pitch.value)
 
     def decode(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, max_keep: int,
-               scale: float, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+               window: int, scale: float, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
         """Fused append + attention of one decode step; v_new may be k_new itself
-        (attention_k_eq_v: one shared K=V buffer).  Returns [numQHeads, headDim] bf16."""
+        (attention_k_eq_v: one shared K=V buffer).  window > 0: the sliding mask (last
+        `window` positions), whatever max_keep evicts.  Returns [numQHeads, headDim] bf16."""
         kvh, n, hd = _rows(k_new, "k_new")
         _rows(v_new, "v_new")
         if n != 1:
@@ -153,7 +154,8 @@ class ESKVCache:
         if out is None:
             out = torch.empty((hq, hd), dtype=torch.bfloat16, device=q.device)
         check(lib().esda_cache_decode(self._h, layer, _dev_ptr(q, torch.bfloat16), hq, _dev_ptr(k_new),
-                                      _dev_ptr(v_new), kvh, hd, max_keep, scale, _dev_ptr(out, torch.bfloat16),
+                                      _dev_ptr(v_new), kvh, hd, max_keep, window, scale,
+                                      _dev_ptr(out, torch.bfloat16),
                                       _stream_ptr(stream)))
         return out
 

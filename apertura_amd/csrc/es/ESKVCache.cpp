@@ -269,12 +269,13 @@ int *ESKVCache::positionWord(int layer, int value, hipStream_t st) {
 }
 
 Tensor ESKVCache::decode(int layer, const Tensor &q, const Tensor &kNew, const Tensor &vNew, int maxKeep,
-                         float scale, hipStream_t st, Tensor *out) {
+                         int window, float scale, hipStream_t st, Tensor *out) {
     checkLayer(layer);
     checkRows(kNew, "ESKVCache::decode kNew");
     checkRows(vNew, "ESKVCache::decode vNew");
     if (kNew.shape[1] != 1 || vNew.shape != kNew.shape)
         throw std::invalid_argument("ESKVCache::decode: kNew / vNew must be [kvHeads, 1, headDim]");
+    if (window < 0) throw std::invalid_argument("ESKVCache::decode: window must be >= 0");
     const int kvH = (int) kNew.shape[0], hd = (int) kNew.shape[2];
     if (!q.defined() || q.dtype != Dtype::bf16 || !q.contiguous() || q.numel() % hd)
         throw std::invalid_argument("ESKVCache::decode: q must be contiguous bf16 [numQHeads, headDim]");
@@ -299,9 +300,13 @@ Tensor ESKVCache::decode(int layer, const Tensor &q, const Tensor &kNew, const T
         growSlot(s, 1, st, true);
     }
     const int cap = (int) s.k->shape[1];
-    // Rows attended after the append: the live range the reference's update() leaves.
+    // Rows attended after the append: the live range the reference's update() leaves,
+    // then the sliding mask's last `window` positions of it.  Rows are positions here
+    // (the slot's row 0 is position 0 until an eviction starts the window elsewhere),
+    // so the window counts back from the new row.
     const int live = s.len + 1 - s.start;
-    const int w = maxKeep > 0 ? std::min(maxKeep, live) : live;
+    int w = maxKeep > 0 ? std::min(maxKeep, live) : live;
+    if (window > 0) w = std::min(w, window);
 
     esda_decode_desc d{};
     d.batch = 1;

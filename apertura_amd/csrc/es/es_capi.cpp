@@ -112,15 +112,15 @@ int esda_cache_current(esda_cache *cache, int32_t layer, int32_t prealloc, esda_
 }
 
 int esda_cache_decode(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads, const void *k_new,
-                      const void *v_new, int32_t kv_heads, int32_t head_dim, int32_t max_keep, float scale,
-                      void *out, void *stream) {
+                      const void *v_new, int32_t kv_heads, int32_t head_dim, int32_t max_keep, int32_t window,
+                      float scale, void *out, void *stream) {
     return guarded([&] {
         needCache(cache);
         if (!q || !out || num_q_heads <= 0) throw std::invalid_argument("esda_cache_decode: null q / out");
         es::Tensor qt = es::Tensor::wrap(const_cast<void *>(q), {num_q_heads, head_dim}, es::Dtype::bf16);
         es::Tensor ot = es::Tensor::wrap(out, {num_q_heads, head_dim}, es::Dtype::bf16);
         cache->impl.decode(layer, qt, rows(k_new, kv_heads, 1, head_dim), rows(v_new, kv_heads, 1, head_dim),
-                           max_keep, scale, asStream(stream), &ot);
+                           max_keep, window, scale, asStream(stream), &ot);
     });
 }
 

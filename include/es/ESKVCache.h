@@ -83,11 +83,15 @@ public:
 
     // Fused decode step for `layer` (prealloc storage): appends the single new row of
     // kNew/vNew ([kvHeads, 1, headDim]) and returns softmax(scale q K^T) V over the rows
-    // the reference would attend after update(maxKeep): [numQHeads, headDim] bf16 in
-    // `out` (allocated when null).  q: numQHeads*headDim bf16, query heads kv-major.
-    // vNew aliasing kNew (same data pointer) is attention_k_eq_v: a slot created that
-    // way keeps one shared K=V buffer, written and read once.
-    Tensor decode(int layer, const Tensor &q, const Tensor &kNew, const Tensor &vNew, int maxKeep,
+    // the reference would attend after update(maxKeep) under its mask: [numQHeads,
+    // headDim] bf16 in `out` (allocated when null).  window > 0 is the sliding layer's
+    // mask (ESGemma4TextModel.mm:68-83: the last `window` positions), applied whatever
+    // maxKeep evicts -- the reference passes maxKeep = 0 with a window when the sliding
+    // cache is off or the layer stores its full K/V (ESAttention.mm:99-103).  q:
+    // numQHeads*headDim bf16, query heads kv-major.  vNew aliasing kNew (same data
+    // pointer) is attention_k_eq_v: a slot created that way keeps one shared K=V buffer,
+    // written and read once.
+    Tensor decode(int layer, const Tensor &q, const Tensor &kNew, const Tensor &vNew, int maxKeep, int window,
                   float scale, hipStream_t stream = nullptr, Tensor *out = nullptr);
 
     // Fused raw-K decode step: updateRaw(layer, kNew, true) and esDecodeAttnGlobal over

@@ -77,10 +77,12 @@ int esda_cache_current_raw(esda_cache *cache, int32_t layer, esda_view *view, in
                            int32_t *pitch);
 
 /* Fused decode step: append one row (v_new == k_new: one shared K=V buffer) and attend.
+ * max_keep evicts as update() does; window > 0 masks all but the last `window` positions
+ * (the sliding layer's mask, applied even when max_keep is 0).
  * q: [num_q_heads, head_dim] bf16; out: [num_q_heads, head_dim] bf16. */
 int esda_cache_decode(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads,
                       const void *k_new, const void *v_new, int32_t kv_heads, int32_t head_dim,
-                      int32_t max_keep, float scale, void *out, void *stream);
+                      int32_t max_keep, int32_t window, float scale, void *out, void *stream);
 
 /* Fused raw-K decode step (head_dim 512): append one raw row and attend.  inv_freq is a
  * host array of n_freq >= 64 floats (the first 64 are used). */

@@ -24,17 +24,33 @@ def rms_rows(rng: np.random.Generator, shape) -> np.ndarray:
     return out.reshape(shape)
 
 
-def make_step_inputs(step: orc.Step, seed: int, pos, shared_kv: bool = False, row_base=None):
+def pooled_rows(rng: np.random.Generator, n_rows: int, D: int, pool: int) -> np.ndarray:
+    """n_rows unit-RMS bf16 rows, each a random pick from `pool` distinct rows: multi-GB
+    caches in seconds.  With a pool of 65536, a row read from the wrong place differs
+    from the right one with probability 1 - 2^-16."""
+    table = rms_rows(rng, (pool, D))
+    return table[rng.integers(0, pool, size=n_rows)]
+
+
+def make_step_inputs(step: orc.Step, seed: int, pos, shared_kv: bool = False, row_base=None,
+                     pool: int = 0):
     """Random q, flat caches and new rows for one decode step.
 
     Every cache element is filled (rows that are not visible hold data too, so a kernel
-    that reads them by mistake changes the result)."""
+    that reads them by mistake changes the result).  pool > 0 draws the cache rows from
+    `pool` distinct rows (pooled_rows)."""
     rng = np.random.default_rng(seed)
     d = step.desc()
     q = rms_rows(rng, (step.B, step.Hq, step.D))
     n_elems = int(d.seq_stride) * step.B
-    kc = rms_rows(rng, (n_elems // step.D, step.D)).reshape(-1)
-    vc = kc if shared_kv else rms_rows(rng, (n_elems // step.D, step.D)).reshape(-1)
+
+    def cache():
+        if pool:
+            return pooled_rows(rng, n_elems // step.D, step.D, pool).reshape(-1)
+        return rms_rows(rng, (n_elems // step.D, step.D)).reshape(-1)
+
+    kc = cache()
+    vc = kc if shared_kv else cache()
     kn = rms_rows(rng, (step.B, step.Hkv, step.D))
     vn = kn if shared_kv else rms_rows(rng, (step.B, step.Hkv, step.D))
     return q, kc, vc, kn, vn

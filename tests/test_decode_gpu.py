@@ -28,7 +28,7 @@ def _host(t: torch.Tensor) -> np.ndarray:
 
 def run_case(name, *, B, Hq, Hkv, D, cap, pos, window=0, ring=False, shared=False, scale=None,
              row_base=None, seed=0, split_rows=0, head_pad=0, seq_pad=0, peaks=0, bump=4.0,
-             refround=True, max_visible=0, workspace=None):
+             refround=True, max_visible=0, workspace=None, pool=0):
     from apertura_amd.decode import DecodeStep, decode_status, decode_step, new_workspace, workspace_bytes
     print(f"\n[case] {name}: B={B} Hq={Hq} Hkv={Hkv} D={D} cap={cap} window={window} "
           f"ring={ring} shared={shared} pos={list(pos)[:4]} split_rows={split_rows}", flush=True)
@@ -37,7 +37,7 @@ def run_case(name, *, B, Hq, Hkv, D, cap, pos, window=0, ring=False, shared=Fals
     ss = Hkv * hs + seq_pad
     step = orc.Step(B=B, Hq=Hq, Hkv=Hkv, D=D, cap=cap, window=window, ring=ring, scale=scale,
                     seq_stride=ss, head_stride=hs)
-    q, kc, vc, kn, vn = make_step_inputs(step, seed, pos, shared_kv=shared)
+    q, kc, vc, kn, vn = make_step_inputs(step, seed, pos, shared_kv=shared, pool=pool)
     if peaks:
         plant_peaked_keys(step, q, kc, pos, peaks, bump, seed + 1, row_base)
     dstep = DecodeStep(batch=B, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D, cap=cap,
@@ -98,7 +98,100 @@ def test_c3_local_ring_b8():
 
 def test_c4_global_k_eq_v_131072_peaked():
     run_case("C4", B=1, Hq=32, Hkv=4, D=512, cap=131072, pos=[131071], shared=True, peaks=64,
-             bump=4.0, seed=4, refround=False)
+             bump=4.0, seed=4)
+
+
+# C5: the 60-layer step at B=32 (ESGemma4TextModel.mm:111-119 runs every layer per token).
+# Lengths as bench.py draws them: U[1024, 32768] from default_rng(55); each sequence's new
+# token is its last position (len - 1).
+C5_LOCAL = dict(Hq=32, Hkv=16, D=256, cap=1024, window=1024, ring=True, shared=False, scale=1 / 16)
+C5_GLOBAL = dict(Hq=32, Hkv=4, D=512, window=0, ring=False, shared=True, scale=512 ** -0.5)
+
+
+def c5_lengths():
+    rng = np.random.default_rng(55)
+    return [int(x) for x in rng.integers(1024, 32769, size=32)]
+
+
+def test_c5_global_layer_full_shape():
+    """A C5 global layer at full shape: 32 ragged sequences up to 32768 rows, k_eq_v,
+    automatic (balanced-share) plan: ~2.2M (sequence, kv head, row) triples.  Every
+    appended row byte-exact, all 32 x 32 output heads against fp64 and reference
+    rounding."""
+    lens = c5_lengths()
+    run_case("C5-global", B=32, cap=max(lens), pos=[n - 1 for n in lens], seed=55, pool=65536,
+             **{k: v for k, v in C5_GLOBAL.items() if k != "window"})
+
+
+def test_c5_two_layer_step_in_graph():
+    """One local ring layer and one global layer of C5's step at full shape, launched
+    through ONE workspace (as the cache layer shares one across layers) and captured in a
+    HIP graph.  The eager step matches both oracles and the cache bytes; three replays,
+    with eager work and synchronisation between them, each equal the eager outputs bit
+    for bit (the appends rewrite the same rows)."""
+    from apertura_amd.decode import DecodeCall, DecodeStep, decode_status, workspace_bytes
+    lens = c5_lengths()
+    pos = [n - 1 for n in lens]
+    B = len(lens)
+    layers = []
+    for i, t in enumerate((C5_LOCAL, dict(C5_GLOBAL, cap=max(lens)))):
+        step = orc.Step(B=B, Hq=t["Hq"], Hkv=t["Hkv"], D=t["D"], cap=t["cap"], window=t["window"],
+                        ring=t["ring"], scale=t["scale"])
+        q, kc, vc, kn, vn = make_step_inputs(step, 60 + i, pos, shared_kv=t["shared"], pool=65536)
+        dstep = DecodeStep(batch=B, num_q_heads=t["Hq"], num_kv_heads=t["Hkv"], head_dim=t["D"], cap=t["cap"],
+                           window=t["window"], ring=t["ring"], kv_shared=t["shared"], scale=t["scale"])
+        layers.append(dict(t=t, step=step, dstep=dstep, host=(q, kc, vc, kn, vn)))
+    ws = torch.zeros(max(workspace_bytes(L["dstep"]) for L in layers), dtype=torch.uint8, device="cuda")
+    for L in layers:
+        t, (q, kc, vc, kn, vn) = L["t"], L["host"]
+        D, Hq, Hkv = t["D"], t["Hq"], t["Hkv"]
+        kc_d = _dev(kc).view(B, Hkv, t["cap"], D)
+        vc_d = kc_d if t["shared"] else _dev(vc).view(B, Hkv, t["cap"], D)
+        L["dev"] = (kc_d, vc_d)
+        L["call"] = DecodeCall(L["dstep"], _dev(q).view(B, Hq, D), _dev(kn).view(B, Hkv, D),
+                               None if t["shared"] else _dev(vn).view(B, Hkv, D), kc_d, vc_d,
+                               torch.tensor(pos, dtype=torch.int32, device="cuda"), workspace=ws)
+    stream = torch.cuda.Stream()
+    print("\n[case] C5 two-layer step: eager", flush=True)
+    with torch.cuda.stream(stream):
+        for L in layers:
+            L["call"](stream)
+    torch.cuda.synchronize()
+    assert decode_status(layers[0]["dstep"], ws) == 0
+    eager = [L["call"].out.clone() for L in layers]
+    for L, o_d in zip(layers, eager):
+        t, step, (q, kc, vc, kn, vn) = L["t"], L["step"], L["host"]
+        shared = t["shared"]
+        orc.append(step, kc, None if shared else vc, kn, None if shared else vn, pos)
+        assert np.array_equal(_host(L["dev"][0]).reshape(-1), kc), "K cache bytes differ after the append"
+        if not shared:
+            assert np.array_equal(_host(L["dev"][1]).reshape(-1), vc), "V cache bytes differ after the append"
+        vref = kc if shared else vc
+        o = orc.from_bf16(_host(o_d)).reshape(B, t["Hq"], t["D"]).astype(np.float64)
+        for name, ref in (("fp64", orc.decode_f64(step, q, kc, vref, pos)),
+                          ("refround", orc.from_bf16(orc.decode_refround(step, q, kc, vref, pos))
+                           .reshape(B, t["Hq"], t["D"]).astype(np.float64))):
+            err = np.abs(o - ref)
+            print(f"[case] C5 two-layer D={t['D']} vs {name}: max_abs={err.max():.3e} "
+                  f"mean_abs={err.mean():.3e}", flush=True)
+            assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            for L in layers:
+                L["call"](stream)
+    for r in range(3):
+        print(f"[case] C5 two-layer step: graph replay {r}", flush=True)
+        with torch.cuda.stream(stream):
+            for L in layers:
+                L["call"].out.zero_()
+            g.replay()
+        torch.cuda.synchronize()
+        for L, e in zip(layers, eager):
+            assert torch.equal(L["call"].out.view(torch.int16), e.view(torch.int16)), f"replay {r} differs"
+        with torch.cuda.stream(stream):  # eager work between replays
+            layers[1]["call"](stream)
+        torch.cuda.synchronize()
 
 
 # ------------------------------------------------------------------ edge cases

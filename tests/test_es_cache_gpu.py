@@ -72,9 +72,11 @@ def test_first_prealloc_store_has_capacity_equal_to_content_then_grows_by_chunks
     assert cache.slot(0)["capacity"] == 512  # roundUp(100 + 1 + 256, 256)
 
 
-def _decode_run(cache, layer, rng, *, kvh, hq, hd, shared, max_keep, steps, prefill, scale):
+def _decode_run(cache, layer, rng, *, kvh, hq, hd, shared, max_keep, steps, prefill, scale, window=None):
     """Prefill with update(prealloc), then decode() steps, each checked against the oracle
-    on the live rows of the host model."""
+    on the live rows of the host model under the sliding mask of `window` (default: a
+    sliding layer's window = max_keep; 0 = full causal)."""
+    window = max_keep if window is None else window
     model_k = rms_rows(rng, (kvh, prefill, hd)) if prefill else np.zeros((kvh, 0, hd), np.uint16)
     model_v = model_k if shared else (rms_rows(rng, (kvh, prefill, hd)) if prefill else model_k.copy())
     if prefill:
@@ -86,7 +88,7 @@ def _decode_run(cache, layer, rng, *, kvh, hq, hd, shared, max_keep, steps, pref
         kn = rms_rows(rng, (kvh, 1, hd))
         vn = kn if shared else rms_rows(rng, (kvh, 1, hd))
         kn_d = _dev(kn)
-        out = cache.decode(layer, _dev(q), kn_d, kn_d if shared else _dev(vn), max_keep, scale)
+        out = cache.decode(layer, _dev(q), kn_d, kn_d if shared else _dev(vn), max_keep, window, scale)
         model_k = np.concatenate([model_k, kn], axis=1)
         model_v = model_k if shared else np.concatenate([model_v, vn], axis=1)
         if max_keep and model_k.shape[1] > max_keep:
@@ -94,7 +96,7 @@ def _decode_run(cache, layer, rng, *, kvh, hq, hd, shared, max_keep, steps, pref
             model_v = model_k if shared else model_v[:, -max_keep:]
         live = model_k.shape[1]
         if i % 7 == 0 or i == steps - 1:
-            step = orc.Step(B=1, Hq=hq, Hkv=kvh, D=hd, cap=live, scale=scale)
+            step = orc.Step(B=1, Hq=hq, Hkv=kvh, D=hd, cap=live, window=min(window, live), scale=scale)
             ref = orc.decode_f64(step, q.reshape(1, hq, hd), np.ascontiguousarray(model_k).reshape(-1),
                                  np.ascontiguousarray(model_v).reshape(-1), [live - 1])
             o = orc.from_bf16(_host(out)).reshape(1, hq, hd).astype(np.float64)
@@ -114,6 +116,19 @@ def test_decode_sliding_layer_across_compaction():
     s = cache.slot(0)
     assert s["len"] - s["start"] == 96 and s["lost"] and not s["shared"]
     print(f"sliding worst max_abs {w:.3e}")
+
+
+def test_decode_sliding_mask_without_eviction():
+    """A sliding layer whose cache keeps every row (maxKeep = 0: the reference's
+    --no-swa-cache, or a layer storing its full K/V, ESAttention.mm:99-103) still masks
+    all but the last `window` positions (ESGemma4TextModel.mm:68-83)."""
+    from apertura_amd.cache import ESKVCache
+    cache = ESKVCache(1)
+    w = _decode_run(cache, 0, np.random.default_rng(15), kvh=4, hq=8, hd=256, shared=False, max_keep=0,
+                    window=64, steps=300, prefill=40, scale=1 / 16)
+    s = cache.slot(0)
+    assert s["len"] == 340 and s["start"] == 0 and not s["lost"]
+    print(f"unevicted sliding worst max_abs {w:.3e}")
 
 
 def test_decode_global_k_eq_v_across_growth():
@@ -152,16 +167,16 @@ def test_mode_mismatch_guards_raise_runtime_error():
         cache.update(1, kv, kv, 0, prealloc=True)
     assert ei.value.code == 2 and "raw-K" in str(ei.value)
     with pytest.raises(EsdaError) as ei:
-        cache.decode(1, _dev(rms_rows(rng, (16, 512))), kv[:, :1].contiguous(), kv[:, :1].contiguous(), 0, 1.0)
+        cache.decode(1, _dev(rms_rows(rng, (16, 512))), kv[:, :1].contiguous(), kv[:, :1].contiguous(), 0, 0, 1.0)
     assert ei.value.code == 2
     assert cache.slot(1)["raw"] and not cache.slot(0)["raw"]
     # a shared K=V slot refuses a distinct V row
     c2 = ESKVCache(1)
     one = _dev(rms_rows(rng, (2, 1, 128)))
-    c2.decode(0, _dev(rms_rows(rng, (4, 128))), one, one, 0, 1.0)
+    c2.decode(0, _dev(rms_rows(rng, (4, 128))), one, one, 0, 0, 1.0)
     other = _dev(rms_rows(rng, (2, 1, 128)))
     with pytest.raises(EsdaError) as ei:
-        c2.decode(0, _dev(rms_rows(rng, (4, 128))), one, other, 0, 1.0)
+        c2.decode(0, _dev(rms_rows(rng, (4, 128))), one, other, 0, 0, 1.0)
     assert ei.value.code == 2
 
 

@@ -78,7 +78,7 @@ def test_chunked_prefill_then_decode(shared, D, Hq, Hkv, window, chunks):
         kn = rms_rows(rng, (Hkv, 1, D))
         vn = kn if shared else rms_rows(rng, (Hkv, 1, D))
         kd = _dev(kn)
-        out = cache.decode(0, _dev(q), kd, kd if shared else _dev(vn), window, scale)
+        out = cache.decode(0, _dev(q), kd, kd if shared else _dev(vn), window, window, scale)
         torch.cuda.synchronize()
         mk = np.concatenate([mk, kn], axis=1)
         mv = mk if shared else np.concatenate([mv, vn], axis=1)

@@ -168,7 +168,7 @@ def test_q8_mode_guards():
         assert ei.value.code == 2 and "composite" in str(ei.value)
     cache.update_raw_q8(1, kv)  # q8
     for call in (lambda: cache.update(1, kv, kv, 0, prealloc=True),
-                 lambda: cache.decode(1, q, one, one, 0, 1.0),
+                 lambda: cache.decode(1, q, one, one, 0, 0, 1.0),
                  lambda: cache.update_raw(1, kv, True),
                  lambda: cache.decode_raw(1, q, one, kw_d, EPS, list(inv))):
         with pytest.raises(EsdaError) as ei:

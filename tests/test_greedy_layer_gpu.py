@@ -120,7 +120,8 @@ def test_greedy_argmax_agreement_in_a_random_init_model():
             # GPU path (its own residual stream)
             qg, kg, vg = toy.qkv(li, x_gpu)
             kd = _dev(kg[:, None])
-            o = cache.decode(li, _dev(qg), kd, kd if L["shared"] else _dev(vg[:, None]), L["window"], 1.0)
+            o = cache.decode(li, _dev(qg), kd, kd if L["shared"] else _dev(vg[:, None]), L["window"], L["window"],
+                             1.0)
             x_gpu = toy.out(li, x_gpu, _host(o))
         lr, lg = toy.logits(x_ref, token), toy.logits(x_gpu, token)
         top = np.sort(lr)[-2:]

@@ -65,19 +65,19 @@ def _step(cache, rng, model, hd=128, raw_hd=512, q_seed=None):
     outs = []
     k, v = rms_rows(rng, (2, 1, hd)), rms_rows(rng, (2, 1, hd))
     q = rms_rows(rng, (4, hd))
-    outs.append(_host(cache.decode(SLIDE, _dev(q), _dev(k), _dev(v), WINDOW, 1.0)))
+    outs.append(_host(cache.decode(SLIDE, _dev(q), _dev(k), _dev(v), WINDOW, WINDOW, 1.0)))
     model[SLIDE] = [np.concatenate([m, x], axis=1)[:, -WINDOW:] for m, x in zip(model[SLIDE], (k, v))]
     s = rms_rows(rng, (1, 1, hd))
     sd = _dev(s)
     q = rms_rows(rng, (8, hd))
-    outs.append(_host(cache.decode(SHARED, _dev(q), sd, sd, 0, 1.0)))
+    outs.append(_host(cache.decode(SHARED, _dev(q), sd, sd, 0, 0, 1.0)))
     model[SHARED] = [np.concatenate([model[SHARED][0], s], axis=1)] * 2
     r = rms_rows(rng, (1, 1, raw_hd))
     cache.update_raw(RAW, _dev(r), True)
     model[RAW] = [np.concatenate([model[RAW][0], r], axis=1)]
     gk, gv = rms_rows(rng, (1, 1, hd)), rms_rows(rng, (1, 1, hd))
     q = rms_rows(rng, (8, hd))
-    outs.append(_host(cache.decode(GLOBAL, _dev(q), _dev(gk), _dev(gv), 0, 1.0)))
+    outs.append(_host(cache.decode(GLOBAL, _dev(q), _dev(gk), _dev(gv), 0, 0, 1.0)))
     model[GLOBAL] = [np.concatenate([m, x], axis=1) for m, x in zip(model[GLOBAL], (gk, gv))]
     return outs
 
@@ -235,8 +235,8 @@ def test_prefix_marker_restores_the_longest_reproducible_prefix(tmp_path):
     win_k, win_v = _live(a, 0)
     for _ in range(40):  # the turn goes on past the marker
         kn, vn = rms_rows(rng, (1, 1, hd)), rms_rows(rng, (1, 1, hd))
-        a.decode(0, _dev(rms_rows(rng, (2, hd))), _dev(kn), _dev(vn), WINDOW, 1.0)
-        a.decode(1, _dev(rms_rows(rng, (2, hd))), _dev(kn), _dev(vn), 0, 1.0)
+        a.decode(0, _dev(rms_rows(rng, (2, hd))), _dev(kn), _dev(vn), WINDOW, WINDOW, 1.0)
+        a.decode(1, _dev(rms_rows(rng, (2, hd))), _dev(kn), _dev(vn), 0, 0, 1.0)
     path = str(tmp_path / "marked.safetensors")
     assert a.save_snapshot(path, "full-4136", 4136)
     b = ESKVCache(2)
