@@ -21,6 +21,7 @@ ERROR_NAMES = {1: "invalid argument", 2: "runtime error", 3: "HIP error", 4: "wo
 EXPORTS = (
     # include/esda.h
     "esda_decode_workspace_size", "esda_decode", "esda_decode_stages", "esda_decode_status",
+    "esda_decode_noalloc",
     "esda_kv_append", "esda_decode_raw_workspace_size", "esda_decode_raw",
     "esda_decode_raw_stages", "esda_decode_raw_q8", "esda_decode_raw_q8_stages", "esda_quantize_raw_rows", "esda_rope_table",
     "esda_fill_i32", "esda_last_error", "esda_version",
@@ -153,6 +154,7 @@ def lib() -> ctypes.CDLL:
         L.esda_decode_stages.argtypes = [ctypes.POINTER(DecodeDesc), ctypes.POINTER(DecodeArgs),
                                          ctypes.c_int, P]
         L.esda_decode_status.argtypes = [ctypes.POINTER(DecodeDesc), P, ctypes.POINTER(i32), P]
+        L.esda_decode_noalloc.argtypes = [ctypes.POINTER(DecodeDesc), ctypes.POINTER(DecodeArgs), P]
         L.esda_kv_append.argtypes = [P, i64, i64, i32, i32, i32, i32, P, i32, P, P]
         L.esda_decode_raw_workspace_size.argtypes = [ctypes.POINTER(RawDesc), ctypes.POINTER(sz)]
         L.esda_decode_raw.argtypes = [ctypes.POINTER(RawDesc), ctypes.POINTER(RawArgs), P]

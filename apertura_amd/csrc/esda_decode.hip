@@ -1501,9 +1501,10 @@ int raw_as_decode(const esda_raw_desc *r, esda_decode_desc *d) {
 }
 
 // Launches the requested stages of one decode step (raw: the raw-K attend kernel).
-// mode: 0 composite, 1 raw-K, 2 q8 raw-K.
+// mode: 0 composite, 1 raw-K, 2 q8 raw-K.  status: the skipped-sequence counter (null =
+// the workspace's first word).
 int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap_in, uint16_t *out,
-               void *workspace, int stages, int mode, hipStream_t st) {
+               void *workspace, int stages, int mode, hipStream_t st, int *status = nullptr) {
     unsigned char *ws = static_cast<unsigned char *>(workspace);
     long long *table = reinterpret_cast<long long *>(ws + pl.off_table);
     float *part_ml = reinterpret_cast<float *>(ws + pl.off_ml);
@@ -1512,7 +1513,7 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         AttendParams ap = ap_in;
         ap.part_acc = part_acc;
         ap.part_ml = part_ml;
-        ap.status = reinterpret_cast<int *>(ws);
+        ap.status = status ? status : reinterpret_cast<int *>(ws);
         ap.seq_stride = d->seq_stride;
         ap.head_stride = d->head_stride;
         ap.B = d->batch;
@@ -1586,6 +1587,70 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
     return ESDA_OK;
 }
 
+// Argument checks shared by esda_decode_stages and esda_decode_noalloc (everything but
+// the workspace).
+int check_decode_args(const esda_decode_desc *d, const esda_decode_args *a) {
+    if (!a) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: null arguments");
+    if (!a->q || !a->k_new || !a->k_cache || !a->v_cache || !a->pos || !a->out)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: null device pointer");
+    if (!d->kv_shared && !a->v_new)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: v_new is required unless kv_shared");
+    if (d->kv_shared && a->v_cache != a->k_cache)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: kv_shared needs v_cache == k_cache");
+    if (!d->kv_shared && a->v_cache == a->k_cache)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: separate K/V need distinct caches");
+    if (!aligned16(a->q) || !aligned16(a->k_new) || (a->v_new && !aligned16(a->v_new)) ||
+        !aligned16(a->k_cache) || !aligned16(a->v_cache) || !aligned16(a->out))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: tensors must be 16-byte aligned");
+    return ESDA_OK;
+}
+
+AttendParams decode_params(const esda_decode_desc *d, const esda_decode_args *a) {
+    AttendParams ap{};
+    ap.q = static_cast<const uint16_t *>(a->q);
+    ap.k_new = static_cast<const uint16_t *>(a->k_new);
+    ap.v_new = static_cast<const uint16_t *>(d->kv_shared ? a->k_new : a->v_new);
+    ap.k_cache = static_cast<uint16_t *>(a->k_cache);
+    ap.v_cache = static_cast<uint16_t *>(a->v_cache);
+    ap.pos = a->pos;
+    ap.row_base = a->row_base;
+    return ap;
+}
+
+}  // namespace
+
+// ------------------------------------------------ static scratch of esda_decode_noalloc
+//
+// The split partials, the batch prefix table and (when the caller passes no status word)
+// the skipped-sequence counter of esda_decode_noalloc live here instead of in a caller
+// workspace.  Every GPU the library runs on holds its own copy for the life of the
+// process.  In host code `scratch` names a host-side stand-in, never the device memory:
+// kernels get the address hipGetSymbolAddress returns for the current device.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per device.
+int scratch_address(void **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(ESDA_ERR_DEVICE, "device index out of range");
+    static std::mutex mu;
+    static void *addr[64] = {nullptr};
+    std::lock_guard<std::mutex> lk(mu);
+    if (!addr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(ESDA_ERR_RUNTIME, "hipGetSymbolAddress(scratch) returned null");
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return ESDA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1608,35 +1673,39 @@ int esda_decode_stages(const esda_decode_desc *d, const esda_decode_args *a, int
     Plan pl;
     int rc = make_plan(d, &pl);
     if (rc) return rc;
-    if (!a) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: null arguments");
-    if (!a->q || !a->k_new || !a->k_cache || !a->v_cache || !a->pos || !a->out)
-        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: null device pointer");
-    if (!d->kv_shared && !a->v_new)
-        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: v_new is required unless kv_shared");
-    if (d->kv_shared && a->v_cache != a->k_cache)
-        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: kv_shared needs v_cache == k_cache");
-    if (!d->kv_shared && a->v_cache == a->k_cache)
-        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: separate K/V need distinct caches");
-    if (!aligned16(a->q) || !aligned16(a->k_new) || (a->v_new && !aligned16(a->v_new)) ||
-        !aligned16(a->k_cache) || !aligned16(a->v_cache) || !aligned16(a->out))
-        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: tensors must be 16-byte aligned");
+    rc = check_decode_args(d, a);
+    if (rc) return rc;
     if (!a->workspace || a->workspace_bytes < pl.bytes || !aligned16(a->workspace))
         return fail(ESDA_ERR_WORKSPACE, "esda_decode: workspace missing or smaller than esda_decode_workspace_size");
     if ((stages & (ESDA_STAGE_ATTEND | ESDA_STAGE_MERGE)) == 0 || (stages & ~3))
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode_stages: bad stage mask");
     rc = check_device();
     if (rc) return rc;
-
-    AttendParams ap{};
-    ap.q = static_cast<const uint16_t *>(a->q);
-    ap.k_new = static_cast<const uint16_t *>(a->k_new);
-    ap.v_new = static_cast<const uint16_t *>(d->kv_shared ? a->k_new : a->v_new);
-    ap.k_cache = static_cast<uint16_t *>(a->k_cache);
-    ap.v_cache = static_cast<uint16_t *>(a->v_cache);
-    ap.pos = a->pos;
-    ap.row_base = a->row_base;
-    return run_stages(d, pl, ap, static_cast<uint16_t *>(a->out), a->workspace, stages, 0,
+    return run_stages(d, pl, decode_params(d, a), static_cast<uint16_t *>(a->out), a->workspace, stages, 0,
                       reinterpret_cast<hipStream_t>(stream));
+}
+
+int esda_decode_noalloc(const esda_decode_desc *d, const esda_decode_args *a, void *stream) {
+    Plan pl;
+    int rc = make_plan(d, &pl);
+    if (rc) return rc;
+    rc = check_decode_args(d, a);
+    if (rc) return rc;
+    // The workspace argument is optional here and only ever the status word.
+    if (a->workspace && (a->workspace_bytes < sizeof(int32_t) || (reinterpret_cast<uintptr_t>(a->workspace) & 3u)))
+        return fail(ESDA_ERR_WORKSPACE, "esda_decode_noalloc: a status word needs >= 4 bytes, 4-byte aligned");
+    if (pl.bytes > kScratchBytes)
+        return fail(ESDA_ERR_WORKSPACE, "esda_decode_noalloc: this step needs " + std::to_string(pl.bytes) +
+                                            " bytes of scratch; the library's static scratch holds " +
+                                            std::to_string(kScratchBytes) + " (use esda_decode with a workspace)");
+    rc = check_device();
+    if (rc) return rc;
+    void *ws = nullptr;
+    rc = scratch_address(&ws);
+    if (rc) return rc;
+    int *status = a->workspace ? static_cast<int *>(a->workspace) : static_cast<int *>(ws);
+    return run_stages(d, pl, decode_params(d, a), static_cast<uint16_t *>(a->out), ws,
+                      ESDA_STAGE_ATTEND | ESDA_STAGE_MERGE, 0, reinterpret_cast<hipStream_t>(stream), status);
 }
 
 int esda_decode(const esda_decode_desc *desc, const esda_decode_args *args, void *stream) {

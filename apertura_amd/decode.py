@@ -113,6 +113,37 @@ def decode_step(step: DecodeStep, q: torch.Tensor, k_new: torch.Tensor, v_new: t
     return out
 
 
+def decode_step_noalloc(step: DecodeStep, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor | None,
+                        k_cache: torch.Tensor, v_cache: torch.Tensor | None, pos: torch.Tensor,
+                        out: torch.Tensor, row_base: torch.Tensor | None = None,
+                        status: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """esda_decode_noalloc: decode_step with the library's static scratch instead of a
+    workspace; nothing is allocated (``out`` is required).  ``status``: an optional int32
+    device word counting skipped sequences (read with decode_status)."""
+    bf = torch.bfloat16
+    if q.shape != (step.batch, step.num_q_heads, step.head_dim) or not q.is_contiguous():
+        raise ValueError(f"q must be contiguous [B, Hq, D], got {tuple(q.shape)}")
+    if k_new.shape != (step.batch, step.num_kv_heads, step.head_dim) or not k_new.is_contiguous():
+        raise ValueError("k_new must be contiguous [B, Hkv, D]")
+    if v_new is not None and (v_new.shape != k_new.shape or not v_new.is_contiguous()):
+        raise ValueError("v_new must be contiguous [B, Hkv, D]")
+    if pos.dtype != torch.int32 or pos.shape != (step.batch,):
+        raise ValueError("pos must be int32 [B]")
+    if out.shape != q.shape or not out.is_contiguous():
+        raise ValueError("out must be contiguous [B, Hq, D]")
+    if status is not None and (status.dtype != torch.int32 or status.numel() < 1):
+        raise ValueError("status must be an int32 device tensor")
+    vc = k_cache if (v_cache is None or step.kv_shared) else v_cache
+    args = DecodeArgs(_dev_ptr(q, bf), _dev_ptr(k_new, bf),
+                      _dev_ptr(v_new, bf) if (v_new is not None and not step.kv_shared) else None,
+                      _dev_ptr(k_cache, bf), _dev_ptr(vc, bf), _dev_ptr(pos),
+                      _dev_ptr(row_base), _dev_ptr(out, bf), _dev_ptr(status),
+                      0 if status is None else status.numel() * 4)
+    d = step.desc()
+    check(lib().esda_decode_noalloc(ctypes.byref(d), ctypes.byref(args), _stream_ptr(stream)))
+    return out
+
+
 def decode_status(step: DecodeStep, workspace: torch.Tensor, stream=None) -> int:
     """Number of sequences the kernels skipped (position outside the cache) since the
     last call; clears the counter."""

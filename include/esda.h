@@ -103,6 +103,22 @@ int esda_decode_stages(const esda_decode_desc *desc, const esda_decode_args *arg
 int esda_decode_status(const esda_decode_desc *desc, void *workspace, int32_t *bad_sequences,
                        void *stream);
 
+/* esda_decode without a workspace and without any allocation: the split partials and the
+ * batch prefix table live in a static device array the library holds on every GPU it runs
+ * on (32 MiB per GPU, until the process ends).  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).
+ * - args->workspace is optional.  When given (device memory, >= 4 bytes, 4-byte aligned)
+ *   it is only the skipped-sequence status word, read and cleared by esda_decode_status;
+ *   zero it once before first use.  When NULL, skipped sequences are not reported.
+ * - A step whose esda_decode_workspace_size exceeds 32 MiB is refused with
+ *   ESDA_ERR_WORKSPACE (nothing is launched); such steps need esda_decode.
+ * - Calls that overlap on one GPU (e.g. on two streams) share the array and race: order
+ *   them on one stream, or use esda_decode with a workspace per stream.
+ * The first call on a device looks up the array's address there (hipGetSymbolAddress),
+ * so make that call outside graph capture.  Same kernels and results as esda_decode. */
+int esda_decode_noalloc(const esda_decode_desc *desc, const esda_decode_args *args, void *stream);
+
 /* Copy n_new rows per (sequence, kv head) into a linear cache at rows
  * row0[b] .. row0[b]+n_new-1: the reference's slice_update append
  * (ESKVCache.mm:97-98).  src: [B, Hkv, n_new, D] bf16. */
