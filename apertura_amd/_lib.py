@@ -27,7 +27,8 @@ EXPORTS = (
     "esda_fill_i32", "esda_last_error", "esda_version",
     # include/esda_cache.h
     "esda_cache_create", "esda_cache_destroy", "esda_cache_update", "esda_cache_update_raw",
-    "esda_cache_current", "esda_cache_current_raw", "esda_cache_decode", "esda_cache_decode_raw", "esda_cache_slot",
+    "esda_cache_current", "esda_cache_current_raw",
+    "esda_cache_begin_step", "esda_cache_end_step", "esda_cache_set_slot", "esda_cache_slot_kv", "esda_cache_take_slot", "esda_cache_decode", "esda_cache_decode_raw", "esda_cache_slot",
     "esda_cache_seq_len", "esda_cache_mark_step", "esda_cache_reset", "esda_cache_save_snapshot",
     "esda_cache_restore_snapshot", "esda_cache_restore_snapshot_ex", "esda_cache_mark_prefix",
     "esda_cache_mark_rewind_point", "esda_cache_rewind_to_mark", "esda_cache_clear_rewind_mark",
@@ -176,6 +177,11 @@ def lib() -> ctypes.CDLL:
         L.esda_cache_update.argtypes = [P, i32, P, P, i32, i32, i32, i32, i32, P, VP, VP]
         L.esda_cache_update_raw.argtypes = [P, i32, P, i32, i32, i32, i32, P, VP, pi32, pi32]
         L.esda_cache_current.argtypes = [P, i32, i32, VP, VP]
+        L.esda_cache_begin_step.argtypes = [P, P, P]
+        L.esda_cache_end_step.argtypes = [P]
+        L.esda_cache_set_slot.argtypes = [P, i32, P, P, i32, i32, i32]
+        L.esda_cache_slot_kv.argtypes = [P, i32, VP, VP]
+        L.esda_cache_take_slot.argtypes = [P, i32, VP, VP]
         L.esda_cache_current_raw.argtypes = [P, i32, VP, pi32, pi32]
         L.esda_cache_decode.argtypes = [P, i32, P, i32, P, P, i32, i32, i32, i32, f32, P, P]
         L.esda_cache_decode_raw.argtypes = [P, i32, P, i32, P, i32, P, f32, P, i32, P, P]

@@ -135,6 +135,40 @@ class ESKVCache:
         check(lib().esda_cache_current(self._h, layer, 1 if prealloc else 0, ctypes.byref(kv), ctypes.byref(vv)))
         return CacheView.of(kv), CacheView.of(vv)
 
+    # -------------------------------------------- compiled-step mode (ESKVCache.h:93-112)
+
+    def begin_step(self, global_idx: torch.Tensor, sliding_idx: torch.Tensor) -> None:
+        """Until end_step, update() writes its one row at the cache row held in the int32
+        device word global_idx (max_keep == 0) or sliding_idx (max_keep > 0)."""
+        for t in (global_idx, sliding_idx):
+            if t.dtype != torch.int32 or t.numel() < 1 or not t.is_cuda:
+                raise ValueError("step indices must be int32 device tensors")
+        self._step_idx = (global_idx, sliding_idx)  # kept alive while the step runs
+        check(lib().esda_cache_begin_step(self._h, _dev_ptr(global_idx), _dev_ptr(sliding_idx)))
+
+    def end_step(self) -> None:
+        check(lib().esda_cache_end_step(self._h))
+        self._step_idx = None
+
+    def set_slot(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Install [kv_heads, cap, head_dim] bf16 buffers (v may be k: shared K=V); the
+        caller keeps them alive while the cache refers to them."""
+        kvh, cap, hd = _rows(k, "k")
+        if v.shape != k.shape:
+            raise ValueError("set_slot: k and v differ in shape")
+        _rows(v, "v")
+        check(lib().esda_cache_set_slot(self._h, layer, _dev_ptr(k), _dev_ptr(v), kvh, cap, hd))
+
+    def slot_kv(self, layer: int) -> tuple[CacheView, CacheView]:
+        kv, vv = View(), View()
+        check(lib().esda_cache_slot_kv(self._h, layer, ctypes.byref(kv), ctypes.byref(vv)))
+        return CacheView.of(kv), CacheView.of(vv)
+
+    def take_slot(self, layer: int) -> tuple[CacheView, CacheView]:
+        kv, vv = View(), View()
+        check(lib().esda_cache_take_slot(self._h, layer, ctypes.byref(kv), ctypes.byref(vv)))
+        return CacheView.of(kv), CacheView.of(vv)
+
     def current_raw(self, layer: int):
         """(view, len, pitch) of a prealloc raw-K slot without appending."""
         v, ln, pitch = View(), ctypes.c_int32(), ctypes.c_int32()

@@ -8,8 +8,10 @@
 #include <optional>
 #include <stdexcept>
 #include <string>
-#include <unordered_map>
+#include <map>
+#include <utility>
 
+#include "es/ESKVCache.h"
 #include "esda.h"
 
 namespace es {
@@ -25,7 +27,7 @@ void esdaCheck(int rc) {
     throw std::runtime_error(esda_last_error());
 }
 
-// Per-thread, per-device scratch: the split workspace, the position word, the last
+// Per-thread, per-device, per-stream scratch: the split workspace, the position word, the last
 // rotary frequencies uploaded (the reference passes them by value on every call) and
 // their cos/sin table (esda_rope_table, grown in 4096-row steps).
 struct Scratch {
@@ -46,11 +48,13 @@ const void *ropeTable(Scratch &s, int rows, hipStream_t st) {
     return s.ropeTab->data;
 }
 
-Scratch &scratch() {
-    thread_local std::unordered_map<int, Scratch> perDevice;
+// One scratch set per (device, stream) of the calling thread: calls on different streams
+// never share a position word, workspace or rebuilt rows, so they may overlap.
+Scratch &scratch(hipStream_t st) {
+    thread_local std::map<std::pair<int, hipStream_t>, Scratch> perStream;
     int dev = 0;
     hipCheck(hipGetDevice(&dev), "hipGetDevice");
-    return perDevice[dev];
+    return perStream[{dev, st}];
 }
 
 }  // namespace
@@ -72,7 +76,7 @@ Tensor esDecodeAttnGlobal(const Tensor &q, const Tensor &rawBuf, int len, int pi
         throw std::invalid_argument("esDecodeAttnGlobal: kw must be contiguous bf16 [512]");
     if (invFreq.size() < 64) throw std::invalid_argument("esDecodeAttnGlobal: invFreq needs >= 64 entries");
 
-    Scratch &s = scratch();
+    Scratch &s = scratch(st);
     if (!s.invFreq || s.invFreqHost.size() != 64 || !std::equal(s.invFreqHost.begin(), s.invFreqHost.end(), invFreq.begin())) {
         if (s.invFreq) hipCheck(hipStreamSynchronize(st), "esDecodeAttnGlobal rotary table");
         s.invFreqHost.assign(invFreq.begin(), invFreq.begin() + 64);
@@ -152,7 +156,7 @@ Tensor esDecodeAttnGlobalQ8(const Tensor &q, const Tensor &qBuf, const Tensor &s
     if (!kw.defined() || kw.dtype != Dtype::bf16 || kw.numel() != 512 || !kw.contiguous())
         throw std::invalid_argument("esDecodeAttnGlobalQ8: kw must be contiguous bf16 [512]");
 
-    Scratch &s = scratch();
+    Scratch &s = scratch(st);
     if (!s.invFreq || s.invFreqHost.size() != 64 || !std::equal(s.invFreqHost.begin(), s.invFreqHost.end(), invFreq.begin())) {
         if (s.invFreq) hipCheck(hipStreamSynchronize(st), "esDecodeAttnGlobalQ8 rotary table");
         s.invFreqHost.assign(invFreq.begin(), invFreq.begin() + 64);
@@ -211,6 +215,10 @@ Tensor esDecodeAttnGlobalQ8(const Tensor &q, const Tensor &qBuf, const Tensor &s
     a.workspace_bytes = s.workspace->nbytes();
     esdaCheck(esda_decode_raw_q8(&d, &a, st));
     return o;
+}
+
+std::array<Tensor, 3> esQuantizeRawRows(const Tensor &kNew, hipStream_t stream) {
+    return ESKVCache::quantizeRawRows(kNew, stream);
 }
 
 }  // namespace es

@@ -139,6 +139,29 @@ std::pair<Tensor, Tensor> ESKVCache::update(int layer, const Tensor &kNew, const
     checkRows(vNew, "ESKVCache::update vNew");
     if (kNew.shape[1] != vNew.shape[1])
         throw std::invalid_argument("ESKVCache::update: kNew and vNew hold different row counts");
+    if (stepMode_) {
+        // Compiled-step append (ESKVCache.mm:21-33): the row comes from the step's index
+        // tensor on the device, so the same launches serve every position; the whole
+        // fixed-capacity buffers are returned (the step's mask hides unwritten rows).
+        Slot &s = slots_[layer];
+        if (!s.k || !s.v) throw std::runtime_error("ESKVCache::update: compiled-step slot not set (setSlot)");
+        if (kNew.shape[1] != 1) throw std::invalid_argument("ESKVCache::update: a compiled step appends one row");
+        const Tensor &idx = maxKeep > 0 ? *stepSlidingIdx_ : *stepGlobalIdx_;
+        auto scatter = [&](const Tensor &buf, const Tensor &row) {
+            if (buf.dim() != 3 || buf.shape[0] != row.shape[0] || buf.shape[2] != row.shape[2] ||
+                buf.strides[2] != 1 || buf.strides[1] != buf.shape[2])
+                throw std::invalid_argument("ESKVCache::update: kNew / vNew do not match the compiled-step slot");
+            // esda_kv_append reads [1, kvH, 1, hd] rows packed head after head
+            const Tensor src = row.strides[0] == row.shape[2] ? row : clone(row, st);
+            const int cap = (int) buf.shape[1], hd = (int) buf.shape[2], kvH = (int) buf.shape[0];
+            esdaCheck(esda_kv_append(buf.data, buf.strides[0] * kvH, buf.strides[0], 1, kvH, hd, cap, src.data, 1,
+                                     static_cast<const int32_t *>(idx.data), st));
+            if (src.data != row.data) hipCheck(hipStreamSynchronize(st), "ESKVCache step append");  // copy released
+        };
+        scatter(*s.k, kNew);
+        if (s.v->data != s.k->data || vNew.data != kNew.data) scatter(*s.v, vNew);
+        return {*s.k, *s.v};
+    }
     if (!prealloc) {
         // Legacy mode (ESKVCache.mm:35-55): concat-grow, then keep the last maxKeep keys.
         auto &K = k_[layer];
@@ -187,6 +210,69 @@ std::pair<Tensor, Tensor> ESKVCache::update(int layer, const Tensor &kNew, const
     // Sliding-window eviction advances the logical start (ESKVCache.mm:102-104).
     if (maxKeep > 0 && s.len - s.start > maxKeep) s.start = s.len - maxKeep;
     return {liveView(*s.k, s.start, s.len), liveView(*s.v, s.start, s.len)};
+}
+
+ESKVCache::QKV ESKVCache::updateQuant(int layer, const Tensor &, const Tensor &, int, int, bool) {
+    checkLayer(layer);
+    throw std::runtime_error("ESKVCache::updateQuant: quantized-KV storage (quantized_matmul groups) is not "
+                             "built by this library; use bf16, raw-K or q8 raw-K storage");
+}
+
+// ------------------------------------------------------------------ compiled-step mode
+
+void ESKVCache::beginStep(const Tensor &globalIdx, const Tensor &slidingIdx) {
+    for (const Tensor *t : {&globalIdx, &slidingIdx})
+        if (!t->defined() || t->dtype != Dtype::i32 || t->numel() < 1)
+            throw std::invalid_argument("ESKVCache::beginStep: indices must be device int32 [1] tensors");
+    stepGlobalIdx_ = globalIdx;
+    stepSlidingIdx_ = slidingIdx;
+    stepMode_ = true;
+}
+
+void ESKVCache::endStep() {
+    stepMode_ = false;
+    stepGlobalIdx_.reset();
+    stepSlidingIdx_.reset();
+}
+
+const Tensor &ESKVCache::slotK(int layer) const {
+    const Slot &s = slotAt(layer);
+    if (!s.k) throw std::runtime_error("ESKVCache::slotK: slot holds no buffer");
+    return *s.k;
+}
+
+const Tensor &ESKVCache::slotV(int layer) const {
+    const Slot &s = slotAt(layer);
+    if (!s.v) throw std::runtime_error("ESKVCache::slotV: slot holds no buffer");
+    return *s.v;
+}
+
+void ESKVCache::setSlot(int layer, Tensor k, Tensor v) {
+    checkLayer(layer);
+    checkRows(k, "ESKVCache::setSlot k");
+    checkRows(v, "ESKVCache::setSlot v");
+    Slot &s = slots_[layer];
+    s.shared = k.data == v.data;
+    s.k = std::move(k);
+    s.v = std::move(v);
+}
+
+Tensor ESKVCache::takeSlotK(int layer) {
+    checkLayer(layer);
+    Slot &s = slots_[layer];
+    if (!s.k) throw std::runtime_error("ESKVCache::takeSlotK: slot holds no buffer");
+    Tensor t = std::move(*s.k);
+    s.k.reset();
+    return t;
+}
+
+Tensor ESKVCache::takeSlotV(int layer) {
+    checkLayer(layer);
+    Slot &s = slots_[layer];
+    if (!s.v) throw std::runtime_error("ESKVCache::takeSlotV: slot holds no buffer");
+    Tensor t = std::move(*s.v);
+    s.v.reset();
+    return t;
 }
 
 std::pair<Tensor, Tensor> ESKVCache::current(int layer, bool prealloc) const {
@@ -270,6 +356,7 @@ int *ESKVCache::positionWord(int layer, int value, hipStream_t st) {
 
 Tensor ESKVCache::decode(int layer, const Tensor &q, const Tensor &kNew, const Tensor &vNew, int maxKeep,
                          int window, float scale, hipStream_t st, Tensor *out) {
+    if (stepMode_) throw std::runtime_error("ESKVCache::decode: not available in compiled-step mode (beginStep .. endStep)");
     checkLayer(layer);
     checkRows(kNew, "ESKVCache::decode kNew");
     checkRows(vNew, "ESKVCache::decode vNew");
@@ -352,6 +439,7 @@ Tensor ESKVCache::decode(int layer, const Tensor &q, const Tensor &kNew, const T
 
 Tensor ESKVCache::decodeRaw(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
                             const std::vector<float> &invFreq, hipStream_t st, Tensor *out) {
+    if (stepMode_) throw std::runtime_error("ESKVCache::decodeRaw: not available in compiled-step mode (beginStep .. endStep)");
     checkLayer(layer);
     checkRows(kNew, "ESKVCache::decodeRaw kNew");
     if (kNew.shape[1] != 1 || kNew.shape[2] != 512)
@@ -552,6 +640,7 @@ ESKVCache::RawQ8 ESKVCache::updateRawQ8(int layer, const Tensor &kNew, hipStream
 
 Tensor ESKVCache::decodeRawQ8(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
                               const std::vector<float> &invFreq, hipStream_t st, Tensor *out) {
+    if (stepMode_) throw std::runtime_error("ESKVCache::decodeRawQ8: not available in compiled-step mode (beginStep .. endStep)");
     checkLayer(layer);
     checkRows(kNew, "ESKVCache::decodeRawQ8 kNew");
     if (kNew.shape[1] != 1 || kNew.shape[2] != 512)

@@ -8,7 +8,8 @@
 #include <optional>
 #include <stdexcept>
 #include <string>
-#include <unordered_map>
+#include <map>
+#include <utility>
 
 #include "es/ESKVCache.h"
 #include "esda.h"
@@ -27,7 +28,7 @@ void esdaCheck(int rc) {
     throw std::runtime_error(esda_last_error());
 }
 
-// Per-thread, per-device scratch: the split workspace, the rebuilt K / V of a raw-K
+// Per-thread, per-device, per-stream scratch: the split workspace, the rebuilt K / V of a raw-K
 // prefill and the last rotary table uploaded.  Growth waits for the stream so that no
 // queued kernel still reads a buffer being released.
 struct Scratch {
@@ -35,11 +36,13 @@ struct Scratch {
     std::vector<float> invFreqHost;
 };
 
-Scratch &scratch() {
-    thread_local std::unordered_map<int, Scratch> perDevice;
+// One scratch set per (device, stream) of the calling thread: calls on different streams
+// never share a position word, workspace or rebuilt rows, so they may overlap.
+Scratch &scratch(hipStream_t st) {
+    thread_local std::map<std::pair<int, hipStream_t>, Scratch> perStream;
     int dev = 0;
     hipCheck(hipGetDevice(&dev), "hipGetDevice");
-    return perDevice[dev];
+    return perStream[{dev, st}];
 }
 
 Tensor &grown(std::optional<Tensor> &slot, size_t elems, Dtype dt, hipStream_t st) {
@@ -52,7 +55,7 @@ Tensor &grown(std::optional<Tensor> &slot, size_t elems, Dtype dt, hipStream_t s
 
 // The rotary table on the device, hd/2 floats (zero-extended).
 const float *deviceInvFreq(const std::vector<float> &invFreq, int hd, hipStream_t st) {
-    Scratch &s = scratch();
+    Scratch &s = scratch(st);
     std::vector<float> want(hd / 2, 0.0f);
     std::copy_n(invFreq.begin(), std::min<size_t>(invFreq.size(), want.size()), want.begin());
     if (!s.invFreq || s.invFreqHost != want) {
@@ -115,7 +118,7 @@ Tensor attend(const Tensor &q, const Tensor &K, const Tensor &V, int qPos0, int 
     a.v = V.data;
     a.out = o.data;
     if (wsBytes) {
-        Tensor &ws = grown(scratch().workspace, wsBytes, Dtype::u8, st);
+        Tensor &ws = grown(scratch(st).workspace, wsBytes, Dtype::u8, st);
         a.workspace = ws.data;
         a.workspace_bytes = ws.nbytes();
     }
@@ -147,7 +150,7 @@ Tensor esPrefillAttnRaw(const Tensor &q, const Tensor &rawView, const Tensor &kw
         throw std::invalid_argument("esPrefillAttnRaw: the raw stream must hold pastLen + seq rows");
     if (!kw.defined() || kw.dtype != Dtype::bf16 || kw.numel() != hd || !kw.contiguous())
         throw std::invalid_argument("esPrefillAttnRaw: kw must be contiguous bf16 [hd]");
-    Scratch &s = scratch();
+    Scratch &s = scratch(st);
     const size_t n = (size_t) numKV * seqK * hd;
     Tensor &kb = grown(s.k, n, Dtype::bf16, st);
     Tensor &vb = grown(s.v, n, Dtype::bf16, st);
@@ -175,7 +178,7 @@ Tensor esPrefillAttnRawQ8(const Tensor &q, const Tensor &qView, const Tensor &sc
         throw std::invalid_argument("esPrefillAttnRawQ8: the raw stream must hold pastLen + seq rows");
     if (!kw.defined() || kw.dtype != Dtype::bf16 || kw.numel() != 512 || !kw.contiguous())
         throw std::invalid_argument("esPrefillAttnRawQ8: kw must be contiguous bf16 [512]");
-    Scratch &s = scratch();
+    Scratch &s = scratch(st);
     const size_t n = (size_t) numKV * seqK * 512;
     Tensor &kb = grown(s.k, n, Dtype::bf16, st);
     Tensor &vb = grown(s.v, n, Dtype::bf16, st);
@@ -192,6 +195,7 @@ Tensor esPrefillAttnRawQ8(const Tensor &q, const Tensor &qView, const Tensor &sc
 
 Tensor ESKVCache::prefill(int layer, const Tensor &q, const Tensor &kNew, const Tensor &vNew, int maxKeep, int window,
                           float scale, int pastLen, bool prealloc, hipStream_t st, Tensor *out) {
+    if (stepMode_) throw std::runtime_error("ESKVCache::prefill: not available in compiled-step mode (beginStep .. endStep)");
     checkQ(q, "ESKVCache::prefill");
     if (kNew.dim() != 3 || kNew.shape[1] != q.shape[1])
         throw std::invalid_argument("ESKVCache::prefill: kNew must hold one row per query");
@@ -202,6 +206,7 @@ Tensor ESKVCache::prefill(int layer, const Tensor &q, const Tensor &kNew, const 
 Tensor ESKVCache::prefillRaw(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
                              const std::vector<float> &invFreq, int pastLen, float scale, bool q8, hipStream_t st,
                              Tensor *out) {
+    if (stepMode_) throw std::runtime_error("ESKVCache::prefillRaw: not available in compiled-step mode (beginStep .. endStep)");
     checkQ(q, "ESKVCache::prefillRaw");
     if (kNew.dim() != 3 || kNew.shape[1] != q.shape[1])
         throw std::invalid_argument("ESKVCache::prefillRaw: kNew must hold one row per query");

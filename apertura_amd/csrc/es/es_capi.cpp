@@ -111,6 +111,49 @@ int esda_cache_current(esda_cache *cache, int32_t layer, int32_t prealloc, esda_
     });
 }
 
+int esda_cache_begin_step(esda_cache *cache, const int32_t *global_idx, const int32_t *sliding_idx) {
+    return guarded([&] {
+        needCache(cache);
+        if (!global_idx || !sliding_idx) throw std::invalid_argument("esda_cache_begin_step: null index");
+        cache->impl.beginStep(es::Tensor::wrap(const_cast<int32_t *>(global_idx), {1}, es::Dtype::i32),
+                              es::Tensor::wrap(const_cast<int32_t *>(sliding_idx), {1}, es::Dtype::i32));
+    });
+}
+
+int esda_cache_end_step(esda_cache *cache) {
+    return guarded([&] {
+        needCache(cache);
+        cache->impl.endStep();
+    });
+}
+
+int esda_cache_set_slot(esda_cache *cache, int32_t layer, void *k, void *v, int32_t kv_heads, int32_t cap,
+                        int32_t head_dim) {
+    return guarded([&] {
+        needCache(cache);
+        cache->impl.setSlot(layer, rows(k, kv_heads, cap, head_dim), rows(v, kv_heads, cap, head_dim));
+    });
+}
+
+int esda_cache_slot_kv(esda_cache *cache, int32_t layer, esda_view *k_out, esda_view *v_out) {
+    return guarded([&] {
+        needCache(cache);
+        toView(cache->impl.slotK(layer), k_out);
+        toView(cache->impl.slotV(layer), v_out);
+    });
+}
+
+int esda_cache_take_slot(esda_cache *cache, int32_t layer, esda_view *k_out, esda_view *v_out) {
+    return guarded([&] {
+        needCache(cache);
+        // both present before either is taken, so a failure leaves the slot as it was
+        (void) cache->impl.slotK(layer);
+        (void) cache->impl.slotV(layer);
+        toView(cache->impl.takeSlotK(layer), k_out);
+        toView(cache->impl.takeSlotV(layer), v_out);
+    });
+}
+
 int esda_cache_decode(esda_cache *cache, int32_t layer, const void *q, int32_t num_q_heads, const void *k_new,
                       const void *v_new, int32_t kv_heads, int32_t head_dim, int32_t max_keep, int32_t window,
                       float scale, void *out, void *stream) {

@@ -9,6 +9,7 @@
 //  then attends the query heads of each kv head, split-K, merged in fp32.
 #include "ESTensor.h"
 
+#include <array>
 #include <vector>
 
 namespace es {
@@ -29,5 +30,10 @@ Tensor esDecodeAttnGlobal(const Tensor &q, const Tensor &rawBuf, int len, int pi
 Tensor esDecodeAttnGlobalQ8(const Tensor &q, const Tensor &qBuf, const Tensor &scBuf, const Tensor &bsBuf,
                             int len, int pitch, const Tensor &kw, float eps, const std::vector<float> &invFreq,
                             hipStream_t stream = nullptr, Tensor *out = nullptr);
+
+// Per-row affine u8 quantizer (esQuantizeRawRows, ESDecodeAttn.h:39-43, ESDecodeAttn.mm:491-539):
+// kNew [kvH, n, 512] bf16 -> {q u8 [kvH, n, 512], scale f32 [kvH, n, 1], bias f32 [kvH, n, 1]}
+// with x ~ q * scale + bias.  One launch of quantize_rows_kernel (esda_quantize_raw_rows).
+std::array<Tensor, 3> esQuantizeRawRows(const Tensor &kNew, hipStream_t stream = nullptr);
 
 }  // namespace es

@@ -13,9 +13,11 @@
 //  chunk and attend it (ESAttention.mm:168-193, 253-332 at seq > 1).
 //  q8 raw-K storage (rawKVQ8: per-row affine u8 rows with an f32 scale and bias,
 //  ESKVCache.mm:506-566), KV snapshots (the reference's safetensors layout), prefix
-//  markers and turn rewind follow the reference (ESKVCache.mm:121-456).  Quantized-KV
-//  storage (quantized_matmul groups) and the compiled step mode are not implemented:
-//  quantized-KV snapshots are refused (-1).
+//  markers and turn rewind follow the reference (ESKVCache.mm:121-456), and so does the
+//  compiled-step mode (ESKVCache.h:93-112: scatter appends at a device position into
+//  full-capacity slots).  Quantized-KV storage (quantized_matmul groups, updateQuant) is
+//  declared with the reference's signature and throws std::runtime_error; quantized-KV
+//  snapshots are refused (-1).
 //
 //  Every call takes a HIP stream (nullptr = the default stream).  Buffer growth and
 //  compaction synchronise that stream before the old buffer is released.  An instance
@@ -30,6 +32,23 @@
 #include <vector>
 
 namespace es {
+
+// Per-forward shared-KV scratch of elastic models (ESKVCache.h:31-42): the last layer of
+// each attention type that stores its full K/V leaves them here for the shared layers of
+// that type.  Type index 0 = sliding (local), 1 = full (global).  get() of a type nothing
+// stored throws std::bad_optional_access.
+struct ESSharedKV {
+    std::optional<Tensor> k_[2], v_[2];
+    void store(bool sliding, const Tensor &k, const Tensor &v) {
+        const int t = sliding ? 0 : 1;
+        k_[t] = k;
+        v_[t] = v;
+    }
+    std::pair<Tensor, Tensor> get(bool sliding) const {
+        const int t = sliding ? 0 : 1;
+        return {k_[t].value(), v_[t].value()};
+    }
+};
 
 class ESKVCache {
 public:
@@ -46,8 +65,34 @@ public:
     // Throws std::runtime_error when the slot holds raw-K content (ESKVCache.mm:59-62).
     // In prealloc mode a slot first filled with vNew aliasing kNew keeps one shared K=V
     // buffer (attention_k_eq_v); later appends to it must alias too.
+    // In compiled-step mode (beginStep .. endStep) the mode arguments are ignored: the
+    // single new row is written at the row the step's position tensor holds (slidingIdx
+    // when maxKeep > 0, else globalIdx) and the full-capacity slot buffers are returned.
     std::pair<Tensor, Tensor> update(int layer, const Tensor &kNew, const Tensor &vNew, int maxKeep = 0,
                                      bool prealloc = false, hipStream_t stream = nullptr);
+
+    // Quantized KV (ESKVCache.h:60-70): {packed, scales, biases} for K and V.  Not built
+    // by this library (a quantized_matmul storage path, not the decode-attention kernels):
+    // always throws std::runtime_error.
+    struct QKV {
+        Tensor kq, ks, kb, vq, vs, vb;
+    };
+    QKV updateQuant(int layer, const Tensor &kNew, const Tensor &vNew, int groupSize, int bits,
+                    bool prealloc = false);
+
+    // Compiled-step mode (ESKVCache.h:93-112).  beginStep takes device int32 [1] tensors
+    // holding the cache ROW of this token for global and for sliding layers; until
+    // endStep, update() scatters there (esda_kv_append with a device row index, so a
+    // captured graph replays for any position).  The step driver owns slot layout and
+    // compaction through slotK / slotV / setSlot / takeSlotK / takeSlotV.  Slot accessors
+    // throw std::runtime_error for an empty slot.
+    void beginStep(const Tensor &globalIdx, const Tensor &slidingIdx);
+    void endStep();
+    const Tensor &slotK(int layer) const;
+    const Tensor &slotV(int layer) const;
+    void setSlot(int layer, Tensor k, Tensor v);
+    Tensor takeSlotK(int layer);
+    Tensor takeSlotV(int layer);
 
     // Raw-K storage: only the pre-norm k_proj rows, one stream (ESKVCache.mm:458-504).
     // {live view [kvHeads, len, headDim], whole buffer, len, pitch (= buffer rows)}.
@@ -186,6 +231,9 @@ private:
     void migrateToQ8(int layer, hipStream_t stream);
     Marker takeMarker(int pos, bool copyLost, hipStream_t stream) const;
     int seqLen_ = 0;
+    // Compiled-step mode state (beginStep): the row index tensors of this token.
+    bool stepMode_ = false;
+    std::optional<Tensor> stepGlobalIdx_, stepSlidingIdx_;
     std::optional<Tensor> posDev_;     // per-layer position words for decode()
     std::optional<Tensor> workspace_;  // esda_decode / esda_decode_raw workspace
     std::optional<Tensor> invFreqDev_; // rotary table of the last decodeRaw()

@@ -14,6 +14,7 @@
  *   esda_cache_update_raw          ESKVCache::updateRaw                ESKVCache.h:78-79, ESKVCache.mm:458-504
  *   esda_cache_current             ESKVCache::current                  ESKVCache.h:117, ESKVCache.mm:112-119
  *   esda_cache_decode              ESKVCache::update + SDPA decode     ESAttention.mm:105, :188
+ *   esda_cache_begin_step .. take_slot  compiled-step members          ESKVCache.h:93-112
  *   esda_cache_decode_raw          updateRaw + esDecodeAttnGlobal      ESAttention.mm:291-300
  *   esda_cache_update_raw_q8       ESKVCache::updateRawQ8              ESKVCache.h:81-88, ESKVCache.mm:513-556
  *   esda_cache_decode_raw_q8       updateRawQ8 + esDecodeAttnGlobalQ8  ESAttention.mm:270-277
@@ -70,6 +71,20 @@ int esda_cache_update_raw(esda_cache *cache, int32_t layer, const void *k_new, i
 
 int esda_cache_current(esda_cache *cache, int32_t layer, int32_t prealloc, esda_view *k_out,
                        esda_view *v_out);
+
+/* Compiled-step mode (ESKVCache::beginStep / endStep / setSlot / slotK / slotV / takeSlotK /
+ * takeSlotV, ESKVCache.h:93-112; driven by ESGenerationLoop.mm:122-238).  Between begin and
+ * end, esda_cache_update writes its one new row at the cache row held in the device int32
+ * word global_idx (max_keep == 0) or sliding_idx (max_keep > 0) and returns the whole slot
+ * buffers.  set_slot installs caller-owned [kv_heads, cap, head_dim] bf16 buffers (v == k:
+ * one shared K=V buffer), which must outlive their use; slot_kv views them; take_slot views
+ * and then empties the slot. */
+int esda_cache_begin_step(esda_cache *cache, const int32_t *global_idx, const int32_t *sliding_idx);
+int esda_cache_end_step(esda_cache *cache);
+int esda_cache_set_slot(esda_cache *cache, int32_t layer, void *k, void *v, int32_t kv_heads, int32_t cap,
+                        int32_t head_dim);
+int esda_cache_slot_kv(esda_cache *cache, int32_t layer, esda_view *k_out, esda_view *v_out);
+int esda_cache_take_slot(esda_cache *cache, int32_t layer, esda_view *k_out, esda_view *v_out);
 /* A prealloc raw-K slot's live rows without appending: no counterpart in the reference,
  * whose callers see the raw view only from updateRaw; for callers and tests that inspect
  * a raw slot (e.g. after a snapshot restore or a rewind). */

@@ -233,3 +233,78 @@ def test_unprimed_cache_failure_values_and_step_counter(tmp_path):
     assert cache.seq_len() == 7
     cache.reset()
     assert cache.seq_len() == 0
+
+
+def test_compiled_step_mode_scatters_at_device_positions():
+    """Compiled-step mode (ESKVCache.h:93-112, driven as ESGenerationLoop.mm:104-238 does):
+    slots adopted with setSlot, then update() inside beginStep .. endStep writes the one
+    new row at the row the device index words hold -- the sliding index for maxKeep > 0,
+    the global index otherwise -- and returns the full-capacity buffers.  The appends are
+    captured once in a HIP graph and replayed for several positions set on the device
+    between replays; every byte of both slots matches a host model after each replay.
+    takeSlot empties a slot; the fused calls refuse to run inside a step."""
+    from apertura_amd._lib import EsdaError
+    from apertura_amd.cache import ESKVCache
+    rng = np.random.default_rng(71)
+    W, capS, capG = 16, 32, 96
+    cache = ESKVCache(2)
+    # layer 0: sliding, separate K / V (hd 256); layer 1: global, one shared K=V buffer (hd 512)
+    sk = torch.zeros((2, capS, 256), dtype=torch.bfloat16, device="cuda")
+    sv = torch.zeros_like(sk)
+    g = torch.zeros((2, capG, 512), dtype=torch.bfloat16, device="cuda")
+    cache.set_slot(0, sk, sv)
+    cache.set_slot(1, g, g)
+    model = {"sk": np.zeros((2, capS, 256), np.uint16), "sv": np.zeros((2, capS, 256), np.uint16),
+             "g": np.zeros((2, capG, 512), np.uint16)}
+    gidx = torch.zeros(1, dtype=torch.int32, device="cuda")
+    sidx = torch.zeros(1, dtype=torch.int32, device="cuda")
+    kn_s, vn_s = torch.empty((2, 1, 256), dtype=torch.bfloat16, device="cuda"), torch.empty(
+        (2, 1, 256), dtype=torch.bfloat16, device="cuda")
+    kn_g = torch.empty((2, 1, 512), dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.Stream()
+
+    def appends():
+        ks, vs = cache.update(0, kn_s, vn_s, W, True, stream)
+        kg, vg = cache.update(1, kn_g, kn_g, 0, True, stream)
+        return ks, vs, kg, vg
+
+    print("\n[case] compiled-step mode: eager step, then a captured graph", flush=True)
+    cache.begin_step(gidx, sidx)
+    with pytest.raises(EsdaError) as ei:
+        cache.decode(1, torch.zeros((16, 512), dtype=torch.bfloat16, device="cuda"), kn_g, kn_g, 0, 0, 1.0)
+    assert ei.value.code == 2
+    graph = None
+    base = 40 - W  # sliding slot 0 holds this position (the adopted window ends at 39)
+    for step, pos in enumerate(range(40, 52)):
+        srow = pos - base
+        rows = {k: rms_rows(rng, (2, 1, d)) for k, d in (("ks", 256), ("vs", 256), ("kg", 512))}
+        kn_s.copy_(_dev(rows["ks"]))
+        vn_s.copy_(_dev(rows["vs"]))
+        kn_g.copy_(_dev(rows["kg"]))
+        gidx.fill_(pos)
+        sidx.fill_(srow)
+        torch.cuda.synchronize()
+        if step == 0:
+            ks, vs, kg, vg = appends()  # eager
+            assert ks.rows == capS and kg.rows == capG and kg.data == vg.data
+            with torch.cuda.stream(stream):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    appends()
+        else:
+            with torch.cuda.stream(stream):
+                graph.replay()
+        torch.cuda.synchronize()
+        model["sk"][:, srow] = rows["ks"][:, 0]
+        model["sv"][:, srow] = rows["vs"][:, 0]
+        model["g"][:, pos] = rows["kg"][:, 0]
+        assert np.array_equal(_host(sk), model["sk"]) and np.array_equal(_host(sv), model["sv"]), f"pos {pos}"
+        assert np.array_equal(_host(g), model["g"]), f"pos {pos}"
+    cache.end_step()
+    k0, v0 = cache.slot_kv(0)
+    assert k0.data == sk.data_ptr() and v0.data == sv.data_ptr() and k0.rows == capS
+    tk, tv = cache.take_slot(1)
+    assert tk.data == g.data_ptr() and tv.data == g.data_ptr()
+    with pytest.raises(EsdaError) as ei:
+        cache.slot_kv(1)
+    assert ei.value.code == 2
