@@ -24,7 +24,7 @@ EXPORTS = (
     "esda_decode_noalloc",
     "esda_kv_append", "esda_decode_raw_workspace_size", "esda_decode_raw",
     "esda_decode_raw_stages", "esda_decode_raw_q8", "esda_decode_raw_q8_stages", "esda_quantize_raw_rows", "esda_rope_table",
-    "esda_fill_i32", "esda_last_error", "esda_version",
+    "esda_fill_i32", "esda_stream_read", "esda_last_error", "esda_version",
     # include/esda_cache.h
     "esda_cache_create", "esda_cache_destroy", "esda_cache_update", "esda_cache_update_raw",
     "esda_cache_current", "esda_cache_current_raw",
@@ -167,6 +167,7 @@ def lib() -> ctypes.CDLL:
         L.esda_quantize_raw_rows.argtypes = [P, i32, i32, P, i64, P, P, i64, i32, P]
         L.esda_rope_table.argtypes = [P, i32, P, P]
         L.esda_fill_i32.argtypes = [P, i32, i32, P]
+        L.esda_stream_read.argtypes = [P, sz, i32, P, P]
         L.esda_last_error.restype = ctypes.c_char_p
         L.esda_last_error.argtypes = []
         L.esda_version.argtypes = []

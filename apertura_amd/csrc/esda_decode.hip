@@ -33,6 +33,7 @@
 #include "esda.h"
 #include "esda_device.h"
 #include "esda_internal.h"
+#include "esda_plan.h"
 
 namespace {
 
@@ -43,35 +44,10 @@ constexpr int kMinRows = 64;        // fewest rows per workgroup the automatic p
 constexpr int kMaxGroups = 16384;   // workgroups per launch
 constexpr int kMaxBatch = 256;      // sequences per call (one per thread of the prefix scan)
 
-// ------------------------------------------------------------------ per-sequence view
-
-struct SeqView {
-    int nvis;    // visible rows
-    int first;   // cache row of the oldest visible position
-    int newrow;  // cache row receiving the new token
-    int ok;
-};
-
-// Visible absolute positions are [lo, pos] with lo = max(0, pos - window + 1) for a
-// sliding layer (ESGemma4TextModel.mm:68-83); rows hold p - row_base (linear) or
-// p mod cap (ring).  Logical row j (0 = oldest) lives at cache row first + j (mod cap).
-__device__ __forceinline__ SeqView seq_view(int pos, int base, int cap, int window, int ring) {
-    SeqView v{0, 0, 0, 0};
-    if (pos < 0) return v;
-    int lo = window > 0 ? max(pos - window + 1, 0) : 0;
-    if (ring) {
-        v.newrow = pos % cap;
-        v.first = lo % cap;
-    } else {
-        if (lo < base) lo = base;
-        v.newrow = pos - base;
-        if (v.newrow < 0 || v.newrow >= cap) return v;
-        v.first = lo - base;
-    }
-    v.nvis = pos - lo + 1;
-    v.ok = 1;
-    return v;
-}
+// Per-sequence views, the prefix table, shares, segments and merge owners: the integer
+// arithmetic of esda_plan.h (shared with the host tests).
+using esda_plan::SeqView;
+using esda_plan::seq_view;
 
 struct AttendParams {
     const uint16_t *q, *k_new, *v_new;
@@ -890,11 +866,8 @@ void attend_kernel(AttendParams p) {
             if (split == 0 && kvh == 0 && tid == 0) atomicAdd(p.status, 1);
             return;
         }
-        const int j0 = split * p.chunk;
-        if (j0 >= sv.nvis) return;
-        const int j1 = min(j0 + p.chunk, sv.nvis);
-        // rows past the last split (max_visible below the real length) are reported
-        if (split == p.S - 1 && j1 < sv.nvis && kvh == 0 && tid == 0) atomicAdd(p.status, 1);
+        int j0, j1;
+        if (!esda_plan::grid_split(split, p.S, p.chunk, sv.nvis, &j0, &j1)) return;
         segment(b, kvh, j0, j1, sv, ((size_t) b * p.Hkv + kvh) * p.S + split, j0 == 0 && j1 == sv.nvis);
         return;
     }
@@ -917,8 +890,7 @@ void attend_kernel(AttendParams p) {
         rows_seq = w_view.ok ? w_view.nvis : 0;
         if (wg == 0 && tid == 0) {
             if (!w_view.ok) atomicAdd(p.status, 1);
-            p.table[0] = 0;
-            p.table[1] = rows_seq;
+            esda_plan::write_prefix_entry(p.table, 0, 1, 0, rows_seq);
         }
     } else {
         const int t = wave_scan ? lane : tid;
@@ -938,8 +910,7 @@ void attend_kernel(AttendParams p) {
             rows_seq = __shfl(x, 63);
             if (wg == 0 && wave == 0) {
                 if (t < p.B && !v.ok) atomicAdd(p.status, 1);
-                if (t < p.B) p.table[t] = x - nv;
-                if (t == 0) p.table[p.B] = rows_seq;
+                esda_plan::write_prefix_entry(p.table, t, p.B, x - nv, rows_seq);
             }
         } else {
             if (lane == 63) s_wtot[wave] = x;
@@ -951,8 +922,7 @@ void attend_kernel(AttendParams p) {
             if (wg == 0 && tid < p.B && !v.ok) atomicAdd(p.status, 1);
             __syncthreads();
             // B + 1 entries (B may be 256 = one per thread): the total goes in separately
-            if (wg == 0 && tid < p.B) p.table[tid] = s_pref[tid];
-            if (wg == 0 && tid == 0) p.table[p.B] = s_pref[p.B];
+            if (wg == 0) esda_plan::write_prefix_entry(p.table, tid, p.B, tid < p.B ? s_pref[tid] : 0, s_pref[p.B]);
             rows_seq = s_pref[p.B];
         }
     }
@@ -982,9 +952,9 @@ void attend_kernel(AttendParams p) {
     // share covers one or more segments; the partial of workgroup wg for pair
     // u = b * Hkv + kvh goes to slot u + wg, so the slots of one pair are consecutive and
     // distinct pairs never share a slot.
-    const int Wr = (int) (rows_total < p.W ? rows_total : p.W);
+    const int Wr = esda_plan::active_shares(rows_total, p.W);
     if (wg >= Wr) return;
-    const long long lo = udiv64(rows_total * wg, Wr), hi = udiv64(rows_total * (wg + 1), Wr);
+    const long long lo = esda_plan::share_begin(rows_total, Wr, wg), hi = esda_plan::share_begin(rows_total, Wr, wg + 1);
     long long x = lo;
     int b = 0;
     while (x < hi) {
@@ -998,19 +968,17 @@ void attend_kernel(AttendParams p) {
             while (pref_at(b + 1) * p.Hkv <= x) ++b;
         }
         const long long pb = pref_at(b);
-        const long long sb = pb * p.Hkv;
         const int n = (int) (pref_at(b + 1) - pb);
-        const int kvh = (int) udiv64(x - sb, n);
-        const int j0 = (int) (x - sb - (long long) kvh * n);
-        const long long pair_end = sb + (long long) (kvh + 1) * n;
-        const long long seg_end = pair_end < hi ? pair_end : hi;
-        const int j1 = j0 + (int) (seg_end - x);
+        const esda_plan::Segment sg = esda_plan::segment_at(x, hi, pb * p.Hkv, n);
+        const int kvh = sg.kvh, j0 = sg.j0, j1 = sg.j1;
+        const long long seg_end = sg.end;
         const SeqView v = view_at(b);
         // Every value of the segment is the same in all lanes (computed from LDS and kernel
         // arguments); saying so keeps the ring's control flow and addresses scalar.
         const SeqView sv{uniform(v.nvis), uniform(v.first), uniform(v.newrow), uniform(v.ok)};
         const int ub = uniform(b), ukvh = uniform(kvh), uj0 = uniform(j0), uj1 = uniform(j1);
-        segment(ub, ukvh, uj0, uj1, sv, (size_t) ub * p.Hkv + ukvh + wg, uj0 == 0 && uj1 == n);
+        segment(ub, ukvh, uj0, uj1, sv, (size_t) esda_plan::share_slot((long long) ub * p.Hkv + ukvh, wg),
+                uj0 == 0 && uj1 == n);
         lds_barrier();  // every wave is done with the ring before the next segment refills it
         x = seg_end;
     }
@@ -1058,27 +1026,16 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
 __device__ __forceinline__ int pair_splits(const MergeParams &p, int b, int kvh, size_t &pbase) {
     int ns;
     if (p.balanced) {
-        // The attend workgroups that covered pair (b, kvh): those holding its first and
-        // last rows in the linearised (sequence, kv head, row) order, each range
-        // [rows_total * w / Wr, rows_total * (w + 1) / Wr).
-        const long long n = p.table[b + 1] - p.table[b];
-        const long long rows_total = p.table[p.B] * p.Hkv;
-        if (n <= 0 || rows_total <= 0) return 0;
-        const long long first = p.table[b] * p.Hkv + (long long) kvh * n, last = first + n - 1;
-        if (first < 0 || last >= rows_total) return 0;  // inconsistent table: read nothing
-        // the attend kernel's share count: every one of workgroups w0 .. w1 holds rows of
-        // the pair and wrote its slot
-        const long long Wr = rows_total < p.W ? rows_total : p.W;
-        const int w0 = (int) udiv64((first + 1) * Wr - 1, rows_total);
-        const int w1 = (int) udiv64((last + 1) * Wr - 1, rows_total);
-        if (w0 < 0 || w1 >= Wr || w0 > w1) return 0;
-        ns = w1 - w0 + 1;
-        pbase = (size_t) b * p.Hkv + kvh + w0;
+        // The attend workgroups w0 .. w1 that covered pair (b, kvh) (every one of them holds
+        // rows of the pair and wrote its slot); an inconsistent table reads nothing.
+        int w0 = 0;
+        ns = esda_plan::pair_owners(p.table[b], p.table[b + 1], p.table[p.B], p.Hkv, kvh, p.W, &w0);
+        if (ns == 0) return 0;
+        pbase = (size_t) esda_plan::share_slot((long long) b * p.Hkv + kvh, w0);
     } else {
         const SeqView sv = seq_view(p.pos[b], p.row_base ? p.row_base[b] : 0, p.cap, p.window, p.ring);
         if (!sv.ok) return 0;
-        ns = (sv.nvis + p.chunk - 1) / p.chunk;
-        if (ns > p.S) ns = p.S;
+        ns = esda_plan::grid_splits(sv.nvis, p.chunk, p.S);
         pbase = ((size_t) b * p.Hkv + kvh) * p.S;
     }
     return ns;
@@ -1300,6 +1257,31 @@ __global__ __launch_bounds__(256) void append_kernel(uint16_t *cache, long long 
         *reinterpret_cast<uint4 *>(cache + (size_t) b * seq_stride + (size_t) h * head_stride +
                                    (size_t) (r0 + r) * D + c * 8) = v;
     }
+}
+
+// Read-only stream over `blocks` 1 KiB blocks through the attend kernel's load path
+// (global_load_lds_dwordx4 ... nt into LDS, 64 lanes x 16 B = 1 KiB per instruction,
+// up to 15 in flight per wave): the memory system's ceiling for that path, and the
+// reference point of the HBM counters for it.  Workgroup w reads blocks [blocks * w / G,
+// blocks * (w + 1) / G) round-robin over its 4 waves; each wave keeps one word of what it
+// read, so the loads feed an output (sink[4 * w + wave]).
+__global__ __launch_bounds__(256) void stream_read_kernel(const unsigned char *src, long long blocks, unsigned *sink) {
+    __shared__ __attribute__((aligned(16))) unsigned char buf[4][16][1024];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const long long b0 = blocks * blockIdx.x / gridDim.x, b1 = blocks * (blockIdx.x + 1) / gridDim.x;
+    int i = 0;
+    for (long long b = b0 + wave; b < b1; b += 4, ++i) {
+        // at most 14 outstanding before this one: the load that last filled slot i % 16
+        // (16 loads ago) has landed
+        ESDA_WAIT_VM(14);
+        lds_dma16(src + b * 1024 + lane * 16, lds_addr(&buf[wave][i & 15][0]));
+    }
+    ESDA_WAIT_VM(0);
+    lds_barrier();
+    const unsigned x = reinterpret_cast<const unsigned *>(&buf[wave][lane & 15][0])[lane];
+    unsigned s = x;
+    for (int o = 32; o > 0; o >>= 1) s ^= __shfl_xor(s, o);
+    if (lane == 0) sink[4 * blockIdx.x + wave] = s;
 }
 
 // ------------------------------------------------------------------------ host side
@@ -1895,6 +1877,20 @@ int esda_kv_append(void *cache, int64_t seq_stride, int64_t head_stride, int32_t
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "append_kernel launch");
     return ESDA_OK;
+}
+
+int esda_stream_read(const void *src, size_t bytes, int32_t workgroups, uint32_t *sink, void *stream) {
+    if (!src || !sink) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_stream_read: null pointer");
+    if (bytes == 0 || (bytes % 1024) || !aligned16(src))
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_stream_read: bytes must be a positive multiple of 1024, src 16-byte aligned");
+    if (workgroups < 1 || workgroups > 65535)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_stream_read: workgroups must be in 1 .. 65535");
+    int rc = check_device();
+    if (rc) return rc;
+    hipLaunchKernelGGL(stream_read_kernel, dim3(workgroups), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       static_cast<const unsigned char *>(src), (long long) (bytes / 1024), sink);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? ESDA_OK : hip_fail(e, "stream_read_kernel launch");
 }
 
 int esda_fill_i32(int32_t *dst, int32_t value, int32_t n, void *stream) {

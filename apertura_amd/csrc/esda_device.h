@@ -106,13 +106,6 @@ __device__ __forceinline__ void lds_dma4(const void *src, unsigned lds) {
 #endif
 }
 
-// a / b for non-negative a, b > 0: 32-bit division when both fit (the common case),
-// which is far shorter than the 64-bit sequence.
-__device__ __forceinline__ long long udiv64(long long a, long long b) {
-    if (((unsigned long long) a | (unsigned long long) b) >> 32 == 0) return (long long) ((unsigned) a / (unsigned) b);
-    return (long long) ((unsigned long long) a / (unsigned long long) b);
-}
-
 // A value that is the same in every lane, as a scalar.
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 

@@ -78,6 +78,33 @@ def _dev_ptr(t: torch.Tensor | None, dtype=None) -> int | None:
     return t.data_ptr()
 
 
+def _check_cache(step, t: torch.Tensor | None, what: str, elem_bytes: int = 2) -> None:
+    """The cache tensor must hold every element the step addresses: (b, kvh, row, d) at
+    b*seq_stride + kvh*head_stride + row*head_dim + d for rows < cap; a 4-D view must be
+    [B, Hkv, cap, D] with exactly the step's strides."""
+    if t is None:
+        return
+    if not t.is_cuda:
+        raise ValueError(f"{what} must live in GPU memory")
+    d = step.desc()
+    B, Hkv, cap, D = step.batch, step.num_kv_heads, step.cap, step.head_dim
+    need = (B - 1) * d.seq_stride + (Hkv - 1) * d.head_stride + cap * D
+    avail = t.untyped_storage().nbytes() // elem_bytes - t.storage_offset()
+    if avail < need:
+        raise ValueError(f"{what} holds {avail} elements from its start; the step addresses {need}")
+    if t.dim() == 4 and (tuple(t.shape) != (B, Hkv, cap, D) or t.stride() != (d.seq_stride, d.head_stride, D, 1)):
+        raise ValueError(f"{what} is {tuple(t.shape)} with strides {t.stride()}; the step describes "
+                         f"({B}, {Hkv}, {cap}, {D}) with strides ({d.seq_stride}, {d.head_stride}, {D}, 1)")
+    if t.dim() != 4 and not t.is_contiguous():
+        raise ValueError(f"{what}: pass a contiguous buffer or a [B, Hkv, cap, D] view")
+
+
+def _check_row_base(step, row_base: torch.Tensor | None) -> None:
+    if row_base is not None and (row_base.dtype != torch.int32 or row_base.shape != (step.batch,)
+                                 or not row_base.is_contiguous()):
+        raise ValueError("row_base must be contiguous int32 [B]")
+
+
 def _stream_ptr(stream) -> int:
     s = stream if stream is not None else torch.cuda.current_stream()
     return int(s.cuda_stream)
@@ -98,11 +125,14 @@ def decode_step(step: DecodeStep, q: torch.Tensor, k_new: torch.Tensor, v_new: t
         raise ValueError("v_new must be contiguous [B, Hkv, D]")
     if pos.dtype != torch.int32 or pos.shape != (step.batch,):
         raise ValueError("pos must be int32 [B]")
+    vc = k_cache if (v_cache is None or step.kv_shared) else v_cache
+    _check_cache(step, k_cache, "k_cache")
+    _check_cache(step, vc, "v_cache")
+    _check_row_base(step, row_base)
     if out is None:
         out = torch.empty_like(q)
     if workspace is None:
         workspace = new_workspace(step, q.device)
-    vc = k_cache if (v_cache is None or step.kv_shared) else v_cache
     args = DecodeArgs(_dev_ptr(q, bf), _dev_ptr(k_new, bf),
                       _dev_ptr(v_new, bf) if (v_new is not None and not step.kv_shared) else None,
                       _dev_ptr(k_cache, bf), _dev_ptr(vc, bf), _dev_ptr(pos),
@@ -134,6 +164,9 @@ def decode_step_noalloc(step: DecodeStep, q: torch.Tensor, k_new: torch.Tensor, 
     if status is not None and (status.dtype != torch.int32 or status.numel() < 1):
         raise ValueError("status must be an int32 device tensor")
     vc = k_cache if (v_cache is None or step.kv_shared) else v_cache
+    _check_cache(step, k_cache, "k_cache")
+    _check_cache(step, vc, "v_cache")
+    _check_row_base(step, row_base)
     args = DecodeArgs(_dev_ptr(q, bf), _dev_ptr(k_new, bf),
                       _dev_ptr(v_new, bf) if (v_new is not None and not step.kv_shared) else None,
                       _dev_ptr(k_cache, bf), _dev_ptr(vc, bf), _dev_ptr(pos),
@@ -176,7 +209,9 @@ class DecodeCall:
             out = torch.empty_like(q)
         if workspace is None:
             workspace = new_workspace(step, q.device)
-        # validate once through the regular path (raises on any mismatch)
+        _check_cache(step, k_cache, "k_cache")
+        _check_cache(step, k_cache if (v_cache is None or step.kv_shared) else v_cache, "v_cache")
+        _check_row_base(step, row_base)
         self._keep = (q, k_new, v_new, k_cache, v_cache, pos, row_base, out, workspace)
         self.step, self.out, self.workspace, self.stages = step, out, workspace, stages
         bf = torch.bfloat16
@@ -280,6 +315,7 @@ def decode_raw(step: RawStep, q: torch.Tensor, k_new: torch.Tensor | None, raw_c
         raise ValueError("pos must be int32 [B]")
     if kw.dtype != bf or kw.numel() != 512 or inv_freq.dtype != torch.float32 or inv_freq.numel() < 64:
         raise ValueError("kw must be bf16 [512] and inv_freq f32 [>= 64]")
+    _check_cache(step, raw_cache, "raw_cache")
     if out is None:
         out = torch.empty_like(q)
     if workspace is None:
@@ -301,6 +337,7 @@ class RawCall:
             out = torch.empty_like(q)
         if workspace is None:
             workspace = new_raw_workspace(step, q.device)
+        _check_cache(step, raw_cache, "raw_cache")
         self._keep = (q, k_new, raw_cache, pos, kw, inv_freq, out, workspace, rope_table)
         self.step, self.out, self.workspace, self.stages = step, out, workspace, stages
         bf = torch.bfloat16
@@ -345,6 +382,7 @@ def _q8_args(step: RawStep, q, k_new, q8, scale, bias, pos, kw, inv_freq, out, w
         raise ValueError("k_new must be contiguous [B, Hkv, 512]")
     if q8.dtype != torch.uint8 or q8.shape != (step.batch, step.num_kv_heads, step.cap, 512):
         raise ValueError("q8 cache must be u8 [B, Hkv, cap, 512]")
+    _check_cache(step, q8, "q8 cache", elem_bytes=1)
     if scale.dtype != torch.float32 or scale.shape != (step.batch, step.num_kv_heads, step.cap) or \
             bias.shape != scale.shape or bias.stride() != scale.stride() or scale.stride(2) != 1:
         raise ValueError("scale / bias must be f32 [B, Hkv, cap] with the same strides")

@@ -54,8 +54,9 @@ WORKLOADS = {
                pos=lambda rng, B: [8192], scale=512 ** -0.5),
     "c3": dict(B=8, Hq=32, Hkv=16, D=256, cap=1024, window=1024, ring=True, shared=False,
                pos=lambda rng, B: [int(x) for x in rng.integers(2048, 32769, size=B)], scale=1 / 16),
+    # C4 plants 64 keys per kv head whose logit rises by +4.0 (plant_peaked_keys)
     "c4": dict(B=1, Hq=32, Hkv=4, D=512, cap=131072, window=0, ring=False, shared=True,
-               pos=lambda rng, B: [131071], scale=512 ** -0.5),
+               pos=lambda rng, B: [131071], scale=512 ** -0.5, peaks=64, bump=4.0),
     # C4's shape in raw-K mode (the reference's esDecodeAttnGlobal path): the cache holds
     # pre-norm k_proj rows; K and V are rebuilt in the kernel; in-model scale 1.0.
     # The same over a q8 raw stream (rawKVQ8: u8 rows + per-row scale / bias, 520 B a row).
@@ -105,6 +106,24 @@ def warm_up(fn, steps: int, seconds: float = WARM_SECONDS) -> int:
     return n
 
 
+def plant_peaked_keys(w, q, k_cache, pos, rng) -> None:
+    """BASELINE config 4's peaked softmax mass: at w["peaks"] cached positions per sequence,
+    add bump * q_hat to every kv head's key, q_hat the unit direction of that kv head's
+    first query head, in fp32 before rounding to bf16 -- with scale * |q| = 1 that head's
+    logit rises by exactly `bump` (the rule the parity tests use)."""
+    import torch
+
+    G = w["Hq"] // w["Hkv"]
+    for b in range(w["B"]):
+        picks = torch.tensor(sorted(int(x) for x in rng.choice(pos[b], size=w["peaks"], replace=False)),
+                             device=k_cache.device)
+        for h in range(w["Hkv"]):
+            qh = q[b, h * G].float()
+            alpha = w["bump"] / (w["scale"] * qh.norm())
+            rows = k_cache[b, h, picks].float() + alpha * qh / qh.norm()
+            k_cache[b, h, picks] = rows.to(torch.bfloat16)
+
+
 def c5_is_global(layer: int) -> bool:
     return layer % 6 == 5 or layer == C5_LAYERS - 1
 
@@ -139,10 +158,18 @@ def main() -> int:
     ap.add_argument("--local-split-rows", type=int, default=0, help="c5: split rows of local layers")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache timing (small configs)")
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="CPU baseline threads (0: OMP_NUM_THREADS, the host's CPU share, else every cpu)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="time a plain device copy of MIB MiB instead (HBM counter calibration)")
+    ap.add_argument("--calibrate-read", type=int, default=0, metavar="MIB",
+                    help="read MIB MiB through the attend kernel's load path instead (esda_stream_read): "
+                         "the measured read ceiling and the counter calibration for that path")
+    ap.add_argument("--read-workgroups", type=int, default=0,
+                    help="calibrate-read: workgroups per launch (0: sweep 256 .. 2048)")
     args = ap.parse_args()
+    if args.cpu_threads <= 0:
+        args.cpu_threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or os.cpu_count() or 1
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         _die_multi_gpu(max(args.gpus, int(os.environ.get("WORLD_SIZE", "1"))))
 
@@ -155,6 +182,8 @@ def main() -> int:
 
     if args.calibrate_copy:
         return calibrate_copy(args)
+    if args.calibrate_read:
+        return calibrate_read(args)
     if args.workload == "c5":
         return bench_c5(args)
     if args.workload in PREFILL_WORKLOADS:
@@ -178,6 +207,8 @@ def main() -> int:
     k_new = rms_bf16((B, Hkv, D))
     v_new = None if w["shared"] else rms_bf16((B, Hkv, D))
     pos_d = torch.tensor(pos, dtype=torch.int32, device=dev)
+    if w.get("peaks"):
+        plant_peaked_keys(w, q, k_cache, pos, np.random.default_rng(4321))
     out = torch.empty_like(q)
     stream = torch.cuda.Stream()  # default priority (side stream for graph capture)
     raw = None
@@ -226,8 +257,6 @@ def main() -> int:
         warm_steps = warm_up(lambda: call(stream), args.warmup)
         # Eager: K steps (append + attend + merge) issued one by one.
         ms_eager = timed(lambda: call(stream), args.steps)
-        # Dominant kernel alone (split-K attend with the fused append), same stream.
-        ms_attend = timed(lambda: call(stream, STAGE_ATTEND), args.steps)
         # Graph: the decode loop's production form -- steps replayed from a HIP graph, so
         # no host launch cost sits between them.  Each replay is checked against eager.
         per_graph = 10
@@ -238,6 +267,15 @@ def main() -> int:
         warm_up(graph.replay, 1, 0.5)
         reps = max(1, args.steps // per_graph)
         ms_graph = timed(graph.replay, reps) / per_graph
+        # Dominant kernel alone (split-K attend with the fused append), same stream, also
+        # replayed from a graph: eager launches of a few-microsecond kernel would time the
+        # host's launch rate instead (C1: ~5 us between back-to-back eager launches).
+        g_att = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_att, stream=stream):
+            for _ in range(per_graph):
+                call(stream, STAGE_ATTEND)
+        warm_up(g_att.replay, 1, 0.5)
+        ms_attend = timed(g_att.replay, reps) / per_graph
         ref = out.clone()
         call(stream)
         torch.cuda.synchronize()
@@ -299,7 +337,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) rows, unit-RMS, bf16)",
+        "data": "synthetic (seeded N(0,1) rows, unit-RMS, bf16" +
+                ("; 64 keys per kv head +4.0 along the query direction)" if w.get("peaks") else ")"),
         "config": {
             "workload": {"c4": "C4 global k_eq_v decode, L=131072", "c2": "C2 global k_eq_v decode, L=8193",
                          "c1": "C1 local decode, L=1024", "c3": "C3 local ring decode, B=8",
@@ -364,6 +403,41 @@ def calibrate_copy(args) -> int:
     ms = e0.elapsed_time(e1) / args.steps
     print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n,
                       "us": round(ms * 1e3, 3), "GB/s": round(2 * n / (ms * 1e-3) / 1e9, 2)}), flush=True)
+    return 0
+
+
+def calibrate_read(args) -> int:
+    """One pass over a buffer of known size through the attend kernel's load path
+    (esda_stream_read: LDS DMA, non-temporal, 1 KiB per wave instruction), timed with HIP
+    events on the launch stream: the stream-read ceiling the attend kernel is measured
+    against, and (under rocprofv3 --pmc FETCH_SIZE) the counter's factor on that path."""
+    import torch
+
+    from apertura_amd._lib import check, lib
+
+    n = args.calibrate_read << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    stream = torch.cuda.current_stream()
+    results = []
+    for wgs in ((args.read_workgroups,) if args.read_workgroups else (256, 512, 1024, 2048)):
+        sink = torch.zeros(4 * wgs, dtype=torch.int32, device="cuda:0")
+
+        def launch():
+            check(lib().esda_stream_read(src.data_ptr(), n, wgs, sink.data_ptr(), stream.cuda_stream))
+
+        warm_up(launch, max(1, args.warmup), 0.5)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            launch()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        results.append({"workgroups": wgs, "us": round(ms * 1e3, 3), "GB/s": round(n / (ms * 1e-3) / 1e9, 2)})
+    best = max(results, key=lambda r: r["GB/s"])
+    print(json.dumps({"calibration": "stream read (global_load_lds_dwordx4 nt, esda_stream_read)",
+                      "bytes_read": n, "best": best, "sweep": results,
+                      "frac_of_8TBs": round(best["GB/s"] / PEAK_HBM_GBS, 4)}), flush=True)
     return 0
 
 

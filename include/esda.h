@@ -61,7 +61,9 @@ typedef struct esda_decode_desc {
     int32_t kv_shared;    /* 1 = V aliases K (attention_k_eq_v, one buffer) */
     int64_t seq_stride;   /* elements; >= num_kv_heads * head_stride        */
     int64_t head_stride;  /* elements; >= cap * head_dim, multiple of 8     */
-    int32_t max_visible;  /* upper bound on visible rows (0 = from cap/window) */
+    int32_t max_visible;  /* expected bound on visible rows, sizes the split (0 = from
+                             cap/window); rows beyond it are still attended (the last
+                             split of a pair, or the balanced shares, take them) */
     int32_t split_rows;   /* rows per workgroup (0 = automatic; multiple of 16) */
     float scale;          /* softmax scale (the model uses 1.0)             */
 } esda_decode_desc;
@@ -231,6 +233,13 @@ int esda_quantize_raw_rows(const void *src, int32_t kv_heads, int32_t n_rows, vo
  * the per-sequence position words that replace the host-built additive mask upload of
  * ESGemma4TextModel.mm:68-83 / ESAttention.mm:17-22. */
 int esda_fill_i32(int32_t *dst, int32_t value, int32_t n, void *stream);
+
+/* Measurement aid (no counterpart in the reference): read `bytes` (a multiple of 1024)
+ * from src once, through the attend kernel's load path (LDS DMA, non-temporal, 1 KiB per
+ * wave instruction), over `workgroups` workgroups of 256 threads; sink receives
+ * 4 * workgroups words.  Gives the memory system's read ceiling for that path and the
+ * calibration of the HBM counters on it. */
+int esda_stream_read(const void *src, size_t bytes, int32_t workgroups, uint32_t *sink, void *stream);
 
 /* Message of the calling thread's last error ("" if none). */
 const char *esda_last_error(void);

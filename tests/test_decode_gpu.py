@@ -229,8 +229,14 @@ EDGE = [
     dict(name="max_visible_hint", B=2, Hq=32, Hkv=4, D=512, cap=4096, pos=[700, 900], shared=True,
          max_visible=901),
     # a hint below the real lengths only sizes the work split: every row is still attended
+    # (balanced shares; a grid of two splits whose last one takes the rest; a grid of one
+    # split that writes the output directly)
     dict(name="max_visible_hint_too_small", B=2, Hq=32, Hkv=4, D=512, cap=4096, pos=[3000, 900],
          shared=True, max_visible=100),
+    dict(name="max_visible_hint_too_small_grid", B=1, Hq=32, Hkv=4, D=512, cap=4096, pos=[3000],
+         shared=True, max_visible=100),
+    dict(name="max_visible_hint_too_small_one_split", B=1, Hq=16, Hkv=8, D=256, cap=2048, pos=[1500],
+         max_visible=40),
     # ragged batches: workgroups take equal shares of all rows, so one workgroup may span the
     # end of one (sequence, kv head) and the start of the next
     dict(name="ragged_batch_16", B=16, Hq=32, Hkv=4, D=512, cap=4096, shared=True,
