@@ -25,6 +25,7 @@ SOURCES = [
     "es/ESKVCache.cpp",
     "es/ESDecodeAttn.cpp",
     "es/ESSnapshot.cpp",
+    "es/safetensors.cpp",
     "es/ESPrefillAttn.cpp",
     "es/es_capi.cpp",
 ]
