@@ -148,6 +148,143 @@ constexpr int q8_extra_lds(int nw, bool tab = false) {
 }
 
 
+// The segments of one launch's workgroup: grid plans give workgroup (split, kv head,
+// sequence) rows [split * chunk, ...) of its pair; balanced plans give workgroup w its share
+// of all visible rows of the batch, walked pair by pair (esda_plan.h).  segment(b, kvh, j0,
+// j1, view, slot, direct) runs each; the ring is free again when it returns (the walk puts
+// a barrier between segments).  NW: waves per workgroup.
+template <int NW, class Seg>
+__device__ __forceinline__ void walk_segments(const AttendParams &p, Seg &&segment) {
+    const int wg = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (!p.balanced) {
+        // Fixed splits (uniform lengths: one sequence, or windowed local layers): workgroup
+        // (split, kvh, b) takes rows [split * chunk, (split + 1) * chunk) of its pair.
+        const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+        const SeqView sv = seq_view(p.pos[b], p.row_base ? p.row_base[b] : 0, p.cap, p.window, p.ring);
+        if (!sv.ok) {
+            if (split == 0 && kvh == 0 && tid == 0) atomicAdd(p.status, 1);
+            return;
+        }
+        int j0, j1;
+        if (!esda_plan::grid_split(split, p.S, p.chunk, sv.nvis, &j0, &j1)) return;
+        segment(b, kvh, j0, j1, sv, ((size_t) b * p.Hkv + kvh) * p.S + split, j0 == 0 && j1 == sv.nvis);
+        return;
+    }
+
+    // Balanced shares (ragged batches).
+    // Visible rows of every sequence and their exclusive prefix sums (the rows that
+    // precede sequence b in the linearised order).  Up to 64 sequences every wave scans
+    // the batch in its own lanes (no LDS, no barrier); larger batches (up to 256, one per
+    // thread) go through LDS.
+    __shared__ long long s_pref[kMaxBatch + 1];
+    __shared__ long long s_wtot[NW];
+    const bool single = p.B == 1;
+    const bool wave_scan = p.B <= 64;
+    long long w_incl = 0, w_nv = 0;  // wave scan: lane t's inclusive sum and rows of sequence t
+    SeqView w_view{0, 0, 0, 0};
+    long long rows_seq = 0;          // sum of visible rows over the batch
+    if (single) {
+        // one sequence: its view straight from the (wave-uniform) position word
+        w_view = seq_view(p.pos[0], p.row_base ? p.row_base[0] : 0, p.cap, p.window, p.ring);
+        rows_seq = w_view.ok ? w_view.nvis : 0;
+        if (wg == 0 && tid == 0) {
+            if (!w_view.ok) atomicAdd(p.status, 1);
+            esda_plan::write_prefix_entry(p.table, 0, 1, 0, rows_seq);
+        }
+    } else {
+        const int t = wave_scan ? lane : tid;
+        SeqView v{0, 0, 0, 0};
+        if (t < p.B) v = seq_view(p.pos[t], p.row_base ? p.row_base[t] : 0, p.cap, p.window, p.ring);
+        const long long nv = v.ok ? v.nvis : 0;
+        long long x = nv;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const long long y = __shfl_up(x, o);
+            if (lane >= o) x += y;
+        }
+        if (wave_scan) {
+            w_incl = x;
+            w_nv = nv;
+            w_view = v;
+            rows_seq = __shfl(x, 63);
+            if (wg == 0 && wave == 0) {
+                if (t < p.B && !v.ok) atomicAdd(p.status, 1);
+                esda_plan::write_prefix_entry(p.table, t, p.B, x - nv, rows_seq);
+            }
+        } else {
+            if (lane == 63) s_wtot[wave] = x;
+            __syncthreads();  // no DMA is in flight yet
+            long long off = 0;
+            for (int i = 0; i < wave; ++i) off += s_wtot[i];
+            if (tid < p.B) s_pref[tid + 1] = off + x;
+            if (tid == 0) s_pref[0] = 0;
+            if (wg == 0 && tid < p.B && !v.ok) atomicAdd(p.status, 1);
+            __syncthreads();
+            // B + 1 entries (B may be 256 = one per thread): the total goes in separately
+            if (wg == 0) esda_plan::write_prefix_entry(p.table, tid, p.B, tid < p.B ? s_pref[tid] : 0, s_pref[p.B]);
+            rows_seq = s_pref[p.B];
+        }
+    }
+    const long long rows_total = rows_seq * p.Hkv;
+    // Rows before sequence b (b <= B) and its view; the same in every lane.
+    auto lane64 = [](long long v, int l) {
+        const unsigned lo = __builtin_amdgcn_readlane((unsigned) v, l);
+        const unsigned hi = __builtin_amdgcn_readlane((unsigned) ((unsigned long long) v >> 32), l);
+        return (long long) (((unsigned long long) hi << 32) | lo);
+    };
+    auto pref_at = [&](int b) -> long long {
+        if (single) return b == 0 ? 0 : rows_seq;
+        if (!wave_scan) return s_pref[b];
+        return b >= p.B ? rows_seq : lane64(w_incl - w_nv, b);
+    };
+    auto view_at = [&](int b) -> SeqView {
+        if (single) return w_view;
+        if (!wave_scan) return seq_view(p.pos[b], p.row_base ? p.row_base[b] : 0, p.cap, p.window, p.ring);
+        return SeqView{__builtin_amdgcn_readlane(w_view.nvis, b), __builtin_amdgcn_readlane(w_view.first, b),
+                       __builtin_amdgcn_readlane(w_view.newrow, b), __builtin_amdgcn_readlane(w_view.ok, b)};
+    };
+
+    // This workgroup's share of all visible rows, linearised as (sequence, kv head, row):
+    // [rows_total * wg / Wr, rows_total * (wg + 1) / Wr) with Wr = min(W, rows_total), so
+    // that every share holds at least one row (W is sized from the bound on rows; early in
+    // a long cache fewer rows are visible) and workgroups wg >= Wr have nothing to do.  A
+    // share covers one or more segments; the partial of workgroup wg for pair
+    // u = b * Hkv + kvh goes to slot u + wg, so the slots of one pair are consecutive and
+    // distinct pairs never share a slot.
+    const int Wr = esda_plan::active_shares(rows_total, p.W);
+    if (wg >= Wr) return;
+    const long long lo = esda_plan::share_begin(rows_total, Wr, wg), hi = esda_plan::share_begin(rows_total, Wr, wg + 1);
+    long long x = lo;
+    int b = 0;
+    while (x < hi) {
+        // the sequence holding row x (x < rows_total): the count of sequences that end at
+        // or before it
+        if (single) {
+            b = 0;
+        } else if (wave_scan) {
+            b = __popcll(__ballot(lane < p.B && w_incl * p.Hkv <= x));
+        } else {
+            while (pref_at(b + 1) * p.Hkv <= x) ++b;
+        }
+        const long long pb = pref_at(b);
+        const int n = (int) (pref_at(b + 1) - pb);
+        const esda_plan::Segment sg = esda_plan::segment_at(x, hi, pb * p.Hkv, n);
+        const int kvh = sg.kvh, j0 = sg.j0, j1 = sg.j1;
+        const long long seg_end = sg.end;
+        const SeqView v = view_at(b);
+        // Every value of the segment is the same in all lanes (computed from LDS and kernel
+        // arguments); saying so keeps the ring's control flow and addresses scalar.
+        const SeqView sv{uniform(v.nvis), uniform(v.first), uniform(v.newrow), uniform(v.ok)};
+        const int ub = uniform(b), ukvh = uniform(kvh), uj0 = uniform(j0), uj1 = uniform(j1);
+        segment(ub, ukvh, uj0, uj1, sv, (size_t) esda_plan::share_slot((long long) ub * p.Hkv + ukvh, wg),
+                uj0 == 0 && uj1 == n);
+        lds_barrier();  // every wave is done with the ring before the next segment refills it
+        x = seg_end;
+    }
+}
+
 // --------------------------------------------------------------------- attend kernel
 //
 // grid (splits, kv heads, sequences), NW = 4 or 8 waves per workgroup, one workgroup per
@@ -857,131 +994,490 @@ void attend_kernel(AttendParams p) {
     }
     };
 
-    if (!p.balanced) {
-        // Fixed splits (uniform lengths: one sequence, or windowed local layers): workgroup
-        // (split, kvh, b) takes rows [split * chunk, (split + 1) * chunk) of its pair.
-        const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-        const SeqView sv = seq_view(p.pos[b], p.row_base ? p.row_base[b] : 0, p.cap, p.window, p.ring);
-        if (!sv.ok) {
-            if (split == 0 && kvh == 0 && tid == 0) atomicAdd(p.status, 1);
-            return;
-        }
-        int j0, j1;
-        if (!esda_plan::grid_split(split, p.S, p.chunk, sv.nvis, &j0, &j1)) return;
-        segment(b, kvh, j0, j1, sv, ((size_t) b * p.Hkv + kvh) * p.S + split, j0 == 0 && j1 == sv.nvis);
-        return;
-    }
+    walk_segments<NW>(p, segment);
+}
 
-    // Balanced shares (ragged batches).
-    // Visible rows of every sequence and their exclusive prefix sums (the rows that
-    // precede sequence b in the linearised order).  Up to 64 sequences every wave scans
-    // the batch in its own lanes (no LDS, no barrier); larger batches (up to 256, one per
-    // thread) go through LDS.
-    __shared__ long long s_pref[kMaxBatch + 1];
-    __shared__ long long s_wtot[NW];
-    const bool single = p.B == 1;
-    const bool wave_scan = p.B <= 64;
-    long long w_incl = 0, w_nv = 0;  // wave scan: lane t's inclusive sum and rows of sequence t
-    SeqView w_view{0, 0, 0, 0};
-    long long rows_seq = 0;          // sum of visible rows over the batch
-    if (single) {
-        // one sequence: its view straight from the (wave-uniform) position word
-        w_view = seq_view(p.pos[0], p.row_base ? p.row_base[0] : 0, p.cap, p.window, p.ring);
-        rows_seq = w_view.ok ? w_view.nvis : 0;
-        if (wg == 0 && tid == 0) {
-            if (!w_view.ok) atomicAdd(p.status, 1);
-            esda_plan::write_prefix_entry(p.table, 0, 1, 0, rows_seq);
-        }
-    } else {
-        const int t = wave_scan ? lane : tid;
-        SeqView v{0, 0, 0, 0};
-        if (t < p.B) v = seq_view(p.pos[t], p.row_base ? p.row_base[t] : 0, p.cap, p.window, p.ring);
-        const long long nv = v.ok ? v.nvis : 0;
-        long long x = nv;
+// ------------------------------------------------- raw-K attend with wave-private rings
+//
+// Raw-K decode (ESDecodeAttn.mm:17-117) when two kv heads share a workgroup and the caller
+// passes the precomputed rotary table -- the ES layer's path.  Four waves, one per SIMD.
+// Each wave owns whole 16-row stages (8 positions of each of the two kv heads) over the
+// full 512-dim head, in turn: wave w takes stages w, w + 4, w + 8, ... of a segment.  It
+// streams them through two LDS slots of its own, filled by its own LDS DMA and waited on
+// with its own vmcnt, so the main loop has no barrier and no exchange between waves.  Per
+// stage a wave:
+//   - reads the 16 raw rows as MFMA A operands (lane (li, lg): row li, dims wdim(kk, lg)
+//     of k-step kk);
+//   - forms their 16x16 Gram matrix with 16 MFMAs: the diagonal is each row's sum of
+//     squares (exact bf16 products, fp32 sums), hence rinv = rsqrt(mean + eps);
+//   - rebuilds K = bf16(rope(kraw * rinv * kw)) in registers -- the rotary partners
+//     (d, d + 256), d < 64, sit in one lane (k-steps 0, 1 and 8, 9), their bf16 cos / sin
+//     come from the table rows DMA'd beside the stage;
+//   - scores its 16 query heads (both GQA groups: heads of the other kv head's rows are
+//     masked) with 16 MFMAs, runs its own online softmax, and accumulates O^T[512 x 16
+//     heads] with 32 MFMAs over V = kraw read back by transpose reads, rinv folded into the
+//     weight: P = bf16(e * rinv), l += P / rinv.
+// Q8 (esDecodeAttnGlobalQ8, ESDecodeAttn.mm:275-369): rows are u8 with a per-row scale and
+// bias (x = q * scale + bias).  The A operand is q itself in bf16 (exact); the Gram diagonal
+// and a product with ones give sum(q^2) and sum(q), hence mean(x^2);
+// K = bf16(rope(fma(q, scale * rinv, bias * rinv) * kw)); q is also written to a bf16 tile
+// of the wave's that the transpose reads use as V, with P = bf16(e * scale * rinv) and the
+// bias entering as sum(P * bias / scale) per head.
+// At the end of a segment the four waves' (m, l, O) merge through LDS into one partial.
+
+constexpr int kWaves = 4;                  // waves of the wave-private-ring kernels
+constexpr int kBlk = 1056;                 // LDS bytes per 1 KiB DMA block (1 KiB + 32 B pad)
+
+// Dims of k-step kk held by lane group lg: 8 consecutive dims, so that a lane's two k-steps
+// 2m, 2m + 1 cover 16 consecutive dims (one 16-byte u8 piece, two bf16 ones) and the rotary
+// partners of k-steps 0, 1 are k-steps 8, 9 of the same lane.
+__device__ __forceinline__ int wdim(int kk, int lg) { return 64 * (kk >> 1) + 16 * lg + 8 * (kk & 1); }
+
+template <bool Q8>
+struct WRing {
+    static constexpr int ROWS = Q8 ? 8 * kBlk : 16 * kBlk;  // rows of a stage (q8: two per block)
+    static constexpr int SB = Q8 ? 128 : 0;                  // q8: 16 scales, 16 biases
+    static constexpr int TAB = 2 * kBlk;                     // 8 cos/sin table rows (swizzled)
+    static constexpr int SLOT = ROWS + SB + TAB;
+    static constexpr int STG = Q8 ? 16 * kBlk : 0;           // q8: the bf16 V tile
+    static constexpr int WAVE = 2 * SLOT + STG;              // one wave's LDS
+    static constexpr int DPS = (Q8 ? 8 + 1 : 16) + 2;        // DMA instructions per stage
+    static constexpr int MERGE = kWaves * 16 * 516 * 4;      // end-of-segment merge area (aliases the rings)
+    static_assert(kWaves * WAVE >= MERGE, "the merge area fits in the rings");
+    static_assert(2 * DPS <= 60, "vmcnt holds the two stages in flight");
+};
+
+template <bool Q8>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kWaves, 64 * kWaves), amdgpu_waves_per_eu(1, 1)))
+void raw_attend_kernel(AttendParams p) {
+    using W = WRing<Q8>;
+    __shared__ __attribute__((aligned(16))) unsigned char wlds[kWaves * W::WAVE];
+    // per-wave row factors of the stage being computed: [0] rinv (q8: scale * rinv), [1] its
+    // inverse, [2] (q8) bias / scale, [3] (q8) bias * rinv
+    __shared__ __attribute__((aligned(16))) float xf[kWaves][4][16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 15, lg = lane >> 4;
+    unsigned char *const wl = wlds + wave * W::WAVE;
+
+    // k-norm weights in fp32, read per k-step (lanes of a lane group read the same 32 bytes);
+    // 128 of them per lane would not fit in registers beside O^T, Q^T and the stage
+    __shared__ __attribute__((aligned(16))) float kwl[kRawDim];
+    {
+        const unsigned t = reinterpret_cast<const unsigned *>(p.kw)[tid];
+        kwl[2 * tid] = bf16_lo(t);
+        kwl[2 * tid + 1] = bf16_hi(t);
+    }
+    __syncthreads();
+
+    auto segment = [&](const int b, const int kvh, const int j0, const int j1, const SeqView sv, const size_t slot,
+                       const bool direct) {
+        const bool append = p.k_new != nullptr;
+        const size_t head_off = (size_t) b * p.seq_stride + (size_t) kvh * 2 * p.head_stride;
+        uint16_t *const kbase = p.k_cache + head_off;
+        const uint16_t *const knew = append ? p.k_new + ((size_t) b * p.Hkv + kvh) * 2 * kRawDim : nullptr;
+        unsigned char *const q8base = Q8 ? p.q8 + head_off : nullptr;
+        const size_t sb_off = Q8 ? (size_t) b * p.sb_seq_stride + (size_t) kvh * 2 * p.sb_head_stride : 0;
+
+        // Q^T operand: head li of the packed pair (zero for padding heads li >= G)
+        bf16x8 qv[16];
+        {
+            const bool qok = li < p.G;
+            const uint16_t *qrow = p.q + ((size_t) b * p.Hq + (size_t) kvh * p.G + (qok ? li : 0)) * kRawDim;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const long long y = __shfl_up(x, o);
-            if (lane >= o) x += y;
-        }
-        if (wave_scan) {
-            w_incl = x;
-            w_nv = nv;
-            w_view = v;
-            rows_seq = __shfl(x, 63);
-            if (wg == 0 && wave == 0) {
-                if (t < p.B && !v.ok) atomicAdd(p.status, 1);
-                esda_plan::write_prefix_entry(p.table, t, p.B, x - nv, rows_seq);
+            for (int kk = 0; kk < 16; ++kk) {
+                const u32x4 t = qok ? *reinterpret_cast<const u32x4 *>(qrow + wdim(kk, lg)) : u32x4{0u, 0u, 0u, 0u};
+                qv[kk] = __builtin_bit_cast(bf16x8, t);
             }
-        } else {
-            if (lane == 63) s_wtot[wave] = x;
-            __syncthreads();  // no DMA is in flight yet
-            long long off = 0;
-            for (int i = 0; i < wave; ++i) off += s_wtot[i];
-            if (tid < p.B) s_pref[tid + 1] = off + x;
-            if (tid == 0) s_pref[0] = 0;
-            if (wg == 0 && tid < p.B && !v.ok) atomicAdd(p.status, 1);
-            __syncthreads();
-            // B + 1 entries (B may be 256 = one per thread): the total goes in separately
-            if (wg == 0) esda_plan::write_prefix_entry(p.table, tid, p.B, tid < p.B ? s_pref[tid] : 0, s_pref[p.B]);
-            rows_seq = s_pref[p.B];
         }
-    }
-    const long long rows_total = rows_seq * p.Hkv;
-    // Rows before sequence b (b <= B) and its view; the same in every lane.
-    auto lane64 = [](long long v, int l) {
-        const unsigned lo = __builtin_amdgcn_readlane((unsigned) v, l);
-        const unsigned hi = __builtin_amdgcn_readlane((unsigned) ((unsigned long long) v >> 32), l);
-        return (long long) (((unsigned long long) hi << 32) | lo);
-    };
-    auto pref_at = [&](int b) -> long long {
-        if (single) return b == 0 ? 0 : rows_seq;
-        if (!wave_scan) return s_pref[b];
-        return b >= p.B ? rows_seq : lane64(w_incl - w_nv, b);
-    };
-    auto view_at = [&](int b) -> SeqView {
-        if (single) return w_view;
-        if (!wave_scan) return seq_view(p.pos[b], p.row_base ? p.row_base[b] : 0, p.cap, p.window, p.ring);
-        return SeqView{__builtin_amdgcn_readlane(w_view.nvis, b), __builtin_amdgcn_readlane(w_view.first, b),
-                       __builtin_amdgcn_readlane(w_view.newrow, b), __builtin_amdgcn_readlane(w_view.ok, b)};
-    };
+        if constexpr (Q8) {
+            // The new row of each kv head is quantized into the cache before any DMA (wave pr:
+            // kv head pr), esQuantizeRawRows' arithmetic (ESDecodeAttn.mm:491-509).
+            if (append && j1 == sv.nvis && wave < 2) {
+                const int pr = wave;
+                const u32x4 t = *reinterpret_cast<const u32x4 *>(knew + pr * kRawDim + lane * 8);
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x[2 * e] = bf16_lo(t[e]);
+                    x[2 * e + 1] = bf16_hi(t[e]);
+                }
+                float mn = x[0], mx = x[0];
+#pragma unroll
+                for (int e = 1; e < 8; ++e) {
+                    mn = fminf(mn, x[e]);
+                    mx = fmaxf(mx, x[e]);
+                }
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) {
+                    mn = fminf(mn, __shfl_xor(mn, o));
+                    mx = fmaxf(mx, __shfl_xor(mx, o));
+                }
+                float scl = (mx - mn) / 255.0f;
+                if (!(scl > 1e-8f)) scl = 1e-8f;
+                unsigned lo = 0u, hi = 0u;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const unsigned qi = (unsigned) fminf(roundf((x[e] - mn) / scl), 255.0f);
+                    if (e < 4) lo |= qi << (8 * e);
+                    else hi |= qi << (8 * (e - 4));
+                }
+                unsigned char *row = q8base + (size_t) pr * p.head_stride + (size_t) sv.newrow * kRawDim;
+                *reinterpret_cast<uint2 *>(row + lane * 8) = uint2{lo, hi};
+                if (lane == 0) {
+                    const size_t at = sb_off + (size_t) pr * p.sb_head_stride + (size_t) sv.newrow;
+                    p.qsc[at] = scl;
+                    p.qbs[at] = mn;
+                }
+            }
+        }
+        ESDA_WAIT_VM(0);  // operands in registers (and the q8 row stored) before the ring counts its loads
+        if constexpr (Q8) {
+            if (append && j1 == sv.nvis) lds_barrier();  // the quantized row is in memory before any DMA
+        }
 
-    // This workgroup's share of all visible rows, linearised as (sequence, kv head, row):
-    // [rows_total * wg / Wr, rows_total * (wg + 1) / Wr) with Wr = min(W, rows_total), so
-    // that every share holds at least one row (W is sized from the bound on rows; early in
-    // a long cache fewer rows are visible) and workgroups wg >= Wr have nothing to do.  A
-    // share covers one or more segments; the partial of workgroup wg for pair
-    // u = b * Hkv + kvh goes to slot u + wg, so the slots of one pair are consecutive and
-    // distinct pairs never share a slot.
-    const int Wr = esda_plan::active_shares(rows_total, p.W);
-    if (wg >= Wr) return;
-    const long long lo = esda_plan::share_begin(rows_total, Wr, wg), hi = esda_plan::share_begin(rows_total, Wr, wg + 1);
-    long long x = lo;
-    int b = 0;
-    while (x < hi) {
-        // the sequence holding row x (x < rows_total): the count of sequences that end at
-        // or before it
-        if (single) {
-            b = 0;
-        } else if (wave_scan) {
-            b = __popcll(__ballot(lane < p.B && w_incl * p.Hkv <= x));
-        } else {
-            while (pref_at(b + 1) * p.Hkv <= x) ++b;
+        const int nst = (j1 - j0 + 7) >> 3;  // 16-row stages: 8 positions x 2 kv heads
+        // DMA of stage st into slot sl.  Rows past the segment end repeat its last row (their
+        // scores are masked); the new token's raw row comes from k_new.
+        auto dma = [&](int st, unsigned char *sl) {
+            const int jst = j0 + 8 * st;
+            const bool interior = jst + 8 < j1;
+            {
+                // table rows of positions jst .. jst + 7: block bt holds positions 4bt .. 4bt+3,
+                // piece c of position rib at 16 * (16 rib + (c + 4 rib) mod 16)
+                const int rib = lane >> 4, c = (lane - 4 * rib) & 15;
+#pragma unroll
+                for (int bt = 0; bt < 2; ++bt) {
+                    const unsigned dst = lds_addr(sl + W::ROWS + W::SB + bt * kBlk);
+                    if (interior) {
+                        lds_dma16_s(p.rope_tab + (size_t) (sv.first + jst + 4 * bt) * kRopePairs,
+                                    (unsigned) (rib * 256 + c * 16), dst);
+                    } else {
+                        const int j = min(jst + 4 * bt + rib, j1 - 1);
+                        lds_dma16(p.rope_tab + (size_t) (sv.first + j) * kRopePairs + c * 4, dst);
+                    }
+                }
+            }
+            if constexpr (Q8) {
+                // block i: rows 2i, 2i + 1 (kv head i / 4), lane l loads row 2i + (l & 1),
+                // 16-byte piece l >> 1
+                const int h = lane & 1, pc = lane >> 1;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int pr = i >> 2, r0 = (2 * i) & 7;
+                    const unsigned dst = lds_addr(sl + i * kBlk);
+                    if (interior) {
+                        lds_dma16_s(q8base + (size_t) pr * p.head_stride + (size_t) (sv.first + jst + r0) * kRawDim,
+                                    (unsigned) (h * kRawDim + pc * 16), dst);
+                    } else {
+                        const int j = min(jst + r0 + h, j1 - 1);
+                        lds_dma16(q8base + (size_t) pr * p.head_stride + (size_t) (sv.first + j) * kRawDim + pc * 16,
+                                  dst);
+                    }
+                }
+                if (lane < 32) {
+                    const int sr = lane & 15, pr = sr >> 3;
+                    const int j = min(jst + (sr & 7), j1 - 1);
+                    lds_dma4((lane < 16 ? p.qsc : p.qbs) + sb_off + (size_t) pr * p.sb_head_stride + (size_t) (sv.first + j),
+                             lds_addr(sl + W::ROWS));
+                }
+            } else {
+#pragma unroll
+                for (int sr = 0; sr < 16; ++sr) {
+                    const int pr = sr >> 3, i = sr & 7;
+                    const unsigned dst = lds_addr(sl + sr * kBlk);
+                    if (interior) {
+                        lds_dma16_s(kbase + (size_t) pr * p.head_stride + (size_t) (sv.first + jst + i) * kRawDim,
+                                    (unsigned) (lane * 16), dst);
+                    } else {
+                        const int j = min(jst + i, j1 - 1);
+                        const uint16_t *src = (append && j == sv.nvis - 1)
+                                                  ? knew + pr * kRawDim
+                                                  : kbase + (size_t) pr * p.head_stride + (size_t) (sv.first + j) * kRawDim;
+                        lds_dma16(src + lane * 8, dst);
+                    }
+                }
+            }
+        };
+
+        // This wave's stages: w, w + 4, ...; local index i uses slot i & 1.
+        const int st0 = wave;
+        if (st0 < nst) dma(st0, wl);
+        if (st0 + kWaves < nst) dma(st0 + kWaves, wl + W::SLOT);
+
+        float m = -INFINITY, l = 0.0f;
+        float bt = 0.0f;  // q8: sum of P * bias / scale of this lane's head
+        f32x4 acc[32];
+#pragma unroll
+        for (int dt = 0; dt < 32; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float *const xfw = &xf[wave][0][0];
+        // stage row 4lg + r belongs to kv head lg / 2; head li to kv head min(li / gk, 1)
+        const bool hmatch = (lg >> 1) == min(li / p.gk, 1);
+
+        for (int st = st0, it = 0; st < nst; st += kWaves, ++it) {
+            unsigned char *const sl = wl + (it & 1) * W::SLOT;
+            if (st + kWaves < nst) {
+                ESDA_WAIT_VM(W::DPS);  // this stage landed; the next may stay in flight
+            } else {
+                ESDA_WAIT_VM(0);
+            }
+            // A operands: row li, dims wdim(kk, lg) (q8: q widened to bf16, exact)
+            u32x4 a[Q8 ? 1 : 16];  // raw: the stage's rows, rebuilt into K in place
+            u32x4 w8[Q8 ? 8 : 1];  // q8: the stage's u8 row pieces (16 dims each)
+            // Gram products of the A operands (q8: also against ones)
+            f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f}, g1 = {0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (Q8) {
+                // Widen each 16-dim piece to bf16 (exact), store it in the wave's V tile for
+                // this stage's transpose reads and feed the norm MFMAs at once.
+                bf16x8 ones;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ones[e] = (__bf16) 1.0f;
+                unsigned char *stg = wl + 2 * W::SLOT;
+#pragma unroll
+                for (int mm = 0; mm < 8; ++mm) {
+                    w8[mm] = *reinterpret_cast<const u32x4 *>(sl + (li >> 1) * kBlk + 32 * (4 * mm + lg) + 16 * (li & 1));
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        unsigned o[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const unsigned word = w8[mm][2 * h + e / 2];
+                            const float f0 = (float) ((word >> (16 * (e & 1))) & 255u);
+                            const float f1 = (float) ((word >> (16 * (e & 1) + 8)) & 255u);
+                            o[e] = __builtin_amdgcn_perm(__builtin_bit_cast(unsigned, f1), __builtin_bit_cast(unsigned, f0),
+                                                         0x07060302u);
+                        }
+                        const u32x4 ab = u32x4{o[0], o[1], o[2], o[3]};
+                        *reinterpret_cast<u32x4 *>(stg + li * kBlk + 2 * wdim(2 * mm + h, lg)) = ab;
+                        const bf16x8 x = __builtin_bit_cast(bf16x8, ab);
+                        g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
+                        g1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, ones, g1, 0, 0, 0);
+                    }
+                    if (mm & 1) __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < 16; ++kk) {
+                    a[kk] = *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg));
+                    const bf16x8 x = __builtin_bit_cast(bf16x8, a[kk]);
+                    g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
+                }
+            }
+            // cos / sin of this lane's rotary pairs 16lg .. 16lg + 15 at row li's position
+            u32x4 tab[4];
+            {
+                const int pos = li & 7, bt2 = pos >> 2, rib = pos & 3;
+#pragma unroll
+                for (int c4 = 0; c4 < 4; ++c4) {
+                    const int c = 4 * lg + c4;
+                    tab[c4] = *reinterpret_cast<const u32x4 *>(sl + W::ROWS + W::SB + bt2 * kBlk +
+                                                               16 * (16 * rib + ((c + 4 * rib) & 15)));
+                }
+            }
+            // Row norms: the Gram diagonal (and, q8, the row sums against ones).  C layout:
+            // lane (li, lg) holds C[4lg + i][li]; row li's diagonal is register li - 4lg of the
+            // lanes with lg == li / 4, which publish the row's factors.
+            {
+                const int i = li - 4 * lg;
+                if (i >= 0 && i < 4) {
+                    const float s2 = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
+                    if constexpr (Q8) {
+                        const float s1 = i == 0 ? g1[0] : i == 1 ? g1[1] : i == 2 ? g1[2] : g1[3];
+                        const float scl = reinterpret_cast<const float *>(sl + W::ROWS)[li];
+                        const float bias = reinterpret_cast<const float *>(sl + W::ROWS)[16 + li];
+                        // mean(x^2) = scale^2 var(q) + mean(x)^2 with 512^2 var(q) = 512 sum(q^2) - sum(q)^2
+                        const float var = fmaxf(__builtin_fmaf(512.0f, s2, -s1 * s1), 0.0f);
+                        const float mean = __builtin_fmaf(scl, s1 * (1.0f / kRawDim), bias);
+                        const float ms = scl * scl * var * (1.0f / (kRawDim * kRawDim)) + __builtin_fmaf(mean, mean, p.eps);
+                        const float rinv = __builtin_amdgcn_rsqf(ms);
+                        const float alpha = scl * rinv;
+                        xfw[0 * 16 + li] = alpha;
+                        xfw[1 * 16 + li] = 1.0f / alpha;
+                        xfw[2 * 16 + li] = bias / scl;
+                        xfw[3 * 16 + li] = bias * rinv;
+                    } else {
+                        const float ms = s2 * (1.0f / kRawDim) + p.eps;
+                        const float rinv = __builtin_amdgcn_rsqf(ms);
+                        xfw[0 * 16 + li] = rinv;
+                        xfw[1 * 16 + li] = ms * rinv;
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);  // the Gram operands die here (q8: a[] is in the V tile)
+            // K = bf16(rope(x * rinv * kw)) (q8: x * rinv = fma(q, scale * rinv, bias * rinv)),
+            // then the scores S^T[16 rows x 16 heads]
+            const float fa = xfw[0 * 16 + li];
+            const float fb = Q8 ? xfw[3 * 16 + li] : 0.0f;
+            // the k-norm weights of k-step kk, dim e of the lane's 8
+            auto kwf = [&](int kk, int e) { return kwl[wdim(kk, lg) + e]; };
+            auto kval = [&](int kk, int e) -> float {
+                if constexpr (Q8) {
+                    const float q = (float) ((w8[kk >> 1][2 * (kk & 1) + (e >> 2)] >> (8 * (e & 3))) & 255u);
+                    return __builtin_fmaf(q, fa, fb) * kwf(kk, e);
+                }
+                else {
+                    const float x = (e & 1) ? bf16_hi(a[Q8 ? 0 : kk][e >> 1]) : bf16_lo(a[Q8 ? 0 : kk][e >> 1]);
+                    return x * fa * kwf(kk, e);
+                }
+            };
+            auto pack = [](const float (&v)[8]) -> bf16x8 {
+                bf16x8 r;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) r[e] = (__bf16) v[e];
+                return r;
+            };
+            f32x4 sp0 = {0.0f, 0.0f, 0.0f, 0.0f}, sp1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kr = 0; kr < 2; ++kr) {
+                // rotary k-steps kr and kr + 8 (dims 16lg + 8kr + e and 256 + ...)
+                float lo[8], hi[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    lo[e] = kval(kr, e);
+                    hi[e] = kval(kr + 8, e);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const unsigned w = tab[2 * kr + e / 4][e & 3];
+                    const float c = bf16_lo(w), s = bf16_hi(w);
+                    const float x0 = lo[e], x1 = hi[e];
+                    lo[e] = x0 * c - x1 * s;
+                    hi[e] = x1 * c + x0 * s;
+                }
+                sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(lo), qv[kr], sp0, 0, 0, 0);
+                sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(hi), qv[kr + 8], sp1, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);  // bound the live rebuilt values
+            }
+#pragma unroll
+            for (int kk = 2; kk < 16; ++kk) {
+                if (kk == 8 || kk == 9) continue;
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = kval(kk, e);
+                if (kk & 1) sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp1, 0, 0, 0);
+                else sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp0, 0, 0, 0);
+                if (kk & 1) __builtin_amdgcn_sched_barrier(0);
+            }
+            f32x4 sc = sp0 + sp1;
+            // Online softmax (log2 domain) over stage rows 4lg .. 4lg + 3: rows past the
+            // segment end and rows of the other kv head are masked.
+            const int jt = j0 + 8 * st + ((4 * lg) & 7);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[r] = hmatch && (jt + r) < j1 ? sc[r] * p.scale_log2e : -INFINITY;
+            const float tmax = wave_max_across_groups(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+            if (__any(tmax > m + kRescaleSlack)) {
+                const float mnew = fmaxf(m, tmax);
+                const float corr = __builtin_amdgcn_exp2f(m - mnew);
+                l *= corr;
+                if constexpr (Q8) bt *= corr;
+#pragma unroll
+                for (int dt = 0; dt < 32; ++dt) acc[dt] *= corr;
+                m = mnew;
+            }
+            short4v pbs;
+            {
+                const f32x4 ri = *reinterpret_cast<const f32x4 *>(xfw + 0 * 16 + 4 * lg);
+                const f32x4 rn = *reinterpret_cast<const f32x4 *>(xfw + 1 * 16 + 4 * lg);
+                f32x4 gm = {0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (Q8) gm = *reinterpret_cast<const f32x4 *>(xfw + 2 * 16 + 4 * lg);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float e = __builtin_amdgcn_exp2f(sc[r] - m);
+                    const __bf16 pw = (__bf16) (e * ri[r]);
+                    l += (float) pw * rn[r];
+                    if constexpr (Q8) bt += (float) pw * gm[r];
+                    pbs[r] = __builtin_bit_cast(short, pw);
+                }
+            }
+            // O^T += V^T . P^T over all 512 dims (V^T by transpose reads: lane (li, lg)
+            // supplies row 4lg + li/4, dims 16dt + 4(li % 4) .. + 4)
+            const unsigned char *vb = Q8 ? wl + 2 * W::SLOT : sl;
+            const int tr_off = (4 * lg + li / 4) * kBlk + (li % 4) * 8;
+#pragma unroll
+            for (int dt = 0; dt < 32; ++dt) {
+                const short4v av = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) short4v *) (vb + tr_off + 32 * dt));
+                acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, pbs, acc[dt], 0, 0, 0);
+                if ((dt & 7) == 7) __builtin_amdgcn_sched_barrier(0);  // at most 8 reads in flight
+            }
+            // refill this slot with the wave's stage after next once its reads are done
+            if (st + 2 * kWaves < nst) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                dma(st + 2 * kWaves, sl);
+            }
         }
-        const long long pb = pref_at(b);
-        const int n = (int) (pref_at(b + 1) - pb);
-        const esda_plan::Segment sg = esda_plan::segment_at(x, hi, pb * p.Hkv, n);
-        const int kvh = sg.kvh, j0 = sg.j0, j1 = sg.j1;
-        const long long seg_end = sg.end;
-        const SeqView v = view_at(b);
-        // Every value of the segment is the same in all lanes (computed from LDS and kernel
-        // arguments); saying so keeps the ring's control flow and addresses scalar.
-        const SeqView sv{uniform(v.nvis), uniform(v.first), uniform(v.newrow), uniform(v.ok)};
-        const int ub = uniform(b), ukvh = uniform(kvh), uj0 = uniform(j0), uj1 = uniform(j1);
-        segment(ub, ukvh, uj0, uj1, sv, (size_t) esda_plan::share_slot((long long) ub * p.Hkv + ukvh, wg),
-                uj0 == 0 && uj1 == n);
-        lds_barrier();  // every wave is done with the ring before the next segment refills it
-        x = seg_end;
-    }
+
+        // Fused append (raw): the workgroup whose rows end at the new token copies k_new
+        // into its cache row (its DMA read the row from k_new; no other workgroup reads it).
+        if (!Q8 && append && j1 == sv.nvis && wave < 2) {
+            const size_t row = (size_t) wave * p.head_stride + (size_t) sv.newrow * kRawDim;
+            *reinterpret_cast<u32x4 *>(kbase + row + lane * 8) = *reinterpret_cast<const u32x4 *>(knew + wave * kRawDim + lane * 8);
+        }
+
+        // This wave's (m, l, O): l and (q8) the bias term summed over the lane groups.
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        if constexpr (Q8) {
+            bt += __shfl_xor(bt, 16);
+            bt += __shfl_xor(bt, 32);
+#pragma unroll
+            for (int dt = 0; dt < 32; ++dt) acc[dt] += bt;
+        }
+        // Merge the four waves through LDS (aliasing the rings, which are all consumed).
+        ESDA_WAIT_VM(0);
+        lds_barrier();
+        float *const accb = reinterpret_cast<float *>(wlds);          // [wave][head][516]
+        float *const mlb = &xf[0][0][0];                               // [wave][2][16] (m, l)
+#pragma unroll
+        for (int dt = 0; dt < 32; ++dt)
+            *reinterpret_cast<f32x4 *>(accb + (wave * 16 + li) * 516 + 16 * dt + 4 * lg) = acc[dt];
+        if (lg == 0) {
+            mlb[wave * 32 + li] = m;
+            mlb[wave * 32 + 16 + li] = l;
+        }
+        lds_barrier();
+        {
+            const int h = tid >> 4, d4 = tid & 15;  // head h, dims 4 d4 + 64 k
+            float mw[kWaves], M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                mw[w] = mlb[w * 32 + h];
+                M = fmaxf(M, mw[w]);
+            }
+            float cw[kWaves], L = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                cw[w] = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
+                L += cw[w] * mlb[w * 32 + 16 + h];
+            }
+            if (h < p.G) {
+                const size_t hq = (size_t) b * p.Hq + (size_t) kvh * p.G + h;
+                const size_t pidx = slot * p.G + h;
+                const float inv = 1.0f / L;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int d = 4 * d4 + 64 * k;
+                    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int w = 0; w < kWaves; ++w) o += *reinterpret_cast<const f32x4 *>(accb + (w * 16 + h) * 516 + d) * cw[w];
+                    if (direct) {
+                        bf16x4 r;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) r[e] = (__bf16) (o[e] * inv);
+                        *reinterpret_cast<uint2 *>(p.out + hq * kRawDim + d) = __builtin_bit_cast(uint2, r);
+                    } else {
+                        *reinterpret_cast<f32x4 *>(p.part_acc + pidx * kRawDim + d) = o;
+                    }
+                }
+                if (!direct && d4 == 0) {
+                    p.part_ml[pidx * 2 + 0] = M;
+                    p.part_ml[pidx * 2 + 1] = L;
+                }
+            }
+        }
+        lds_barrier();  // the merge area is read before the next segment's DMA overwrites it
+    };
+    walk_segments<kWaves>(p, segment);
 }
 
 struct MergeParams {
@@ -1516,15 +2012,22 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         ap.out = out;
         const dim3 grid = pl.balanced ? dim3(pl.W) : dim3(pl.S, d->num_kv_heads / pl.pk, d->batch);
         hipError_t e;
-        if (mode == 0) e = dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
-        // a precomputed cos/sin table is read where two kv heads share a workgroup; the
-        // one-kv-head form computes its table (its 16-row stages would need twice the rows)
-        else if (mode == 1) e = pl.pk == 2 ? (ap.rope_tab ? launch_attend<kRawDim, true, true, 2, false, true>(ap, grid, st)
-                                                          : launch_attend<kRawDim, true, true, 2>(ap, grid, st))
-                                           : launch_attend<kRawDim, true, true, 1>(ap, grid, st);
-        else e = pl.pk == 2 ? (ap.rope_tab ? launch_attend<kRawDim, true, true, 2, true, true>(ap, grid, st)
-                                           : launch_attend<kRawDim, true, true, 2, true>(ap, grid, st))
-                            : launch_attend<kRawDim, true, true, 1, true>(ap, grid, st);
+        if (mode == 0) {
+            e = dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
+        } else if (pl.pk == 2 && ap.rope_tab) {
+            // two kv heads per workgroup with the precomputed cos/sin table (the ES layer's
+            // form): the wave-private-ring kernel
+            if (mode == 1) hipLaunchKernelGGL(raw_attend_kernel<false>, grid, dim3(64 * kWaves), 0, st, ap);
+            else hipLaunchKernelGGL(raw_attend_kernel<true>, grid, dim3(64 * kWaves), 0, st, ap);
+            e = hipGetLastError();
+        } else if (mode == 1) {
+            // without a table (or with one kv head per workgroup) the 8-wave kernel computes
+            // its cos/sin per stage
+            e = pl.pk == 2 ? launch_attend<kRawDim, true, true, 2>(ap, grid, st) : launch_attend<kRawDim, true, true, 1>(ap, grid, st);
+        } else {
+            e = pl.pk == 2 ? launch_attend<kRawDim, true, true, 2, true>(ap, grid, st)
+                           : launch_attend<kRawDim, true, true, 1, true>(ap, grid, st);
+        }
         if (e != hipSuccess) return hip_fail(e, "attend_kernel launch");
     }
     // One split per pair: the attend workgroups wrote every output themselves.

@@ -100,12 +100,19 @@ def run_q8(name, *, B=1, Hq=32, Hkv=4, cap, pos, scale=1.0, seed=0, split_rows=0
     return o, errs
 
 
-def test_q8_small_with_append():
-    run_q8("small", cap=512, pos=[299], scale=512 ** -0.5)
+# table=True is the ES layer's form (precomputed rotary table, two kv heads per workgroup):
+# the wave-private-ring kernel; table=False the 8-wave kernel that computes its cos / sin.
+TABLE = pytest.mark.parametrize("table", [False, True], ids=["own-sincos", "table"])
 
 
-def test_q8_in_model_scale_one():
-    run_q8("scale1", cap=1024, pos=[1000], scale=1.0, seed=3)
+@TABLE
+def test_q8_small_with_append(table):
+    run_q8("small", cap=512, pos=[299], scale=512 ** -0.5, table=table)
+
+
+@TABLE
+def test_q8_in_model_scale_one(table):
+    run_q8("scale1", cap=1024, pos=[1000], scale=1.0, seed=3, table=table)
 
 
 def test_q8_long_context_131072():
@@ -113,29 +120,34 @@ def test_q8_long_context_131072():
     run_q8("c4-q8", cap=131072, pos=[131071], scale=512 ** -0.5, seed=5)
 
 
-def test_q8_batched_ragged_positions():
-    run_q8("batched", B=3, cap=4096, pos=[17, 2500, 4095], scale=512 ** -0.5, seed=7)
+@TABLE
+def test_q8_batched_ragged_positions(table):
+    run_q8("batched", B=3, cap=4096, pos=[17, 2500, 4095], scale=512 ** -0.5, seed=7, table=table)
 
 
-def test_q8_no_append_reads_cached_rows():
-    run_q8("no-append", cap=2048, pos=[1500], append=False, seed=9)
+@TABLE
+def test_q8_no_append_reads_cached_rows(table):
+    run_q8("no-append", cap=2048, pos=[1500], append=False, seed=9, table=table)
 
 
+@TABLE
 @pytest.mark.parametrize("split_rows", [16, 48, 512])
-def test_q8_split_sizes(split_rows):
-    run_q8(f"split{split_rows}", cap=1024, pos=[777], split_rows=split_rows, seed=11)
+def test_q8_split_sizes(split_rows, table):
+    run_q8(f"split{split_rows}", cap=1024, pos=[777], split_rows=split_rows, seed=11, table=table)
 
 
 def test_q8_unpacked_odd_kv_heads():
     run_q8("unpacked-hkv3", B=2, Hq=24, Hkv=3, cap=1024, pos=[1000, 333], scale=512 ** -0.5, seed=19)
 
 
-def test_q8_single_row():
-    run_q8("one-row", cap=64, pos=[0], seed=15)
+@TABLE
+def test_q8_single_row(table):
+    run_q8("one-row", cap=64, pos=[0], seed=15, table=table)
 
 
-def test_q8_rope_sign_fault_is_detected():
-    _, errs = run_q8("rope-fault", cap=2048, pos=[2047], scale=1.0, seed=17, fault=5)
+@TABLE
+def test_q8_rope_sign_fault_is_detected(table):
+    _, errs = run_q8("rope-fault", cap=2048, pos=[2047], scale=1.0, seed=17, fault=5, table=table)
     assert max(e.max() for e in errs) > 10 * TOL_MAX
 
 
@@ -144,9 +156,11 @@ def test_q8_long_context_131072_with_rope_table():
     run_q8("c4-q8-table", cap=131072, pos=[131071], scale=512 ** -0.5, seed=31, table=True)
 
 
-def test_q8_rope_table_matches_the_kernel_table_bit_for_bit():
-    """q8 decode with the precomputed table equals the kernel-computed table's result bit for
-    bit, over ragged batched positions with the new rows quantized in."""
+def test_q8_table_and_own_sincos_kernels_agree():
+    """q8 decode with the precomputed table (the wave-private-ring kernel) and with the
+    kernel's own cos/sin (the 8-wave kernel), over ragged batched positions with the new rows
+    quantized in: the quantized cache bytes are identical, and each output is within the
+    tolerance of the fp64 q8 oracle and of the other (different fp32 summation orders)."""
     from apertura_amd.decode import decode_raw_q8, new_raw_workspace, q8_step_for, rope_table
     rng = np.random.default_rng(33)
     B, cap = 2, 4096
@@ -157,12 +171,25 @@ def test_q8_rope_table_matches_the_kernel_table_bit_for_bit():
     kw = orc.to_bf16((1.0 + 0.25 * rng.standard_normal(512)).astype(np.float32))
     inv_d = torch.from_numpy(orc.rope_inv_freq(512, 1.0e6, 0.25)).cuda()
     pos = torch.tensor([4095, 2500], dtype=torch.int32, device="cuda")
-    outs = []
+    outs, caches = [], []
     for t in (None, rope_table(inv_d, cap)):
         q8_d = torch.from_numpy(qc).cuda()
         sc_d, bs_d = torch.from_numpy(sc).cuda(), torch.from_numpy(bs).cuda()
-        step = q8_step_for(q8_d, 32, eps=EPS, scale=1.0)
+        step = q8_step_for(q8_d, 32, eps=EPS, scale=512 ** -0.5)  # the configs' scale
         outs.append(decode_raw_q8(step, _dev(q), _dev(kn), q8_d, sc_d, bs_d, pos, _dev(kw), inv_d,
                                   workspace=new_raw_workspace(step, "cuda"), rope_table=t).clone())
+        caches.append((q8_d, sc_d, bs_d))
     torch.cuda.synchronize()
-    assert torch.equal(outs[0], outs[1])
+    for x, y in zip(caches[0], caches[1]):
+        assert torch.equal(x, y), "the two kernels quantized the new rows differently"
+    o = [orc.from_bf16(_host(t)).reshape(B, 32, 512).astype(np.float64) for t in outs]
+    inv = orc.rope_inv_freq(512, 1.0e6, 0.25)
+    q8h, sch, bsh = (c.cpu().numpy() for c in caches[1])
+    for b, pb in enumerate((4095, 2500)):
+        ref = orc.decode_raw_q8_f64(q[b], q8h[b], sch[b], bsh[b], pb + 1, kw, EPS, inv, 512 ** -0.5)
+        for name, ob in (("own-sincos", o[0][b]), ("table", o[1][b])):
+            err = np.abs(ob - ref)
+            print(f"[q8] {name} b={b}: max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
+            assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN
+    d = np.abs(o[1] - o[0])
+    assert d.max() <= TOL_MAX and d.mean() <= TOL_MEAN
