@@ -40,6 +40,13 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
+# Per-source additions.  The raw-K ring kernel multiplies each row by diag(kw) with MFMAs whose
+# results feed VALU work; the default heuristic gives every MFMA of a kernel that uses the
+# accumulation registers an AGPR result, which would cost four copies per product.
+EXTRA_FLAGS = {
+    "esda_decode.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"],
+}
+
 
 def sources() -> list[str]:
     return [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
@@ -53,7 +60,7 @@ def build(verbose: bool = False) -> str:
         obj = os.path.join(CSRC, os.path.basename(src) + ".o")
         # ES* C++ layer: host code only (HIP runtime API and the esda C ABI), built by
         # the host compiler so no device code is generated for it.
-        cmd = [HIPCC] + HIP_FLAGS + inc + ["-c", src, "-o", obj]
+        cmd = [HIPCC] + HIP_FLAGS + EXTRA_FLAGS.get(os.path.basename(src), []) + inc + ["-c", src, "-o", obj]
         if src.endswith(".cpp"):
             cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
                    "-I", os.path.join(ROCM, "include")] + inc + ["-c", src, "-o", obj]

@@ -1010,9 +1010,13 @@ void attend_kernel(AttendParams p) {
 //     of k-step kk);
 //   - forms their 16x16 Gram matrix with 16 MFMAs: the diagonal is each row's sum of
 //     squares (exact bf16 products, fp32 sums), hence rinv = rsqrt(mean + eps);
-//   - rebuilds K = bf16(rope(kraw * rinv * kw)) in registers -- the rotary partners
-//     (d, d + 256), d < 64, sit in one lane (k-steps 0, 1 and 8, 9), their bf16 cos / sin
-//     come from the table rows DMA'd beside the stage;
+//   - rebuilds K = bf16(rope(kraw * rinv * kw)), rounded where the reference rounds it:
+//     kraw * kw comes exactly (a product of two bf16 values fits fp32) from MFMAs of the
+//     lane's own rows against diag(kw) operands built once per kernel, whose C layout
+//     hands every lane the dims it supplied; one multiply by rinv, the rotation and the
+//     bf16 rounding remain per element.  The rotary partners (d, d + 256), d < 64, sit in
+//     one lane (k-steps 0, 1 and 8, 9); their bf16 cos / sin come from the table rows
+//     DMA'd beside the stage;
 //   - scores its 16 query heads (both GQA groups: heads of the other kv head's rows are
 //     masked) with 16 MFMAs, runs its own online softmax, and accumulates O^T[512 x 16
 //     heads] with 32 MFMAs over V = kraw read back by transpose reads, rinv folded into the
@@ -1032,6 +1036,16 @@ constexpr int kBlk = 1056;                 // LDS bytes per 1 KiB DMA block (1 K
 // 2m, 2m + 1 cover 16 consecutive dims (one 16-byte u8 piece, two bf16 ones) and the rotary
 // partners of k-steps 0, 1 are k-steps 8, 9 of the same lane.
 __device__ __forceinline__ int wdim(int kk, int lg) { return 64 * (kk >> 1) + 16 * lg + 8 * (kk & 1); }
+// The rotary k-steps (dims 0 .. 63 and their partners 256 .. 319) and their index 0 .. 3.
+__device__ __forceinline__ constexpr bool rot_step(int kk) { return (kk & 7) < 2; }
+__device__ __forceinline__ constexpr int rot_idx(int kk) { return (kk & 1) | ((kk >> 2) & 2); }
+
+// Lazy-rescale threshold of the raw kernels (log2 units).  Their V rows are RMS-normalised
+// (|v_d| <= sqrt(512)), so with probabilities up to 2^64 before normalisation the partial
+// sums stay below rows * 2^64 * 2^6 < 2^101 for any row count under 2^31, far from fp32's
+// limit.  The in-model scale of these layers is 1.0, which spreads the scores widely:
+// with the generic threshold of 8 about half of all stages would rescale.
+constexpr float kRawRescaleSlack = 64.0f;
 
 template <bool Q8>
 struct WRing {
@@ -1069,6 +1083,24 @@ void raw_attend_kernel(AttendParams p) {
         kwl[2 * tid + 1] = bf16_hi(t);
     }
     __syncthreads();
+    // Raw: the A operands of the x * kw products, diag(kw) over 16 dims.  For k-step kk and
+    // half hh the B operand is the lane's own dims wdim(kk, lg) + 4hh .. + 3 of row li;
+    // lane (li, lg) then holds kw of dim wdim(kk, lg) + 4hh + (li & 3) at slot li & 3 when
+    // lg == li / 4 and zeros elsewhere, and the product's C layout hands every lane x * kw
+    // of the same dims it supplied.
+    short4v dg[16][2];
+    if constexpr (!Q8) {
+        const short *kwb = reinterpret_cast<const short *>(p.kw);
+        const int s = li & 3;
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const short w = (li >> 2) == lg ? kwb[wdim(kk, lg) + 4 * hh + s] : (short) 0;
+                dg[kk][hh] = short4v{s == 0 ? w : (short) 0, s == 1 ? w : (short) 0, s == 2 ? w : (short) 0,
+                                     s == 3 ? w : (short) 0};
+            }
+    }
 
     auto segment = [&](const int b, const int kvh, const int j0, const int j1, const SeqView sv, const size_t slot,
                        const bool direct) {
@@ -1221,14 +1253,42 @@ void raw_attend_kernel(AttendParams p) {
             } else {
                 ESDA_WAIT_VM(0);
             }
-            // A operands: row li, dims wdim(kk, lg) (q8: q widened to bf16, exact)
-            u32x4 a[Q8 ? 1 : 16];  // raw: the stage's rows, rebuilt into K in place
-            u32x4 w8[Q8 ? 8 : 1];  // q8: the stage's u8 row pieces (16 dims each)
-            // Gram products of the A operands (q8: also against ones)
-            f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f}, g1 = {0.0f, 0.0f, 0.0f, 0.0f};
+            // Scores S^T[16 rows x 16 heads] of K = bf16(rope(x * rinv * kw)) (q8: x = q * scale
+            // + bias), rounded where ESDecodeAttn.mm:51-93 rounds it.
+            f32x4 sp0 = {0.0f, 0.0f, 0.0f, 0.0f}, sp1 = {0.0f, 0.0f, 0.0f, 0.0f};
+            // cos / sin of row li's position for the rotary pairs this lane holds
+            auto load_tab = [&](u32x4 (&tab)[4]) {
+                const int pos = li & 7, bt2 = pos >> 2, rib = pos & 3;
+#pragma unroll
+                for (int c4 = 0; c4 < 4; ++c4) {
+                    const int c = 4 * lg + c4;
+                    tab[c4] = *reinterpret_cast<const u32x4 *>(sl + W::ROWS + W::SB + bt2 * kBlk +
+                                                               16 * (16 * rib + ((c + 4 * rib) & 15)));
+                }
+            };
+            auto pack = [](const float (&v)[8]) -> bf16x8 {
+                bf16x8 r;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) r[e] = (__bf16) v[e];
+                return r;
+            };
+            // rope over rotary k-steps kr, kr + 8 (dims 16lg + 8kr + e and their partners + 256)
+            auto rotate = [](const u32x4 (&tab)[4], int kr, float (&lo)[8], float (&hi)[8]) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const unsigned w = tab[2 * kr + e / 4][e & 3];
+                    const float c = bf16_lo(w), s = bf16_hi(w);
+                    const float x0 = lo[e], x1 = hi[e];
+                    lo[e] = x0 * c - x1 * s;
+                    hi[e] = x1 * c + x0 * s;
+                }
+            };
             if constexpr (Q8) {
                 // Widen each 16-dim piece to bf16 (exact), store it in the wave's V tile for
-                // this stage's transpose reads and feed the norm MFMAs at once.
+                // this stage's transpose reads and feed the norm MFMAs (Gram diagonal: sum(q^2);
+                // against ones: sum(q)) at once.
+                u32x4 w8[8];  // the stage's u8 row pieces (16 dims each)
+                f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f}, g1 = {0.0f, 0.0f, 0.0f, 0.0f};
                 bf16x8 ones;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) ones[e] = (__bf16) 1.0f;
@@ -1255,33 +1315,14 @@ void raw_attend_kernel(AttendParams p) {
                     }
                     if (mm & 1) __builtin_amdgcn_sched_barrier(0);
                 }
-            } else {
-#pragma unroll
-                for (int kk = 0; kk < 16; ++kk) {
-                    a[kk] = *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg));
-                    const bf16x8 x = __builtin_bit_cast(bf16x8, a[kk]);
-                    g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
-                }
-            }
-            // cos / sin of this lane's rotary pairs 16lg .. 16lg + 15 at row li's position
-            u32x4 tab[4];
-            {
-                const int pos = li & 7, bt2 = pos >> 2, rib = pos & 3;
-#pragma unroll
-                for (int c4 = 0; c4 < 4; ++c4) {
-                    const int c = 4 * lg + c4;
-                    tab[c4] = *reinterpret_cast<const u32x4 *>(sl + W::ROWS + W::SB + bt2 * kBlk +
-                                                               16 * (16 * rib + ((c + 4 * rib) & 15)));
-                }
-            }
-            // Row norms: the Gram diagonal (and, q8, the row sums against ones).  C layout:
-            // lane (li, lg) holds C[4lg + i][li]; row li's diagonal is register li - 4lg of the
-            // lanes with lg == li / 4, which publish the row's factors.
-            {
-                const int i = li - 4 * lg;
-                if (i >= 0 && i < 4) {
-                    const float s2 = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
-                    if constexpr (Q8) {
+                u32x4 tab[4];
+                load_tab(tab);
+                // Row factors (C layout: lane (li, lg) holds C[4lg + i][li]; row li's diagonal
+                // is register li - 4lg of the lanes with lg == li / 4, which publish them).
+                {
+                    const int i = li - 4 * lg;
+                    if (i >= 0 && i < 4) {
+                        const float s2 = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
                         const float s1 = i == 0 ? g1[0] : i == 1 ? g1[1] : i == 2 ? g1[2] : g1[3];
                         const float scl = reinterpret_cast<const float *>(sl + W::ROWS)[li];
                         const float bias = reinterpret_cast<const float *>(sl + W::ROWS)[16 + li];
@@ -1295,68 +1336,97 @@ void raw_attend_kernel(AttendParams p) {
                         xfw[1 * 16 + li] = 1.0f / alpha;
                         xfw[2 * 16 + li] = bias / scl;
                         xfw[3 * 16 + li] = bias * rinv;
-                    } else {
+                    }
+                }
+                // Other lanes read the factors back: a compiler memory barrier keeps those
+                // loads after the stores above (the lanes' LDS accesses then run in order).
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);  // the Gram operands die here (a[] is in the V tile)
+                // K = bf16(rope(fma(q, scale * rinv, bias * rinv) * kw))
+                const float fa = xfw[0 * 16 + li], fb = xfw[3 * 16 + li];
+                auto kval = [&](int kk, int e) -> float {
+                    const float q = (float) ((w8[kk >> 1][2 * (kk & 1) + (e >> 2)] >> (8 * (e & 3))) & 255u);
+                    return __builtin_fmaf(q, fa, fb) * kwl[wdim(kk, lg) + e];
+                };
+#pragma unroll
+                for (int kr = 0; kr < 2; ++kr) {
+                    float lo[8], hi[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        lo[e] = kval(kr, e);
+                        hi[e] = kval(kr + 8, e);
+                    }
+                    rotate(tab, kr, lo, hi);
+                    sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(lo), qv[kr], sp0, 0, 0, 0);
+                    sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(hi), qv[kr + 8], sp1, 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);  // bound the live rebuilt values
+                }
+#pragma unroll
+                for (int kk = 2; kk < 16; ++kk) {
+                    if (rot_step(kk)) continue;
+                    float v[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = kval(kk, e);
+                    if (kk & 1) sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp1, 0, 0, 0);
+                    else sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp0, 0, 0, 0);
+                    if (kk & 1) __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+                // Pass 1: the Gram diagonal of the stage's rows (sum of squares).
+                f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int kk = 0; kk < 16; ++kk) {
+                    const bf16x8 x = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg)));
+                    g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
+                }
+                {
+                    const int i = li - 4 * lg;
+                    if (i >= 0 && i < 4) {
+                        const float s2 = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
                         const float ms = s2 * (1.0f / kRawDim) + p.eps;
                         const float rinv = __builtin_amdgcn_rsqf(ms);
                         xfw[0 * 16 + li] = rinv;
                         xfw[1 * 16 + li] = ms * rinv;
                     }
                 }
-            }
-            __builtin_amdgcn_sched_barrier(0);  // the Gram operands die here (q8: a[] is in the V tile)
-            // K = bf16(rope(x * rinv * kw)) (q8: x * rinv = fma(q, scale * rinv, bias * rinv)),
-            // then the scores S^T[16 rows x 16 heads]
-            const float fa = xfw[0 * 16 + li];
-            const float fb = Q8 ? xfw[3 * 16 + li] : 0.0f;
-            // the k-norm weights of k-step kk, dim e of the lane's 8
-            auto kwf = [&](int kk, int e) { return kwl[wdim(kk, lg) + e]; };
-            auto kval = [&](int kk, int e) -> float {
-                if constexpr (Q8) {
-                    const float q = (float) ((w8[kk >> 1][2 * (kk & 1) + (e >> 2)] >> (8 * (e & 3))) & 255u);
-                    return __builtin_fmaf(q, fa, fb) * kwf(kk, e);
-                }
-                else {
-                    const float x = (e & 1) ? bf16_hi(a[Q8 ? 0 : kk][e >> 1]) : bf16_lo(a[Q8 ? 0 : kk][e >> 1]);
-                    return x * fa * kwf(kk, e);
-                }
-            };
-            auto pack = [](const float (&v)[8]) -> bf16x8 {
-                bf16x8 r;
+                // Other lanes read the factors back: a compiler memory barrier keeps those
+                // loads after the stores above (the lanes' LDS accesses then run in order).
+                asm volatile("" ::: "memory");
+                u32x4 tab[4];
+                load_tab(tab);
+                const float rk = xfw[0 * 16 + li];  // rinv of row li
+                // Pass 2: x * kw exactly (fp32 products of bf16 values) by MFMAs against the
+                // diagonal kw operands, times rinv, rotated, rounded to bf16, scored.
+                auto xkw = [&](int kk, float (&v)[8]) {
+                    const u32x4 t = *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg));
+                    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    const f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                        dg[kk][0], __builtin_bit_cast(short4v, uint2{t[0], t[1]}), z, 0, 0, 0);
+                    const f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                        dg[kk][1], __builtin_bit_cast(short4v, uint2{t[2], t[3]}), z, 0, 0, 0);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) r[e] = (__bf16) v[e];
-                return r;
-            };
-            f32x4 sp0 = {0.0f, 0.0f, 0.0f, 0.0f}, sp1 = {0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int e = 0; e < 4; ++e) {
+                        v[e] = d0[e] * rk;
+                        v[4 + e] = d1[e] * rk;
+                    }
+                };
 #pragma unroll
-            for (int kr = 0; kr < 2; ++kr) {
-                // rotary k-steps kr and kr + 8 (dims 16lg + 8kr + e and 256 + ...)
-                float lo[8], hi[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    lo[e] = kval(kr, e);
-                    hi[e] = kval(kr + 8, e);
+                for (int kr = 0; kr < 2; ++kr) {
+                    float lo[8], hi[8];
+                    xkw(kr, lo);
+                    xkw(kr + 8, hi);
+                    rotate(tab, kr, lo, hi);
+                    sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(lo), qv[kr], sp0, 0, 0, 0);
+                    sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(hi), qv[kr + 8], sp1, 0, 0, 0);
                 }
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const unsigned w = tab[2 * kr + e / 4][e & 3];
-                    const float c = bf16_lo(w), s = bf16_hi(w);
-                    const float x0 = lo[e], x1 = hi[e];
-                    lo[e] = x0 * c - x1 * s;
-                    hi[e] = x1 * c + x0 * s;
+                for (int kk = 2; kk < 16; ++kk) {
+                    if (rot_step(kk)) continue;
+                    float v[8];
+                    xkw(kk, v);
+                    if (kk & 1) sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp1, 0, 0, 0);
+                    else sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp0, 0, 0, 0);
                 }
-                sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(lo), qv[kr], sp0, 0, 0, 0);
-                sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(hi), qv[kr + 8], sp1, 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);  // bound the live rebuilt values
-            }
-#pragma unroll
-            for (int kk = 2; kk < 16; ++kk) {
-                if (kk == 8 || kk == 9) continue;
-                float v[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = kval(kk, e);
-                if (kk & 1) sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp1, 0, 0, 0);
-                else sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp0, 0, 0, 0);
-                if (kk & 1) __builtin_amdgcn_sched_barrier(0);
             }
             f32x4 sc = sp0 + sp1;
             // Online softmax (log2 domain) over stage rows 4lg .. 4lg + 3: rows past the
@@ -1365,13 +1435,20 @@ void raw_attend_kernel(AttendParams p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) sc[r] = hmatch && (jt + r) < j1 ? sc[r] * p.scale_log2e : -INFINITY;
             const float tmax = wave_max_across_groups(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-            if (__any(tmax > m + kRescaleSlack)) {
+            m = m == -INFINITY ? tmax : m;  // first stage: nothing accumulated to rescale
+            if (__builtin_expect(__any(tmax > m + kRawRescaleSlack), 0)) {
                 const float mnew = fmaxf(m, tmax);
                 const float corr = __builtin_amdgcn_exp2f(m - mnew);
                 l *= corr;
                 if constexpr (Q8) bt *= corr;
 #pragma unroll
-                for (int dt = 0; dt < 32; ++dt) acc[dt] *= corr;
+                for (int dt = 0; dt < 32; ++dt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float x = acc[dt][e];
+                        acc_scale(x, corr);
+                        acc[dt][e] = x;
+                    }
                 m = mnew;
             }
             short4v pbs;

@@ -48,6 +48,22 @@ __device__ __forceinline__ float wave_max_across_groups(float x) {
 // far from fp32 / bf16 limits, and the final division by l is unchanged.
 constexpr float kRescaleSlack = 8.0f;
 
+// x *= c for a value that lives in an accumulation register (AGPR): read, multiply and
+// write back in place.  With a plain multiply of the PV accumulators the compiler keeps
+// VGPR copies of all of them, refreshed at every stage, for a rescale that is rare.
+// (The MFMAs that next read x come dozens of instructions later, past any wait-state
+// requirement of an AGPR write.)
+__device__ __forceinline__ void acc_scale(float &x, float c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    float t;
+    asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32_e32 %1, %2, %1\n\tv_accvgpr_write_b32 %0, %1"
+                 : "+a"(x), "=&v"(t)
+                 : "v"(c));
+#else
+    x *= c;
+#endif
+}
+
 // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
 // lgkmcnt[11:8], vmcnt[5:4] at [15:14]).
 #define ESDA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
