@@ -1074,21 +1074,21 @@ void raw_attend_kernel(AttendParams p) {
     const int li = lane & 15, lg = lane >> 4;
     unsigned char *const wl = wlds + wave * W::WAVE;
 
-    // k-norm weights in fp32, read per k-step (lanes of a lane group read the same 32 bytes);
-    // 128 of them per lane would not fit in registers beside O^T, Q^T and the stage
-    __shared__ __attribute__((aligned(16))) float kwl[kRawDim];
-    {
+    // q8: the k-norm weights in fp32, read per k-step (the lanes of a lane group read the
+    // same 32 bytes); 128 of them per lane would not fit in registers beside O^T and Q^T.
+    __shared__ __attribute__((aligned(16))) float kwl[Q8 ? kRawDim : 1];
+    if constexpr (Q8) {
         const unsigned t = reinterpret_cast<const unsigned *>(p.kw)[tid];
         kwl[2 * tid] = bf16_lo(t);
         kwl[2 * tid + 1] = bf16_hi(t);
+        __syncthreads();
     }
-    __syncthreads();
-    // Raw: the A operands of the x * kw products, diag(kw) over 16 dims.  For k-step kk and
-    // half hh the B operand is the lane's own dims wdim(kk, lg) + 4hh .. + 3 of row li;
-    // lane (li, lg) then holds kw of dim wdim(kk, lg) + 4hh + (li & 3) at slot li & 3 when
+    // Raw: the A operands of the x * kw products, diag(kw) over 16 dims.  For k-step kk and half
+    // hh the B operand is the lane's own dims wdim(kk, lg) + 4hh .. + 3 of row li; lane
+    // (li, lg) then holds kw of dim wdim(kk, lg) + 4hh + (li & 3) at slot li & 3 when
     // lg == li / 4 and zeros elsewhere, and the product's C layout hands every lane x * kw
     // of the same dims it supplied.
-    short4v dg[16][2];
+    short4v dg[Q8 ? 1 : 16][2];
     if constexpr (!Q8) {
         const short *kwb = reinterpret_cast<const short *>(p.kw);
         const int s = li & 3;
@@ -1173,61 +1173,66 @@ void raw_attend_kernel(AttendParams p) {
         // scores are masked); the new token's raw row comes from k_new.
         auto dma = [&](int st, unsigned char *sl) {
             const int jst = j0 + 8 * st;
-            const bool interior = jst + 8 < j1;
-            {
-                // table rows of positions jst .. jst + 7: block bt holds positions 4bt .. 4bt+3,
-                // piece c of position rib at 16 * (16 rib + (c + 4 rib) mod 16)
-                const int rib = lane >> 4, c = (lane - 4 * rib) & 15;
+            const unsigned lb = lds_addr(sl);
+            // table rows of positions jst .. jst + 7: block bt holds positions 4bt .. 4bt+3,
+            // piece c of position rib at 16 * (16 rib + (c + 4 rib) mod 16)
+            const int rib = lane >> 4, c = (lane - 4 * rib) & 15;
+            const unsigned tdst = lb + W::ROWS + W::SB;
+            // q8 block i: rows 2i, 2i + 1 (kv head i / 4); lane l loads row 2i + (l & 1), 16-byte
+            // piece l >> 1
+            const int h = lane & 1, pc = lane >> 1;
+            if (jst + 8 < j1) {
+                // Interior stage: all eight positions exist.  One scalar base per stream, the
+                // rows 1 KiB apart, so each DMA costs a scalar add and an M0 write.
+                const uint32_t *tab0 = p.rope_tab + (size_t) (sv.first + jst) * kRopePairs;
+                lds_dma16_s(tab0, (unsigned) (rib * 256 + c * 16), tdst);
+                lds_dma16_s(tab0 + 4 * kRopePairs, (unsigned) (rib * 256 + c * 16), tdst + kBlk);
+                if constexpr (Q8) {
+                    const unsigned char *r0 = q8base + (size_t) (sv.first + jst) * kRawDim;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        lds_dma16_s(r0 + (size_t) (i >> 2) * p.head_stride + ((2 * i) & 7) * kRawDim,
+                                    (unsigned) (h * kRawDim + pc * 16), lb + i * kBlk);
+                } else {
+                    const unsigned char *r0 = reinterpret_cast<const unsigned char *>(kbase + (size_t) (sv.first + jst) * kRawDim);
+                    const unsigned char *r1 = r0 + (size_t) p.head_stride * sizeof(uint16_t);
+#pragma unroll
+                    for (int sr = 0; sr < 16; ++sr)
+                        lds_dma16_s((sr < 8 ? r0 : r1) + (sr & 7) * kRawDim * sizeof(uint16_t), (unsigned) (lane * 16),
+                                    lb + sr * kBlk);
+                }
+            } else {
+                // The segment's last stage: rows past its end repeat its last row (their scores
+                // are masked); the new token's raw row comes from k_new.
 #pragma unroll
                 for (int bt = 0; bt < 2; ++bt) {
-                    const unsigned dst = lds_addr(sl + W::ROWS + W::SB + bt * kBlk);
-                    if (interior) {
-                        lds_dma16_s(p.rope_tab + (size_t) (sv.first + jst + 4 * bt) * kRopePairs,
-                                    (unsigned) (rib * 256 + c * 16), dst);
-                    } else {
-                        const int j = min(jst + 4 * bt + rib, j1 - 1);
-                        lds_dma16(p.rope_tab + (size_t) (sv.first + j) * kRopePairs + c * 4, dst);
+                    const int j = min(jst + 4 * bt + rib, j1 - 1);
+                    lds_dma16(p.rope_tab + (size_t) (sv.first + j) * kRopePairs + c * 4, tdst + bt * kBlk);
+                }
+                if constexpr (Q8) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int j = min(jst + ((2 * i) & 7) + h, j1 - 1);
+                        lds_dma16(q8base + (size_t) (i >> 2) * p.head_stride + (size_t) (sv.first + j) * kRawDim + pc * 16,
+                                  lb + i * kBlk);
+                    }
+                } else {
+#pragma unroll
+                    for (int sr = 0; sr < 16; ++sr) {
+                        const int pr = sr >> 3, j = min(jst + (sr & 7), j1 - 1);
+                        const uint16_t *src = (append && j == sv.nvis - 1)
+                                                  ? knew + pr * kRawDim
+                                                  : kbase + (size_t) pr * p.head_stride + (size_t) (sv.first + j) * kRawDim;
+                        lds_dma16(src + lane * 8, lb + sr * kBlk);
                     }
                 }
             }
             if constexpr (Q8) {
-                // block i: rows 2i, 2i + 1 (kv head i / 4), lane l loads row 2i + (l & 1),
-                // 16-byte piece l >> 1
-                const int h = lane & 1, pc = lane >> 1;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int pr = i >> 2, r0 = (2 * i) & 7;
-                    const unsigned dst = lds_addr(sl + i * kBlk);
-                    if (interior) {
-                        lds_dma16_s(q8base + (size_t) pr * p.head_stride + (size_t) (sv.first + jst + r0) * kRawDim,
-                                    (unsigned) (h * kRawDim + pc * 16), dst);
-                    } else {
-                        const int j = min(jst + r0 + h, j1 - 1);
-                        lds_dma16(q8base + (size_t) pr * p.head_stride + (size_t) (sv.first + j) * kRawDim + pc * 16,
-                                  dst);
-                    }
-                }
                 if (lane < 32) {
                     const int sr = lane & 15, pr = sr >> 3;
                     const int j = min(jst + (sr & 7), j1 - 1);
                     lds_dma4((lane < 16 ? p.qsc : p.qbs) + sb_off + (size_t) pr * p.sb_head_stride + (size_t) (sv.first + j),
-                             lds_addr(sl + W::ROWS));
-                }
-            } else {
-#pragma unroll
-                for (int sr = 0; sr < 16; ++sr) {
-                    const int pr = sr >> 3, i = sr & 7;
-                    const unsigned dst = lds_addr(sl + sr * kBlk);
-                    if (interior) {
-                        lds_dma16_s(kbase + (size_t) pr * p.head_stride + (size_t) (sv.first + jst + i) * kRawDim,
-                                    (unsigned) (lane * 16), dst);
-                    } else {
-                        const int j = min(jst + i, j1 - 1);
-                        const uint16_t *src = (append && j == sv.nvis - 1)
-                                                  ? knew + pr * kRawDim
-                                                  : kbase + (size_t) pr * p.head_stride + (size_t) (sv.first + j) * kRawDim;
-                        lds_dma16(src + lane * 8, dst);
-                    }
+                             lb + W::ROWS);
                 }
             }
         };
@@ -1283,46 +1288,52 @@ void raw_attend_kernel(AttendParams p) {
                     hi[e] = x1 * c + x0 * s;
                 }
             };
-            if constexpr (Q8) {
-                // Widen each 16-dim piece to bf16 (exact), store it in the wave's V tile for
-                // this stage's transpose reads and feed the norm MFMAs (Gram diagonal: sum(q^2);
-                // against ones: sum(q)) at once.
-                u32x4 w8[8];  // the stage's u8 row pieces (16 dims each)
+            // Pass 1: the row norms from Gram products of the operands.  Raw: the rows as
+            // stored.  q8: each 16-dim u8 piece widened to bf16 (exact) and stored in the
+            // wave's V tile for the transpose reads, with a product against ones for the row
+            // sums.
+            u32x4 w8[Q8 ? 8 : 1];  // q8: the stage's u8 row pieces (16 dims each)
+            {
                 f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f}, g1 = {0.0f, 0.0f, 0.0f, 0.0f};
-                bf16x8 ones;
+                if constexpr (Q8) {
+                    bf16x8 ones;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) ones[e] = (__bf16) 1.0f;
-                unsigned char *stg = wl + 2 * W::SLOT;
+                    for (int e = 0; e < 8; ++e) ones[e] = (__bf16) 1.0f;
 #pragma unroll
-                for (int mm = 0; mm < 8; ++mm) {
-                    w8[mm] = *reinterpret_cast<const u32x4 *>(sl + (li >> 1) * kBlk + 32 * (4 * mm + lg) + 16 * (li & 1));
+                    for (int mm = 0; mm < 8; ++mm) {
+                        w8[mm] = *reinterpret_cast<const u32x4 *>(sl + (li >> 1) * kBlk + 32 * (4 * mm + lg) + 16 * (li & 1));
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        unsigned o[4];
+                        for (int h = 0; h < 2; ++h) {
+                            unsigned o[4];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const unsigned word = w8[mm][2 * h + e / 2];
-                            const float f0 = (float) ((word >> (16 * (e & 1))) & 255u);
-                            const float f1 = (float) ((word >> (16 * (e & 1) + 8)) & 255u);
-                            o[e] = __builtin_amdgcn_perm(__builtin_bit_cast(unsigned, f1), __builtin_bit_cast(unsigned, f0),
-                                                         0x07060302u);
+                            for (int e = 0; e < 4; ++e) {
+                                const unsigned word = w8[mm][2 * h + e / 2];
+                                const float f0 = (float) ((word >> (16 * (e & 1))) & 255u);
+                                const float f1 = (float) ((word >> (16 * (e & 1) + 8)) & 255u);
+                                o[e] = __builtin_amdgcn_perm(__builtin_bit_cast(unsigned, f1), __builtin_bit_cast(unsigned, f0),
+                                                             0x07060302u);
+                            }
+                            const u32x4 ab = u32x4{o[0], o[1], o[2], o[3]};
+                            *reinterpret_cast<u32x4 *>(wl + 2 * W::SLOT + li * kBlk + 2 * wdim(2 * mm + h, lg)) = ab;
+                            const bf16x8 x = __builtin_bit_cast(bf16x8, ab);
+                            g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
+                            g1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, ones, g1, 0, 0, 0);
                         }
-                        const u32x4 ab = u32x4{o[0], o[1], o[2], o[3]};
-                        *reinterpret_cast<u32x4 *>(stg + li * kBlk + 2 * wdim(2 * mm + h, lg)) = ab;
-                        const bf16x8 x = __builtin_bit_cast(bf16x8, ab);
-                        g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
-                        g1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, ones, g1, 0, 0, 0);
+                        if (mm & 1) __builtin_amdgcn_sched_barrier(0);
                     }
-                    if (mm & 1) __builtin_amdgcn_sched_barrier(0);
+                } else {
+#pragma unroll
+                    for (int kk = 0; kk < 16; ++kk) {
+                        const bf16x8 x = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg)));
+                        g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
+                    }
                 }
-                u32x4 tab[4];
-                load_tab(tab);
                 // Row factors (C layout: lane (li, lg) holds C[4lg + i][li]; row li's diagonal
                 // is register li - 4lg of the lanes with lg == li / 4, which publish them).
-                {
-                    const int i = li - 4 * lg;
-                    if (i >= 0 && i < 4) {
-                        const float s2 = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
+                const int i = li - 4 * lg;
+                if (i >= 0 && i < 4) {
+                    const float s2 = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
+                    if constexpr (Q8) {
                         const float s1 = i == 0 ? g1[0] : i == 1 ? g1[1] : i == 2 ? g1[2] : g1[3];
                         const float scl = reinterpret_cast<const float *>(sl + W::ROWS)[li];
                         const float bias = reinterpret_cast<const float *>(sl + W::ROWS)[16 + li];
@@ -1336,68 +1347,33 @@ void raw_attend_kernel(AttendParams p) {
                         xfw[1 * 16 + li] = 1.0f / alpha;
                         xfw[2 * 16 + li] = bias / scl;
                         xfw[3 * 16 + li] = bias * rinv;
-                    }
-                }
-                // Other lanes read the factors back: a compiler memory barrier keeps those
-                // loads after the stores above (the lanes' LDS accesses then run in order).
-                asm volatile("" ::: "memory");
-                __builtin_amdgcn_sched_barrier(0);  // the Gram operands die here (a[] is in the V tile)
-                // K = bf16(rope(fma(q, scale * rinv, bias * rinv) * kw))
-                const float fa = xfw[0 * 16 + li], fb = xfw[3 * 16 + li];
-                auto kval = [&](int kk, int e) -> float {
-                    const float q = (float) ((w8[kk >> 1][2 * (kk & 1) + (e >> 2)] >> (8 * (e & 3))) & 255u);
-                    return __builtin_fmaf(q, fa, fb) * kwl[wdim(kk, lg) + e];
-                };
-#pragma unroll
-                for (int kr = 0; kr < 2; ++kr) {
-                    float lo[8], hi[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        lo[e] = kval(kr, e);
-                        hi[e] = kval(kr + 8, e);
-                    }
-                    rotate(tab, kr, lo, hi);
-                    sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(lo), qv[kr], sp0, 0, 0, 0);
-                    sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(hi), qv[kr + 8], sp1, 0, 0, 0);
-                    __builtin_amdgcn_sched_barrier(0);  // bound the live rebuilt values
-                }
-#pragma unroll
-                for (int kk = 2; kk < 16; ++kk) {
-                    if (rot_step(kk)) continue;
-                    float v[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = kval(kk, e);
-                    if (kk & 1) sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp1, 0, 0, 0);
-                    else sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp0, 0, 0, 0);
-                    if (kk & 1) __builtin_amdgcn_sched_barrier(0);
-                }
-            } else {
-                // Pass 1: the Gram diagonal of the stage's rows (sum of squares).
-                f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int kk = 0; kk < 16; ++kk) {
-                    const bf16x8 x = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg)));
-                    g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
-                }
-                {
-                    const int i = li - 4 * lg;
-                    if (i >= 0 && i < 4) {
-                        const float s2 = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
+                    } else {
                         const float ms = s2 * (1.0f / kRawDim) + p.eps;
                         const float rinv = __builtin_amdgcn_rsqf(ms);
                         xfw[0 * 16 + li] = rinv;
                         xfw[1 * 16 + li] = ms * rinv;
                     }
                 }
-                // Other lanes read the factors back: a compiler memory barrier keeps those
-                // loads after the stores above (the lanes' LDS accesses then run in order).
-                asm volatile("" ::: "memory");
-                u32x4 tab[4];
-                load_tab(tab);
-                const float rk = xfw[0 * 16 + li];  // rinv of row li
-                // Pass 2: x * kw exactly (fp32 products of bf16 values) by MFMAs against the
-                // diagonal kw operands, times rinv, rotated, rounded to bf16, scored.
-                auto xkw = [&](int kk, float (&v)[8]) {
+            }
+            // Other lanes read the factors back: a compiler memory barrier keeps those loads
+            // after the stores above (the lanes' LDS accesses then run in order).
+            asm volatile("" ::: "memory");
+            u32x4 tab[4];
+            load_tab(tab);
+            const float rk = xfw[0 * 16 + li];  // rinv of row li (q8: scale * rinv)
+            // Pass 2: x * rinv * kw of k-step kk, dims wdim(kk, lg) .. + 7 of row li.
+            auto xkw = [&](int kk, float (&v)[8]) {
+                if constexpr (Q8) {
+                    // fma(q, scale * rinv, bias * rinv) * kw, per element
+                    const float fb = xfw[3 * 16 + li];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float q = (float) ((w8[kk >> 1][2 * (kk & 1) + (e >> 2)] >> (8 * (e & 3))) & 255u);
+                        v[e] = __builtin_fmaf(q, rk, fb) * kwl[wdim(kk, lg) + e];
+                    }
+                } else {
+                    // x * kw exactly (a product of two bf16 values fits fp32) by MFMAs against
+                    // the diagonal kw operands, then times rinv
                     const u32x4 t = *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg));
                     const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
                     const f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
@@ -1409,24 +1385,24 @@ void raw_attend_kernel(AttendParams p) {
                         v[e] = d0[e] * rk;
                         v[4 + e] = d1[e] * rk;
                     }
-                };
-#pragma unroll
-                for (int kr = 0; kr < 2; ++kr) {
-                    float lo[8], hi[8];
-                    xkw(kr, lo);
-                    xkw(kr + 8, hi);
-                    rotate(tab, kr, lo, hi);
-                    sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(lo), qv[kr], sp0, 0, 0, 0);
-                    sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(hi), qv[kr + 8], sp1, 0, 0, 0);
                 }
+            };
 #pragma unroll
-                for (int kk = 2; kk < 16; ++kk) {
-                    if (rot_step(kk)) continue;
-                    float v[8];
-                    xkw(kk, v);
-                    if (kk & 1) sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp1, 0, 0, 0);
-                    else sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp0, 0, 0, 0);
-                }
+            for (int kr = 0; kr < 2; ++kr) {
+                float lo[8], hi[8];
+                xkw(kr, lo);
+                xkw(kr + 8, hi);
+                rotate(tab, kr, lo, hi);
+                sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(lo), qv[kr], sp0, 0, 0, 0);
+                sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(hi), qv[kr + 8], sp1, 0, 0, 0);
+            }
+#pragma unroll
+            for (int kk = 2; kk < 16; ++kk) {
+                if (rot_step(kk)) continue;
+                float v[8];
+                xkw(kk, v);
+                if (kk & 1) sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp1, 0, 0, 0);
+                else sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp0, 0, 0, 0);
             }
             f32x4 sc = sp0 + sp1;
             // Online softmax (log2 domain) over stage rows 4lg .. 4lg + 3: rows past the
