@@ -1956,8 +1956,13 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
     } else {
         long long chunk = d->split_rows;
         if (chunk == 0) {
-            chunk = (rows_max + kTargetGroups - 1) / kTargetGroups;
-            chunk = (chunk + kMinRows - 1) / kMinRows * kMinRows;
+            // The fewest rows per split that keep the grid within one workgroup per CU, in
+            // whole 16-row tiles (C2, 4 pairs of 8193 rows: 64-row rounding gave 192-row
+            // splits and 176 workgroups, 11.4 us; 16-row rounding gives 144 and 228, 10.3).
+            const long long pairs = (long long) d->batch * (d->num_kv_heads / pl->pk);
+            const long long per_pair = std::max(1LL, kTargetGroups / pairs);
+            chunk = (maxvis + per_pair - 1) / per_pair;
+            chunk = (chunk + kTile - 1) / kTile * kTile;
             if (chunk < kMinRows) chunk = kMinRows;
             if (chunk > 8192) chunk = 8192;
         }
