@@ -1036,9 +1036,8 @@ constexpr int kBlk = 1056;                 // LDS bytes per 1 KiB DMA block (1 K
 // 2m, 2m + 1 cover 16 consecutive dims (one 16-byte u8 piece, two bf16 ones) and the rotary
 // partners of k-steps 0, 1 are k-steps 8, 9 of the same lane.
 __device__ __forceinline__ int wdim(int kk, int lg) { return 64 * (kk >> 1) + 16 * lg + 8 * (kk & 1); }
-// The rotary k-steps (dims 0 .. 63 and their partners 256 .. 319) and their index 0 .. 3.
+// The rotary k-steps: dims 0 .. 63 (k-steps 0, 1) and their partners 256 .. 319 (8, 9).
 __device__ __forceinline__ constexpr bool rot_step(int kk) { return (kk & 7) < 2; }
-__device__ __forceinline__ constexpr int rot_idx(int kk) { return (kk & 1) | ((kk >> 2) & 2); }
 
 // Lazy-rescale threshold of the raw kernels (log2 units).  Their V rows are RMS-normalised
 // (|v_d| <= sqrt(512)), so with probabilities up to 2^64 before normalisation the partial
