@@ -271,6 +271,221 @@ int32_t orc_decode_refround(const orc_desc *d, const uint16_t *q, const uint16_t
     return j.status;
 }
 
+/* ------------------------------------------- grouped reference rounding */
+
+/* orc_decode_refround with each K and V row read once for the query heads of its kv head
+ * and the rows of one (sequence, kv head) spread over threads: the CPU baseline that
+ * bench.py times.  Same rounding points as item_refround (ESAttention.mm:136-165): f32 dot
+ * products summed in dimension order, bf16 scores, bf16(scaling), a precise softmax over
+ * all visible rows, bf16 weights, f32 accumulation, bf16 output.  Only the order in which
+ * the splits' partial sums (softmax denominator, output accumulation) combine differs; with
+ * one split per (sequence, kv head) the output is that of orc_decode_refround bit for bit.
+ * The query heads of a kv head are the innermost loop (blocks of 8), so the compiler can
+ * vectorise across heads without reordering any head's sums. */
+#define ORC_HB 8
+
+/* bf16 <-> fp32 as orc_bf16_to_f32 / orc_f32_to_bf16, local to this file so the compiler
+ * inlines them into the loops (the exported functions are called through the PLT). */
+static inline float bf2f(uint16_t h) {
+    const uint32_t u = ((uint32_t) h) << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+static inline float bfr(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return x;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+typedef struct {
+    const orc_desc *d;
+    const uint16_t *q, *k, *v;
+    const int32_t *pos, *row_base;
+    uint16_t *out;
+    int32_t G, nsplit;
+    int32_t **rows;      /* [B] visible rows */
+    int32_t *nvis;       /* [B] */
+    float **sc;          /* [B * Hkv] scores, then exp(s - max): [G][n] */
+    float *smax, *sden;  /* [B * Hkv * nsplit][G] */
+    float *pacc;         /* [B * Hkv * nsplit][D][ORC_HB * nhb] */
+    int32_t status;
+} gjob_t;
+
+static void split_range(int32_t n, int32_t ns, int32_t s, int32_t *t0, int32_t *t1) {
+    *t0 = (int32_t) ((int64_t) n * s / ns);
+    *t1 = (int32_t) ((int64_t) n * (s + 1) / ns);
+}
+
+/* Scores of split s of (b, kvh): sc[h][t] and the split's max per head. */
+__attribute__((target_clones("avx2", "default"), optimize("O3,tree-vectorize")))
+static void gitem_scores(void *ctx, int64_t it) {
+    gjob_t *j = (gjob_t *) ctx;
+    const orc_desc *d = j->d;
+    const int32_t D = d->D, G = j->G, ns = j->nsplit;
+    const int32_t pair = (int32_t) (it / ns), s = (int32_t) (it % ns);
+    const int32_t b = pair / d->Hkv, kvh = pair % d->Hkv, n = j->nvis[b];
+    if (n <= 0) return;
+    int32_t t0, t1;
+    split_range(n, ns, s, &t0, &t1);
+    const size_t base = (size_t) b * d->seq_stride + (size_t) kvh * d->head_stride;
+    const float sc = eff_scale(d), scb = bf(sc);
+    float *qt = (float *) malloc(sizeof(float) * (size_t) D * ORC_HB);
+    for (int32_t h0 = 0; h0 < G; h0 += ORC_HB) {
+        for (int32_t i = 0; i < D; ++i)
+            for (int32_t e = 0; e < ORC_HB; ++e) {
+                const int32_t h = h0 + e;
+                qt[(size_t) i * ORC_HB + e] =
+                    h < G ? bf2f(j->q[((size_t) b * d->Hq + (size_t) kvh * G + h) * D + i]) : 0.0f;
+            }
+        float mx[ORC_HB];
+        for (int32_t e = 0; e < ORC_HB; ++e) mx[e] = -INFINITY;
+        for (int32_t t = t0; t < t1; ++t) {
+            const uint16_t *kr = j->k + base + (size_t) j->rows[b][t] * D;
+            float a[ORC_HB] = {0};
+            for (int32_t i = 0; i < D; ++i) {
+                const float kf = bf2f(kr[i]);
+                for (int32_t e = 0; e < ORC_HB; ++e) a[e] += qt[(size_t) i * ORC_HB + e] * kf;
+            }
+            for (int32_t e = 0; e < ORC_HB && h0 + e < G; ++e) {
+                float v = bfr(a[e]);
+                if (sc != 1.0f) v = bfr(v * scb);
+                j->sc[pair][(size_t) (h0 + e) * n + t] = v;
+                if (v > mx[e]) mx[e] = v;
+            }
+        }
+        for (int32_t e = 0; e < ORC_HB && h0 + e < G; ++e) j->smax[(size_t) it * G + h0 + e] = mx[e];
+    }
+    free(qt);
+}
+
+/* exp(s - max) in place over split s, and the split's sum per head. */
+static void gitem_exp(void *ctx, int64_t it) {
+    gjob_t *j = (gjob_t *) ctx;
+    const orc_desc *d = j->d;
+    const int32_t G = j->G, ns = j->nsplit;
+    const int32_t pair = (int32_t) (it / ns), s = (int32_t) (it % ns);
+    const int32_t b = pair / d->Hkv, n = j->nvis[b];
+    if (n <= 0) return;
+    int32_t t0, t1;
+    split_range(n, ns, s, &t0, &t1);
+    for (int32_t h = 0; h < G; ++h) {
+        float mx = -INFINITY;
+        for (int32_t u = 0; u < ns; ++u) mx = fmaxf(mx, j->smax[((size_t) pair * ns + u) * G + h]);
+        float *row = j->sc[pair] + (size_t) h * n;
+        float den = 0.0f;
+        for (int32_t t = t0; t < t1; ++t) { row[t] = expf(row[t] - mx); den += row[t]; }
+        j->sden[(size_t) it * G + h] = den;
+    }
+}
+
+/* Weights bf16(e / den) of split s and its share of the output accumulation. */
+__attribute__((target_clones("avx2", "default"), optimize("O3,tree-vectorize")))
+static void gitem_pv(void *ctx, int64_t it) {
+    gjob_t *j = (gjob_t *) ctx;
+    const orc_desc *d = j->d;
+    const int32_t D = d->D, G = j->G, ns = j->nsplit, HW = ((G + ORC_HB - 1) / ORC_HB) * ORC_HB;
+    const int32_t pair = (int32_t) (it / ns), s = (int32_t) (it % ns);
+    const int32_t b = pair / d->Hkv, kvh = pair % d->Hkv, n = j->nvis[b];
+    float *acc = j->pacc + (size_t) it * D * HW;
+    memset(acc, 0, sizeof(float) * (size_t) D * HW);
+    if (n <= 0) return;
+    int32_t t0, t1;
+    split_range(n, ns, s, &t0, &t1);
+    float *den = (float *) malloc(sizeof(float) * HW);
+    for (int32_t h = 0; h < HW; ++h) {
+        float v = 0.0f;
+        if (h < G)
+            for (int32_t u = 0; u < ns; ++u) v += j->sden[((size_t) pair * ns + u) * G + h];
+        den[h] = v;
+    }
+    const size_t base = (size_t) b * d->seq_stride + (size_t) kvh * d->head_stride;
+    for (int32_t h0 = 0; h0 < G; h0 += ORC_HB) {
+        for (int32_t t = t0; t < t1; ++t) {
+            const uint16_t *vr = j->v + base + (size_t) j->rows[b][t] * D;
+            float w[ORC_HB];
+            for (int32_t e = 0; e < ORC_HB; ++e)
+                w[e] = h0 + e < G ? bfr(j->sc[pair][(size_t) (h0 + e) * n + t] / den[h0 + e]) : 0.0f;
+            for (int32_t i = 0; i < D; ++i) {
+                const float vf = bf2f(vr[i]);
+                float *a = acc + (size_t) i * HW + h0;
+                for (int32_t e = 0; e < ORC_HB; ++e) a[e] += w[e] * vf;
+            }
+        }
+    }
+    free(den);
+}
+
+/* out = bf16(sum of the splits' accumulations), splits in order. */
+static void gitem_out(void *ctx, int64_t pair) {
+    gjob_t *j = (gjob_t *) ctx;
+    const orc_desc *d = j->d;
+    const int32_t D = d->D, G = j->G, ns = j->nsplit, HW = ((G + ORC_HB - 1) / ORC_HB) * ORC_HB;
+    const int32_t b = (int32_t) pair / d->Hkv, kvh = (int32_t) pair % d->Hkv;
+    if (j->nvis[b] <= 0) return;
+    for (int32_t h = 0; h < G; ++h) {
+        uint16_t *out = j->out + ((size_t) b * d->Hq + (size_t) kvh * G + h) * D;
+        for (int32_t i = 0; i < D; ++i) {
+            float v = 0.0f;
+            for (int32_t u = 0; u < ns; ++u) v += j->pacc[(((size_t) pair * ns + u) * D + i) * HW + h];
+            out[i] = orc_f32_to_bf16(v);
+        }
+    }
+}
+
+int32_t orc_decode_refround_grouped(const orc_desc *d, const uint16_t *q, const uint16_t *k_cache,
+                                    const uint16_t *v_cache, const int32_t *pos, const int32_t *row_base,
+                                    int32_t nsplit, uint16_t *out, int32_t nthreads) {
+    if (!desc_ok(d) || nsplit < 0) return -1;
+    if (g_fault == 1) return -1; /* the grouping assumes the kv-major map */
+    const int32_t G = d->Hq / d->Hkv, HW = ((G + ORC_HB - 1) / ORC_HB) * ORC_HB;
+    const int32_t pairs = d->B * d->Hkv;
+    gjob_t j;
+    memset(&j, 0, sizeof(j));
+    j.d = d; j.q = q; j.k = k_cache; j.v = v_cache; j.pos = pos; j.row_base = row_base; j.out = out;
+    j.G = G;
+    j.rows = (int32_t **) calloc((size_t) d->B, sizeof(int32_t *));
+    j.nvis = (int32_t *) calloc((size_t) d->B, sizeof(int32_t));
+    int32_t nmax = 0;
+    for (int32_t b = 0; b < d->B; ++b) {
+        j.rows[b] = alloc_rows(d);
+        j.nvis[b] = orc_visible(d, pos[b], row_base ? row_base[b] : 0, j.rows[b]);
+        if (j.nvis[b] <= 0) j.status = -1;
+        if (j.nvis[b] > nmax) nmax = j.nvis[b];
+    }
+    /* splits: enough items for the threads, at least 256 rows each */
+    int32_t ns = nsplit;
+    if (ns == 0) {
+        const int32_t want = (4 * (nthreads > 0 ? nthreads : 1) + pairs - 1) / pairs;
+        const int32_t cap = nmax / 256 > 1 ? nmax / 256 : 1;
+        ns = want < cap ? want : cap;
+        if (ns < 1) ns = 1;
+    }
+    j.nsplit = ns;
+    j.sc = (float **) calloc((size_t) pairs, sizeof(float *));
+    for (int32_t u = 0; u < pairs; ++u) {
+        const int32_t n = j.nvis[u / d->Hkv];
+        j.sc[u] = (float *) malloc(sizeof(float) * (size_t) G * (size_t) (n > 0 ? n : 1));
+    }
+    const int64_t items = (int64_t) pairs * ns;
+    j.smax = (float *) malloc(sizeof(float) * (size_t) items * G);
+    j.sden = (float *) malloc(sizeof(float) * (size_t) items * G);
+    j.pacc = (float *) malloc(sizeof(float) * (size_t) items * d->D * HW);
+    run_items(gitem_scores, &j, items, nthreads);
+    run_items(gitem_exp, &j, items, nthreads);
+    run_items(gitem_pv, &j, items, nthreads);
+    run_items(gitem_out, &j, pairs, nthreads);
+    for (int32_t b = 0; b < d->B; ++b) free(j.rows[b]);
+    for (int32_t u = 0; u < pairs; ++u) free(j.sc[u]);
+    free(j.rows); free(j.nvis); free(j.sc); free(j.smax); free(j.sden); free(j.pacc);
+    return j.status;
+}
+
 /* ----------------------------------------------------------- split-K mode */
 
 /* Online softmax per split as in ESDecodeAttn.mm:44-110 (m starts at -3e38, l at 0,

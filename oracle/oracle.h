@@ -15,6 +15,9 @@
  *                        O = softmax(scale * q K^T + M) V, GQA kv-major (ESOps.h:64-68)
  *   orc_decode_refround  ESAttention.mm:136-165 (the unfused composite), including its
  *                        bf16 rounding points (scores, scaling, probabilities, output)
+ *   orc_decode_refround_grouped  the same, each K / V row read once per kv head and the
+ *                        rows split over threads (the CPU baseline); pinned to
+ *                        orc_decode_refround bit for bit with one split
  *   orc_decode_splitk    ESDecodeAttn.mm:17-117 attention loop (online softmax, m init
  *                        -3e38, fp32 accumulation, rows = ceil(L/S)) and the split merge
  *                        of ESDecodeAttn.mm:253-273, applied to plain bf16 K/V
@@ -91,6 +94,14 @@ int32_t orc_decode_f64(const orc_desc *d, const uint16_t *q, const uint16_t *k_c
 int32_t orc_decode_refround(const orc_desc *d, const uint16_t *q, const uint16_t *k_cache,
                             const uint16_t *v_cache, const int32_t *pos,
                             const int32_t *row_base, uint16_t *out, int32_t nthreads);
+
+/* orc_decode_refround with the query heads of a kv head sharing each K / V row read and
+ * the rows of a (sequence, kv head) in nsplit splits over threads (0: as many as the
+ * threads need); bit-identical to orc_decode_refround with one split, otherwise up to the
+ * order in which split partial sums combine.  The CPU baseline of bench.py. */
+int32_t orc_decode_refround_grouped(const orc_desc *d, const uint16_t *q, const uint16_t *k_cache,
+                                    const uint16_t *v_cache, const int32_t *pos, const int32_t *row_base,
+                                    int32_t nsplit, uint16_t *out, int32_t nthreads);
 
 /* Split-K fp32 mode with nsplit splits per (sequence, kv head); out fp32. */
 int32_t orc_decode_splitk(const orc_desc *d, const uint16_t *q, const uint16_t *k_cache,

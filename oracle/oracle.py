@@ -64,6 +64,8 @@ def _declare(L: ctypes.CDLL) -> None:
         f.restype = i32
     L.orc_decode_splitk.argtypes = [ctypes.POINTER(Desc), _P, _P, _P, _P, _P, i32, _P, i32]
     L.orc_decode_splitk.restype = i32
+    L.orc_decode_refround_grouped.argtypes = [ctypes.POINTER(Desc), _P, _P, _P, _P, _P, i32, _P, i32]
+    L.orc_decode_refround_grouped.restype = i32
     L.orc_rope_inv_freq.argtypes = [i32, ctypes.c_float, ctypes.c_float, _P]
     L.orc_rms_norm_rows.argtypes = [_P, _P, ctypes.c_int64, i32, ctypes.c_float, _P]
     L.orc_decode_raw_f64.argtypes = [_P, _P, i32, i32, i32, _P, ctypes.c_float, _P,
@@ -169,7 +171,7 @@ def _decode(fn: str, step: Step, q, k_cache, v_cache, pos, row_base, out, thread
     pos_a = _i32(pos)
     rb_a = None if row_base is None else _i32(row_base)
     args = [ctypes.byref(d), _ptr(q), _ptr(k_cache), _ptr(vc), _ptr(pos_a), _ptr(rb_a)]
-    if fn == "orc_decode_splitk":
+    if fn in ("orc_decode_splitk", "orc_decode_refround_grouped"):
         args.append(ctypes.c_int32(extra[0]))
     args += [_ptr(out), _threads(threads)]
     rc = getattr(lib(), fn)(*args)
@@ -186,6 +188,15 @@ def decode_f64(step: Step, q, k_cache, v_cache, pos, row_base=None, threads=None
 def decode_refround(step: Step, q, k_cache, v_cache, pos, row_base=None, threads=None) -> np.ndarray:
     out = np.empty((step.B, step.Hq, step.D), dtype=np.uint16)
     return _decode("orc_decode_refround", step, q, k_cache, v_cache, pos, row_base, out, threads)
+
+
+def decode_refround_grouped(step: Step, q, k_cache, v_cache, pos, row_base=None, threads=None,
+                            nsplit: int = 0) -> np.ndarray:
+    """decode_refround with each K / V row read once per kv head and the rows split over
+    threads (the CPU baseline); equal to decode_refround bit for bit when nsplit == 1."""
+    out = np.empty((step.B, step.Hq, step.D), dtype=np.uint16)
+    return _decode("orc_decode_refround_grouped", step, q, k_cache, v_cache, pos, row_base, out,
+                   threads, nsplit)
 
 
 def decode_splitk(step: Step, q, k_cache, v_cache, pos, nsplit: int, row_base=None,

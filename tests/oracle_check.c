@@ -62,6 +62,12 @@ static void decode_case(int B, int Hq, int Hkv, int D, int cap, int window, int 
     CHECK(orc_decode_f64(&d, q, k, v, pos, r, o64, 3) == 0, "decode_f64");
     CHECK(orc_decode_refround(&d, q, k, v, pos, r, orr, 2) == 0, "decode_refround");
     CHECK(orc_decode_splitk(&d, q, k, v, pos, r, irand(1, 9), osk, 4) == 0, "decode_splitk");
+    /* the grouped restatement (the CPU baseline): one split equals refround bit for bit */
+    uint16_t *og = malloc(sizeof(uint16_t) * (size_t) B * Hq * D);
+    CHECK(orc_decode_refround_grouped(&d, q, k, v, pos, r, 1, og, 2) == 0, "decode_refround_grouped");
+    CHECK(memcmp(og, orr, sizeof(uint16_t) * (size_t) B * Hq * D) == 0, "grouped with one split equals refround");
+    CHECK(orc_decode_refround_grouped(&d, q, k, v, pos, r, irand(2, 9), og, 3) == 0, "decode_refround_grouped splits");
+    free(og);
     double worst = 0.0;
     for (size_t i = 0; i < (size_t) B * Hq * D; ++i) {
         CHECK(isfinite(o64[i]) && isfinite(osk[i]), "finite output");

@@ -14,6 +14,8 @@ The reference holds no attention goldens (its fixtures are gitignored and need t
   GQA order          ESPrimitivesTests.mm:118-128 (repeatKV is kv-major: [h0,h0,h1,h1])
   decode_refround    within the north-star tolerance of fp64; bit-level spot checks
                      of its rounding points on a hand-computed case
+  refround_grouped   decode_refround bit for bit with one split; within one bf16 ulp
+                     with several
   decode_splitk      S = 1 vs many splits vs fp64 (split invariance)
   rope inv_freq      ESPrimitivesTests.mm:130-139, 191-210 (zero tail, full rotation)
   rms norm           ESPrimitivesTests.mm:93-116 (unit weight, weightless [2,2,2,2])
@@ -331,6 +333,37 @@ def test_refround_rounding_points_hand_case():
     assert out[0] == orc.from_bf16(orc.to_bf16(np.array([w0], np.float32)))[0]
     assert out[1] == orc.from_bf16(orc.to_bf16(np.array([w1], np.float32)))[0]
     assert abs(out[0] - e / (e + 1)) < 4e-3
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(B=2, Hq=8, Hkv=2, D=128, cap=300, window=0, ring=False, shared=False, pos=[299, 120]),
+    dict(B=1, Hq=32, Hkv=4, D=512, cap=700, window=0, ring=False, shared=True, pos=[650]),
+    dict(B=3, Hq=16, Hkv=8, D=256, cap=256, window=256, ring=True, shared=False, pos=[900, 300, 255]),
+    dict(B=2, Hq=24, Hkv=1, D=128, cap=400, window=100, ring=False, shared=False, pos=[399, 50]),
+])
+def test_refround_grouped_equals_refround(cfg):
+    """The CPU baseline's grouped restatement: one split per (sequence, kv head) gives
+    orc_decode_refround bit for bit (G = 24 covers a partial block of 8 heads); many splits
+    differ only where the order of the split sums moves a bf16 rounding (one ulp)."""
+    step = orc.Step(B=cfg["B"], Hq=cfg["Hq"], Hkv=cfg["Hkv"], D=cfg["D"], cap=cfg["cap"],
+                    window=cfg["window"], ring=cfg["ring"], scale=cfg["D"] ** -0.5)
+    pos, shared = cfg["pos"], cfg["shared"]
+    q, kc, vc, kn, vn = make_step_inputs(step, 29, pos, shared_kv=shared)
+    orc.append(step, kc, None if shared else vc, kn, None if shared else vn, pos)
+    ref = orc.decode_refround(step, q, kc, vc, pos)
+    np.testing.assert_array_equal(orc.decode_refround_grouped(step, q, kc, vc, pos, nsplit=1), ref)
+    many = orc.decode_refround_grouped(step, q, kc, vc, pos, nsplit=5, threads=4)
+    a, b = orc.from_bf16(ref).astype(np.float64), orc.from_bf16(many).astype(np.float64)
+    assert np.all(np.abs(a - b) <= 2.0 ** -7 * np.maximum(np.abs(a), 2.0 ** -8))
+    assert (ref != many).mean() < 0.02
+
+
+def test_refround_grouped_planted_gqa_fault_is_refused():
+    step = orc.Step(B=1, Hq=8, Hkv=2, D=64, cap=64, scale=0.125)
+    q, kc, vc, _, _ = make_step_inputs(step, 3, [63])
+    with orc.planted_fault(1):
+        with pytest.raises(ValueError):
+            orc.decode_refround_grouped(step, q, kc, vc, [63])
 
 
 @pytest.mark.parametrize("nsplit", [1, 2, 7, 64])
