@@ -1548,26 +1548,13 @@ constexpr int kMergeThreads = 256;
 constexpr int kMergeDims = 64;      // output dims per merge workgroup (16 lanes x float4)
 constexpr int kMergeGroups = kMergeThreads / (kMergeDims / 4);  // split groups reduced in parallel (16)
 
-__device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) {
-    for (int o = 32; o > 0; o >>= 1) {
-        const float w = __shfl_xor(v, o);
-        v = is_max ? fmaxf(v, w) : v + w;
-    }
-    const int wave = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[wave] = v;
-    __syncthreads();
-    v = red[0];
-    for (int w = 1; w < kMergeThreads / 64; ++w) v = is_max ? fmaxf(v, red[w]) : v + red[w];
-    return v;
-}
-
 // Cross-split merge (ESDecodeAttn.mm:253-273 restated in the log2 domain):
 // M = max_s m_s; O = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
 // One workgroup per (sequence, query head, 64 output dims); 16 split groups x 16 float4
 // lanes.  Each thread issues its partial loads together with the (m, l) loads, so the
-// whole merge is one memory round trip; the per-split weights are then formed from the
-// block-wide max.  (Against 128 dims x 8 groups, the narrower workgroups and one 8-byte
+// whole merge is one memory round trip; each split group weighs its splits against its
+// own max, and the final sum over the groups rescales them to the largest (no block-wide
+// reduction before the weights).  (Against 128 dims x 8 groups, the narrower workgroups and one 8-byte
 // (m, l) load per split took 1.8 us off the C4 step and 1.2 us off C2's.)
 // REGS: splits per thread held in registers (S <= 16 * REGS in one pass): 4, or 16 for
 // more splits (the raw-K C4 shape packs two kv heads into 128 splits).
@@ -1594,9 +1581,8 @@ __device__ __forceinline__ int pair_splits(const MergeParams &p, int b, int kvh,
 
 template <int REGS>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
-    __shared__ float red[kMergeThreads / 64];
     __shared__ f32x4 part[kMergeGroups][kMergeDims / 4];
-    __shared__ float lsum[kMergeGroups];
+    __shared__ float lsum[kMergeGroups], gmax[kMergeGroups];
     const int h = blockIdx.y, b = blockIdx.z;
     const int kvh = h / p.G, g = h % p.G;
     const int tid = threadIdx.x;
@@ -1631,7 +1617,9 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
     } else {
         for (int s = sg; s < ns; s += kMergeGroups) mloc = fmaxf(mloc, p.part_ml[((pbase + s) * p.G + g) * 2]);
     }
-    const float mx = block_reduce(mloc, red, true);
+    // Each split group combines its splits against its own max (the same in the group's 16
+    // lanes: m is per split); the groups are rescaled to their common max in the final sum.
+    const float mx = mloc == -INFINITY ? 0.0f : mloc;  // a group without splits: weights 0
 
     f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
     float lt = 0.0f;
@@ -1651,15 +1639,23 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p) {
         }
     }
     part[sg][dq] = o;
-    if (dq == 0) lsum[sg] = lt;
+    if (dq == 0) {
+        lsum[sg] = lt;
+        gmax[sg] = mloc;
+    }
     __syncthreads();
     if (tid < kMergeDims / 4) {
-        f32x4 t = part[0][tid];
-        float l = lsum[0];
+        float M = gmax[0];
 #pragma unroll
-        for (int u = 1; u < kMergeGroups; ++u) {
-            t += part[u][tid];
-            l += lsum[u];
+        for (int u = 1; u < kMergeGroups; ++u) M = fmaxf(M, gmax[u]);
+        f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+        float l = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kMergeGroups; ++u) {
+            // a group with no split (its max -inf) adds nothing
+            const float c = gmax[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(gmax[u] - M);
+            t += part[u][tid] * c;
+            l += lsum[u] * c;
         }
         const float inv = 1.0f / l;
         uint16_t *dst = p.out + ((size_t) b * p.Hq + h) * p.D + blockIdx.x * kMergeDims + tid * 4;
