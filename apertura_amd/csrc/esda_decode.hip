@@ -9,7 +9,8 @@
 //
 // Kernels
 //   attend_kernel  grid (splits, kv heads, sequences) or balanced shares of a ragged
-//                  batch; 4 or 8 waves, one workgroup per CU.  A workgroup streams
+//                  batch; 4 or 8 waves, one workgroup per CU (two at D = 256, each with
+//                  half the LDS).  A workgroup streams
 //                  visible rows of one (sequence, kv head) -- or of 2 or 4 kv heads
 //                  packed together -- through an LDS ring filled by LDS DMA, splits the head dim across its
 //                  waves for the QK and PV MFMAs (the GQA group is the MFMA N dimension),
@@ -39,7 +40,9 @@ namespace {
 
 constexpr int kTile = 16;          // MFMA row block; split sizes are multiples of it
 constexpr int kMaxGroup = 16;
-constexpr int kTargetGroups = 256;  // one workgroup per MI355X CU (the ring LDS allows one per CU)
+constexpr int kTargetGroups = 256;  // workgroups of one per MI355X CU (a full-LDS ring allows one per CU)
+constexpr int kWaves256 = 4;        // waves per workgroup of the plain kernels at D = 256
+constexpr int kOcc256 = 2;          // and their workgroups per CU
 constexpr int kMinRows = 64;        // fewest rows per workgroup the automatic plan gives
 constexpr int kMaxGroups = 16384;   // workgroups per launch
 constexpr int kMaxBatch = 256;      // sequences per call (one per thread of the prefix scan)
@@ -91,7 +94,7 @@ struct AttendParams {
 // makes both read patterns conflict-free with every address a base plus an immediate.
 // EXTRA: LDS bytes the kernel variant needs beside the ring and the score exchange; PSX:
 // LDS bytes it keeps per ring stage beside the rows.
-template <int D, bool SHARED, int NW, int EXTRA = 0, int PSX = 0>
+template <int D, bool SHARED, int NW, int EXTRA = 0, int PSX = 0, int LDSB = 160 * 1024>
 struct Ring {
     static constexpr int RPI = 512 / D;                     // rows per DMA instruction
     static constexpr int NI = 16 / RPI;                     // DMA instructions per stage
@@ -108,7 +111,7 @@ struct Ring {
     static constexpr int XB = 2 * NW * 64 * 16;             // score-exchange bytes
     // reserve: kernel arguments' spill room (256 B) and the batch prefix scan (int64 per
     // sequence + one per wave)
-    static constexpr int NS_ = (160 * 1024 - XB - 256 - ((kMaxBatch + 1) + NW) * 8 - EXTRA) / (SB + PSX);
+    static constexpr int NS_ = (LDSB - XB - 256 - ((kMaxBatch + 1) + NW) * 8 - EXTRA) / (SB + PSX);
     static constexpr int NS = NS_ > 16 ? 16 : NS_;          // stages in the ring
     static_assert(DW % 32 == 0 && NI % NW == 0, "wave slices must cover whole MFMA steps");
     static_assert(NS >= 4, "the ring needs at least 4 stages");
@@ -287,8 +290,8 @@ __device__ __forceinline__ void walk_segments(const AttendParams &p, Seg &&segme
 
 // --------------------------------------------------------------------- attend kernel
 //
-// grid (splits, kv heads, sequences), NW = 4 or 8 waves per workgroup, one workgroup per
-// CU.  A workgroup owns `chunk` consecutive visible rows of one (sequence, kv head)
+// grid (splits, kv heads, sequences), NW = 4 or 8 waves per workgroup, OCC workgroups per
+// CU (the ring takes 1/OCC of the LDS).  A workgroup owns `chunk` consecutive visible rows of one (sequence, kv head)
 // and streams them through the LDS ring in 16-row stages.  When each pair needs one
 // split and pairs are plentiful, pk = 2 or 4 kv heads of a sequence share a workgroup:
 // a stage then holds 16 / pk rows of each, their query heads fill the MFMA N dimension
@@ -328,11 +331,11 @@ __device__ __forceinline__ void walk_segments(const AttendParams &p, Seg &&segme
 // from the caller's precomputed table (esda_rope_table: the same sincos_f32 and bf16
 // rounding as publish_tab) by one 256-byte LDS DMA per row beside the stage's rows, into a
 // table area per ring slot, instead of being computed in every step.
-template <int D, bool SHARED, int NW, bool RAW, int RPK = 1, bool Q8 = false, bool TAB = false>
-// The LDS ring allows one workgroup per CU, i.e. NW/4 waves per SIMD: telling the
+template <int D, bool SHARED, int NW, bool RAW, int RPK = 1, bool Q8 = false, bool TAB = false, int OCC = 1>
+// The LDS ring allows OCC workgroups per CU, i.e. OCC * NW/4 waves per SIMD: telling the
 // compiler so lifts the register limit it would otherwise keep for higher occupancy,
 // which it meets by serialising LDS reads behind their uses.
-__global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(NW / 4, NW / 4)))
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(OCC * NW / 4, OCC * NW / 4)))
 void attend_kernel(AttendParams p) {
     static_assert(!RAW || (D == kRawDim && SHARED && (NW == 4 || NW == 8)), "raw mode: one 512-dim stream, 4 or 8 waves");
     static_assert(RPK == 1 || (RAW && RPK == 2), "kv-head packing is a runtime choice outside raw mode");
@@ -341,8 +344,11 @@ void attend_kernel(AttendParams p) {
     // bytes of one ring slot's cos/sin rows (TAB)
     constexpr int TABB = TAB ? (16 / RPK) * kTabStride * 4 : 0;
     // R: the compute layout of a stage (and, outside q8 mode, the DMA ring); RD: the DMA ring.
-    using R = Ring<D, SHARED, NW, RAW && !Q8 ? raw_extra_lds(NW, false, TAB) : 0, RAW && !Q8 ? TABB : 0>;
+    using R = Ring<D, SHARED, NW, RAW && !Q8 ? raw_extra_lds(NW, false, TAB) : 0, RAW && !Q8 ? TABB : 0, 160 * 1024 / OCC>;
     using RD = std::conditional_t<Q8, Ring<256, true, NW, q8_extra_lds(NW, TAB), TABB>, R>;
+    static_assert(OCC == 1 || !RAW, "raw mode holds one workgroup per CU");
+    // D = 512 exchanges only the live heads' partial scores (the padding columns are zero)
+    constexpr bool kLiveX = D == 512 && !RAW;
     constexpr int NS = RD::NS, DW = R::DW, KKW = R::KKW, DTW = R::DTW;
     // DMA instructions per wave per stage (q8: the u8 rows plus one scale / bias piece;
     // TAB: plus its share of the cos/sin rows)
@@ -640,7 +646,9 @@ void attend_kernel(AttendParams p) {
             const bf16x8 a = *reinterpret_cast<const bf16x8 *>(kb + qk_off + 64 * qk_chunk(kk));
             sp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qv[kk], sp, 0, 0, 0);
         }
-        xch[par][wave][lane] = sp;
+        // D = 512: only the live heads' columns (lanes li < G) are exchanged; the padding
+        // heads' partials are zero (their Q^T operand is)
+        if (!kLiveX || li < p.G) xch[par][wave][lane] = sp;
     };
 
     // ---- raw mode helpers
@@ -873,9 +881,22 @@ void attend_kernel(AttendParams p) {
         if constexpr (Q8) {
             if (st + 3 < nst) convert(st + 3, ring(std::integral_constant<int, (u + 3) % NS>{}));
         }
-        f32x4 sc = xch[st & 1][0][lane];
+        f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (RAW || !kLiveX || li < p.G) {
+            sc = xch[st & 1][0][lane];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) sc += xch[st & 1][w][lane];
+            for (int w = 1; w < NW; ++w) sc += xch[st & 1][w][lane];
+        }
+        // V^T operands of this stage (plain kernels), read behind the exchange so that
+        // their latency hides under the softmax instead of following it
+        const unsigned char *vb = cbuf(st, uc) + VOFF;
+        short4v va[RAW ? 1 : DTW];
+        if constexpr (!RAW) {
+#pragma unroll
+            for (int dt = 0; dt < DTW; ++dt)
+                va[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) short4v *) (vb + tr_off + 32 * dt));
+        }
         // The look-ahead work runs unconditionally (one basic block with the softmax, so
         // the two interleave): past the last stage it reads stale but in-bounds LDS and
         // writes exchange slots that are never read again.
@@ -929,12 +950,15 @@ void attend_kernel(AttendParams p) {
             }
         }
         // O^T (this wave's dims) += V^T . P^T
-        const unsigned char *vb = cbuf(st, uc) + VOFF;
 #pragma unroll
         for (int dt = 0; dt < DTW; ++dt) {
-            const short4v a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) short4v *) (vb + tr_off + 32 * dt));
-            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pbs, acc[dt], 0, 0, 0);
+            if constexpr (RAW) {
+                const short4v a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) short4v *) (vb + tr_off + 32 * dt));
+                acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pbs, acc[dt], 0, 0, 0);
+            } else {
+                acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pbs, acc[dt], 0, 0, 0);
+            }
         }
     };
     for (int s0 = 0; s0 < nst; s0 += NS) unroll<NS>([&](auto uc) { stage(s0, uc); });
@@ -1888,11 +1912,11 @@ struct Plan {
 // MFMA's N dimension) gives each workgroup one pk-times longer stream instead of pk short
 // ones, each of which would pay the ring's fill and drain.  Local layers (G = 2) at C5's
 // batch: 512 pairs -> 256 workgroups of two kv heads.
-int choose_pack(const esda_decode_desc *d, int G, long long S) {
+int choose_pack(const esda_decode_desc *d, int G, long long S, int target) {
     const long long pairs = (long long) d->batch * d->num_kv_heads;
     int pk = 1;
     while (pk < 4 && S == 1 && G * pk * 2 <= kMaxGroup && d->num_kv_heads % (pk * 2) == 0 &&
-           pairs / (pk * 2) >= kTargetGroups &&
+           pairs / (pk * 2) >= target &&
            (long long) d->head_stride * 2 * (pk * 2) + 16LL * d->head_dim * 2 < (1LL << 31))
         pk *= 2;
     return pk;
@@ -1925,6 +1949,8 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: split_rows must be a multiple of 16");
     int bound = d->ring ? d->window : (d->window > 0 ? std::min(d->window, d->cap) : d->cap);
     int maxvis = d->max_visible > 0 ? std::min(d->max_visible, bound) : bound;
+    // workgroups that fill the GPU: one per CU, or two at D = 256 (their rings fit twice)
+    const int target = (!raw && d->head_dim == 256) ? kOcc256 * kTargetGroups : kTargetGroups;
     pl->pk = 1;
     if (raw && G * 2 <= kMaxGroup && d->num_kv_heads % 2 == 0 &&
         (long long) d->head_stride * 2 * 2 + 16LL * d->head_dim * 2 < (1LL << 31))
@@ -1945,7 +1971,7 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
     size_t slots;
     if (pl->balanced) {
         long long W = (rows_max + per - 1) / per;
-        if (d->split_rows == 0 && W > kTargetGroups) W = kTargetGroups;
+        if (d->split_rows == 0 && W > target) W = target;
         if (W > kMaxGroups) W = kMaxGroups;
         if (W < 1) W = 1;
         pl->W = (int) W;
@@ -1958,7 +1984,7 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
             // whole 16-row tiles (C2, 4 pairs of 8193 rows: 64-row rounding gave 192-row
             // splits and 176 workgroups, 11.4 us; 16-row rounding gives 144 and 228, 10.3).
             const long long pairs = (long long) d->batch * (d->num_kv_heads / pl->pk);
-            const long long per_pair = std::max(1LL, kTargetGroups / pairs);
+            const long long per_pair = std::max(1LL, target / pairs);
             chunk = (maxvis + per_pair - 1) / per_pair;
             chunk = (chunk + kTile - 1) / kTile * kTile;
             if (chunk < kMinRows) chunk = kMinRows;
@@ -1973,7 +1999,7 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
         pl->W = 0;
         pl->S = (int) S;
         pl->chunk = (int) chunk;
-        if (!raw && d->split_rows == 0) pl->pk = choose_pack(d, G, S);
+        if (!raw && d->split_rows == 0) pl->pk = choose_pack(d, G, S, target);
         slots = (size_t) d->batch * (d->num_kv_heads / pl->pk) * S;
     }
     const size_t parts = slots * G * pl->pk;
@@ -1984,13 +2010,19 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
     return ESDA_OK;
 }
 
-// Waves per workgroup (the head dim is split across them).  D = 256: 8 waves, two per
-// SIMD, so one wave's softmax and exchange latency overlaps the other's MFMAs (measured:
-// C3 attend 25.3 -> 24.0 us, C5 local layers -2.3%).  D = 512 keeps 4: its 8-wave form
-// loses a ring stage to the larger score exchange and runs C4 ~6% slower.  D = 128 has
-// too few dims for 8 waves of 32-dim MFMA steps.
+// Waves per workgroup (the head dim is split across them) and workgroups per CU.  D = 256:
+// two workgroups of 4 waves per CU, each with half the LDS for its ring (4 stages of 16
+// rows), so each SIMD runs two waves of independent workgroups that never wait on each
+// other's barriers.  Against one workgroup of 8 waves (two per SIMD in barrier lockstep,
+// the softmax repeated by all 8): C3 attend 23.9 -> 22.3 us, C5 step 7.80 -> 7.61 ms, C1
+// 5.7 -> 5.3 us.  D = 512 keeps one workgroup of 4: its 8-wave form loses a ring stage to
+// the larger score exchange and runs C4 ~6% slower.  D = 128 has too few dims for 8 waves
+// of 32-dim MFMA steps.
 template <int D>
-constexpr int ring_waves() { return D == 256 ? 8 : 4; }
+constexpr int ring_waves() { return D == 256 ? kWaves256 : 4; }
+// Workgroups per CU of the plain kernels (their rings split the LDS).
+template <int D>
+constexpr int ring_occ() { return D == 256 ? kOcc256 : 1; }
 
 // Raw mode: 8 waves, two per SIMD, so one wave's dependency stalls overlap the other's
 // reconstruction work.
@@ -1999,7 +2031,8 @@ constexpr int kRawWaves = 8;
 template <int D, bool SHARED, bool RAW = false, int RPK = 1, bool Q8 = false, bool TAB = false>
 hipError_t launch_attend(const AttendParams &ap, dim3 grid, hipStream_t st) {
     constexpr int NW = RAW ? kRawWaves : ring_waves<D>();
-    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW, RPK, Q8, TAB>), grid, dim3(64 * NW), 0, st, ap);
+    constexpr int OCC = RAW ? 1 : ring_occ<D>();
+    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW, RPK, Q8, TAB, OCC>), grid, dim3(64 * NW), 0, st, ap);
     return hipGetLastError();
 }
 
