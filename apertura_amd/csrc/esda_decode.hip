@@ -1903,7 +1903,8 @@ namespace {
 
 struct Plan {
     int G, maxvis, balanced, W, S, chunk;
-    int pk;  // kv heads packed per workgroup (the kernels see Hkv / pk heads of G * pk)
+    int pk;   // kv heads packed per workgroup (the kernels see Hkv / pk heads of G * pk)
+    int occ;  // attend workgroups per CU the plan is sized for (1 or 2)
     size_t off_table, off_ml, off_acc, bytes;
 };
 
@@ -1949,8 +1950,17 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: split_rows must be a multiple of 16");
     int bound = d->ring ? d->window : (d->window > 0 ? std::min(d->window, d->cap) : d->cap);
     int maxvis = d->max_visible > 0 ? std::min(d->max_visible, bound) : bound;
-    // workgroups that fill the GPU: one per CU, or two at D = 256 (their rings fit twice)
-    const int target = (!raw && d->head_dim == 256) ? kOcc256 * kTargetGroups : kTargetGroups;
+    // Several full-causal sequences have ragged lengths: workgroups then take balanced
+    // shares of all rows (the kernel scans the lengths).  Otherwise (one sequence, or
+    // windowed local layers whose lengths are nearly equal) a plain grid of fixed splits
+    // per (sequence, kv head) starts faster.
+    pl->balanced = d->batch > 1 && !d->ring;
+    // Workgroups per CU: two at D = 256, and for balanced shares of a 512-dim shared stream
+    // (each ring in half the LDS; one workgroup's segment fill and drain then overlap the
+    // other's streaming: C5's global layers -1.4%).  A 512-dim grid plan keeps one: twice
+    // the splits cost more in its merge than they gain (C4 step 82.7 -> 85.1 us).
+    pl->occ = raw ? 1 : d->head_dim == 256 ? kOcc256 : (d->head_dim == 512 && d->kv_shared && pl->balanced) ? 2 : 1;
+    const int target = pl->occ * kTargetGroups;  // workgroups that fill the GPU
     pl->pk = 1;
     if (raw && G * 2 <= kMaxGroup && d->num_kv_heads % 2 == 0 &&
         (long long) d->head_stride * 2 * 2 + 16LL * d->head_dim * 2 < (1LL << 31))
@@ -1961,11 +1971,6 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
     // asks for that many rows per workgroup.
     const long long rows_max = (long long) maxvis * d->batch * (d->num_kv_heads / pl->pk);
     const long long per = d->split_rows > 0 ? d->split_rows : kMinRows;
-    // Several full-causal sequences have ragged lengths: workgroups then take balanced
-    // shares of all rows (the kernel scans the lengths).  Otherwise (one sequence, or
-    // windowed local layers whose lengths are nearly equal) a plain grid of fixed splits
-    // per (sequence, kv head) starts faster.
-    pl->balanced = d->batch > 1 && !d->ring;
     pl->G = G;
     pl->maxvis = maxvis;
     size_t slots;
@@ -2010,7 +2015,7 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
     return ESDA_OK;
 }
 
-// Waves per workgroup (the head dim is split across them) and workgroups per CU.  D = 256:
+// Waves per workgroup (the head dim is split across them); workgroups per CU: Plan::occ.  D = 256:
 // two workgroups of 4 waves per CU, each with half the LDS for its ring (4 stages of 16
 // rows), so each SIMD runs two waves of independent workgroups that never wait on each
 // other's barriers.  Against one workgroup of 8 waves (two per SIMD in barrier lockstep,
@@ -2021,26 +2026,29 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
 template <int D>
 constexpr int ring_waves() { return D == 256 ? kWaves256 : 4; }
 // Workgroups per CU of the plain kernels (their rings split the LDS).
-template <int D>
-constexpr int ring_occ() { return D == 256 ? kOcc256 : 1; }
 
 // Raw mode: 8 waves, two per SIMD, so one wave's dependency stalls overlap the other's
 // reconstruction work.
 constexpr int kRawWaves = 8;
 
-template <int D, bool SHARED, bool RAW = false, int RPK = 1, bool Q8 = false, bool TAB = false>
+template <int D, bool SHARED, bool RAW = false, int RPK = 1, bool Q8 = false, bool TAB = false, int OCC = 1>
 hipError_t launch_attend(const AttendParams &ap, dim3 grid, hipStream_t st) {
     constexpr int NW = RAW ? kRawWaves : ring_waves<D>();
-    constexpr int OCC = RAW ? 1 : ring_occ<D>();
     hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW, RPK, Q8, TAB, OCC>), grid, dim3(64 * NW), 0, st, ap);
     return hipGetLastError();
 }
 
-hipError_t dispatch_attend(int D, bool shared, const AttendParams &ap, dim3 grid, hipStream_t st) {
+hipError_t dispatch_attend(int D, bool shared, int occ, const AttendParams &ap, dim3 grid, hipStream_t st) {
+    constexpr int O256 = kOcc256;
     switch (D) {
         case 128: return shared ? launch_attend<128, true>(ap, grid, st) : launch_attend<128, false>(ap, grid, st);
-        case 256: return shared ? launch_attend<256, true>(ap, grid, st) : launch_attend<256, false>(ap, grid, st);
-        default:  return shared ? launch_attend<512, true>(ap, grid, st) : launch_attend<512, false>(ap, grid, st);
+        case 256:
+            return shared ? launch_attend<256, true, false, 1, false, false, O256>(ap, grid, st)
+                          : launch_attend<256, false, false, 1, false, false, O256>(ap, grid, st);
+        default:
+            if (!shared) return launch_attend<512, false>(ap, grid, st);
+            return occ == 2 ? launch_attend<512, true, false, 1, false, false, 2>(ap, grid, st)
+                            : launch_attend<512, true>(ap, grid, st);
     }
 }
 
@@ -2102,7 +2110,7 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         const dim3 grid = pl.balanced ? dim3(pl.W) : dim3(pl.S, d->num_kv_heads / pl.pk, d->batch);
         hipError_t e;
         if (mode == 0) {
-            e = dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
+            e = dispatch_attend(d->head_dim, d->kv_shared != 0, pl.occ, ap, grid, st);
         } else if (pl.pk == 2 && ap.rope_tab) {
             // two kv heads per workgroup with the precomputed cos/sin table (the ES layer's
             // form): the wave-private-ring kernel
