@@ -2161,11 +2161,12 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         mp.W = pl.W;
         mp.S = pl.S;
         mp.chunk = pl.chunk;
-        if (pl.balanced) {
+        if (pl.balanced || pl.S <= kMergeRowsChunk) {
             // Balanced shares give each pair a few splits: thread-per-output merge (C5's
-            // global layers: 11 -> 4.4 us).  Grids keep merge_kernel, whose workgroups
-            // reduce 8 splits side by side (at C1's 16 splits over 8 pairs the rows
-            // kernel would run 4 workgroups and two round trips: 9.0 -> 11.8 us a step).
+            // global layers: 11 -> 4.4 us), as do grids of at most kMergeRowsChunk splits
+            // (one memory round trip per thread).  Larger grids keep merge_kernel, whose
+            // workgroups reduce 16 split groups side by side (at C1's 16 splits over 8 pairs
+            // the rows kernel would run 4 workgroups and two round trips: 9.0 -> 11.8 us a step).
             const int threads = d->num_q_heads * (d->head_dim / 4);
             dim3 grid((threads + kMergeRowsThreads - 1) / kMergeRowsThreads, d->batch);
             hipLaunchKernelGGL(merge_rows_kernel, grid, dim3(kMergeRowsThreads), 0, st, mp);
