@@ -40,7 +40,7 @@ namespace {
 
 constexpr int kTile = 16;          // MFMA row block; split sizes are multiples of it
 constexpr int kMaxGroup = 16;
-constexpr int kTargetGroups = 256;  // workgroups of one per MI355X CU (a full-LDS ring allows one per CU)
+constexpr int kTargetGroups = 256;  // one workgroup per MI355X CU; plans of two per CU aim at twice that
 constexpr int kWaves256 = 4;        // waves per workgroup of the plain kernels at D = 256
 constexpr int kOcc256 = 2;          // and their workgroups per CU
 constexpr int kMinRows = 64;        // fewest rows per workgroup the automatic plan gives
@@ -293,9 +293,10 @@ __device__ __forceinline__ void walk_segments(const AttendParams &p, Seg &&segme
 // --------------------------------------------------------------------- attend kernel
 //
 // grid (splits, kv heads, sequences), NW = 4 or 8 waves per workgroup, OCC workgroups per
-// CU (the ring takes 1/OCC of the LDS).  A workgroup owns `chunk` consecutive visible rows of one (sequence, kv head)
-// and streams them through the LDS ring in 16-row stages.  When each pair needs one
-// split and pairs are plentiful, pk = 2 or 4 kv heads of a sequence share a workgroup:
+// CU (the ring takes 1/OCC of the LDS).  A workgroup owns `chunk` consecutive visible rows
+// of one (sequence, kv head) and streams them through the LDS ring in 16-row stages.
+// When each pair needs one split and pairs are plentiful, pk = 2 or 4 kv heads of a
+// sequence share a workgroup:
 // a stage then holds 16 / pk rows of each, their query heads fill the MFMA N dimension
 // side by side, and scores of a head against another kv head's rows are masked.
 // Ragged batches use balanced shares instead: workgroup w takes rows
@@ -1972,7 +1973,7 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
     pl->balanced = d->batch > 1 && !d->ring;
     // Workgroups per CU: two at D = 256, and for balanced shares of a 512-dim shared stream
     // (each ring in half the LDS; one workgroup's segment fill and drain then overlap the
-    // other's streaming: C5's global layers -1.4%).  A 512-dim grid plan keeps one: twice
+    // other's streaming: C5 step -0.8%).  A 512-dim grid plan keeps one: twice
     // the splits cost more in its merge than they gain (C4 step 82.7 -> 85.1 us).
     pl->occ = raw ? 1 : d->head_dim == 256 ? kOcc256 : (d->head_dim == 512 && d->kv_shared && pl->balanced) ? 2 : 1;
     const int target = pl->occ * kTargetGroups;  // workgroups that fill the GPU
@@ -2036,12 +2037,12 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
 // rows), so each SIMD runs two waves of independent workgroups that never wait on each
 // other's barriers.  Against one workgroup of 8 waves (two per SIMD in barrier lockstep,
 // the softmax repeated by all 8): C3 attend 23.9 -> 22.3 us, C5 step 7.80 -> 7.61 ms, C1
-// 5.7 -> 5.3 us.  D = 512 keeps one workgroup of 4: its 8-wave form loses a ring stage to
-// the larger score exchange and runs C4 ~6% slower.  D = 128 has too few dims for 8 waves
-// of 32-dim MFMA steps.
+// 5.7 -> 5.3 us.  D = 512 keeps 4 waves (its 8-wave form loses a ring stage to the larger
+// score exchange and runs C4 ~6% slower), one workgroup per CU on grid plans and two on
+// balanced shares of a shared stream.  D = 128 has too few dims for 8 waves of 32-dim MFMA
+// steps.
 template <int D>
 constexpr int ring_waves() { return D == 256 ? kWaves256 : 4; }
-// Workgroups per CU of the plain kernels (their rings split the LDS).
 
 // Raw mode: 8 waves, two per SIMD, so one wave's dependency stalls overlap the other's
 // reconstruction work.
