@@ -260,6 +260,14 @@ EDGE = [
     dict(name="scale_one_in_model", B=1, Hq=32, Hkv=4, D=512, cap=512, pos=[511], shared=True,
          scale=1.0, refround=False),
     dict(name="dominant_key", B=1, Hq=8, Hkv=1, D=256, cap=2048, pos=[2047], peaks=1, bump=30.0),
+    # head dim 256 runs two workgroups per CU: a shared K = V ring over many pairs (kv heads
+    # packed per workgroup), and a one-sequence grid of the automatic 32-row splits
+    dict(name="d256_shared_ring_packed", B=64, Hq=32, Hkv=16, D=256, cap=128, window=100, ring=True,
+         shared=True, pos=[int(x) for x in np.random.default_rng(8).integers(0, 600, size=64)], seed=8),
+    dict(name="d256_auto_32_row_splits", B=1, Hq=8, Hkv=4, D=256, cap=700, pos=[699]),
+    # balanced shares of a 512-dim shared stream run two workgroups per CU, sized for 512
+    # shares: here far fewer visible rows than shares, with one empty-ish sequence
+    dict(name="balanced_two_per_cu_tiny", B=3, Hq=16, Hkv=2, D=512, cap=8192, shared=True, pos=[0, 40, 300]),
 ]
 
 
