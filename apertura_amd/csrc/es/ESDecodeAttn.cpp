@@ -12,6 +12,7 @@
 #include <utility>
 
 #include "es/ESKVCache.h"
+#include "es/es_fill.h"
 #include "esda.h"
 
 namespace es {
@@ -107,7 +108,7 @@ Tensor esDecodeAttnGlobal(const Tensor &q, const Tensor &rawBuf, int len, int pi
     if (!s.workspace || s.workspace->nbytes() < bytes) {
         if (s.workspace) hipCheck(hipStreamSynchronize(st), "esDecodeAttnGlobal workspace growth");
         s.workspace = Tensor::empty({(int64_t) std::max<size_t>(bytes, 1 << 20)}, Dtype::u8);
-        hipCheck(hipMemsetAsync(s.workspace->data, 0, 256, st), "esDecodeAttnGlobal workspace clear");
+        zeroFill(s.workspace->data, 256, st);
     }
     Tensor o;
     if (out) {
@@ -187,7 +188,7 @@ Tensor esDecodeAttnGlobalQ8(const Tensor &q, const Tensor &qBuf, const Tensor &s
     if (!s.workspace || s.workspace->nbytes() < bytes) {
         if (s.workspace) hipCheck(hipStreamSynchronize(st), "esDecodeAttnGlobalQ8 workspace growth");
         s.workspace = Tensor::empty({(int64_t) std::max<size_t>(bytes, 1 << 20)}, Dtype::u8);
-        hipCheck(hipMemsetAsync(s.workspace->data, 0, 256, st), "esDecodeAttnGlobalQ8 workspace clear");
+        zeroFill(s.workspace->data, 256, st);
     }
     Tensor o;
     if (out) {

@@ -8,6 +8,7 @@
 #include <string>
 
 #include "es/ESDecodeAttn.h"
+#include "es/es_fill.h"
 #include "esda.h"
 
 namespace es {
@@ -51,7 +52,7 @@ void copyRows(const Tensor &dst, int dr0, const Tensor &src, int sr0, int n, hip
 
 Tensor zeros(const std::vector<int64_t> &shape, hipStream_t st) {
     Tensor t = Tensor::empty(shape, Dtype::bf16);
-    hipCheck(hipMemsetAsync(t.data, 0, t.nbytes(), st), "ESKVCache zero fill");
+    zeroFill(t.data, t.nbytes(), st);
     return t;
 }
 
@@ -331,7 +332,7 @@ void *ESKVCache::workspace(size_t bytes, hipStream_t st) {
         const size_t n = std::max<size_t>(bytes, 1 << 20);
         workspace_ = Tensor::empty({(int64_t) n}, Dtype::u8);
         // The status word at the front starts at zero (esda workspace contract).
-        hipCheck(hipMemsetAsync(workspace_->data, 0, 256, st), "ESKVCache workspace clear");
+        zeroFill(workspace_->data, 256, st);
     }
     return workspace_->data;
 }
@@ -541,7 +542,7 @@ namespace {
 // A [kvH, cap, w] tensor of `dtype`, zero-filled.
 Tensor zerosOf(const std::vector<int64_t> &shape, Dtype dt, hipStream_t st) {
     Tensor t = Tensor::empty(shape, dt);
-    hipCheck(hipMemsetAsync(t.data, 0, t.nbytes(), st), "ESKVCache zero fill");
+    zeroFill(t.data, t.nbytes(), st);
     return t;
 }
 // dst[h, 0 .. n) = src[h, 0 .. n) for every head h of [kvH, rows, w] tensors of one dtype.

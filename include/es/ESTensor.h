@@ -54,7 +54,8 @@ struct Tensor {
         return st;
     }
 
-    // New device allocation (uninitialised) on the current device.
+    // New device allocation (uninitialised) on the current device, sized in whole 4-byte
+    // words so that a word-wise fill of the tensor stays inside it.
     static Tensor empty(const std::vector<int64_t> &shape, Dtype dtype) {
         Tensor t;
         t.shape = shape;
@@ -62,7 +63,7 @@ struct Tensor {
         t.dtype = dtype;
         if (hipGetDevice(&t.device) != hipSuccess) throw std::runtime_error("ESTensor: hipGetDevice failed");
         void *p = nullptr;
-        const size_t bytes = t.nbytes() ? t.nbytes() : 16;
+        const size_t bytes = t.nbytes() ? (t.nbytes() + 3) / 4 * 4 : 16;
         if (hipMalloc(&p, bytes) != hipSuccess) throw std::runtime_error("ESTensor: hipMalloc failed");
         t.storage = std::shared_ptr<void>(p, [](void *q) { (void) hipFree(q); });
         t.data = p;
