@@ -213,12 +213,17 @@ EDGE = [
          seq_pad=40),
     dict(name="mixed_lengths_global", B=4, Hq=32, Hkv=4, D=512, cap=3000, pos=[2999, 1, 1024, 777],
          shared=True),
-    # Packed kv heads (one split per pair and >= 512 pairs: a workgroup takes 2 or 4 kv
-    # heads of a sequence, RPP = 16 / pk rows of each per stage).  C5's local layers;
-    # short sequences make the rows ragged across the batch.
+    # Packed kv heads (one split per pair and at least twice as many pairs as the plan's
+    # workgroups: a workgroup takes 2 or 4 kv heads of a sequence, RPP = 16 / pk rows of each
+    # per stage).  C5's local shape (512 pairs: one pair per workgroup at two workgroups per
+    # CU) with short sequences ragged across the batch; then twice its batch, which packs two
+    # kv heads per workgroup.
     dict(name="packed2_c5_local_shape", B=32, Hq=32, Hkv=16, D=256, cap=1024, window=1024, ring=True,
          pos=[5, 1023, 1024, 31000] + [int(x) for x in np.random.default_rng(5).integers(0, 32768, size=28)],
          scale=1 / 16, seed=5),
+    dict(name="packed2_d256_separate_b64", B=64, Hq=32, Hkv=16, D=256, cap=1024, window=1024, ring=True,
+         pos=[3, 1022] + [int(x) for x in np.random.default_rng(9).integers(0, 40000, size=62)],
+         scale=1 / 16, seed=9),
     dict(name="packed4_d128_padded", B=128, Hq=16, Hkv=8, D=128, cap=64, window=48, ring=True,
          pos=[int(x) for x in np.random.default_rng(6).integers(0, 200, size=128)], head_pad=40,
          seq_pad=8, seed=6),
