@@ -45,6 +45,41 @@ def test_workspace_size_of_the_global_config():
     assert _ws(split_rows=64) > _ws(split_rows=1024)
 
 
+def _plan_bytes(B, D, slots, heads):
+    """Workspace of a plan with `slots` split partials of `heads` query heads each: 256-byte
+    status area, the batch prefix table, the (m, l) pairs, then the fp32 partial rows."""
+    up = lambda n: (n + 255) // 256 * 256
+    parts = slots * heads
+    return 256 + up((B + 1) * 8) + up(parts * 8) + parts * D * 4
+
+
+# The automatic plan of each BASELINE config, pinned through its workspace size:
+#   C1  D=256, two workgroups per CU: 8 pairs x 32 splits of the 32-row minimum
+#   C2  D=512 shared, one per CU: 4 pairs x 57 splits of 144 rows (whole 16-row tiles)
+#   C3  D=256 rings: 128 pairs x 4 splits of 256 rows (512 workgroups)
+#   C4  D=512 shared: 4 pairs x 64 splits of 2048 rows
+#   C5 local  D=256 rings at B=32: 512 pairs, one split each (the size cannot show kv-head
+#             packing: pk heads per slot over 1/pk the slots)
+#   C5 global D=512 shared, ragged B=32: 512 balanced shares (two per CU) + one slot per pair
+PLANS = [
+    ("C1", dict(batch=1, num_q_heads=16, num_kv_heads=8, head_dim=256, cap=1024, window=1024), 8 * 32, 2),
+    ("C2", dict(batch=1, num_q_heads=32, num_kv_heads=4, head_dim=512, cap=8193, kv_shared=True), 4 * 57, 8),
+    ("C3", dict(batch=8, num_q_heads=32, num_kv_heads=16, head_dim=256, cap=1024, window=1024, ring=True),
+     8 * 16 * 4, 2),
+    ("C4", dict(batch=1, num_q_heads=32, num_kv_heads=4, head_dim=512, cap=131072, kv_shared=True), 4 * 64, 8),
+    ("C5-local", dict(batch=32, num_q_heads=32, num_kv_heads=16, head_dim=256, cap=1024, window=1024, ring=True),
+     32 * 16, 2),
+    ("C5-global", dict(batch=32, num_q_heads=32, num_kv_heads=4, head_dim=512, cap=32768, kv_shared=True),
+     32 * 4 + 512, 8),
+]
+
+
+@pytest.mark.parametrize("name,desc,slots,heads", PLANS, ids=[p[0] for p in PLANS])
+def test_automatic_plans_of_the_baseline_configs(name, desc, slots, heads):
+    n = workspace_bytes(DecodeStep(scale=1.0, **desc))
+    assert n == _plan_bytes(desc["batch"], desc["head_dim"], slots, heads), name
+
+
 @pytest.mark.parametrize("bad", [
     dict(head_dim=96), dict(head_dim=64), dict(num_q_heads=30), dict(num_q_heads=68),
     dict(cap=0), dict(window=-1), dict(ring=True, window=0), dict(ring=True, window=9000),
