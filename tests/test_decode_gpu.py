@@ -303,7 +303,7 @@ def _random_case(seed):
     return case
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(24))
 def test_randomized_configurations(seed):
     run_case(**_random_case(seed))
 
