@@ -140,7 +140,7 @@ def test_chunked_prefill_benchmark_shape_sampled_rows():
                 rows=[0, 1, 200, 511])
 
 
-@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("seed", range(14))
 def test_randomized_shapes_sampled_rows(seed):
     """Seeded random prefill calls inside the API's contract: head dim, GQA group, chunk
     length, cached past, window (with the evicted prefix a sliding layer drops), forced or

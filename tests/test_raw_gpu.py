@@ -163,7 +163,7 @@ def test_rope_table_shorter_than_the_cache_is_refused():
                    _dev(kw), inv_d, workspace=new_raw_workspace(step, "cuda"), rope_table=rope_table(inv_d, 255))
 
 
-@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("seed", range(12))
 def test_raw_randomized_configurations(seed):
     """Seeded random raw-K steps: batch, kv heads (odd counts run unpacked), cache size,
     ragged positions, split sizes, scale, append or not, with or without the rotary table."""
