@@ -9,8 +9,8 @@
 //
 // Kernels
 //   attend_kernel  grid (splits, kv heads, sequences) or balanced shares of a ragged
-//                  batch; 4 or 8 waves, one workgroup per CU (two at D = 256, each with
-//                  half the LDS).  A workgroup streams
+//                  batch; 4 or 8 waves, one workgroup per CU (two at D = 256), the
+//                  ring in the whole LDS or in half of it.  A workgroup streams
 //                  visible rows of one (sequence, kv head) -- or of 2 or 4 kv heads
 //                  packed together -- through an LDS ring filled by LDS DMA, splits the head dim across its
 //                  waves for the QK and PV MFMAs (the GQA group is the MFMA N dimension),
@@ -43,6 +43,9 @@ constexpr int kMaxGroup = 16;
 constexpr int kTargetGroups = 256;  // one workgroup per MI355X CU; plans of two per CU aim at twice that
 constexpr int kWaves256 = 4;        // waves per workgroup of the plain kernels at D = 256
 constexpr int kOcc256 = 2;          // and their workgroups per CU
+// The 512-dim shared stream's kernel is built with its ring in half the LDS (4 stages) although
+// its plans place one workgroup per CU: see dispatch_attend.
+constexpr int kOcc512Shared = 2;
 constexpr int kMinRows = 64;        // fewest rows per workgroup the automatic plan gives
 constexpr int kMinRowsOcc2 = 32;    // the same for grids of two workgroups per CU (C1: step
                                     // 8.3 -> 7.8 us with 32-row splits; 16 rows: 8.0)
@@ -292,8 +295,8 @@ __device__ __forceinline__ void walk_segments(const AttendParams &p, Seg &&segme
 
 // --------------------------------------------------------------------- attend kernel
 //
-// grid (splits, kv heads, sequences), NW = 4 or 8 waves per workgroup, OCC workgroups per
-// CU (the ring takes 1/OCC of the LDS).  A workgroup owns `chunk` consecutive visible rows
+// grid (splits, kv heads, sequences), NW = 4 or 8 waves per workgroup, the ring in 1/OCC of
+// the LDS (so that OCC workgroups fit per CU).  A workgroup owns `chunk` consecutive visible rows
 // of one (sequence, kv head) and streams them through the LDS ring in 16-row stages.
 // When each pair needs one split and pairs are plentiful, pk = 2 or 4 kv heads of a
 // sequence share a workgroup:
@@ -337,7 +340,8 @@ __device__ __forceinline__ void walk_segments(const AttendParams &p, Seg &&segme
 template <int D, bool SHARED, int NW, bool RAW, int RPK = 1, bool Q8 = false, bool TAB = false, int OCC = 1>
 // The LDS ring allows OCC workgroups per CU, i.e. OCC * NW/4 waves per SIMD: telling the
 // compiler so lifts the register limit it would otherwise keep for higher occupancy,
-// which it meets by serialising LDS reads behind their uses.
+// which it meets by serialising LDS reads behind their uses.  (Plans may still place one
+// workgroup per CU on a kernel built with OCC = 2: its shallower ring is what they want.)
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(OCC * NW / 4, OCC * NW / 4)))
 void attend_kernel(AttendParams p) {
     static_assert(!RAW || (D == kRawDim && SHARED && (NW == 4 || NW == 8)), "raw mode: one 512-dim stream, 4 or 8 waves");
@@ -1920,7 +1924,7 @@ namespace {
 struct Plan {
     int G, maxvis, balanced, W, S, chunk;
     int pk;   // kv heads packed per workgroup (the kernels see Hkv / pk heads of G * pk)
-    int occ;  // attend workgroups per CU the plan is sized for (1 or 2)
+    int per_cu;  // attend workgroups per CU the plan is sized for (1 or 2)
     size_t off_table, off_ml, off_acc, bytes;
 };
 
@@ -1971,12 +1975,12 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
     // windowed local layers whose lengths are nearly equal) a plain grid of fixed splits
     // per (sequence, kv head) starts faster.
     pl->balanced = d->batch > 1 && !d->ring;
-    // Workgroups per CU: two at D = 256, and for balanced shares of a 512-dim shared stream
-    // (each ring in half the LDS; one workgroup's segment fill and drain then overlap the
-    // other's streaming: C5 step -0.8%).  A 512-dim grid plan keeps one: twice
-    // the splits cost more in its merge than they gain (C4 step 82.7 -> 85.1 us).
-    pl->occ = raw ? 1 : d->head_dim == 256 ? kOcc256 : (d->head_dim == 512 && d->kv_shared && pl->balanced) ? 2 : 1;
-    const int target = pl->occ * kTargetGroups;  // workgroups that fill the GPU
+    // Workgroups per CU: two at D = 256 (C5 step 7.47 ms against 7.58 with plans of one per
+    // CU), else one.  At D = 512 two per CU measured slower on grid plans (twice the splits
+    // cost more in the merge than they gain: C4 step 82.7 -> 85.1 us) and on balanced shares
+    // (C5 7.64 against 7.52 ms with 256 shares).
+    pl->per_cu = (!raw && d->head_dim == 256) ? kOcc256 : 1;
+    const int target = pl->per_cu * kTargetGroups;  // workgroups that fill the GPU
     pl->pk = 1;
     if (raw && G * 2 <= kMaxGroup && d->num_kv_heads % 2 == 0 &&
         (long long) d->head_stride * 2 * 2 + 16LL * d->head_dim * 2 < (1LL << 31))
@@ -2008,7 +2012,7 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
             const long long per_pair = std::max(1LL, target / pairs);
             chunk = (maxvis + per_pair - 1) / per_pair;
             chunk = (chunk + kTile - 1) / kTile * kTile;
-            const int min_rows = pl->occ == 2 ? kMinRowsOcc2 : kMinRows;
+            const int min_rows = pl->per_cu == 2 ? kMinRowsOcc2 : kMinRows;
             if (chunk < min_rows) chunk = min_rows;
             if (chunk > 8192) chunk = 8192;
         }
@@ -2032,14 +2036,13 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
     return ESDA_OK;
 }
 
-// Waves per workgroup (the head dim is split across them); workgroups per CU: Plan::occ.  D = 256:
+// Waves per workgroup (the head dim is split across them); workgroups per CU: Plan::per_cu.  D = 256:
 // two workgroups of 4 waves per CU, each with half the LDS for its ring (4 stages of 16
 // rows), so each SIMD runs two waves of independent workgroups that never wait on each
 // other's barriers.  Against one workgroup of 8 waves (two per SIMD in barrier lockstep,
 // the softmax repeated by all 8): C3 attend 23.9 -> 22.3 us, C5 step 7.80 -> 7.61 ms, C1
 // 5.7 -> 5.3 us.  D = 512 keeps 4 waves (its 8-wave form loses a ring stage to the larger
-// score exchange and runs C4 ~6% slower), one workgroup per CU on grid plans and two on
-// balanced shares of a shared stream.  D = 128 has too few dims for 8 waves of 32-dim MFMA
+// score exchange and runs C4 ~6% slower).  D = 128 has too few dims for 8 waves of 32-dim MFMA
 // steps.
 template <int D>
 constexpr int ring_waves() { return D == 256 ? kWaves256 : 4; }
@@ -2055,17 +2058,24 @@ hipError_t launch_attend(const AttendParams &ap, dim3 grid, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t dispatch_attend(int D, bool shared, int occ, const AttendParams &ap, dim3 grid, hipStream_t st) {
-    constexpr int O256 = kOcc256;
+// The 512-dim shared stream (C2, C4, C5's global layers) runs the kernel whose ring takes half
+// the LDS -- 4 stages of 16 rows, 3 in flight, 48 KB -- at one workgroup per CU.  Shallower
+// rings measured faster there, the register budget of two waves per SIMD making no difference:
+// C4 step 78.8-79.1 us at 4 stages (80 KB budget), 79.9-80.1 at 5, 80.4-80.6 at 6, 81.5-81.9 at
+// 9 (the full LDS), and C2 13.4 against 14.2 us.  With 256 workgroups, 3 stages each keep
+// ~12.6 MB in flight, which already saturates HBM (a read probe at 256 workgroups x 60 KB in
+// flight reads 7.3 TB/s, and more workgroups read less); deeper rings only add contention.
+// A separate 512-dim V needs the whole LDS for 4 stages; D = 128 stages are 4 KB.
+hipError_t dispatch_attend(int D, bool shared, const AttendParams &ap, dim3 grid, hipStream_t st) {
+    constexpr int O256 = kOcc256, O512 = kOcc512Shared;
     switch (D) {
         case 128: return shared ? launch_attend<128, true>(ap, grid, st) : launch_attend<128, false>(ap, grid, st);
         case 256:
             return shared ? launch_attend<256, true, false, 1, false, false, O256>(ap, grid, st)
                           : launch_attend<256, false, false, 1, false, false, O256>(ap, grid, st);
         default:
-            if (!shared) return launch_attend<512, false>(ap, grid, st);
-            return occ == 2 ? launch_attend<512, true, false, 1, false, false, 2>(ap, grid, st)
-                            : launch_attend<512, true>(ap, grid, st);
+            return shared ? launch_attend<512, true, false, 1, false, false, O512>(ap, grid, st)
+                          : launch_attend<512, false>(ap, grid, st);
     }
 }
 
@@ -2127,7 +2137,7 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         const dim3 grid = pl.balanced ? dim3(pl.W) : dim3(pl.S, d->num_kv_heads / pl.pk, d->batch);
         hipError_t e;
         if (mode == 0) {
-            e = dispatch_attend(d->head_dim, d->kv_shared != 0, pl.occ, ap, grid, st);
+            e = dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
         } else if (pl.pk == 2 && ap.rope_tab) {
             // two kv heads per workgroup with the precomputed cos/sin table (the ES layer's
             // form): the wave-private-ring kernel

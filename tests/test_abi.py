@@ -60,7 +60,7 @@ def _plan_bytes(B, D, slots, heads):
 #   C4  D=512 shared: 4 pairs x 64 splits of 2048 rows
 #   C5 local  D=256 rings at B=32: 512 pairs, one split each (the size cannot show kv-head
 #             packing: pk heads per slot over 1/pk the slots)
-#   C5 global D=512 shared, ragged B=32: 512 balanced shares (two per CU) + one slot per pair
+#   C5 global D=512 shared, ragged B=32: 256 balanced shares (one per CU) + one slot per pair
 PLANS = [
     ("C1", dict(batch=1, num_q_heads=16, num_kv_heads=8, head_dim=256, cap=1024, window=1024), 8 * 32, 2),
     ("C2", dict(batch=1, num_q_heads=32, num_kv_heads=4, head_dim=512, cap=8193, kv_shared=True), 4 * 57, 8),
@@ -70,7 +70,7 @@ PLANS = [
     ("C5-local", dict(batch=32, num_q_heads=32, num_kv_heads=16, head_dim=256, cap=1024, window=1024, ring=True),
      32 * 16, 2),
     ("C5-global", dict(batch=32, num_q_heads=32, num_kv_heads=4, head_dim=512, cap=32768, kv_shared=True),
-     32 * 4 + 512, 8),
+     32 * 4 + 256, 8),
 ]
 
 
