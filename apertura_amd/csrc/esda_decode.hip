@@ -2059,13 +2059,13 @@ hipError_t launch_attend(const AttendParams &ap, dim3 grid, hipStream_t st) {
 }
 
 // The 512-dim shared stream (C2, C4, C5's global layers) runs the kernel whose ring takes half
-// the LDS -- 4 stages of 16 rows, 3 in flight, 48 KB -- at one workgroup per CU.  Shallower
-// rings measured faster there, the register budget of two waves per SIMD making no difference:
-// C4 step 78.8-79.1 us at 4 stages (80 KB budget), 79.9-80.1 at 5, 80.4-80.6 at 6, 81.5-81.9 at
-// 9 (the full LDS), and C2 13.4 against 14.2 us.  With 256 workgroups, 3 stages each keep
-// ~12.6 MB in flight, which already saturates HBM (a read probe at 256 workgroups x 60 KB in
-// flight reads 7.3 TB/s, and more workgroups read less); deeper rings only add contention.
-// A separate 512-dim V needs the whole LDS for 4 stages; D = 128 stages are 4 KB.
+// the LDS -- 4 stages of 16 rows, two of them in flight (32 KB) -- at one workgroup per CU.
+// Shallower rings measured faster there, the register budget of two waves per SIMD making no
+// difference: C4 step 78.8-79.1 us at 4 stages (80 KB budget), 79.9-80.1 at 5, 80.4-80.6 at 6,
+// 81.5-81.9 at 9 (the full LDS), 108.6 at 3; C2 13.4 against 14.2 us at 9.  Over 256
+// workgroups two stages each keep ~8.4 MB in flight, enough to saturate HBM (a read probe reads
+// 7.1-7.3 TB/s with 6-15 MB in flight, less with ~30 MB), where 9 stages keep ~29 MB.  A
+// separate 512-dim V needs the whole LDS for 4 stages; D = 128 stages are 4 KB.
 hipError_t dispatch_attend(int D, bool shared, const AttendParams &ap, dim3 grid, hipStream_t st) {
     constexpr int O256 = kOcc256, O512 = kOcc512Shared;
     switch (D) {
