@@ -4,6 +4,11 @@ CPU oracle, called through the C ABI (apertura_amd.decode -> libesda.so).
 Bar (north star): max-abs-err <= 2e-2 and mean-abs-err <= 2e-3 against the fp64
 oracle and against the reference-rounding oracle; the cache bytes after the append
 must equal the oracle's append bit for bit (every byte of the cache is compared).
+The reference-rounding oracle's outputs are bf16 like the kernel's, so where one bf16
+step of an output is coarser than the absolute bar (|out| >= 4: step 0.03125) the two
+may sit on neighbouring bf16 values; that one step is allowed there (_refround_close).
+Random seed 261 (window 2, outputs up to |4.35|) shows it: kernel -4.15625, oracle
+-4.125, fp64 -4.1434.  The fp64 bar and both mean bars have no such allowance.
 Configs C1-C4 run at their full sizes.
 """
 import numpy as np
@@ -16,6 +21,16 @@ from _synth import make_step_inputs, plant_peaked_keys
 pytestmark = pytest.mark.gpu
 
 TOL_MAX, TOL_MEAN = 2e-2, 2e-3
+
+
+def _refround_close(o: np.ndarray, rr: np.ndarray) -> bool:
+    """Kernel output o against the reference-rounding oracle rr (both bf16 values held as
+    float64): each element within TOL_MAX or within one bf16 step at the larger of the two
+    magnitudes (2**(floor(log2|x|) - 7)), and the mean error within TOL_MEAN."""
+    mag = np.maximum(np.maximum(np.abs(o), np.abs(rr)), 2.0 ** -126)
+    step = 2.0 ** (np.floor(np.log2(mag)) - 7)
+    err = np.abs(o - rr)
+    return bool(np.all(err <= np.maximum(TOL_MAX, step))) and err.mean() <= TOL_MEAN
 
 
 def _dev(a: np.ndarray) -> torch.Tensor:
@@ -75,7 +90,8 @@ def run_case(name, *, B, Hq, Hkv, D, cap, pos, window=0, ring=False, shared=Fals
     if refround:
         rr = orc.from_bf16(orc.decode_refround(step, q, kc, vref, list(pos), row_base)).astype(np.float64)
         e2 = np.abs(o - rr.reshape(B, Hq, D))
-        assert e2.max() <= TOL_MAX and e2.mean() <= TOL_MEAN
+        print(f"[case] {name}: vs refround max_abs={e2.max():.3e} mean_abs={e2.mean():.3e}", flush=True)
+        assert _refround_close(o, rr.reshape(B, Hq, D))
     return o, ref
 
 
@@ -174,7 +190,10 @@ def test_c5_two_layer_step_in_graph():
             err = np.abs(o - ref)
             print(f"[case] C5 two-layer D={t['D']} vs {name}: max_abs={err.max():.3e} "
                   f"mean_abs={err.mean():.3e}", flush=True)
-            assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN
+            if name == "fp64":
+                assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN
+            else:
+                assert _refround_close(o, ref)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         with torch.cuda.graph(g, stream=stream):
@@ -303,7 +322,7 @@ def _random_case(seed):
     return case
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", list(range(24)) + [261])
 def test_randomized_configurations(seed):
     run_case(**_random_case(seed))
 
