@@ -24,6 +24,10 @@
 //                       straight from the score registers (the 32 keys are ordered so
 //                       that the score layout is the B-operand layout).  O^T stays in
 //                       registers (D/16 x QB tiles: QB * D / 16 accumulators per lane).
+//   prefill_kernel<256, 1, true>  the same with 64-row tiles whose even and odd stages go
+//                       to the two wave groups (waves 0-3 and 4-7 on the same query
+//                       blocks), folded together through LDS at the end: short chunks
+//                       at D = 256 fill the CUs with tiles instead of key splits.
 //   prefill_merge_kernel  reduces split partials (m, l, acc) per (query row, head).
 //   raw_prefill_kv_kernel rebuilds K and V of a raw-K (or q8 raw-K) stream by the
 //                       reference's op-level rounding points.
@@ -59,9 +63,10 @@ struct PrefillParams {
     float *part_ml;    // [splits][Sq * Hq][2]
     long long q_hs, q_rs, kv_hs, o_rs, o_hs;
     int Hq, Hkv, G, Sq, Sk, q_pos0, k_pos0, window;
-    int qb;                  // 16-query blocks per wave (query tile: 128 qb rows)
+    int qb;                  // 16-query blocks per wave (query tile: 128 qb rows, 64 with kh)
     int tiles, splits, kps;  // query tiles per kv head, key splits, keys per split
     float scale_log2e;
+    int kh;                  // 1: the two wave groups split each tile's stages (even / odd)
 };
 
 // Keys [j0, j1) that some row of query tile `tile` (QT rows) can see.
@@ -90,28 +95,41 @@ __host__ __device__ inline void tile_keys(const PrefillParams &p, int tile, int 
 // four waves of two blocks -- one wave per SIMD -- ran 6% slower than eight waves of one
 // block, and forming the next stage's scores during this stage's softmax -- a second set
 // of score registers, forcing one block per wave at D = 256 -- was 5-20% slower.)
+//
+// KH (stage halves, D = 256 with one block per wave): waves w and w + 4 own the same query
+// block and take the even and the odd stages of the tile's keys, over a ring of four
+// stages per tensor (132 KB), and fold their (m, l, O^T) together through LDS at the end.
+// A tile is then 64 query rows, so a chunk whose 128-row tiles would leave CUs idle gets
+// twice the tiles instead of key splits -- no fp32 partials and no merge launch -- while
+// each wave's work per stage and the barriers per stage stay those of the plain kernel.
 constexpr int kWaves = 8;
 
-template <int D>
+template <int D, int NSL>
 struct PRing {
     static constexpr int NI = D / 32;                 // DMA blocks per 16-key half
     static constexpr int HB = NI * kBlk;              // one half stage of one tensor
-    static constexpr int BYTES = 8 * HB;              // two K and two V stages
+    static constexpr int BYTES = 4 * NSL * HB;        // NSL K stages, then NSL V stages
     static constexpr int CPR = D / 8;                 // 16-byte chunks per row
     static_assert(BYTES <= kRingBudget, "the K / V slots must fit the LDS budget");
     __host__ __device__ static constexpr int off(int r) { return (r % NI) * kBlk + (r / NI) * 2 * D; }
 };
 
-template <int D, int QB>
+template <int D, int QB, bool KH = false>
 __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p) {
-    using R = PRing<D>;
-    constexpr int QT = 16 * QB * kWaves;  // query rows per tile
+    constexpr int NQW = KH ? kWaves / 2 : kWaves;  // waves with distinct query blocks
+    constexpr int NSL = KH ? 4 : 2;                // ring stages per tensor
+    constexpr int SPI = KH ? 2 : 1;                // stages per iteration (one per wave group)
+    using R = PRing<D, NSL>;
+    constexpr int QT = 16 * QB * NQW;   // query rows per tile
     constexpr int KS = D / 32;          // QK k-steps
     constexpr int DT = D / 16;          // PV dim tiles
     __shared__ __attribute__((aligned(16))) unsigned char ring[R::BYTES];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int li = lane & 15, lg = lane >> 4;
+    // Query-block wave and stage parity (both constant for the plain kernel, whose code
+    // does not change: a wave-dependent parity there measured 3% slower).
+    const int wq = KH ? wave % NQW : wave, kh = KH ? wave / NQW : 0;
     // Workgroup -> (tile, kv head, split): consecutive workgroups go to consecutive XCDs
     // (dispatch is round-robin over the 8), so the (kv head, split) pair is the fastest
     // index and the workgroups on one XCD share one K / V stream in its L2; tiles run
@@ -127,18 +145,18 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
     const int j0 = min(tj1, tj0 + split * p.kps);
     const int j1 = min(tj1, j0 + p.kps);
 
-    // This lane's query row in block qb: tile row wave*16*QB + 16qb + li, global row gr
+    // This lane's query row in block qb: tile row wq*16*QB + 16qb + li, global row gr
     // (position gr / G, head kvh*G + gr % G); rows past the end repeat the last row and
     // are not written.
     const long long nq = (long long) p.Sq * p.G;
     auto qrow = [&](int qb) -> long long {
-        const long long gr = (long long) tile * QT + wave * 16 * QB + qb * 16 + li;
+        const long long gr = (long long) tile * QT + wq * 16 * QB + qb * 16 + li;
         return gr < nq ? gr : nq - 1;
     };
-    auto qvalid = [&](int qb) { return (long long) tile * QT + wave * 16 * QB + qb * 16 + li < nq; };
+    auto qvalid = [&](int qb) { return (long long) tile * QT + wq * 16 * QB + qb * 16 + li < nq; };
 
     if (j0 >= j1) {  // an empty split: no keys for this tile; the merge skips it
-        if (p.splits > 1 && lg == 0) {
+        if (p.splits > 1 && lg == 0 && kh == 0) {
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb)
                 if (qvalid(qb)) {
@@ -166,10 +184,11 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
         }
     }
 
-    // LDS: two K slots then two V slots, each a 32-key stage (two 16-key halves).  Stage
-    // s's K sits in K slot s % 2 and its V in V slot s % 2.  After iteration s's barrier,
-    // K(s+1) and V(s+1) replace the stage s-1 slots (every wave is done with them); they
-    // land while iteration s computes.
+    // LDS: NSL K slots then NSL V slots, each a 32-key stage (two 16-key halves).  Stage
+    // s's K sits in K slot s % NSL and its V in V slot s % NSL.  Iteration i computes the
+    // SPI stages SPI*i .. (one per wave group); after its barrier the stages of iteration
+    // i+1 replace those of iteration i-1 (every wave is done with them) and land while
+    // iteration i computes.
     //
     // DMA: K instruction t of this wave (ii = wave*KPW + t of the stage's 2 NI) fills block
     // b = ii % NI of half hh = ii / NI; lane l reads chunk l % CPR of stage row
@@ -189,8 +208,9 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
         voff[t] = (unsigned) ((vrow[t] * D + (lane % R::CPR) * 8) * 2);
         ldso[t] = hh * R::HB + b * kBlk;
     }
-    auto kslot = [&](int s) { return ring + (s & 1) * 2 * R::HB; };
-    auto vslot = [&](int s) { return ring + 4 * R::HB + (s & 1) * 2 * R::HB; };
+    static_assert((NSL & (NSL - 1)) == 0, "stage slots: a power of two");
+    auto kslot = [&](int s) { return ring + (s & (NSL - 1)) * 2 * R::HB; };
+    auto vslot = [&](int s) { return ring + 2 * NSL * R::HB + (s & (NSL - 1)) * 2 * R::HB; };
     auto issue = [&](const uint16_t *head, int s, unsigned char *slot) {
         const int jb = j0 + s * kStageKeys;
         if (jb + kStageKeys <= j1) {
@@ -245,18 +265,28 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
         return sc;
     };
 
-    issue(kvb, 0, kslot(0));
+    issue(kvb, 0, kslot(0));  // nst >= 1 here
     issue(vvb, 0, vslot(0));
+    if (KH && nst > 1) {
+        issue(kvb, 1, kslot(1));
+        issue(vvb, 1, vslot(1));
+    }
 
-    for (int s = 0; s < nst; ++s) {
-        // Stage s landed (this wave's loads; the barrier covers the other waves') and every
-        // wave is done with iteration s-1
+    for (int s0 = 0; s0 < nst; s0 += SPI) {
+        // The iteration's stages s0 .. s0+SPI-1 landed (this wave's loads; the barrier covers
+        // the other waves') and every wave is done with the previous iteration
         ESDA_WAIT_VM(0);
         lds_barrier();
-        if (s + 1 < nst) {
-            issue(kvb, s + 1, kslot(s + 1));
-            issue(vvb, s + 1, vslot(s + 1));
+        if (s0 + SPI < nst) {
+            issue(kvb, s0 + SPI, kslot(s0 + SPI));
+            issue(vvb, s0 + SPI, vslot(s0 + SPI));
         }
+        if (KH && s0 + SPI + 1 < nst) {
+            issue(kvb, s0 + SPI + 1, kslot(s0 + SPI + 1));
+            issue(vvb, s0 + SPI + 1, vslot(s0 + SPI + 1));
+        }
+        const int s = s0 + kh;  // this wave group's stage
+        if (KH && s >= nst) continue;  // an odd stage count: the odd group's last iteration is empty
         const Scores cur = qk(kslot(s));
         const unsigned char *vb = vslot(s);
         const int jb = j0 + s * kStageKeys;
@@ -347,6 +377,42 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb)
                 acc[qb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qb], acc[qb][dt], 0, 0, 0);
+        }
+    }
+
+    if constexpr (KH) {
+        // The odd-stage wave of each query block hands its (m, l, O^T) to the even-stage
+        // wave through the ring's LDS (no DMA is outstanding and, after the barrier, no wave
+        // reads the ring): lane-major, so each store and load of a wave is one contiguous
+        // 1 KB.  A group that saw no key of a row holds m = -inf, l = 0 and adds nothing.
+        constexpr int XA = QB * DT * 64 * 16;  // O^T bytes per wave
+        constexpr int XW = XA + QB * 64 * 8;   // + (m, l)
+        static_assert(NQW * XW <= R::BYTES, "the hand-over must fit the ring");
+        unsigned char *xb = ring + wq * XW;
+        lds_barrier();
+        if (kh) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+                    *reinterpret_cast<f32x4 *>(xb + ((qb * DT + dt) * 64 + lane) * 16) = acc[qb][dt];
+                *reinterpret_cast<f32x2 *>(xb + XA + (qb * 64 + lane) * 8) = f32x2{m[qb], l[qb]};
+            }
+        }
+        lds_barrier();
+        if (kh) return;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            const f32x2 mlb = *reinterpret_cast<const f32x2 *>(xb + XA + (qb * 64 + lane) * 8);
+            const float M = fmaxf(m[qb], mlb[0]);
+            const float wa = m[qb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[qb] - M);
+            const float wb = mlb[0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mlb[0] - M);
+            l[qb] = l[qb] * wa + mlb[1] * wb;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                acc[qb][dt] = acc[qb][dt] * wa +
+                              *reinterpret_cast<const f32x4 *>(xb + ((qb * DT + dt) * 64 + lane) * 16) * wb;
+            m[qb] = M;
         }
     }
 
@@ -493,6 +559,14 @@ int pick_qb(int D, long long rows, int Hkv) {
     return tiles2 * Hkv >= kTargetGroups ? 2 : 1;
 }
 
+// Stage halves (the KH kernel, 64-row tiles) at D = 256 with one block per wave, when the
+// 128-row tiles alone would leave CUs idle: twice the tiles instead of key splits.
+bool pick_kh(int D, int qb, long long rows, int Hkv) {
+    if (D != 256 || qb != 1) return false;
+    const long long tiles1 = (rows + 16 * kWaves - 1) / (16 * kWaves);
+    return tiles1 * Hkv < kTargetGroups;
+}
+
 // Validates a description and fills the kernel parameters' shape fields and plan.
 int plan_prefill(const esda_prefill_desc *d, PrefillParams *p) {
     if (!d) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: null description");
@@ -534,7 +608,8 @@ int plan_prefill(const esda_prefill_desc *d, PrefillParams *p) {
     p->o_hs = d->out_head_stride;
     p->scale_log2e = d->scale * 1.4426950408889634f;
     p->qb = pick_qb(D, (long long) d->seq_q * p->G, d->num_kv_heads);
-    const int QT = 16 * p->qb * kWaves;
+    p->kh = pick_kh(D, p->qb, (long long) d->seq_q * p->G, d->num_kv_heads) ? 1 : 0;
+    const int QT = 16 * p->qb * (p->kh ? kWaves / 2 : kWaves);
     const long long tiles = ((long long) d->seq_q * p->G + QT - 1) / QT;
     if (tiles * d->num_kv_heads > (1LL << 24))
         return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_prefill: too many query tiles");
@@ -582,6 +657,8 @@ void launch_prefill(const PrefillParams &p, int stages, hipStream_t st) {
             hipLaunchKernelGGL((prefill_kernel<128, 2>), grid, block, 0, st, p);
         else if (p.qb == 2)
             hipLaunchKernelGGL((prefill_kernel<256, 2>), grid, block, 0, st, p);
+        else if (p.kh)
+            hipLaunchKernelGGL((prefill_kernel<256, 1, true>), grid, block, 0, st, p);
         else
             hipLaunchKernelGGL((prefill_kernel<256, 1>), grid, block, 0, st, p);
     }

@@ -184,6 +184,12 @@ def test_prefill_descriptions_are_validated_without_device():
     n = prefill_workspace_bytes(PrefillStep(**good))
     assert n > 0  # 16 query tiles per kv head: the keys are split to cover the CUs
     assert prefill_workspace_bytes(PrefillStep(**{**good, "seq_q": 16384, "q_pos0": 0})) == 0  # enough tiles
+    # a 512-query sliding chunk at GQA 32/16: 128 tiles of 128 rows would split the keys; the
+    # 64-row tiles of the stage-halves kernel cover the 256 CUs, so no partials
+    local = dict(num_q_heads=32, num_kv_heads=16, head_dim=256, seq_q=512, seq_k=1536, q_pos0=15872,
+                 k_pos0=14848, window=1024)
+    assert prefill_workspace_bytes(PrefillStep(**local)) == 0
+    assert prefill_workspace_bytes(PrefillStep(**{**local, "num_kv_heads": 4, "num_q_heads": 8})) > 0
     for bad in (dict(head_dim=64), dict(num_q_heads=30), dict(seq_q=0), dict(window=-1),
                 dict(k_pos0=15873),                              # the first query's own key missing
                 dict(seq_k=100),                                 # the last queries' keys missing

@@ -112,6 +112,29 @@ def test_local_fresh_prefill_benchmark_shape_sampled_rows():
                 rows=[0, 1, 127, 128, 1023, 1024, 1025, 2047, 4095])
 
 
+def test_local_chunk_benchmark_shape_stage_halves_sampled_rows():
+    """512 queries of a sliding layer over window + chunk = 1536 keys (GQA 32/16): 128-row
+    tiles would cover only 128 CUs, so the plan runs 64-row tiles whose even and odd stages
+    go to the two wave groups, with no key splits; rows on tile edges and at both ends."""
+    run_prefill("bench-local-chunk", Hq=32, Hkv=16, D=256, Sq=512, Sk=1536, q_pos0=15872, k_pos0=14848,
+                window=1024, seed=14, rows=[0, 1, 31, 32, 63, 64, 255, 511])
+
+
+def test_local_one_block_per_wave_without_stage_halves():
+    """1024 queries at GQA 32/16: the 128-row tiles alone fill the 256 CUs and two-block
+    tiles would not, so eight waves of one block each on distinct rows."""
+    run_prefill("local-qb1", Hq=32, Hkv=16, D=256, Sq=1024, Sk=1024, q_pos0=0, k_pos0=0, window=300, seed=15,
+                rows=[0, 63, 64, 127, 128, 600, 1023])
+
+
+@pytest.mark.parametrize("split_keys", [32, 96])
+def test_stage_halves_with_forced_key_splits(split_keys):
+    """Stage halves and key splits together (one- and three-stage splits: the odd-stage
+    group of a one-stage split sees no key and adds nothing)."""
+    run_prefill(f"kh-split{split_keys}", Hq=8, Hkv=4, D=256, Sq=200, Sk=264, q_pos0=500, k_pos0=436, window=64,
+                split_keys=split_keys, seed=16)
+
+
 @pytest.mark.parametrize("split_keys", [32, 96, 4096])
 def test_forced_split_sizes_including_empty_splits(split_keys):
     run_prefill(f"split{split_keys}", Hq=8, Hkv=2, D=128, Sq=150, Sk=400, q_pos0=250, k_pos0=0,
