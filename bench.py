@@ -364,9 +364,22 @@ def main() -> int:
             "kernel_us": round(ms_attend * 1e3, 3),
         },
         "cpu_baseline": cpu,
+        "device": device_facts(),
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def device_facts() -> dict:
+    """What the runtime reports for cuda:0, beside the figures the roofline assumes (256 CUs,
+    wave64, 288 GB of HBM3E, 160 KB of LDS per CU)."""
+    import torch
+
+    p = torch.cuda.get_device_properties(0)
+    return {"name": p.name, "arch": getattr(p, "gcnArchName", None), "compute_units": p.multi_processor_count,
+            "wave_size": getattr(p, "warp_size", None), "hbm_bytes": p.total_memory,
+            "l2_bytes": getattr(p, "L2_cache_size", None),
+            "lds_bytes_per_workgroup": getattr(p, "shared_memory_per_block", None)}
 
 
 def profiled_traffic(workload: str, kind: str = "attend"):
@@ -528,6 +541,7 @@ def bench_prefill(args) -> int:
             "kernel_us": round(ms_attend * 1e3, 3),
         },
         "cpu_baseline": cpu,
+        "device": device_facts(),
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -667,6 +681,7 @@ def bench_c5(args) -> int:
                      "unit": "GB/s", "frac": round(nbytes / (ms_att * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                      "traffic": None, "kernel_us": round(ms_att * 1e3, 3)},
         "cpu_baseline": None,
+        "device": device_facts(),
     }
     print(json.dumps(line), flush=True)
     return 0
