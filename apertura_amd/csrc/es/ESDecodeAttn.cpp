@@ -8,10 +8,10 @@
 #include <optional>
 #include <stdexcept>
 #include <string>
-#include <map>
 #include <utility>
 
 #include "es/ESKVCache.h"
+#include "es/stream_scratch.h"
 #include "es/es_fill.h"
 #include "esda.h"
 
@@ -49,14 +49,10 @@ const void *ropeTable(Scratch &s, int rows, hipStream_t st) {
     return s.ropeTab->data;
 }
 
-// One scratch set per (device, stream) of the calling thread: calls on different streams
-// never share a position word, workspace or rebuilt rows, so they may overlap.
-Scratch &scratch(hipStream_t st) {
-    thread_local std::map<std::pair<int, hipStream_t>, Scratch> perStream;
-    int dev = 0;
-    hipCheck(hipGetDevice(&dev), "hipGetDevice");
-    return perStream[{dev, st}];
-}
+// One scratch set per (device, stream) of the calling thread (at most kMaxStreamScratch of
+// them; stream_scratch.h): calls on different streams never share a position word,
+// workspace or rebuilt rows, so they may overlap.
+Scratch &scratch(hipStream_t st) { return streamScratch<Scratch>(st); }
 
 }  // namespace
 

@@ -135,6 +135,7 @@ void ESKVCache::growSlot(Slot &s, int nNew, hipStream_t st, bool compactStart) {
 
 std::pair<Tensor, Tensor> ESKVCache::update(int layer, const Tensor &kNew, const Tensor &vNew, int maxKeep,
                                             bool prealloc, hipStream_t st) {
+    lastStream_ = st;
     checkLayer(layer);
     checkRows(kNew, "ESKVCache::update kNew");
     checkRows(vNew, "ESKVCache::update vNew");
@@ -148,19 +149,31 @@ std::pair<Tensor, Tensor> ESKVCache::update(int layer, const Tensor &kNew, const
         if (!s.k || !s.v) throw std::runtime_error("ESKVCache::update: compiled-step slot not set (setSlot)");
         if (kNew.shape[1] != 1) throw std::invalid_argument("ESKVCache::update: a compiled step appends one row");
         const Tensor &idx = maxKeep > 0 ? *stepSlidingIdx_ : *stepGlobalIdx_;
-        auto scatter = [&](const Tensor &buf, const Tensor &row) {
+        const bool slotShared = s.v->data == s.k->data;
+        // One shared K=V buffer takes one row: a distinct vNew would overwrite the K row just
+        // scattered (the reference's functional scatter keeps two arrays instead), so it is refused.
+        if (slotShared && vNew.data != kNew.data)
+            throw std::invalid_argument("ESKVCache::update: compiled-step slot holds one shared K=V buffer; "
+                                        "vNew must alias kNew");
+        // Every check runs before the first launch, so a refused step writes nothing.  The rows
+        // must be packed [kvH, 1, hd] (what esda_kv_append reads): a strided row would need a
+        // copy whose release waits on the stream, which a graph capture of the step forbids.
+        auto check = [&](const Tensor &buf, const Tensor &row) {
             if (buf.dim() != 3 || buf.shape[0] != row.shape[0] || buf.shape[2] != row.shape[2] ||
                 buf.strides[2] != 1 || buf.strides[1] != buf.shape[2])
                 throw std::invalid_argument("ESKVCache::update: kNew / vNew do not match the compiled-step slot");
-            // esda_kv_append reads [1, kvH, 1, hd] rows packed head after head
-            const Tensor src = row.strides[0] == row.shape[2] ? row : clone(row, st);
+            if (row.strides[0] != row.shape[2])
+                throw std::invalid_argument("ESKVCache::update: a compiled step needs packed [kvH, 1, hd] rows");
+        };
+        check(*s.k, kNew);
+        check(*s.v, vNew);
+        auto scatter = [&](const Tensor &buf, const Tensor &row) {
             const int cap = (int) buf.shape[1], hd = (int) buf.shape[2], kvH = (int) buf.shape[0];
-            esdaCheck(esda_kv_append(buf.data, buf.strides[0] * kvH, buf.strides[0], 1, kvH, hd, cap, src.data, 1,
+            esdaCheck(esda_kv_append(buf.data, buf.strides[0] * kvH, buf.strides[0], 1, kvH, hd, cap, row.data, 1,
                                      static_cast<const int32_t *>(idx.data), st));
-            if (src.data != row.data) hipCheck(hipStreamSynchronize(st), "ESKVCache step append");  // copy released
         };
         scatter(*s.k, kNew);
-        if (s.v->data != s.k->data || vNew.data != kNew.data) scatter(*s.v, vNew);
+        if (!slotShared) scatter(*s.v, vNew);
         return {*s.k, *s.v};
     }
     if (!prealloc) {
@@ -295,6 +308,7 @@ ESKVCache::Raw ESKVCache::currentRaw(int layer) const {
 }
 
 ESKVCache::Raw ESKVCache::updateRaw(int layer, const Tensor &kNew, bool prealloc, hipStream_t st) {
+    lastStream_ = st;
     checkLayer(layer);
     checkRows(kNew, "ESKVCache::updateRaw kNew");
     const int nNew = (int) kNew.shape[1];
@@ -357,6 +371,7 @@ int *ESKVCache::positionWord(int layer, int value, hipStream_t st) {
 
 Tensor ESKVCache::decode(int layer, const Tensor &q, const Tensor &kNew, const Tensor &vNew, int maxKeep,
                          int window, float scale, hipStream_t st, Tensor *out) {
+    lastStream_ = st;
     if (stepMode_) throw std::runtime_error("ESKVCache::decode: not available in compiled-step mode (beginStep .. endStep)");
     checkLayer(layer);
     checkRows(kNew, "ESKVCache::decode kNew");
@@ -440,6 +455,7 @@ Tensor ESKVCache::decode(int layer, const Tensor &q, const Tensor &kNew, const T
 
 Tensor ESKVCache::decodeRaw(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
                             const std::vector<float> &invFreq, hipStream_t st, Tensor *out) {
+    lastStream_ = st;
     if (stepMode_) throw std::runtime_error("ESKVCache::decodeRaw: not available in compiled-step mode (beginStep .. endStep)");
     checkLayer(layer);
     checkRows(kNew, "ESKVCache::decodeRaw kNew");
@@ -607,6 +623,7 @@ ESKVCache::RawQ8 ESKVCache::currentRawQ8(int layer) const {
 }
 
 ESKVCache::RawQ8 ESKVCache::updateRawQ8(int layer, const Tensor &kNew, hipStream_t st) {
+    lastStream_ = st;
     // ESKVCache.mm:513-556.
     checkLayer(layer);
     checkRows(kNew, "ESKVCache::updateRawQ8 kNew");
@@ -641,6 +658,7 @@ ESKVCache::RawQ8 ESKVCache::updateRawQ8(int layer, const Tensor &kNew, hipStream
 
 Tensor ESKVCache::decodeRawQ8(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
                               const std::vector<float> &invFreq, hipStream_t st, Tensor *out) {
+    lastStream_ = st;
     if (stepMode_) throw std::runtime_error("ESKVCache::decodeRawQ8: not available in compiled-step mode (beginStep .. endStep)");
     checkLayer(layer);
     checkRows(kNew, "ESKVCache::decodeRawQ8 kNew");

@@ -8,10 +8,10 @@
 #include <optional>
 #include <stdexcept>
 #include <string>
-#include <map>
 #include <utility>
 
 #include "es/ESKVCache.h"
+#include "es/stream_scratch.h"
 #include "esda.h"
 #include "esda_prefill.h"
 
@@ -36,14 +36,10 @@ struct Scratch {
     std::vector<float> invFreqHost;
 };
 
-// One scratch set per (device, stream) of the calling thread: calls on different streams
-// never share a position word, workspace or rebuilt rows, so they may overlap.
-Scratch &scratch(hipStream_t st) {
-    thread_local std::map<std::pair<int, hipStream_t>, Scratch> perStream;
-    int dev = 0;
-    hipCheck(hipGetDevice(&dev), "hipGetDevice");
-    return perStream[{dev, st}];
-}
+// One scratch set per (device, stream) of the calling thread (at most kMaxStreamScratch of
+// them; stream_scratch.h): calls on different streams never share a position word,
+// workspace or rebuilt rows, so they may overlap.
+Scratch &scratch(hipStream_t st) { return streamScratch<Scratch>(st); }
 
 Tensor &grown(std::optional<Tensor> &slot, size_t elems, Dtype dt, hipStream_t st) {
     if (!slot || slot->numel() < (int64_t) elems) {
@@ -195,6 +191,7 @@ Tensor esPrefillAttnRawQ8(const Tensor &q, const Tensor &qView, const Tensor &sc
 
 Tensor ESKVCache::prefill(int layer, const Tensor &q, const Tensor &kNew, const Tensor &vNew, int maxKeep, int window,
                           float scale, int pastLen, bool prealloc, hipStream_t st, Tensor *out) {
+    lastStream_ = st;
     if (stepMode_) throw std::runtime_error("ESKVCache::prefill: not available in compiled-step mode (beginStep .. endStep)");
     checkQ(q, "ESKVCache::prefill");
     if (kNew.dim() != 3 || kNew.shape[1] != q.shape[1])
@@ -206,6 +203,7 @@ Tensor ESKVCache::prefill(int layer, const Tensor &q, const Tensor &kNew, const 
 Tensor ESKVCache::prefillRaw(int layer, const Tensor &q, const Tensor &kNew, const Tensor &kw, float eps,
                              const std::vector<float> &invFreq, int pastLen, float scale, bool q8, hipStream_t st,
                              Tensor *out) {
+    lastStream_ = st;
     if (stepMode_) throw std::runtime_error("ESKVCache::prefillRaw: not available in compiled-step mode (beginStep .. endStep)");
     checkQ(q, "ESKVCache::prefillRaw");
     if (kNew.dim() != 3 || kNew.shape[1] != q.shape[1])

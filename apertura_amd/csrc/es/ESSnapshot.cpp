@@ -11,8 +11,10 @@
 // layer whose V is its K buffer (attention_k_eq_v decode), written as two equal tensors so
 // that the reference's reader sees an ordinary k/v layer.
 //
-// Device <-> host copies are synchronous: snapshots and marks are rare, and each begins
-// with a device-wide synchronisation so that appends queued on any stream have landed.
+// Device work runs on the stream of the cache's last update / decode / prefill call
+// (lastStream_): each member first waits for that stream, so the appends queued there have
+// landed, and waits again for its own copies before it returns (snapshots and marks are rare).
+// Nothing here synchronises the whole device.
 #include "es/ESKVCache.h"
 
 #include <algorithm>
@@ -49,7 +51,7 @@ int chunkUp(int n) {
 // ------------------------------------------------------------------ device <-> host
 
 // Rows [r0, r0 + n) of every head of a [kvHeads, cap, headDim] buffer -> host [kvHeads, n, headDim].
-StTensor download(const Tensor &buf, int r0, int n) {
+StTensor download(const Tensor &buf, int r0, int n, hipStream_t st) {
     StTensor t;
     t.dtype = buf.dtype == Dtype::bf16 ? "BF16" : buf.dtype == Dtype::f32 ? "F32" : "U8";
     t.shape = {buf.shape[0], n, buf.shape[2]};
@@ -57,49 +59,56 @@ StTensor download(const Tensor &buf, int r0, int n) {
     const size_t rowBytes = (size_t) buf.shape[2] * es;
     t.bytes.resize((size_t) buf.shape[0] * n * rowBytes);
     if (n > 0)
-        hipOk(hipMemcpy2D(t.bytes.data(), (size_t) n * rowBytes,
-                          static_cast<const char *>(buf.data) + (size_t) r0 * buf.strides[1] * es,
-                          (size_t) buf.strides[0] * es, (size_t) n * rowBytes, (size_t) buf.shape[0],
-                          hipMemcpyDeviceToHost),
+    {
+        hipOk(hipMemcpy2DAsync(t.bytes.data(), (size_t) n * rowBytes,
+                               static_cast<const char *>(buf.data) + (size_t) r0 * buf.strides[1] * es,
+                               (size_t) buf.strides[0] * es, (size_t) n * rowBytes, (size_t) buf.shape[0],
+                               hipMemcpyDeviceToHost, st),
               "ESKVCache snapshot download");
+        hipOk(hipStreamSynchronize(st), "ESKVCache snapshot download");
+    }
     return t;
 }
 
 // A fresh zeroed [kvHeads, cap, w] buffer of `dt` holding `rows` rows of host data
 // [kvHeads, rowsStored, w] (rows <= rowsStored; the rest of the buffer is zero).
+// The copy has finished when it returns (the host bytes may be released).
 Tensor upload(const std::vector<uint8_t> &src, int64_t kvH, int64_t rowsStored, int64_t hd, int rows, int cap,
-              Dtype dt = Dtype::bf16) {
+              hipStream_t st, Dtype dt = Dtype::bf16) {
     Tensor t = Tensor::empty({kvH, cap, hd}, dt);
-    hipOk(hipMemset(t.data, 0, t.nbytes()), "ESKVCache snapshot clear");
+    hipOk(hipMemsetAsync(t.data, 0, t.nbytes(), st), "ESKVCache snapshot clear");
     const size_t rowBytes = (size_t) hd * dtypeSize(dt);
     if (rows > 0)
-        hipOk(hipMemcpy2D(t.data, (size_t) cap * rowBytes, src.data(), (size_t) rowsStored * rowBytes,
-                          (size_t) rows * rowBytes, (size_t) kvH, hipMemcpyHostToDevice),
+        hipOk(hipMemcpy2DAsync(t.data, (size_t) cap * rowBytes, src.data(), (size_t) rowsStored * rowBytes,
+                               (size_t) rows * rowBytes, (size_t) kvH, hipMemcpyHostToDevice, st),
               "ESKVCache snapshot upload");
+    hipOk(hipStreamSynchronize(st), "ESKVCache snapshot upload");
     return t;
 }
 
 // A device copy of rows [r0, r0 + n) of every head (the marker / rewind window copies).
-Tensor copyWindow(const Tensor &buf, int r0, int n) {
+// Queued on st; the caller waits for st before the copy is used or its source changes.
+Tensor copyWindow(const Tensor &buf, int r0, int n, hipStream_t st) {
     Tensor t = Tensor::empty({buf.shape[0], n, buf.shape[2]}, Dtype::bf16);
     const size_t rowBytes = (size_t) buf.shape[2] * 2;
     if (n > 0)
-        hipOk(hipMemcpy2D(t.data, (size_t) n * rowBytes,
-                          static_cast<const char *>(buf.data) + (size_t) r0 * buf.strides[1] * 2,
-                          (size_t) buf.strides[0] * 2, (size_t) n * rowBytes, (size_t) buf.shape[0],
-                          hipMemcpyDeviceToDevice),
+        hipOk(hipMemcpy2DAsync(t.data, (size_t) n * rowBytes,
+                               static_cast<const char *>(buf.data) + (size_t) r0 * buf.strides[1] * 2,
+                               (size_t) buf.strides[0] * 2, (size_t) n * rowBytes, (size_t) buf.shape[0],
+                               hipMemcpyDeviceToDevice, st),
               "ESKVCache window copy");
     return t;
 }
 
 // A fresh chunk-aligned buffer with `src`'s rows at the front (the compaction layout).
-Tensor rehomeDevice(const Tensor &src, int cap) {
+// Queued on st, as copyWindow.
+Tensor rehomeDevice(const Tensor &src, int cap, hipStream_t st) {
     const int64_t kvH = src.shape[0], n = src.shape[1], hd = src.shape[2];
     Tensor t = Tensor::empty({kvH, cap, hd}, Dtype::bf16);
-    hipOk(hipMemset(t.data, 0, t.nbytes()), "ESKVCache rewind clear");
+    hipOk(hipMemsetAsync(t.data, 0, t.nbytes(), st), "ESKVCache rewind clear");
     if (n > 0)
-        hipOk(hipMemcpy2D(t.data, (size_t) cap * hd * 2, src.data, (size_t) src.strides[0] * 2,
-                          (size_t) n * hd * 2, (size_t) kvH, hipMemcpyDeviceToDevice),
+        hipOk(hipMemcpy2DAsync(t.data, (size_t) cap * hd * 2, src.data, (size_t) src.strides[0] * 2,
+                               (size_t) n * hd * 2, (size_t) kvH, hipMemcpyDeviceToDevice, st),
               "ESKVCache rewind install");
     return t;
 }
@@ -138,8 +147,8 @@ int parseInt(const std::map<std::string, std::string> &meta, const std::string &
 
 // ------------------------------------------------------------------ markers and rewind
 
-ESKVCache::Marker ESKVCache::takeMarker(int pos, bool copyLost, hipStream_t) const {
-    hipOk(hipDeviceSynchronize(), "ESKVCache mark");
+ESKVCache::Marker ESKVCache::takeMarker(int pos, bool copyLost, hipStream_t st) const {
+    hipOk(hipStreamSynchronize(st), "ESKVCache mark");
     Marker m;
     m.pos = pos;
     for (size_t i = 0; i < slots_.size(); ++i) {
@@ -148,10 +157,11 @@ ESKVCache::Marker ESKVCache::takeMarker(int pos, bool copyLost, hipStream_t) con
         const int live = s.len - s.start;
         if (live >= pos && !(copyLost && s.lost)) continue;  // the full prefix is still there
         // Deep copy now: later appends overwrite these rows in place.
-        Tensor k = copyWindow(*s.k, s.start, live);
-        Tensor v = s.shared ? k : copyWindow(*s.v, s.start, live);
+        Tensor k = copyWindow(*s.k, s.start, live, st);
+        Tensor v = s.shared ? k : copyWindow(*s.v, s.start, live, st);
         m.slidingKV.push_back({(int) i, {k, v}});
     }
+    hipOk(hipStreamSynchronize(st), "ESKVCache mark");  // later appends overwrite the source rows
     return m;
 }
 
@@ -160,7 +170,7 @@ void ESKVCache::markPrefix(int pos, const std::string &fingerprint) {
     // a never-evicting one (ESKVCache.mm:121-146).
     if (pos < 4096)
         throw std::invalid_argument("ESKVCache::markPrefix: marker positions below 4096 unsupported");
-    Marker m = takeMarker(pos, /*copyLost=*/false, nullptr);
+    Marker m = takeMarker(pos, /*copyLost=*/false, lastStream_);
     m.fp = fingerprint;
     markers_.push_back(std::move(m));
 }
@@ -175,7 +185,7 @@ bool ESKVCache::markRewindPoint(int pos) {
     for (const Slot &s : slots_) prealloc = prealloc || s.k.has_value();
     for (const RQ8Slot &s : rq8slots_) prealloc = prealloc || s.q.has_value();
     if (!prealloc) return false;
-    rewindMark_ = takeMarker(pos, /*copyLost=*/true, nullptr);
+    rewindMark_ = takeMarker(pos, /*copyLost=*/true, lastStream_);
     return true;
 }
 
@@ -201,8 +211,8 @@ int ESKVCache::rewindToMark() {
             const Tensor &k = copyFor[i]->first;
             const int content = (int) k.shape[1];
             const int cap = chunkUp(content + kGrowChunk);
-            s.k = rehomeDevice(k, cap);
-            s.v = s.shared ? *s.k : rehomeDevice(copyFor[i]->second, cap);
+            s.k = rehomeDevice(k, cap, lastStream_);
+            s.v = s.shared ? *s.k : rehomeDevice(copyFor[i]->second, cap, lastStream_);
             s.len = content;
             s.start = 0;
             s.lost = content < P;
@@ -211,7 +221,7 @@ int ESKVCache::rewindToMark() {
             s.start = 0;
         }
     }
-    hipOk(hipDeviceSynchronize(), "ESKVCache rewind");
+    hipOk(hipStreamSynchronize(lastStream_), "ESKVCache rewind");
     slots_ = std::move(next);
     for (RQ8Slot &s : rq8slots_)
         if (s.q) s.len = P;  // q8 rows never evict: cursor truncation
@@ -223,7 +233,7 @@ int ESKVCache::rewindToMark() {
 
 bool ESKVCache::saveSnapshot(const std::string &path, const std::string &fingerprint, int pos) const {
     try {
-        hipOk(hipDeviceSynchronize(), "ESKVCache snapshot");
+        hipOk(hipStreamSynchronize(lastStream_), "ESKVCache snapshot");
         std::vector<std::pair<std::string, StTensor>> ts;
         std::map<std::string, std::string> meta;
         for (size_t i = 0; i < slots_.size(); ++i) {
@@ -231,15 +241,15 @@ bool ESKVCache::saveSnapshot(const std::string &path, const std::string &fingerp
             const std::string id = std::to_string(i);
             if (const RQ8Slot &r = rq8slots_[i]; r.q) {
                 // q8 raw layer: packed rows and the per-row scale / bias, live [0, len)
-                ts.emplace_back("rq_" + id, download(*r.q, 0, r.len));
-                ts.emplace_back("rs_" + id, download(*r.sc, 0, r.len));
-                ts.emplace_back("rb_" + id, download(*r.bs, 0, r.len));
+                ts.emplace_back("rq_" + id, download(*r.q, 0, r.len, lastStream_));
+                ts.emplace_back("rs_" + id, download(*r.sc, 0, r.len, lastStream_));
+                ts.emplace_back("rb_" + id, download(*r.bs, 0, r.len, lastStream_));
                 continue;
             }
             if (!s.k) return false;  // a snapshot needs every layer primed
-            StTensor k = download(*s.k, s.start, s.len - s.start);
+            StTensor k = download(*s.k, s.start, s.len - s.start, lastStream_);
             if (s.v) {
-                StTensor v = s.shared ? k : download(*s.v, s.start, s.len - s.start);
+                StTensor v = s.shared ? k : download(*s.v, s.start, s.len - s.start, lastStream_);
                 if (s.shared) meta["shared_" + id] = "1";
                 ts.emplace_back("k_" + id, std::move(k));
                 ts.emplace_back("v_" + id, std::move(v));
@@ -259,9 +269,9 @@ bool ESKVCache::saveSnapshot(const std::string &path, const std::string &fingerp
             for (const auto &lkv : m.slidingKV) {
                 const std::string sfx = "_" + std::to_string(lkv.first);
                 const Tensor &k = lkv.second.first;
-                ts.emplace_back("m" + std::to_string(mi) + "_k" + sfx, download(k, 0, (int) k.shape[1]));
+                ts.emplace_back("m" + std::to_string(mi) + "_k" + sfx, download(k, 0, (int) k.shape[1], lastStream_));
                 ts.emplace_back("m" + std::to_string(mi) + "_v" + sfx,
-                                download(lkv.second.second, 0, (int) k.shape[1]));
+                                download(lkv.second.second, 0, (int) k.shape[1], lastStream_));
             }
         }
         return writeSafetensors(path, ts, meta);
@@ -368,10 +378,10 @@ int ESKVCache::restoreSnapshot(const std::string &path, const std::string &finge
                 const StTensor &k = T.at(mk), &v = T.at("m" + std::to_string(markerIdx) + "_v_" + id);
                 const int content = (int) k.shape[1];
                 const int cap = chunkUp(content + kGrowChunk);
-                s.k = upload(k.bytes, k.shape[0], content, k.shape[2], content, cap);
+                s.k = upload(k.bytes, k.shape[0], content, k.shape[2], content, cap, lastStream_);
                 const bool shared = meta.count("shared_" + id) && meta.at("shared_" + id) == "1" &&
                                     v.bytes == k.bytes;
-                s.v = shared ? *s.k : upload(v.bytes, v.shape[0], content, v.shape[2], content, cap);
+                s.v = shared ? *s.k : upload(v.bytes, v.shape[0], content, v.shape[2], content, cap, lastStream_);
                 s.shared = shared;
                 s.len = content;
                 s.lost = content < targetPos;
@@ -384,9 +394,9 @@ int ESKVCache::restoreSnapshot(const std::string &path, const std::string &finge
                 const int content = (int) std::min<int64_t>(rows, targetPos);
                 const int cap = chunkUp(content + kGrowChunk);
                 RQ8Slot &r = nextQ8[i];
-                r.q = upload(q.bytes, kvH, rows, 512, content, cap, Dtype::u8);
-                r.sc = upload(sc.bytes, kvH, rows, 1, content, cap, Dtype::f32);
-                r.bs = upload(bs.bytes, kvH, rows, 1, content, cap, Dtype::f32);
+                r.q = upload(q.bytes, kvH, rows, 512, content, cap, lastStream_, Dtype::u8);
+                r.sc = upload(sc.bytes, kvH, rows, 1, content, cap, lastStream_, Dtype::f32);
+                r.bs = upload(bs.bytes, kvH, rows, 1, content, cap, lastStream_, Dtype::f32);
                 r.len = content;
                 continue;
             }
@@ -397,17 +407,17 @@ int ESKVCache::restoreSnapshot(const std::string &path, const std::string &finge
                 const int content = (int) std::min<int64_t>(rows, targetPos);
                 const int cap = chunkUp(content + kGrowChunk);
                 RQ8Slot &r = nextQ8[i];
-                r.q = upload({}, kvH, 0, 512, 0, cap, Dtype::u8);
-                r.sc = upload({}, kvH, 0, 1, 0, cap, Dtype::f32);
-                r.bs = upload({}, kvH, 0, 1, 0, cap, Dtype::f32);
+                r.q = upload({}, kvH, 0, 512, 0, cap, lastStream_, Dtype::u8);
+                r.sc = upload({}, kvH, 0, 1, 0, cap, lastStream_, Dtype::f32);
+                r.bs = upload({}, kvH, 0, 1, 0, cap, lastStream_, Dtype::f32);
                 r.len = content;
                 if (content > 0) {
-                    const Tensor rowsDev = upload(k.bytes, kvH, rows, 512, content, content);
+                    const Tensor rowsDev = upload(k.bytes, kvH, rows, 512, content, content, lastStream_);
                     const int rc = esda_quantize_raw_rows(rowsDev.data, (int32_t) kvH, content, r.q->data,
                                                           (int64_t) cap * 512, static_cast<float *>(r.sc->data),
-                                                          static_cast<float *>(r.bs->data), cap, 0, nullptr);
+                                                          static_cast<float *>(r.bs->data), cap, 0, lastStream_);
                     if (rc != 0) throw std::runtime_error("ESKVCache restore: row quantization failed");
-                    hipOk(hipDeviceSynchronize(), "ESKVCache restore quantize");
+                    hipOk(hipStreamSynchronize(lastStream_), "ESKVCache restore quantize");
                 }
                 continue;
             }
@@ -430,7 +440,7 @@ int ESKVCache::restoreSnapshot(const std::string &path, const std::string &finge
                             std::memcpy(&dq[e * 2], &b, 2);
                         }
                     }
-                s.k = upload(dq, kvH, rows, hd, content, chunkUp(content + kGrowChunk));
+                s.k = upload(dq, kvH, rows, hd, content, chunkUp(content + kGrowChunk), lastStream_);
                 s.len = content;
                 s.lost = content < targetPos;
                 continue;
@@ -438,18 +448,18 @@ int ESKVCache::restoreSnapshot(const std::string &path, const std::string &finge
             const StTensor &k = T.at("k_" + id);
             const int content = (int) std::min<int64_t>(k.shape[1], targetPos);
             const int cap = chunkUp(content + kGrowChunk);
-            s.k = upload(k.bytes, k.shape[0], k.shape[1], k.shape[2], content, cap);
+            s.k = upload(k.bytes, k.shape[0], k.shape[1], k.shape[2], content, cap, lastStream_);
             if (kind[i] == Composite) {
                 const StTensor &v = T.at("v_" + id);
                 const bool shared = meta.count("shared_" + id) && meta.at("shared_" + id) == "1" &&
                                     v.bytes == k.bytes;
-                s.v = shared ? *s.k : upload(v.bytes, v.shape[0], v.shape[1], v.shape[2], content, cap);
+                s.v = shared ? *s.k : upload(v.bytes, v.shape[0], v.shape[1], v.shape[2], content, cap, lastStream_);
                 s.shared = shared;
             }
             s.len = content;
             s.lost = content < targetPos;  // a stored sliding window is not a full prefix
         }
-        hipOk(hipDeviceSynchronize(), "ESKVCache restore");
+        hipOk(hipStreamSynchronize(lastStream_), "ESKVCache restore");
         slots_ = std::move(next);
         rq8slots_ = std::move(nextQ8);
         return targetPos;

@@ -231,6 +231,11 @@ private:
     void migrateToQ8(int layer, hipStream_t stream);
     Marker takeMarker(int pos, bool copyLost, hipStream_t stream) const;
     int seqLen_ = 0;
+    // The stream of the last update / decode / prefill call.  The persistence and rewind
+    // members (which take no stream in the reference's signatures) wait for it and run their
+    // copies on it, so appends queued there have landed; a caller that writes the cache's
+    // buffers from several streams orders them before that stream, as its own calls need.
+    hipStream_t lastStream_ = nullptr;
     // Compiled-step mode state (beginStep): the row index tensors of this token.
     bool stepMode_ = false;
     std::optional<Tensor> stepGlobalIdx_, stepSlidingIdx_;

@@ -289,9 +289,10 @@ EDGE = [
     dict(name="d256_shared_ring_packed", B=64, Hq=32, Hkv=16, D=256, cap=128, window=100, ring=True,
          shared=True, pos=[int(x) for x in np.random.default_rng(8).integers(0, 600, size=64)], seed=8),
     dict(name="d256_auto_32_row_splits", B=1, Hq=8, Hkv=4, D=256, cap=700, pos=[699]),
-    # balanced shares of a 512-dim shared stream run two workgroups per CU, sized for 512
-    # shares: here far fewer visible rows than shares, with one empty-ish sequence
-    dict(name="balanced_two_per_cu_tiny", B=3, Hq=16, Hkv=2, D=512, cap=8192, shared=True, pos=[0, 40, 300]),
+    # balanced shares of a 512-dim shared stream run one workgroup per CU, 256 shares (the
+    # plan C5's global layers use): here far fewer visible rows than shares, with one
+    # empty-ish sequence
+    dict(name="balanced_256_shares_tiny", B=3, Hq=16, Hkv=2, D=512, cap=8192, shared=True, pos=[0, 40, 300]),
 ]
 
 

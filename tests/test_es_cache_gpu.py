@@ -308,3 +308,35 @@ def test_compiled_step_mode_scatters_at_device_positions():
     with pytest.raises(EsdaError) as ei:
         cache.slot_kv(1)
     assert ei.value.code == 2
+
+
+def test_compiled_step_shared_slot_refuses_a_distinct_v():
+    """A compiled-step slot adopted with one shared K=V buffer (setSlot(k, k)) takes one row per
+    update: a vNew that does not alias kNew would be scattered over the K row just written, so
+    update() refuses it with invalid_argument before any launch, and the buffer is unchanged.
+    The aliased update of the same step then writes its row."""
+    from apertura_amd._lib import EsdaError
+    from apertura_amd.cache import ESKVCache
+    rng = np.random.default_rng(72)
+    cap = 64
+    cache = ESKVCache(1)
+    g = _dev(rms_rows(rng, (2, cap, 512)))
+    before = _host(g)
+    cache.set_slot(0, g, g)
+    gidx = torch.full((1,), 7, dtype=torch.int32, device="cuda")
+    sidx = torch.zeros(1, dtype=torch.int32, device="cuda")
+    kn = _dev(rms_rows(rng, (2, 1, 512)))
+    vn = _dev(rms_rows(rng, (2, 1, 512)))
+    print("\n[case] compiled step, shared slot, distinct vNew", flush=True)
+    cache.begin_step(gidx, sidx)
+    with pytest.raises(EsdaError) as ei:
+        cache.update(0, kn, vn, 0, True)
+    assert ei.value.code == 1 and "alias" in str(ei.value)
+    torch.cuda.synchronize()
+    assert np.array_equal(_host(g), before), "a refused step wrote the slot"
+    cache.update(0, kn, kn, 0, True)
+    torch.cuda.synchronize()
+    cache.end_step()
+    want = before.copy()
+    want[:, 7] = _host(kn)[:, 0]
+    assert np.array_equal(_host(g), want)

@@ -175,6 +175,16 @@ def test_raw_randomized_configurations(seed):
             append=bool(r.integers(0, 2)), table=bool(r.integers(0, 2)))
 
 
+@pytest.mark.parametrize("seed", [23, 29])
+def test_raw_table_in_model_scale_one_ragged_batch(seed):
+    """The ES layer's raw-K form (precomputed rotary table, two kv heads per workgroup) at the
+    in-model scale 1.0 over a ragged batch with appends, each sequence against the fp64 oracle.
+    (The table and own-sincos kernels are compared with each other at the configs' scale in
+    test_rope_table_kernels_agree_and_the_table_matches_fp64.)"""
+    run_raw(f"scale1-ragged-table-{seed}", B=3, cap=4096, pos=[4095, 1000, 2777], scale=1.0, seed=seed,
+            table=True)
+
+
 @TABLE
 def test_raw_batched_ragged_positions(table):
     run_raw("batched", B=3, cap=4096, pos=[17, 2500, 4095], scale=512 ** -0.5, seed=7, table=table)
