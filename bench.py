@@ -659,14 +659,30 @@ def bench_c5(args) -> int:
         ms_att = timed(g_att.replay, max(2, args.steps // 10))
         ms_local = timed(graph_of(3, "l").replay, max(2, args.steps // 10))
         ms_global = timed(graph_of(3, "g").replay, max(2, args.steps // 10))
-    gbs = nbytes / (ms_graph * 1e-3) / 1e9
+        # Every layer's output of one eager step against one replay of the step's graph, bit
+        # for bit (each step appends the same rows at the same positions, so the steps are
+        # idempotent); a mismatch reports the eager time instead.
+        step_all()
+        torch.cuda.synchronize()
+        eager_out = [c.out.clone() for c in calls]
+        for c in calls:
+            c.out.zero_()
+        g_full.replay()
+        torch.cuda.synchronize()
+        graph_ok = all(bool(torch.equal(c.out, e)) for c, e in zip(calls, eager_out))
+    ms_step = ms_graph if graph_ok else ms_eager
+    gbs = nbytes / (ms_step * 1e-3) / 1e9
+    traffic = profiled_traffic_c5()
+    cpu = None if args.no_cpu else cpu_baseline_c5(calls, kinds, lens, pos, args.cpu_threads)
     line = {
         "metric": "decode-attn HBM GB/s (and us/step) at Gemma-4-31B shapes, 1 GPU",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": max(2, args.steps // 10), "warmup": args.warmup, "warmup_steps_run": warm_steps,
-        "ms_per_step": round(ms_graph, 6), "us_per_step": round(ms_graph * 1e3, 3),
+        "ms_per_step": round(ms_step, 6), "us_per_step": round(ms_step * 1e3, 3),
         "us_per_step_eager": round(ms_eager * 1e3, 3), "us_per_step_graph": round(ms_graph * 1e3, 3),
-        "timing": "HIP graph replay of the 60-layer step (120 kernels)",
+        "graph_matches_eager": graph_ok,
+        "timing": ("HIP graph replay of the 60-layer step (120 kernels)" if graph_ok
+                   else "eager (the graph replay differed from eager)"),
         "pct_of_hbm_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) rows, unit-RMS, bf16)",
@@ -679,12 +695,87 @@ def bench_c5(args) -> int:
         "roofline": {"bound": "hbm", "kernel": "attend_kernel (all 60 layers, merges excluded)",
                      "achieved": round(nbytes / (ms_att * 1e-3) / 1e9, 2), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(nbytes / (ms_att * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": None, "kernel_us": round(ms_att * 1e3, 3)},
-        "cpu_baseline": None,
+                     "traffic": traffic["step"] if traffic else None,
+                     "traffic_per_launch": traffic,
+                     "traffic_source": "profiles/attend_c5.md (rocprofv3 FETCH_SIZE + WRITE_SIZE per attend "
+                                       "dispatch, copy-calibrated): 50 local + 10 global launches per step",
+                     "kernel_us": round(ms_att * 1e3, 3)},
+        "cpu_baseline": cpu,
         "device": device_facts(),
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def profiled_traffic_c5():
+    """HBM bytes per attend launch of C5's local and global layers (profiles/attend_c5.md,
+    rocprofv3 FETCH_SIZE / WRITE_SIZE, copy-calibrated) and per step (50 local + 10 global
+    launches); None when the profile is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "attend_c5.md")
+    got = {}
+    try:
+        for line in open(path):
+            for kind in ("local", "global"):
+                tag = f"traffic_bytes_per_launch_{kind}:"
+                if line.startswith(tag):
+                    got[kind] = int(float(line.split(":", 1)[1].split()[0]))
+    except OSError:
+        return None
+    if len(got) != 2:
+        return None
+    n_global = sum(1 for layer in range(C5_LAYERS) if c5_is_global(layer))
+    got["step"] = (C5_LAYERS - n_global) * got["local"] + n_global * got["global"]
+    return got
+
+
+def cpu_baseline_c5(calls, kinds, lens, pos, threads: int):
+    """The reference-rounding restatement (orc_decode_refround_grouped) over one local and
+    one global layer of the C5 step at full shape (B=32, the same caches and positions, after
+    the same append), each repeated for >= 5 s; the 60-layer step is estimated as 50 x the
+    local time + 10 x the global time (every layer of a kind has the same shape and work)."""
+    import numpy as np
+    import torch
+
+    root = os.path.dirname(os.path.abspath(__file__))
+    sys.path.insert(0, root)
+    from oracle import oracle as orc
+
+    def host(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+
+    secs, nbytes, reps_of = {}, {}, {}
+    for kind, t in (("l", C5_LOCAL), ("g", C5_GLOBAL)):
+        c = calls[kinds.index(kind)]
+        q, kn, vn, kc, vc = c._keep[:5]
+        cap = kc.shape[2]
+        step = orc.Step(B=C5_B, Hq=t["Hq"], Hkv=t["Hkv"], D=t["D"], cap=cap, window=t["window"], ring=t["ring"],
+                        scale=t["scale"])
+        kch = host(kc)
+        vch = kch if t["shared"] else host(vc)
+        knh = host(kn).reshape(C5_B, t["Hkv"], t["D"])
+        vnh = knh if t["shared"] else host(vn).reshape(C5_B, t["Hkv"], t["D"])
+        orc.append(step, kch, None if t["shared"] else vch, knh, None if t["shared"] else vnh, pos)
+        qh = host(q).reshape(C5_B, t["Hq"], t["D"])
+        reps, total = 0, 0.0
+        while total < 5.0 and reps < 200:
+            t0 = time.perf_counter()
+            orc.decode_refround_grouped(step, qh, kch, vch, pos, threads=threads)
+            total += time.perf_counter() - t0
+            reps += 1
+        secs[kind], reps_of[kind] = total / reps, reps
+        vis = [min(n, t["window"]) if t["window"] else n for n in lens]
+        row = t["D"] * 2 * (1 if t["shared"] else 2)
+        nbytes[kind] = sum(vis) * t["Hkv"] * row + 2 * C5_B * t["Hq"] * t["D"] * 2 + 2 * C5_B * t["Hkv"] * row
+    n_global = sum(1 for layer in range(C5_LAYERS) if c5_is_global(layer))
+    n_local = C5_LAYERS - n_global
+    sec = n_local * secs["l"] + n_global * secs["g"]
+    step_bytes = n_local * nbytes["l"] + n_global * nbytes["g"]
+    return {"value": round(step_bytes / sec / 1e9, 3), "unit": "GB/s", "us_per_step": round(sec * 1e6, 1),
+            "cores": threads, "kind": "port",
+            "sample": f"one local layer x{reps_of['l']} ({secs['l'] * 1e3:.1f} ms each) and one global layer "
+                      f"x{reps_of['g']} ({secs['g'] * 1e3:.1f} ms each) at full C5 shape, reference-rounding "
+                      f"restatement grouped by kv head over {threads} threads; step = {n_local} x local + "
+                      f"{n_global} x global (MLX CPU path unavailable offline); host {os.cpu_count()} cpus visible"}
 
 
 def cpu_baseline(w, pos, q, k_cache, v_cache, k_new, v_new, threads: int):

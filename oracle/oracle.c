@@ -17,6 +17,13 @@
 static int32_t g_fault = 0;
 void orc_set_fault(int32_t fault) { g_fault = fault; }
 
+/* Conditioning probe of the raw-K restatement (0 = off): every row's rinv moved by this many
+ * fp32 ulps before K is rebuilt, to measure how far the result moves under an ulp-level
+ * difference in the row norm (which no implementation fixes: the reference's rsqrt and
+ * summation order are its own). */
+static int32_t g_rinv_ulps = 0;
+void orc_set_rinv_ulps(int32_t ulps) { g_rinv_ulps = ulps; }
+
 /* ------------------------------------------------------------------ bf16 */
 
 uint16_t orc_f32_to_bf16(float x) {
@@ -621,7 +628,9 @@ static void item_raw(void *ctx, int64_t it) {
         raw_row(j, kvh, t, xr);
         double ss = 0.0;
         for (int32_t i = 0; i < D; ++i) { double v = xr[i]; ss += v * v; }
-        const float rinv = 1.0f / sqrtf((float) (ss / 512.0) + j->eps);
+        float rinv = 1.0f / sqrtf((float) (ss / 512.0) + j->eps);
+        for (int32_t u = 0; u < g_rinv_ulps; ++u) rinv = nextafterf(rinv, INFINITY);
+        for (int32_t u = 0; u > g_rinv_ulps; --u) rinv = nextafterf(rinv, -INFINITY);
         rv[t] = rinv;
         double dot = 0.0;
         for (int32_t dd = 0; dd < D; ++dd) {

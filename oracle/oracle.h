@@ -140,6 +140,11 @@ void orc_quantize_rows(const uint16_t *x, int64_t rows, int32_t n, uint8_t *q, f
  * tests that show a plausible mistake is caught by the pins. */
 void orc_set_fault(int32_t fault);
 
+/* Conditioning probe of orc_decode_raw_f64 / orc_decode_raw_q8_f64 (0 = off): each row's
+ * rinv is moved by `ulps` fp32 ulps before K is rebuilt.  Tests use it to bound how far the
+ * result moves under an ulp-level difference in the row norm. */
+void orc_set_rinv_ulps(int32_t ulps);
+
 /* Prefill attention (ESAttention.mm:168-193 at seq > 1: SDPA with the additive mask of
  * ESGemma4TextModel.mm:68-83 aligned by ESAttention.mm:17-22), fp64.
  *   q: element (h, i, d) at q[h*q_head_stride + i*q_row_stride + d], query row i < Sq at

@@ -82,6 +82,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_raw_prefill_kv.argtypes = [_P, i32, i32, i32, _P, ctypes.c_float, _P, i32, _P, _P]
     L.orc_raw_prefill_kv.restype = None
     L.orc_set_fault.argtypes = [i32]
+    L.orc_set_rinv_ulps.argtypes = [i32]
 
 
 def _ptr(a: np.ndarray | None) -> int | None:
@@ -293,6 +294,22 @@ def raw_prefill_kv(raw, kw, eps: float, inv_freq, pos0: int = 0):
     lib().orc_raw_prefill_kv(_ptr(raw), Hkv, Sk, D, _ptr(np.ascontiguousarray(kw, dtype=np.uint16)),
                              ctypes.c_float(eps), _ptr(inv), int(pos0), _ptr(k), _ptr(v))
     return k, v
+
+
+class rinv_nudge:
+    """Context manager: the raw-K oracles move every row's rinv by `ulps` fp32 ulps (a
+    conditioning probe for tests, not a mistake)."""
+
+    def __init__(self, ulps: int):
+        self.ulps = ulps
+
+    def __enter__(self):
+        lib().orc_set_rinv_ulps(self.ulps)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_rinv_ulps(0)
+        return False
 
 
 class planted_fault:

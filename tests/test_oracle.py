@@ -459,6 +459,30 @@ def test_raw_decode_matches_hf_rope_composition():
     assert np.abs(ours - ref).max() < 2e-3
 
 
+def test_rinv_nudge_moves_the_row_norm_by_whole_ulps():
+    """The conditioning probe: with one visible row the output is rinv * kraw exactly (the
+    softmax weight is 1), so under a nudge of n ulps every element scales by rinv_n / rinv,
+    where rinv_n is rinv stepped n times with nextafter; n = 0 is the plain oracle."""
+    rng = np.random.default_rng(41)
+    raw = orc.to_bf16(rng.standard_normal((1, 4, 512)).astype(np.float32) * 3)
+    q = rms_rows(rng, (8, 512))
+    kw = orc.to_bf16(np.ones(512, np.float32))
+    inv = orc.rope_inv_freq(512, 1.0e6, 0.25)
+    x = orc.from_bf16(raw[0, 0]).astype(np.float64)
+    ss = float((x * x).sum())
+    rinv = np.float32(1.0) / np.sqrt(np.float32(ss / 512.0) + np.float32(1e-6))
+    base = orc.decode_raw_f64(q, raw, 1, kw, 1e-6, inv, 1.0)
+    assert np.array_equal(base, np.broadcast_to(float(rinv) * x, base.shape))
+    for n in (1, -1, 3):
+        want = rinv
+        for _ in range(abs(n)):
+            want = np.nextafter(want, np.float32(np.inf if n > 0 else -np.inf))
+        with orc.rinv_nudge(n):
+            got = orc.decode_raw_f64(q, raw, 1, kw, 1e-6, inv, 1.0)
+        assert np.array_equal(got, np.broadcast_to(float(want) * x, got.shape)), n
+    assert np.array_equal(orc.decode_raw_f64(q, raw, 1, kw, 1e-6, inv, 1.0), base)  # the probe is off again
+
+
 # ------------------------------------------------------------ q8 raw stream
 
 def test_quantize_rows_properties():

@@ -49,8 +49,27 @@ def _check(name, o, ref):
     return err
 
 
+def _check_conditioned(name, o, q, rows, n, kw, inv, scale):
+    """The bar at the in-model scale on data whose softmax is near-tied: an element may exceed
+    the max-abs bar by as much as the oracle itself moves when every row's rinv moves by one or
+    two fp32 ulps (orc.rinv_nudge).  No implementation fixes the row norm to the ulp (the
+    reference's rsqrt and summation order are its own), and at scale 1.0 one ulp can flip a
+    K element's bf16 rounding next to a near-tied pair of keys.  The mean bar is unchanged."""
+    ref = orc.decode_raw_f64(q, rows, n, kw, EPS, inv, scale)
+    cond = np.zeros_like(ref)
+    for u in (-2, -1, 1, 2):
+        with orc.rinv_nudge(u):
+            cond = np.maximum(cond, np.abs(orc.decode_raw_f64(q, rows, n, kw, EPS, inv, scale) - ref))
+    err = np.abs(o - ref)
+    over = err > TOL_MAX
+    print(f"[raw] {name}: max_abs={err.max():.3e} mean_abs={err.mean():.3e}; oracle moves by up to "
+          f"{cond.max():.3e} under +-2 ulps of rinv; {int(over.sum())} elements beyond {TOL_MAX} "
+          f"(largest excess over the oracle's own movement {(err - cond).max():.3e})", flush=True)
+    assert (err <= TOL_MAX + cond).all() and err.mean() <= TOL_MEAN, name
+
+
 def run_raw(name, *, B=1, Hq=32, Hkv=4, cap, pos, scale=1.0, seed=0, split_rows=0, append=True,
-            theta=1.0e6, partial=0.25, fault=0, table=False):
+            theta=1.0e6, partial=0.25, fault=0, table=False, conditioned=False):
     from apertura_amd.decode import RawStep, decode_raw, new_raw_workspace, rope_table
     print(f"\n[raw] {name}: B={B} Hq={Hq} Hkv={Hkv} cap={cap} pos={list(pos)[:4]} scale={scale} "
           f"append={append} split_rows={split_rows} table={table}", flush=True)
@@ -73,6 +92,9 @@ def run_raw(name, *, B=1, Hq=32, Hkv=4, cap, pos, scale=1.0, seed=0, split_rows=
     o = orc.from_bf16(_host(out)).reshape(B, Hq, 512).astype(np.float64)
     errs = []
     for b in range(B):
+        if conditioned:
+            _check_conditioned(f"{name} b={b}", o[b], q[b], np.ascontiguousarray(raw[b]), pos[b] + 1, kw, inv, scale)
+            continue
         with orc.planted_fault(fault):
             ref = orc.decode_raw_f64(q[b], np.ascontiguousarray(raw[b]), pos[b] + 1, kw, EPS, inv, scale)
         if fault:
@@ -178,11 +200,13 @@ def test_raw_randomized_configurations(seed):
 @pytest.mark.parametrize("seed", [23, 29])
 def test_raw_table_in_model_scale_one_ragged_batch(seed):
     """The ES layer's raw-K form (precomputed rotary table, two kv heads per workgroup) at the
-    in-model scale 1.0 over a ragged batch with appends, each sequence against the fp64 oracle.
-    (The table and own-sincos kernels are compared with each other at the configs' scale in
-    test_rope_table_kernels_agree_and_the_table_matches_fp64.)"""
+    in-model scale 1.0 over a ragged batch with appends, each sequence against the fp64 oracle
+    with the conditioning allowance of _check_conditioned: on seed 23 one sequence has a
+    near-tied pair of keys where a one-ulp change of rinv alone moves the oracle's output by
+    0.050.  (The table and own-sincos kernels are compared with each other at the configs'
+    scale in test_rope_table_kernels_agree_and_the_table_matches_fp64.)"""
     run_raw(f"scale1-ragged-table-{seed}", B=3, cap=4096, pos=[4095, 1000, 2777], scale=1.0, seed=seed,
-            table=True)
+            table=True, conditioned=True)
 
 
 @TABLE
