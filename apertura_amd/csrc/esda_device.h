@@ -113,6 +113,32 @@ __device__ __forceinline__ void lds_dma16_s(const void *sbase, unsigned voff, un
 #endif
 }
 
+// A wave-uniform 64-bit address as a scalar pair (the base operand of lds_dma16_o).
+__device__ __forceinline__ uint64_t sbase64(const void *p) {
+    const uintptr_t a = (uintptr_t) p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned) a);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned) (a >> 32));
+    return ((uint64_t) hi << 32) | lo;
+}
+
+// The DMA of lds_dma16_s with the instruction's immediate offset OFF (0 .. 3072 here),
+// which gfx950 adds to both addresses: lane l's 16 bytes come from sbase + voff + OFF and
+// land at LDS byte m0 + OFF + 16 l.  M0 is set to lds + MOFF by one scalar add, so rows
+// that are OFF apart in memory but spaced otherwise in LDS (padded blocks) share one
+// scalar base: a row costs one scalar instruction beside its DMA.
+template <int OFF, int MOFF, bool NT = true>
+__device__ __forceinline__ void lds_dma16_o(uint64_t sbase, unsigned voff, unsigned lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    static_assert(OFF >= 0 && OFF < 4096, "the immediate offset is a 12-bit field here");
+    if constexpr (NT)
+        asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dwordx4 %0, %1 offset:%4 nt"
+                     ::"v"(voff), "s"(sbase), "s"(lds), "i"(MOFF), "i"(OFF) : "memory");
+    else
+        asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dwordx4 %0, %1 offset:%4"
+                     ::"v"(voff), "s"(sbase), "s"(lds), "i"(MOFF), "i"(OFF) : "memory");
+#endif
+}
+
 // One 4-byte LDS DMA per active lane (global_load_lds_dword): active lane l's 4 bytes land
 // at LDS byte address lds + 4*l.  Counted by the ring like lds_dma16.
 __device__ __forceinline__ void lds_dma4(const void *src, unsigned lds) {
