@@ -8,9 +8,10 @@ Gemma-4's global (D=512, 8 query heads per kv head) and local (D=256, 2 per kv h
 sliding window with evicted keys) layers, fresh causal prefill and chunks after a cached
 past, tiles padded past the last query, key splits (automatic, forced, empty), strided
 query / cache / output layouts, a shared K = V buffer, and both query-block
-configurations of head dim 256 (one and two 16-query blocks per wave).  At the
-benchmark shapes (512 queries over 16384 keys; 4096 fresh tokens of a sliding layer)
-sampled query rows are checked (query rows are independent).  The raw-K reconstruction is compared with the oracle's op-level
+configurations of head dim 256 (one and two 16-query blocks per wave).  At the local
+benchmark shapes (4096 fresh tokens of a sliding layer; 512 queries over window + chunk) every
+row is checked; at 512 queries over 16384 global keys 25 sampled query rows (query rows are
+independent).  The raw-K reconstruction is compared with the oracle's op-level
 restatement element by element (at most two bf16 steps apart, on a tiny fraction).
 """
 import numpy as np
@@ -105,19 +106,19 @@ def test_local_two_query_blocks_per_wave_with_padded_tile():
     run_prefill("local-qb2", Hq=128, Hkv=128, D=256, Sq=257, Sk=257, q_pos0=0, k_pos0=0, window=64, seed=12)
 
 
-def test_local_fresh_prefill_benchmark_shape_sampled_rows():
-    """4096 fresh tokens of a sliding layer (window 1024, GQA 32/16): two query blocks
-    per wave, no key splits; rows on tile edges and around the window's reach."""
-    run_prefill("bench-local", Hq=32, Hkv=16, D=256, Sq=4096, Sk=4096, q_pos0=0, k_pos0=0, window=1024, seed=13,
-                rows=[0, 1, 127, 128, 1023, 1024, 1025, 2047, 4095])
+def test_local_fresh_prefill_benchmark_shape_all_rows():
+    """4096 fresh tokens of a sliding layer (window 1024, GQA 32/16; the p4kl benchmark
+    shape): two query blocks per wave, no key splits; every query row of every head against
+    the fp64 oracle (~10 s of host time)."""
+    run_prefill("bench-local", Hq=32, Hkv=16, D=256, Sq=4096, Sk=4096, q_pos0=0, k_pos0=0, window=1024, seed=13)
 
 
-def test_local_chunk_benchmark_shape_stage_halves_sampled_rows():
-    """512 queries of a sliding layer over window + chunk = 1536 keys (GQA 32/16): 128-row
-    tiles would cover only 128 CUs, so the plan runs 64-row tiles whose even and odd stages
-    go to the two wave groups, with no key splits; rows on tile edges and at both ends."""
+def test_local_chunk_benchmark_shape_stage_halves_all_rows():
+    """512 queries of a sliding layer over window + chunk = 1536 keys (GQA 32/16; the p512l
+    benchmark shape): 128-row tiles would cover only 128 CUs, so the plan runs 64-row tiles
+    whose even and odd stages go to the two wave groups, with no key splits; every row."""
     run_prefill("bench-local-chunk", Hq=32, Hkv=16, D=256, Sq=512, Sk=1536, q_pos0=15872, k_pos0=14848,
-                window=1024, seed=14, rows=[0, 1, 31, 32, 63, 64, 255, 511])
+                window=1024, seed=14)
 
 
 def test_local_one_block_per_wave_without_stage_halves():
@@ -158,9 +159,19 @@ def test_single_query_and_single_key():
 
 
 def test_chunked_prefill_benchmark_shape_sampled_rows():
-    """512 queries over a 16384-key global cache (the chunked-prefill benchmark shape)."""
+    """512 queries over a 16384-key global cache (the p512g benchmark shape, two key splits):
+    25 query rows (all heads) on the 16-position tile edges, in the middle and at both ends; a
+    full check would take ~1 min of fp64 host time (541 GFLOP)."""
     run_prefill("bench-global", Hq=32, Hkv=4, D=512, Sq=512, Sk=16384, q_pos0=15872, k_pos0=0, seed=10,
-                rows=[0, 1, 200, 511])
+                rows=[0, 1, 15, 16, 17, 31, 32, 100, 127, 128, 200, 255, 256, 300, 383, 384, 400, 447, 448,
+                      480, 495, 496, 500, 510, 511])
+
+
+def test_global_fresh_prefill_benchmark_shape_sampled_rows():
+    """4096 fresh tokens of a global layer (causal, D=512, GQA 32/4; the p4kg benchmark
+    shape): 16 query rows (all heads) on tile edges, in the middle and at both ends."""
+    run_prefill("bench-global-fresh", Hq=32, Hkv=4, D=512, Sq=4096, Sk=4096, q_pos0=0, k_pos0=0, seed=17,
+                rows=[0, 1, 15, 16, 17, 127, 128, 1000, 2047, 2048, 2049, 3000, 4079, 4080, 4094, 4095])
 
 
 @pytest.mark.parametrize("seed", range(14))
