@@ -281,3 +281,30 @@ def test_es_decode_attn_global_matches_oracle():
     assert np.array_equal(_host(raw_d), raw[0])
     ref = orc.decode_raw_f64(q[0], np.ascontiguousarray(raw[0]), length, kw, EPS, inv, 1.0)
     _check("esDecodeAttnGlobal", orc.from_bf16(_host(out)).reshape(8 * Hkv, 512).astype(np.float64), ref)
+
+
+def test_es_decode_attn_global_over_more_streams_than_scratch_sets():
+    """esDecodeAttnGlobal keeps one scratch set per (thread, device, stream), at most eight per
+    thread: twelve streams used in turn, twice, release the least recently used sets and
+    rebuild them. Every call's output equals the first call's, bit for bit (the same inputs and
+    plan), and the last round still matches the oracle (the in-model scale 1.0: the bar of
+    _check_conditioned)."""
+    from apertura_amd.cache import es_decode_attn_global
+    rng = np.random.default_rng(25)
+    Hkv, pitch, length = 4, 1536, 1200
+    q, raw, _, kw = _raw_inputs(rng, 1, 8 * Hkv, Hkv, pitch)
+    inv = list(orc.rope_inv_freq(512, 1.0e6, 0.25))
+    qd, raw_d, kw_d = _dev(q[0]), _dev(raw[0]), _dev(kw)
+    streams = [torch.cuda.Stream() for _ in range(12)]
+    outs = []
+    print("\n[raw] esDecodeAttnGlobal over 12 streams, two rounds", flush=True)
+    for _ in range(2):
+        for st in streams:
+            with torch.cuda.stream(st):
+                outs.append(es_decode_attn_global(qd, raw_d, length, pitch, kw_d, EPS, inv, stream=st))
+            st.synchronize()
+    torch.cuda.synchronize()
+    first = _host(outs[0])
+    assert all(np.array_equal(_host(o), first) for o in outs[1:])
+    _check_conditioned("12 streams", orc.from_bf16(_host(outs[-1])).reshape(8 * Hkv, 512).astype(np.float64), q[0],
+                       np.ascontiguousarray(raw[0]), length, kw, np.asarray(inv, np.float32), 1.0)
