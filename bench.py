@@ -820,8 +820,8 @@ def cpu_baseline(w, pos, q, k_cache, v_cache, k_new, v_new, threads: int):
 
 def cpu_baseline_raw(w, pos, q, k_cache, kw, inv_freq, threads: int):
     """CPU oracle of the raw-K step (orc_decode_raw_f64: the reconstruction of
-    ESDecodeAttn.mm:17-117 in fp64) on a bounded sample: the first `rows` cached rows of
-    every kv head, repeated for >= 10 s; throughput in the step's bytes per row."""
+    ESDecodeAttn.mm:17-117 in fp64, query heads over the threads) over the full step's rows,
+    repeated for >= 10 s; throughput in the step's algorithmic bytes."""
     import numpy as np
     import torch
 
@@ -833,9 +833,9 @@ def cpu_baseline_raw(w, pos, q, k_cache, kw, inv_freq, threads: int):
         return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
     B, Hq, Hkv, D = w["B"], w["Hq"], w["Hkv"], w["D"]
-    rows = 16384
+    rows = visible_rows(w, pos)[0]
     qh = host(q).reshape(B, Hq, D)[0]
-    raw = np.ascontiguousarray(host(k_cache).reshape(B, Hkv, -1, D)[0, :, :rows])
+    raw = np.ascontiguousarray(host(k_cache).reshape(B, Hkv, -1, D)[0])  # the appended row is in place
     kwh = host(kw).reshape(-1)
     inv = inv_freq.detach().cpu().numpy()
     reps, t_total = 0, 0.0
@@ -845,17 +845,17 @@ def cpu_baseline_raw(w, pos, q, k_cache, kw, inv_freq, threads: int):
         t_total += time.perf_counter() - t0
         reps += 1
     sec = t_total / reps
-    nbytes = rows * Hkv * D * 2
-    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "us_per_step": None,
+    nbytes = algorithmic_bytes(w, pos)
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "us_per_step": round(sec * 1e6, 1),
             "cores": threads, "kind": "port",
-            "sample": f"{rows} of {visible_rows(w, pos)[0]} rows per kv head x{reps} repeats "
-                      f"({t_total:.1f} s), fp64 raw-K oracle (MLX CPU path unavailable offline); "
+            "sample": f"full step ({rows} rows per kv head) x{reps} repeats ({t_total:.1f} s), fp64 raw-K "
+                      f"oracle, query heads over {threads} threads (MLX CPU path unavailable offline); "
                       f"host {os.cpu_count()} cpus visible"}
 
 
 def cpu_baseline_q8(w, pos, q, raw, threads: int):
-    """CPU oracle of the q8 raw-K step (orc_decode_raw_q8_f64) on a bounded sample, as
-    cpu_baseline_raw; throughput in the q8 stream's bytes per row (520)."""
+    """CPU oracle of the q8 raw-K step (orc_decode_raw_q8_f64) over the full step's rows, as
+    cpu_baseline_raw; throughput in the step's algorithmic bytes (520 per row)."""
     import numpy as np
     import torch
 
@@ -865,11 +865,11 @@ def cpu_baseline_q8(w, pos, q, raw, threads: int):
 
     kw, inv_freq, q8, sc, bs = raw
     B, Hq, Hkv, D = w["B"], w["Hq"], w["Hkv"], w["D"]
-    rows = 16384
+    rows = visible_rows(w, pos)[0]
     qh = q.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16).reshape(B, Hq, D)[0]
-    q8h = np.ascontiguousarray(q8[0, :, :rows].cpu().numpy())
-    sch = np.ascontiguousarray(sc[0, :, :rows].cpu().numpy())
-    bsh = np.ascontiguousarray(bs[0, :, :rows].cpu().numpy())
+    q8h = np.ascontiguousarray(q8[0].cpu().numpy())  # the appended row is quantized in place
+    sch = np.ascontiguousarray(sc[0].cpu().numpy())
+    bsh = np.ascontiguousarray(bs[0].cpu().numpy())
     kwh = kw.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1)
     inv = inv_freq.detach().cpu().numpy()
     reps, t_total = 0, 0.0
@@ -879,11 +879,11 @@ def cpu_baseline_q8(w, pos, q, raw, threads: int):
         t_total += time.perf_counter() - t0
         reps += 1
     sec = t_total / reps
-    nbytes = rows * Hkv * Q8_ROW_BYTES
-    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "us_per_step": None,
+    nbytes = algorithmic_bytes(w, pos)
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "us_per_step": round(sec * 1e6, 1),
             "cores": threads, "kind": "port",
-            "sample": f"{rows} of {visible_rows(w, pos)[0]} rows per kv head x{reps} repeats "
-                      f"({t_total:.1f} s), fp64 q8 raw-K oracle (MLX CPU path unavailable offline); "
+            "sample": f"full step ({rows} rows per kv head) x{reps} repeats ({t_total:.1f} s), fp64 q8 "
+                      f"raw-K oracle, query heads over {threads} threads (MLX CPU path unavailable offline); "
                       f"host {os.cpu_count()} cpus visible"}
 
 
