@@ -1345,15 +1345,26 @@ void raw_attend_kernel(AttendParams p) {
             // wave's V tile for the transpose reads, with a product against ones for the row
             // sums.
             u32x4 w8[Q8 ? 8 : 1];  // q8: the stage's u8 row pieces (16 dims each)
+            float rq = 0.0f, fq = 0.0f;  // q8: scale * rinv and bias * rinv of row li
             {
-                f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f}, g1 = {0.0f, 0.0f, 0.0f, 0.0f};
                 if constexpr (Q8) {
-                    bf16x8 ones;
+                    // All eight u8 reads go out before the first V-tile write: LDS accesses
+                    // complete in order, so a read issued after a write would wait for it.
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) ones[e] = (__bf16) 1.0f;
+                    for (int mm = 0; mm < 8; ++mm)
+                        w8[mm] = *reinterpret_cast<const u32x4 *>(sl + (li >> 1) * kBlk + 32 * (4 * mm + lg) + 16 * (li & 1));
+                    const float scl = reinterpret_cast<const float *>(sl + W::ROWS)[li];
+                    const float bias = reinterpret_cast<const float *>(sl + W::ROWS)[16 + li];
+                    __builtin_amdgcn_sched_barrier(0);
+                    // sum(q^2) and sum(q) of the lane's quarter of row li, exact in integers
+                    unsigned s2 = 0u, s1 = 0u;
 #pragma unroll
                     for (int mm = 0; mm < 8; ++mm) {
-                        w8[mm] = *reinterpret_cast<const u32x4 *>(sl + (li >> 1) * kBlk + 32 * (4 * mm + lg) + 16 * (li & 1));
+#pragma unroll
+                        for (int w = 0; w < 4; ++w) {
+                            s2 = __builtin_amdgcn_udot4(w8[mm][w], w8[mm][w], s2, false);
+                            s1 = __builtin_amdgcn_udot4(w8[mm][w], 0x01010101u, s1, false);
+                        }
 #pragma unroll
                         for (int h = 0; h < 2; ++h) {
                             unsigned o[4];
@@ -1365,41 +1376,39 @@ void raw_attend_kernel(AttendParams p) {
                                 o[e] = __builtin_amdgcn_perm(__builtin_bit_cast(unsigned, f1), __builtin_bit_cast(unsigned, f0),
                                                              0x07060302u);
                             }
-                            const u32x4 ab = u32x4{o[0], o[1], o[2], o[3]};
-                            *reinterpret_cast<u32x4 *>(wl + 2 * W::SLOT + li * kBlk + 2 * wdim(2 * mm + h, lg)) = ab;
-                            const bf16x8 x = __builtin_bit_cast(bf16x8, ab);
-                            g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
-                            g1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, ones, g1, 0, 0, 0);
+                            *reinterpret_cast<u32x4 *>(wl + 2 * W::SLOT + li * kBlk + 2 * wdim(2 * mm + h, lg)) =
+                                u32x4{o[0], o[1], o[2], o[3]};
                         }
                         if (mm & 1) __builtin_amdgcn_sched_barrier(0);
                     }
+                    // whole-row sums in every lane of row li's column (lanes li + 16 lg)
+                    s2 = wave_sum_across_groups(s2);
+                    s1 = wave_sum_across_groups(s1);
+                    // mean(x^2) = scale^2 var(q) + mean(x)^2 with 512^2 var(q) = 512 sum(q^2) - sum(q)^2,
+                    // formed exactly in fp64 (below 2^35) and rounded once
+                    const float var = (float) (512.0 * (double) s2 - (double) s1 * (double) s1);
+                    const float mean = __builtin_fmaf(scl, (float) s1 * (1.0f / kRawDim), bias);
+                    const float ms = scl * scl * var * (1.0f / (kRawDim * kRawDim)) + __builtin_fmaf(mean, mean, p.eps);
+                    const float rinv = __builtin_amdgcn_rsqf(ms);
+                    rq = scl * rinv;
+                    fq = bias * rinv;
+                    if (lg == 0) {
+                        xfw[0 * 16 + li] = rq;
+                        xfw[1 * 16 + li] = __builtin_amdgcn_rcpf(rq);
+                        xfw[2 * 16 + li] = bias * __builtin_amdgcn_rcpf(scl);
+                    }
                 } else {
+                    f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int kk = 0; kk < 16; ++kk) {
                         const bf16x8 x = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg)));
                         g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
                     }
-                }
-                // Row factors (C layout: lane (li, lg) holds C[4lg + i][li]; row li's diagonal
-                // is register li - 4lg of the lanes with lg == li / 4, which publish them).
-                const int i = li - 4 * lg;
-                if (i >= 0 && i < 4) {
-                    const float s2 = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
-                    if constexpr (Q8) {
-                        const float s1 = i == 0 ? g1[0] : i == 1 ? g1[1] : i == 2 ? g1[2] : g1[3];
-                        const float scl = reinterpret_cast<const float *>(sl + W::ROWS)[li];
-                        const float bias = reinterpret_cast<const float *>(sl + W::ROWS)[16 + li];
-                        // mean(x^2) = scale^2 var(q) + mean(x)^2 with 512^2 var(q) = 512 sum(q^2) - sum(q)^2
-                        const float var = fmaxf(__builtin_fmaf(512.0f, s2, -s1 * s1), 0.0f);
-                        const float mean = __builtin_fmaf(scl, s1 * (1.0f / kRawDim), bias);
-                        const float ms = scl * scl * var * (1.0f / (kRawDim * kRawDim)) + __builtin_fmaf(mean, mean, p.eps);
-                        const float rinv = __builtin_amdgcn_rsqf(ms);
-                        const float alpha = scl * rinv;
-                        xfw[0 * 16 + li] = alpha;
-                        xfw[1 * 16 + li] = 1.0f / alpha;
-                        xfw[2 * 16 + li] = bias / scl;
-                        xfw[3 * 16 + li] = bias * rinv;
-                    } else {
+                    // Row factors (C layout: lane (li, lg) holds C[4lg + i][li]; row li's diagonal
+                    // is register li - 4lg of the lanes with lg == li / 4, which publish them).
+                    const int i = li - 4 * lg;
+                    if (i >= 0 && i < 4) {
+                        const float s2 = i == 0 ? g[0] : i == 1 ? g[1] : i == 2 ? g[2] : g[3];
                         const float ms = s2 * (1.0f / kRawDim) + p.eps;
                         const float rinv = __builtin_amdgcn_rsqf(ms);
                         xfw[0 * 16 + li] = rinv;
@@ -1419,12 +1428,12 @@ void raw_attend_kernel(AttendParams p) {
             asm volatile("" ::: "memory");
             u32x4 tab[4];
             load_tab(tab);
-            const float rk = xfw[0 * 16 + li];  // rinv of row li (q8: scale * rinv)
+            const float rk = Q8 ? rq : xfw[0 * 16 + li];  // rinv of row li (q8: scale * rinv)
             // Pass 2: x * rinv * kw of k-step kk, dims wdim(kk, lg) .. + 7 of row li.
             auto xkw = [&](int kk, float (&v)[8]) {
                 if constexpr (Q8) {
                     // fma(q, scale * rinv, bias * rinv) * kw, per element
-                    const float fb = xfw[3 * 16 + li];
+                    const float fb = fq;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const float q = (float) ((w8[kk >> 1][2 * (kk & 1) + (e >> 2)] >> (8 * (e & 3))) & 255u);

@@ -43,6 +43,21 @@ __device__ __forceinline__ float wave_max_across_groups(float x) {
 #endif
 }
 
+// Sum over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48), by the same
+// swaps; integer adds, so the sum is exact and the same in all four lanes.
+__device__ __forceinline__ unsigned wave_sum_across_groups(unsigned x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    unsigned a = x, b = x;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    a += b;
+    b = a;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return a + b;
+#else
+    return x;
+#endif
+}
+
 // The running max is only raised (and O rescaled) once a score exceeds it by this
 // much in log2 units; until then probabilities may reach 2^8 before normalisation,
 // far from fp32 / bf16 limits, and the final division by l is unchanged.
