@@ -1059,8 +1059,9 @@ void attend_kernel(AttendParams p) {
 //     heads] with 32 MFMAs over V = kraw read back by transpose reads, rinv folded into the
 //     weight: P = bf16(e * rinv), l += P / rinv.
 // Q8 (esDecodeAttnGlobalQ8, ESDecodeAttn.mm:275-369): rows are u8 with a per-row scale and
-// bias (x = q * scale + bias).  The A operand is q itself in bf16 (exact); the Gram diagonal
-// and a product with ones give sum(q^2) and sum(q), hence mean(x^2);
+// bias (x = q * scale + bias).  sum(q^2) and sum(q) of each row are exact integer dot products
+// of the u8 bytes (v_dot4_u32_u8, summed over the four lane groups), hence mean(x^2), and every
+// lane computes its own row's factors;
 // K = bf16(rope(fma(q, scale * rinv, bias * rinv) * kw)); q is also written to a bf16 tile
 // of the wave's that the transpose reads use as V, with P = bf16(e * scale * rinv) and the
 // bias entering as sum(P * bias / scale) per head.
