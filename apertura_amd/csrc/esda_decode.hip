@@ -1341,10 +1341,8 @@ void raw_attend_kernel(AttendParams p) {
                     hi[e] = x1 * c + x0 * s;
                 }
             };
-            // Pass 1: the row norms from Gram products of the operands.  Raw: the rows as
-            // stored.  q8: each 16-dim u8 piece widened to bf16 (exact) and stored in the
-            // wave's V tile for the transpose reads, with a product against ones for the row
-            // sums.
+            // Pass 1: the row norms.  Raw: from Gram products of the rows as stored.  q8: from
+            // integer sums of the u8 bytes (the rebuild below widens them to bf16 for the V tile).
             u32x4 w8[Q8 ? 8 : 1];  // q8: the stage's u8 row pieces (16 dims each)
             float rq = 0.0f, fq = 0.0f;  // q8: scale * rinv and bias * rinv of row li
             {
@@ -1360,28 +1358,12 @@ void raw_attend_kernel(AttendParams p) {
                     // sum(q^2) and sum(q) of the lane's quarter of row li, exact in integers
                     unsigned s2 = 0u, s1 = 0u;
 #pragma unroll
-                    for (int mm = 0; mm < 8; ++mm) {
+                    for (int mm = 0; mm < 8; ++mm)
 #pragma unroll
                         for (int w = 0; w < 4; ++w) {
                             s2 = __builtin_amdgcn_udot4(w8[mm][w], w8[mm][w], s2, false);
                             s1 = __builtin_amdgcn_udot4(w8[mm][w], 0x01010101u, s1, false);
                         }
-#pragma unroll
-                        for (int h = 0; h < 2; ++h) {
-                            unsigned o[4];
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const unsigned word = w8[mm][2 * h + e / 2];
-                                const float f0 = (float) ((word >> (16 * (e & 1))) & 255u);
-                                const float f1 = (float) ((word >> (16 * (e & 1) + 8)) & 255u);
-                                o[e] = __builtin_amdgcn_perm(__builtin_bit_cast(unsigned, f1), __builtin_bit_cast(unsigned, f0),
-                                                             0x07060302u);
-                            }
-                            *reinterpret_cast<u32x4 *>(wl + 2 * W::SLOT + li * kBlk + 2 * wdim(2 * mm + h, lg)) =
-                                u32x4{o[0], o[1], o[2], o[3]};
-                        }
-                        if (mm & 1) __builtin_amdgcn_sched_barrier(0);
-                    }
                     // whole-row sums in every lane of row li's column (lanes li + 16 lg)
                     s2 = wave_sum_across_groups(s2);
                     s1 = wave_sum_across_groups(s1);
@@ -1433,13 +1415,19 @@ void raw_attend_kernel(AttendParams p) {
             // Pass 2: x * rinv * kw of k-step kk, dims wdim(kk, lg) .. + 7 of row li.
             auto xkw = [&](int kk, float (&v)[8]) {
                 if constexpr (Q8) {
-                    // fma(q, scale * rinv, bias * rinv) * kw, per element
-                    const float fb = fq;
+                    // fma(q, scale * rinv, bias * rinv) * kw, per element; the same floats of q,
+                    // packed to bf16 (exact), are the k-step's part of the V tile
+                    float q[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float q = (float) ((w8[kk >> 1][2 * (kk & 1) + (e >> 2)] >> (8 * (e & 3))) & 255u);
-                        v[e] = __builtin_fmaf(q, rk, fb) * kwl[wdim(kk, lg) + e];
-                    }
+                    for (int e = 0; e < 8; ++e) q[e] = (float) ((w8[kk >> 1][2 * (kk & 1) + (e >> 2)] >> (8 * (e & 3))) & 255u);
+                    unsigned o[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        o[e] = __builtin_amdgcn_perm(__builtin_bit_cast(unsigned, q[2 * e + 1]), __builtin_bit_cast(unsigned, q[2 * e]),
+                                                     0x07060302u);
+                    *reinterpret_cast<u32x4 *>(wl + 2 * W::SLOT + li * kBlk + 2 * wdim(kk, lg)) = u32x4{o[0], o[1], o[2], o[3]};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(q[e], rk, fq) * kwl[wdim(kk, lg) + e];
                 } else {
                     // x * kw exactly (a product of two bf16 values fits fp32) by MFMAs against
                     // the diagonal kw operands, then times rinv
