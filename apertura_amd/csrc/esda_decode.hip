@@ -1344,6 +1344,7 @@ void raw_attend_kernel(AttendParams p) {
             // Pass 1: the row norms.  Raw: from Gram products of the rows as stored.  q8: from
             // integer sums of the u8 bytes (the rebuild below widens them to bf16 for the V tile).
             u32x4 w8[Q8 ? 8 : 1];  // q8: the stage's u8 row pieces (16 dims each)
+            u32x4 xr[Q8 ? 1 : 16];  // raw: the lane's row pieces, k-step kk (pass 1, kept for the rebuild)
             float rq = 0.0f, fq = 0.0f;  // q8: scale * rinv and bias * rinv of row li
             {
                 if constexpr (Q8) {
@@ -1384,7 +1385,8 @@ void raw_attend_kernel(AttendParams p) {
                     f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int kk = 0; kk < 16; ++kk) {
-                        const bf16x8 x = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg)));
+                        xr[kk] = *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg));
+                        const bf16x8 x = __builtin_bit_cast(bf16x8, xr[kk]);
                         g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
                     }
                     // Row factors (C layout: lane (li, lg) holds C[4lg + i][li]; row li's diagonal
@@ -1431,7 +1433,7 @@ void raw_attend_kernel(AttendParams p) {
                 } else {
                     // x * kw exactly (a product of two bf16 values fits fp32) by MFMAs against
                     // the diagonal kw operands, then times rinv
-                    const u32x4 t = *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg));
+                    const u32x4 t = xr[kk];
                     const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
                     const f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
                         dg[kk][0], __builtin_bit_cast(short4v, uint2{t[0], t[1]}), z, 0, 0, 0);
