@@ -59,12 +59,14 @@ def test_quantize_raw_rows_matches_the_oracle_bit_for_bit():
 
 
 def run_q8(name, *, B=1, Hq=32, Hkv=4, cap, pos, scale=1.0, seed=0, split_rows=0, append=True,
-           partial=0.25, fault=0, table=False):
+           partial=0.25, fault=0, table=False, rows_fn=None):
     from apertura_amd.decode import decode_raw_q8, new_raw_workspace, q8_step_for, rope_table
     print(f"\n[q8] {name}: B={B} Hq={Hq} Hkv={Hkv} cap={cap} pos={list(pos)[:4]} scale={scale} "
           f"append={append} split_rows={split_rows} table={table}", flush=True)
     rng = np.random.default_rng(seed)
     raw = _raw_rows(rng, (B, Hkv, cap, 512))
+    if rows_fn is not None:
+        raw = orc.to_bf16(rows_fn(orc.from_bf16(raw).astype(np.float32), rng))
     qc, sc, bs = orc.quantize_rows(raw)
     q = orc.to_bf16(rng.standard_normal((B, Hq, 512), dtype=np.float32))
     q = orc.rms_norm_rows(q, None, 1e-6)
@@ -138,6 +140,25 @@ def test_q8_split_sizes(split_rows, table):
 
 def test_q8_unpacked_odd_kv_heads():
     run_q8("unpacked-hkv3", B=2, Hq=24, Hkv=3, cap=1024, pos=[1000, 333], scale=512 ** -0.5, seed=19)
+
+
+def _degenerate_rows(x, rng):
+    """Cached rows the quantizer handles at its edges: constant rows (every code 0, the scale
+    clamped to 1e-8), rows of a large offset with a tiny spread (bias >> range: mean(x^2)
+    dominated by the mean), and rows that are zero but for one spike."""
+    x[..., ::7, :] = 0.5
+    x[..., 3::11, :] = 64.0 + rng.standard_normal(x[..., 3::11, :].shape).astype(np.float32)
+    x[..., 5::13, :] = 0.0
+    x[..., 5::13, 17] = 8.0
+    return x
+
+
+@TABLE
+def test_q8_degenerate_rows(table):
+    """Row sums, variance and row factors on the quantizer's edge cases: the exact integer
+    sums give var(q) = 0 for the constant rows and the large-offset rows keep their
+    normalisation; outputs within the fp64 q8 oracle's bars."""
+    run_q8("degenerate", cap=1024, pos=[1000], scale=512 ** -0.5, seed=37, table=table, rows_fn=_degenerate_rows)
 
 
 @TABLE
