@@ -13,7 +13,7 @@ write + new-row read and write.  `roofline` prices the dominant kernel (the spli
 attend kernel, timed alone with HIP events on the launch stream); `cpu_baseline` times
 the CPU oracle's reference-rounding restatement on the same inputs.
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c2|c1|c3|c5|p512g|p4kg|p512l|p4kl] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c2|c1|c3|c4raw|c4q8|c5|p512g|p4kg|p512l|p4kl] [--no-cpu]
 
 Workload c5 is the full Gemma-4-31B-shaped attention step: 60 layers (every 6th
 global: D=512, Hkv=4, k_eq_v, linear caches; the rest local: D=256, Hkv=16, window
