@@ -1113,9 +1113,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * kWaves, 64 * kWaves),
 void raw_attend_kernel(AttendParams p) {
     using W = WRing<Q8>;
     __shared__ __attribute__((aligned(16))) unsigned char wlds[kWaves * W::WAVE];
-    // per-wave row factors of the stage being computed: [0] rinv (q8: scale * rinv), [1] its
-    // inverse, [2] (q8) bias / scale, [3] (q8) bias * rinv
-    __shared__ __attribute__((aligned(16))) float xf[kWaves][4][16];
+    // per-wave row factors of the stage being computed (the softmax's rows 4lg .. 4lg + 3):
+    // [0] rinv (q8: scale * rinv), [1] its inverse, [2] (q8) bias / scale
+    __shared__ __attribute__((aligned(16))) float xf[kWaves][3][16];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, lg = lane >> 4;
