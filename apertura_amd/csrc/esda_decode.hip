@@ -1043,7 +1043,7 @@ void attend_kernel(AttendParams p) {
 // streams them through two LDS slots of its own, filled by its own LDS DMA and waited on
 // with its own vmcnt, so the main loop has no barrier and no exchange between waves.  Per
 // stage a wave:
-//   - reads the 16 raw rows as MFMA A operands (lane (li, lg): row li, dims wdim(kk, lg)
+//   - reads the 16 raw rows as MFMA A operands (lane (li, lg): row li, dims kdim(kk, lg)
 //     of k-step kk);
 //   - forms their 16x16 Gram matrix with 16 MFMAs: the diagonal is each row's sum of
 //     squares (exact bf16 products, fp32 sums), hence rinv = rsqrt(mean + eps);
@@ -1074,6 +1074,12 @@ constexpr int kBlk = 1056;                 // LDS bytes per 1 KiB DMA block (1 K
 // 2m, 2m + 1 cover 16 consecutive dims (one 16-byte u8 piece, two bf16 ones) and the rotary
 // partners of k-steps 0, 1 are k-steps 8, 9 of the same lane.
 __device__ __forceinline__ int wdim(int kk, int lg) { return 64 * (kk >> 1) + 16 * lg + 8 * (kk & 1); }
+// Raw-K (bf16 rows): the lane groups' 8 dims of k-step kk side by side, 32 kk + 8 lg, so that
+// the four lane groups of a row read adjacent 16-byte pieces (no LDS bank conflicts); the
+// rotary partners of k-steps 0, 1 are again k-steps 8, 9 of the same lane.  q8 keeps wdim,
+// whose pairs of k-steps are one 16-byte u8 piece.
+template <bool Q8>
+__device__ __forceinline__ int kdim(int kk, int lg) { return Q8 ? wdim(kk, lg) : 32 * kk + 8 * lg; }
 // The rotary k-steps: dims 0 .. 63 (k-steps 0, 1) and their partners 256 .. 319 (8, 9).
 __device__ __forceinline__ constexpr bool rot_step(int kk) { return (kk & 7) < 2; }
 
@@ -1131,8 +1137,8 @@ void raw_attend_kernel(AttendParams p) {
         __syncthreads();
     }
     // Raw: the A operands of the x * kw products, diag(kw) over 16 dims.  For k-step kk and half
-    // hh the B operand is the lane's own dims wdim(kk, lg) + 4hh .. + 3 of row li; lane
-    // (li, lg) then holds kw of dim wdim(kk, lg) + 4hh + (li & 3) at slot li & 3 when
+    // hh the B operand is the lane's own dims kdim(kk, lg) + 4hh .. + 3 of row li; lane
+    // (li, lg) then holds kw of dim kdim(kk, lg) + 4hh + (li & 3) at slot li & 3 when
     // lg == li / 4 and zeros elsewhere, and the product's C layout hands every lane x * kw
     // of the same dims it supplied.
     short4v dg[Q8 ? 1 : 16][2];
@@ -1143,7 +1149,7 @@ void raw_attend_kernel(AttendParams p) {
         for (int kk = 0; kk < 16; ++kk)
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
-                const short w = (li >> 2) == lg ? kwb[wdim(kk, lg) + 4 * hh + s] : (short) 0;
+                const short w = (li >> 2) == lg ? kwb[kdim<Q8>(kk, lg) + 4 * hh + s] : (short) 0;
                 dg[kk][hh] = short4v{s == 0 ? w : (short) 0, s == 1 ? w : (short) 0, s == 2 ? w : (short) 0,
                                      s == 3 ? w : (short) 0};
             }
@@ -1165,7 +1171,7 @@ void raw_attend_kernel(AttendParams p) {
             const uint16_t *qrow = p.q + ((size_t) b * p.Hq + (size_t) kvh * p.G + (qok ? li : 0)) * kRawDim;
 #pragma unroll
             for (int kk = 0; kk < 16; ++kk) {
-                const u32x4 t = qok ? *reinterpret_cast<const u32x4 *>(qrow + wdim(kk, lg)) : u32x4{0u, 0u, 0u, 0u};
+                const u32x4 t = qok ? *reinterpret_cast<const u32x4 *>(qrow + kdim<Q8>(kk, lg)) : u32x4{0u, 0u, 0u, 0u};
                 qv[kk] = __builtin_bit_cast(bf16x8, t);
             }
         }
@@ -1319,7 +1325,8 @@ void raw_attend_kernel(AttendParams p) {
                 const int pos = li & 7, bt2 = pos >> 2, rib = pos & 3;
 #pragma unroll
                 for (int c4 = 0; c4 < 4; ++c4) {
-                    const int c = 4 * lg + c4;
+                    // the pieces (4 frequencies each) of the lane's rotary dims kdim(kr, lg) .. + 7
+                    const int c = Q8 ? 4 * lg + c4 : 8 * (c4 >> 1) + 2 * lg + (c4 & 1);
                     tab[c4] = *reinterpret_cast<const u32x4 *>(sl + W::ROWS + W::SB + bt2 * kBlk +
                                                                16 * (16 * rib + ((c + 4 * rib) & 15)));
                 }
@@ -1330,7 +1337,7 @@ void raw_attend_kernel(AttendParams p) {
                 for (int e = 0; e < 8; ++e) r[e] = (__bf16) v[e];
                 return r;
             };
-            // rope over rotary k-steps kr, kr + 8 (dims 16lg + 8kr + e and their partners + 256)
+            // rope over rotary k-steps kr, kr + 8 (dims kdim(kr, lg) + e and their partners + 256)
             auto rotate = [](const u32x4 (&tab)[4], int kr, float (&lo)[8], float (&hi)[8]) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -1385,7 +1392,7 @@ void raw_attend_kernel(AttendParams p) {
                     f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int kk = 0; kk < 16; ++kk) {
-                        xr[kk] = *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * wdim(kk, lg));
+                        xr[kk] = *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * kdim<Q8>(kk, lg));
                         const bf16x8 x = __builtin_bit_cast(bf16x8, xr[kk]);
                         g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
                     }
@@ -1414,7 +1421,7 @@ void raw_attend_kernel(AttendParams p) {
             u32x4 tab[4];
             load_tab(tab);
             const float rk = Q8 ? rq : xfw[0 * 16 + li];  // rinv of row li (q8: scale * rinv)
-            // Pass 2: x * rinv * kw of k-step kk, dims wdim(kk, lg) .. + 7 of row li.
+            // Pass 2: x * rinv * kw of k-step kk, dims kdim(kk, lg) .. + 7 of row li.
             auto xkw = [&](int kk, float (&v)[8]) {
                 if constexpr (Q8) {
                     // fma(q, scale * rinv, bias * rinv) * kw, per element; the same floats of q,
