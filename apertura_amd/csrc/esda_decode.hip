@@ -1070,16 +1070,11 @@ void attend_kernel(AttendParams p) {
 constexpr int kWaves = 4;                  // waves of the wave-private-ring kernels
 constexpr int kBlk = 1056;                 // LDS bytes per 1 KiB DMA block (1 KiB + 32 B pad)
 
-// Dims of k-step kk held by lane group lg: 8 consecutive dims, so that a lane's two k-steps
-// 2m, 2m + 1 cover 16 consecutive dims (one 16-byte u8 piece, two bf16 ones) and the rotary
-// partners of k-steps 0, 1 are k-steps 8, 9 of the same lane.
-__device__ __forceinline__ int wdim(int kk, int lg) { return 64 * (kk >> 1) + 16 * lg + 8 * (kk & 1); }
-// Raw-K (bf16 rows): the lane groups' 8 dims of k-step kk side by side, 32 kk + 8 lg, so that
-// the four lane groups of a row read adjacent 16-byte pieces (no LDS bank conflicts); the
-// rotary partners of k-steps 0, 1 are again k-steps 8, 9 of the same lane.  q8 keeps wdim,
-// whose pairs of k-steps are one 16-byte u8 piece.
-template <bool Q8>
-__device__ __forceinline__ int kdim(int kk, int lg) { return Q8 ? wdim(kk, lg) : 32 * kk + 8 * lg; }
+// Dims of k-step kk held by lane group lg: 8 consecutive dims, the four lane groups side by
+// side (32 kk + 8 lg), so that a row's lane groups read (and the q8 V tile's writes write)
+// adjacent 16-byte pieces, without LDS bank conflicts; the rotary partners of k-steps 0, 1 are
+// k-steps 8, 9 of the same lane.
+__device__ __forceinline__ int kdim(int kk, int lg) { return 32 * kk + 8 * lg; }
 // The rotary k-steps: dims 0 .. 63 (k-steps 0, 1) and their partners 256 .. 319 (8, 9).
 __device__ __forceinline__ constexpr bool rot_step(int kk) { return (kk & 7) < 2; }
 
@@ -1149,7 +1144,7 @@ void raw_attend_kernel(AttendParams p) {
         for (int kk = 0; kk < 16; ++kk)
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
-                const short w = (li >> 2) == lg ? kwb[kdim<Q8>(kk, lg) + 4 * hh + s] : (short) 0;
+                const short w = (li >> 2) == lg ? kwb[kdim(kk, lg) + 4 * hh + s] : (short) 0;
                 dg[kk][hh] = short4v{s == 0 ? w : (short) 0, s == 1 ? w : (short) 0, s == 2 ? w : (short) 0,
                                      s == 3 ? w : (short) 0};
             }
@@ -1171,7 +1166,7 @@ void raw_attend_kernel(AttendParams p) {
             const uint16_t *qrow = p.q + ((size_t) b * p.Hq + (size_t) kvh * p.G + (qok ? li : 0)) * kRawDim;
 #pragma unroll
             for (int kk = 0; kk < 16; ++kk) {
-                const u32x4 t = qok ? *reinterpret_cast<const u32x4 *>(qrow + kdim<Q8>(kk, lg)) : u32x4{0u, 0u, 0u, 0u};
+                const u32x4 t = qok ? *reinterpret_cast<const u32x4 *>(qrow + kdim(kk, lg)) : u32x4{0u, 0u, 0u, 0u};
                 qv[kk] = __builtin_bit_cast(bf16x8, t);
             }
         }
@@ -1326,7 +1321,7 @@ void raw_attend_kernel(AttendParams p) {
 #pragma unroll
                 for (int c4 = 0; c4 < 4; ++c4) {
                     // the pieces (4 frequencies each) of the lane's rotary dims kdim(kr, lg) .. + 7
-                    const int c = Q8 ? 4 * lg + c4 : 8 * (c4 >> 1) + 2 * lg + (c4 & 1);
+                    const int c = 8 * (c4 >> 1) + 2 * lg + (c4 & 1);
                     tab[c4] = *reinterpret_cast<const u32x4 *>(sl + W::ROWS + W::SB + bt2 * kBlk +
                                                                16 * (16 * rib + ((c + 4 * rib) & 15)));
                 }
@@ -1350,27 +1345,32 @@ void raw_attend_kernel(AttendParams p) {
             };
             // Pass 1: the row norms.  Raw: from Gram products of the rows as stored.  q8: from
             // integer sums of the u8 bytes (the rebuild below widens them to bf16 for the V tile).
-            u32x4 w8[Q8 ? 8 : 1];  // q8: the stage's u8 row pieces (16 dims each)
+            uint2 w8[Q8 ? 16 : 1];  // q8: the lane's 8 u8 values of row li for k-step kk
             u32x4 xr[Q8 ? 1 : 16];  // raw: the lane's row pieces, k-step kk (pass 1, kept for the rebuild)
             float rq = 0.0f, fq = 0.0f;  // q8: scale * rinv and bias * rinv of row li
             {
                 if constexpr (Q8) {
-                    // All eight u8 reads go out before the first V-tile write: LDS accesses
+                    // All sixteen u8 reads go out before the first V-tile write: LDS accesses
                     // complete in order, so a read issued after a write would wait for it.
+                    // Row r's 16-byte piece pc (dims 16 pc ..) sits at (r / 2) * kBlk + 32 pc +
+                    // 16 (r % 2) (two rows interleaved per DMA block); the lane's dims kdim(kk, lg)
+                    // are half of piece 2kk + lg / 2.
 #pragma unroll
-                    for (int mm = 0; mm < 8; ++mm)
-                        w8[mm] = *reinterpret_cast<const u32x4 *>(sl + (li >> 1) * kBlk + 32 * (4 * mm + lg) + 16 * (li & 1));
+                    for (int kk = 0; kk < 16; ++kk)
+                        w8[kk] = *reinterpret_cast<const uint2 *>(sl + (li >> 1) * kBlk + 32 * (2 * kk + (lg >> 1)) +
+                                                                  16 * (li & 1) + 8 * (lg & 1));
                     const float scl = reinterpret_cast<const float *>(sl + W::ROWS)[li];
                     const float bias = reinterpret_cast<const float *>(sl + W::ROWS)[16 + li];
                     __builtin_amdgcn_sched_barrier(0);
                     // sum(q^2) and sum(q) of the lane's quarter of row li, exact in integers
                     unsigned s2 = 0u, s1 = 0u;
 #pragma unroll
-                    for (int mm = 0; mm < 8; ++mm)
+                    for (int kk = 0; kk < 16; ++kk)
 #pragma unroll
-                        for (int w = 0; w < 4; ++w) {
-                            s2 = __builtin_amdgcn_udot4(w8[mm][w], w8[mm][w], s2, false);
-                            s1 = __builtin_amdgcn_udot4(w8[mm][w], 0x01010101u, s1, false);
+                        for (int w = 0; w < 2; ++w) {
+                            const unsigned x = w ? w8[kk].y : w8[kk].x;
+                            s2 = __builtin_amdgcn_udot4(x, x, s2, false);
+                            s1 = __builtin_amdgcn_udot4(x, 0x01010101u, s1, false);
                         }
                     // whole-row sums in every lane of row li's column (lanes li + 16 lg)
                     s2 = wave_sum_across_groups(s2);
@@ -1392,7 +1392,7 @@ void raw_attend_kernel(AttendParams p) {
                     f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int kk = 0; kk < 16; ++kk) {
-                        xr[kk] = *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * kdim<Q8>(kk, lg));
+                        xr[kk] = *reinterpret_cast<const u32x4 *>(sl + li * kBlk + 2 * kdim(kk, lg));
                         const bf16x8 x = __builtin_bit_cast(bf16x8, xr[kk]);
                         g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, x, g, 0, 0, 0);
                     }
@@ -1413,7 +1413,7 @@ void raw_attend_kernel(AttendParams p) {
             // and park them in accumulation registers)
             if constexpr (Q8) {
 #pragma unroll
-                for (int mm = 0; mm < 8; ++mm) asm volatile("" : "+v"(w8[mm]));
+                for (int kk = 0; kk < 16; ++kk) asm volatile("" : "+v"(w8[kk]));
             }
             // Other lanes read the factors back: a compiler memory barrier keeps those loads
             // after the stores above (the lanes' LDS accesses then run in order).
@@ -1428,15 +1428,15 @@ void raw_attend_kernel(AttendParams p) {
                     // packed to bf16 (exact), are the k-step's part of the V tile
                     float q[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) q[e] = (float) ((w8[kk >> 1][2 * (kk & 1) + (e >> 2)] >> (8 * (e & 3))) & 255u);
+                    for (int e = 0; e < 8; ++e) q[e] = (float) ((((e >> 2) ? w8[kk].y : w8[kk].x) >> (8 * (e & 3))) & 255u);
                     unsigned o[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         o[e] = __builtin_amdgcn_perm(__builtin_bit_cast(unsigned, q[2 * e + 1]), __builtin_bit_cast(unsigned, q[2 * e]),
                                                      0x07060302u);
-                    *reinterpret_cast<u32x4 *>(wl + 2 * W::SLOT + li * kBlk + 2 * wdim(kk, lg)) = u32x4{o[0], o[1], o[2], o[3]};
+                    *reinterpret_cast<u32x4 *>(wl + 2 * W::SLOT + li * kBlk + 2 * kdim(kk, lg)) = u32x4{o[0], o[1], o[2], o[3]};
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(q[e], rk, fq) * kwl[wdim(kk, lg) + e];
+                    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(q[e], rk, fq) * kwl[kdim(kk, lg) + e];
                 } else {
                     // x * kw exactly (a product of two bf16 values fits fp32) by MFMAs against
                     // the diagonal kw operands, then times rinv
