@@ -1408,9 +1408,9 @@ void raw_attend_kernel(AttendParams p) {
                     }
                 }
             }
-            // q8: pass 2 converts the u8 pieces again instead of keeping pass 1's 128 floats
-            // live across the row-factor exchange (the compiler would otherwise share them
-            // and park them in accumulation registers)
+            // q8: the u8 values are converted once, in pass 2; this keeps the compiler from
+            // hoisting the conversions above the row-factor exchange, which would hold 128 floats
+            // live across it (it parks such values in accumulation registers)
             if constexpr (Q8) {
 #pragma unroll
                 for (int kk = 0; kk < 16; ++kk) asm volatile("" : "+v"(w8[kk]));
