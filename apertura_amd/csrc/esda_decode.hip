@@ -140,10 +140,9 @@ constexpr int kRopePairs = 64;
 constexpr int kTabStride = 68;  // words per cos/sin table row: 64 + 4 (conflict-free 128-bit reads)
 // LDS of the raw-mode exchanges for NW waves, in this order: row sums of squares
 // [3][16][NW], the row factors [2][3][16], (q8) the row sums [3][16][NW], and the cos/sin
-// tables [2][16][kTabStride] computed in the kernel (absent when a precomputed table is
-// DMA'd per ring stage instead).
-constexpr int raw_extra_lds(int nw, bool q8 = false, bool tab = false) {
-    return 3 * 16 * nw * 4 + 2 * 3 * 16 * 4 + (q8 ? 3 * 16 * nw * 4 : 0) + (tab ? 0 : 2 * 16 * kTabStride * 4);
+// tables [2][16][kTabStride] computed in the kernel.
+constexpr int raw_extra_lds(int nw, bool q8 = false) {
+    return 3 * 16 * nw * 4 + 2 * 3 * 16 * 4 + (q8 ? 3 * 16 * nw * 4 : 0) + 2 * 16 * kTabStride * 4;
 }
 // q8 raw-K mode: u8 stages are widened into bf16 staging slots laid out as the D = 512
 // ring (16 rows of 1056-byte blocks), four deep; per-row scale / bias ride beside each
@@ -151,8 +150,8 @@ constexpr int raw_extra_lds(int nw, bool q8 = false, bool tab = false) {
 constexpr int kQ8Stage = 16 * 1056;
 constexpr int kQ8Slots = 4;
 constexpr int kQ8SbStages = 16;
-constexpr int q8_extra_lds(int nw, bool tab = false) {
-    return raw_extra_lds(nw, true, tab) + kQ8Slots * kQ8Stage + kQ8SbStages * 2 * 16 * 4;
+constexpr int q8_extra_lds(int nw) {
+    return raw_extra_lds(nw, true) + kQ8Slots * kQ8Stage + kQ8SbStages * 2 * 16 * 4;
 }
 
 
@@ -321,9 +320,6 @@ __device__ __forceinline__ void walk_segments(const AttendParams &p, Seg &&segme
 // The new token's row is copied from k_new/v_new into the cache by the workgroup whose
 // split ends at it (bit-exact copy); that workgroup's own loads read the row from
 // k_new/v_new and no other workgroup reads it, so the copy needs no ordering.
-// RPK (raw mode): kv heads per workgroup, 1 or 2 (the host's pk).  With 2, a stage holds 8
-// rows of each of two kv heads of one sequence at the same 8 positions, so the cos/sin
-// table of a stage has 8 rows instead of 16: half the table work per stage.
 //
 // Q8 (raw mode over a q8 raw stream, esDecodeAttnGlobalQ8, ESDecodeAttn.mm:275-369): rows
 // are u8 with a per-row scale and bias, x = q * scale + bias.  The u8 ring (512-byte rows)
@@ -332,12 +328,7 @@ __device__ __forceinline__ void walk_segments(const AttendParams &p, Seg &&segme
 // exactly, hence sum(x^2); K = bf16(rope(fma(q, scale*rinv, bias*rinv) * kw)); V enters
 // as q with the weight P = bf16(e * scale * rinv) and the bias as sum P * bias / scale.
 // The workgroup holding a sequence's new row quantizes it into the cache first.
-//
-// TAB (raw mode, two kv heads per workgroup): the cos/sin rows of a stage's positions come
-// from the caller's precomputed table (esda_rope_table: the same sincos_f32 and bf16
-// rounding as publish_tab) by one 256-byte LDS DMA per row beside the stage's rows, into a
-// table area per ring slot, instead of being computed in every step.
-template <int D, bool SHARED, int NW, bool RAW, int RPK = 1, bool Q8 = false, bool TAB = false, int OCC = 1>
+template <int D, bool SHARED, int NW, bool RAW, bool Q8 = false, int OCC = 1>
 // The LDS ring allows OCC workgroups per CU, i.e. OCC * NW/4 waves per SIMD: telling the
 // compiler so lifts the register limit it would otherwise keep for higher occupancy,
 // which it meets by serialising LDS reads behind their uses.  (Plans may still place one
@@ -345,21 +336,16 @@ template <int D, bool SHARED, int NW, bool RAW, int RPK = 1, bool Q8 = false, bo
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(OCC * NW / 4, OCC * NW / 4)))
 void attend_kernel(AttendParams p) {
     static_assert(!RAW || (D == kRawDim && SHARED && (NW == 4 || NW == 8)), "raw mode: one 512-dim stream, 4 or 8 waves");
-    static_assert(RPK == 1 || (RAW && RPK == 2), "kv-head packing is a runtime choice outside raw mode");
     static_assert(!Q8 || (RAW && NW == 8), "q8 mode is raw mode with 8 waves");
-    static_assert(!TAB || (RAW && RPK == 2 && (16 / RPK) % NW == 0), "table rows: raw mode, two kv heads");
-    // bytes of one ring slot's cos/sin rows (TAB)
-    constexpr int TABB = TAB ? (16 / RPK) * kTabStride * 4 : 0;
     // R: the compute layout of a stage (and, outside q8 mode, the DMA ring); RD: the DMA ring.
-    using R = Ring<D, SHARED, NW, RAW && !Q8 ? raw_extra_lds(NW, false, TAB) : 0, RAW && !Q8 ? TABB : 0, 160 * 1024 / OCC>;
-    using RD = std::conditional_t<Q8, Ring<256, true, NW, q8_extra_lds(NW, TAB), TABB>, R>;
+    using R = Ring<D, SHARED, NW, RAW && !Q8 ? raw_extra_lds(NW) : 0, 0, 160 * 1024 / OCC>;
+    using RD = std::conditional_t<Q8, Ring<256, true, NW, q8_extra_lds(NW)>, R>;
     static_assert(OCC == 1 || !RAW, "raw mode holds one workgroup per CU");
     // D = 512 exchanges only the live heads' partial scores (the padding columns are zero)
     constexpr bool kLiveX = D == 512 && !RAW;
     constexpr int NS = RD::NS, DW = R::DW, KKW = R::KKW, DTW = R::DTW;
-    // DMA instructions per wave per stage (q8: the u8 rows plus one scale / bias piece;
-    // TAB: plus its share of the cos/sin rows)
-    constexpr int DPW = (Q8 ? RD::DPT + 1 : RD::DPW) + (TAB ? (16 / RPK) / NW : 0);
+    // DMA instructions per wave per stage (q8: the u8 rows plus one scale / bias piece)
+    constexpr int DPW = Q8 ? RD::DPT + 1 : RD::DPW;
     // Stages between the one being accumulated and the newest one that must have landed.
     constexpr int AHEAD = Q8 ? 3 : RAW ? 2 : 1;
     static_assert(NS >= AHEAD + 3, "the ring must hold the look-ahead stages and one in flight");
@@ -393,7 +379,7 @@ void attend_kernel(AttendParams p) {
     // Raw mode: per-row partial sums of squares xss[stage % 3][row][wave], the per-row
     // norm factors xr, and the cos/sin table xtab[stage % 2][row][pair] (bf16 cos in the low
     // half, sin in the high half) when the kernel computes it.
-    __shared__ __attribute__((aligned(16))) unsigned char rawlds[RAW ? raw_extra_lds(NW, Q8, TAB) : 16];
+    __shared__ __attribute__((aligned(16))) unsigned char rawlds[RAW ? raw_extra_lds(NW, Q8) : 16];
     auto *xss = reinterpret_cast<float (*)[16][NW]>(rawlds);
     // xr[stage % 2][0][row] = the weight factor (rinv; q8: scale * rinv), [1] its inverse,
     // [2] (q8) bias / scale
@@ -402,14 +388,11 @@ void attend_kernel(AttendParams p) {
     auto *xsq = reinterpret_cast<float (*)[16][NW]>(rawlds + 3 * 16 * NW * 4 + 2 * 3 * 16 * 4);
     auto *xtab = reinterpret_cast<unsigned (*)[16][kTabStride]>(rawlds + 3 * 16 * NW * 4 + 2 * 3 * 16 * 4 +
                                                                 (Q8 ? 3 * 16 * NW * 4 : 0));
-    // TAB: the cos/sin rows of the stage in ring slot u, rtab[u][row][pair] (rows past 64
-    // pairs are padding for conflict-free reads)
-    __shared__ __attribute__((aligned(16))) unsigned rtab[TAB ? NS : 1][TAB ? 16 / RPK : 1][kTabStride];
     // q8: bf16 staging slots and the per-stage scale / bias rows
     __shared__ __attribute__((aligned(16))) unsigned char q8stg[Q8 ? kQ8Slots * kQ8Stage : 16];
     __shared__ __attribute__((aligned(16))) float q8sb[Q8 ? kQ8SbStages : 1][2][16];
     // cos/sin table of a stage: TR rows (one per position) x 64 pairs over 64*NW threads
-    constexpr int TR = 16 / RPK;
+    constexpr int TR = 16;
     constexpr int EPT = TR * 64 / (64 * NW);
     static_assert(EPT >= 1, "every thread computes at least one table entry");
     constexpr int TPR = 64 / EPT;  // threads per table row
@@ -544,16 +527,6 @@ void attend_kernel(AttendParams p) {
     // DMA of stage st into ring buffer `buf` (ring slot `slot`).
     auto dma = [&](int st, unsigned char *buf, int slot) {
         const int jst = j0 + st * RPP;
-        if constexpr (TAB) {
-            // cos/sin rows of the stage's positions (cache rows; rows past the range repeat
-            // the last one): wave w loads rows w, w + NW, .., 64 lanes x 4 bytes each
-#pragma unroll
-            for (int k = 0; k < (16 / RPK) / NW; ++k) {
-                const int row = wave + NW * k;
-                const int j = jst + row, jj = j < j1 ? j : j1 - 1;
-                lds_dma4(p.rope_tab + (size_t) (sv.first + jj) * 64 + lane, lds_addr(&rtab[slot][row][0]));
-            }
-        }
         if constexpr (Q8) {
             // scale / bias of the stage's rows: wave w loads the scales (w < 4) or biases of
             // stage rows 4(w % 4) .. +3, one row per lane
@@ -785,9 +758,7 @@ void attend_kernel(AttendParams p) {
             if (wave < 2) {
                 // chunk `wave` (k-step 0) holds dims d = 32*wave + 8lg + e < 64; chunk wave + 8
                 // (k-step KP) their rotary partners.
-                const unsigned *tb;
-                if constexpr (TAB) tb = &rtab[sbslot][li & (TR - 1)][32 * wave + 8 * lg];
-                else tb = &xtab[tabbuf][li & (TR - 1)][32 * wave + 8 * lg];
+                const unsigned *tb = &xtab[tabbuf][li][32 * wave + 8 * lg];
                 const u32x4 t0 = *reinterpret_cast<const u32x4 *>(tb);
                 const u32x4 t1 = *reinterpret_cast<const u32x4 *>(tb + 4);
     #pragma unroll
@@ -839,11 +810,11 @@ void attend_kernel(AttendParams p) {
         }
         load_raw(cbuf(0, std::integral_constant<int, 0>{}));
         publish_ss(0);
-        if constexpr (!TAB) publish_tab(0, 0);
+        publish_tab(0, 0);
         if (nst > 1) {
             load_raw(cbuf(1, std::integral_constant<int, 1>{}));
             publish_ss(1);
-            if constexpr (!TAB) publish_tab(1, 1);
+            publish_tab(1, 1);
         }
         lds_barrier();
         // scores of stage 0 (its raw operand is read again; araw keeps stage 1's)
@@ -911,7 +882,7 @@ void attend_kernel(AttendParams p) {
             qk_raw((st + 1) % 3, (st + 1) & 1, (st + 1) & 1, (u + 1) % NS);
             load_raw(cbuf(st + 2, std::integral_constant<int, (u + 2) % NS>{}));
             publish_ss((st + 2) % 3);
-            if constexpr (!TAB) publish_tab(st + 2, st & 1);
+            publish_tab(st + 2, st & 1);
         } else {
             qk_partial(ring(std::integral_constant<int, (u + 1) % NS>{}), (st + 1) & 1);
         }
@@ -1036,13 +1007,14 @@ void attend_kernel(AttendParams p) {
 
 // ------------------------------------------------- raw-K attend with wave-private rings
 //
-// Raw-K decode (ESDecodeAttn.mm:17-117) when two kv heads share a workgroup and the caller
-// passes the precomputed rotary table -- the ES layer's path.  Four waves, one per SIMD.
-// Each wave owns whole 16-row stages (8 positions of each of the two kv heads) over the
-// full 512-dim head, in turn: wave w takes stages w, w + 4, w + 8, ... of a segment.  It
-// streams them through two LDS slots of its own, filled by its own LDS DMA and waited on
-// with its own vmcnt, so the main loop has no barrier and no exchange between waves.  Per
-// stage a wave:
+// Raw-K decode (ESDecodeAttn.mm:17-117) when the caller passes the precomputed rotary table
+// -- the ES layer's path.  A workgroup serves one kv head (a contiguous run of its rows, as
+// the composite kernel's) with four waves, one per SIMD.  Each wave owns whole 16-row stages
+// (16 consecutive positions) over the full 512-dim head, in turn: wave w takes stages w,
+// w + 4, w + 8, ... of a segment.  It streams their rows through two LDS slots of its own and
+// their cos / sin table rows through a table buffer of its own, filled by its own LDS DMA and
+// waited on with its own vmcnt, so the main loop has no barrier and no exchange between
+// waves.  Per stage a wave:
 //   - reads the 16 raw rows as MFMA A operands (lane (li, lg): row li, dims kdim(kk, lg)
 //     of k-step kk);
 //   - forms their 16x16 Gram matrix with 16 MFMAs: the diagonal is each row's sum of
@@ -1052,12 +1024,12 @@ void attend_kernel(AttendParams p) {
 //     lane's own rows against diag(kw) operands built once per kernel, whose C layout
 //     hands every lane the dims it supplied; one multiply by rinv, the rotation and the
 //     bf16 rounding remain per element.  The rotary partners (d, d + 256), d < 64, sit in
-//     one lane (k-steps 0, 1 and 8, 9); their bf16 cos / sin come from the table rows
-//     DMA'd beside the stage;
-//   - scores its 16 query heads (both GQA groups: heads of the other kv head's rows are
-//     masked) with 16 MFMAs, runs its own online softmax, and accumulates O^T[512 x 16
-//     heads] with 32 MFMAs over V = kraw read back by transpose reads, rinv folded into the
-//     weight: P = bf16(e * rinv), l += P / rinv.
+//     one lane (k-steps 0, 1 and 8, 9); their bf16 cos / sin come from the table rows,
+//     whose buffer takes the next stage's table rows once the rotary k-steps have read it;
+//   - scores the kv head's query heads (up to 16: the MFMA's N dimension, zero-padded) with
+//     16 MFMAs, runs its own online softmax, and accumulates O^T[512 x 16 heads] with 32
+//     MFMAs over V = kraw read back by transpose reads, rinv folded into the weight:
+//     P = bf16(e * rinv), l += P / rinv.
 // Q8 (esDecodeAttnGlobalQ8, ESDecodeAttn.mm:275-369): rows are u8 with a per-row scale and
 // bias (x = q * scale + bias).  sum(q^2) and sum(q) of each row are exact integer dot products
 // of the u8 bytes (v_dot4_u32_u8, summed over the four lane groups), hence mean(x^2), and every
@@ -1087,12 +1059,12 @@ constexpr float kRawRescaleSlack = 64.0f;
 
 template <bool Q8>
 struct WRing {
-    static constexpr int ROWS = Q8 ? 8 * kBlk : 16 * kBlk;  // rows of a stage (q8: two per block)
+    static constexpr int ROWS = Q8 ? 8 * kBlk : 16 * kBlk;  // a stage's 16 rows (q8: two per block)
     static constexpr int SB = Q8 ? 128 : 0;                  // q8: 16 scales, 16 biases
-    static constexpr int TAB = 2 * kBlk;                     // 8 cos/sin table rows (swizzled)
-    static constexpr int SLOT = ROWS + SB + TAB;
+    static constexpr int SLOT = ROWS + SB;
     static constexpr int STG = Q8 ? 16 * kBlk : 0;           // q8: the bf16 V tile
-    static constexpr int WAVE = 2 * SLOT + STG;              // one wave's LDS
+    static constexpr int TAB = 4 * kBlk;                     // the stage's 16 cos/sin table rows (swizzled)
+    static constexpr int WAVE = 2 * SLOT + STG + TAB;        // one wave's LDS: two slots, the V tile, the table
     static constexpr int MERGE = kWaves * 16 * 516 * 4;      // end-of-segment merge area (aliases the rings)
     static_assert(kWaves * WAVE >= MERGE, "the merge area fits in the rings");
 };
@@ -1153,11 +1125,11 @@ void raw_attend_kernel(AttendParams p) {
     auto segment = [&](const int b, const int kvh, const int j0, const int j1, const SeqView sv, const size_t slot,
                        const bool direct) {
         const bool append = p.k_new != nullptr;
-        const size_t head_off = (size_t) b * p.seq_stride + (size_t) kvh * 2 * p.head_stride;
+        const size_t head_off = (size_t) b * p.seq_stride + (size_t) kvh * p.head_stride;
         uint16_t *const kbase = p.k_cache + head_off;
-        const uint16_t *const knew = append ? p.k_new + ((size_t) b * p.Hkv + kvh) * 2 * kRawDim : nullptr;
+        const uint16_t *const knew = append ? p.k_new + ((size_t) b * p.Hkv + kvh) * kRawDim : nullptr;
         unsigned char *const q8base = Q8 ? p.q8 + head_off : nullptr;
-        const size_t sb_off = Q8 ? (size_t) b * p.sb_seq_stride + (size_t) kvh * 2 * p.sb_head_stride : 0;
+        const size_t sb_off = Q8 ? (size_t) b * p.sb_seq_stride + (size_t) kvh * p.sb_head_stride : 0;
 
         // Q^T operand: head li of the packed pair (zero for padding heads li >= G)
         bf16x8 qv[16];
@@ -1171,11 +1143,10 @@ void raw_attend_kernel(AttendParams p) {
             }
         }
         if constexpr (Q8) {
-            // The new row of each kv head is quantized into the cache before any DMA (wave pr:
-            // kv head pr), esQuantizeRawRows' arithmetic (ESDecodeAttn.mm:491-509).
-            if (append && j1 == sv.nvis && wave < 2) {
-                const int pr = wave;
-                const u32x4 t = *reinterpret_cast<const u32x4 *>(knew + pr * kRawDim + lane * 8);
+            // The new row is quantized into the cache before any DMA (wave 0),
+            // esQuantizeRawRows' arithmetic (ESDecodeAttn.mm:491-509).
+            if (append && j1 == sv.nvis && wave == 0) {
+                const u32x4 t = *reinterpret_cast<const u32x4 *>(knew + lane * 8);
                 float x[8];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -1202,10 +1173,10 @@ void raw_attend_kernel(AttendParams p) {
                     if (e < 4) lo |= qi << (8 * e);
                     else hi |= qi << (8 * (e - 4));
                 }
-                unsigned char *row = q8base + (size_t) pr * p.head_stride + (size_t) sv.newrow * kRawDim;
+                unsigned char *row = q8base + (size_t) sv.newrow * kRawDim;
                 *reinterpret_cast<uint2 *>(row + lane * 8) = uint2{lo, hi};
                 if (lane == 0) {
-                    const size_t at = sb_off + (size_t) pr * p.sb_head_stride + (size_t) sv.newrow;
+                    const size_t at = sb_off + (size_t) sv.newrow;
                     p.qsc[at] = scl;
                     p.qbs[at] = mn;
                 }
@@ -1216,74 +1187,72 @@ void raw_attend_kernel(AttendParams p) {
             if (append && j1 == sv.nvis) lds_barrier();  // the quantized row is in memory before any DMA
         }
 
-        const int nst = (j1 - j0 + 7) >> 3;  // 16-row stages: 8 positions x 2 kv heads
-        // DMA of stage st into slot sl.  Rows past the segment end repeat its last row (their
-        // scores are masked); the new token's raw row comes from k_new.
-        auto dma = [&](int st, unsigned char *sl) {
-            const int jst = j0 + 8 * st;
+        const int nst = (j1 - j0 + 15) >> 4;  // 16-row stages: 16 positions
+        // DMA of stage st's rows into slot sl.  Rows past the segment end repeat its last row
+        // (their scores are masked); the new token's raw row comes from k_new.
+        auto dma_rows = [&](int st, unsigned char *sl) {
+            const int jst = j0 + 16 * st;
             const unsigned lb = lds_addr(sl);
-            // table rows of positions jst .. jst + 7: block bt holds positions 4bt .. 4bt+3,
-            // piece c of position rib at 16 * (16 rib + (c + 4 rib) mod 16)
-            const int rib = lane >> 4, c = (lane - 4 * rib) & 15;
-            const unsigned tdst = lb + W::ROWS + W::SB;
-            // q8 block i: rows 2i, 2i + 1 (kv head i / 4); lane l loads row 2i + (l & 1), 16-byte
-            // piece l >> 1
+            // q8 block i: rows 2i, 2i + 1; lane l loads row 2i + (l & 1), 16-byte piece l >> 1
             const int h = lane & 1, pc = lane >> 1;
-            // The table rows are loaded temporal (the rows non-temporal): the workgroup of the
-            // other kv-head pair at the same split, on the same XCD, reads them from the L2
-            // (c4raw traffic 1.110 -> 1.064 x the algorithmic bytes).
-            if (jst + 8 < j1) {
-                // Interior stage: all eight positions exist.  Consecutive 1 KiB blocks of memory
-                // (table rows of four positions; raw rows; pairs of q8 rows) share one scalar base
-                // through the DMA's immediate offset (ring_blocks).
-                const uint64_t tb = sbase64(p.rope_tab + (size_t) (sv.first + jst) * kRopePairs);
-                const unsigned tvoff = (unsigned) (rib * 256 + c * 16);
-                lds_dma16_o<0, 0, false>(tb, tvoff, tdst);
-                lds_dma16_o<1024, kBlk - 1024, false>(tb, tvoff, tdst);
+            if (jst + 16 < j1) {
+                // Interior stage: all sixteen positions exist (the segment's last row is in the
+                // last stage).  Four consecutive 1 KiB blocks of memory (raw rows; pairs of q8
+                // rows) share one scalar base through the DMA's immediate offset (ring_blocks).
                 if constexpr (Q8) {
-                    // block i: rows 2i, 2i + 1 of kv head i / 4
                     const unsigned char *r0 = q8base + (size_t) (sv.first + jst) * kRawDim;
-                    const uint64_t base[2] = {sbase64(r0), sbase64(r0 + p.head_stride)};
-                    ring_blocks<0, 8>(base, (unsigned) (h * kRawDim + pc * 16), lb);
+                    const uint64_t base[2] = {sbase64(r0), sbase64(r0 + 4096)};
+                    const unsigned v = (unsigned) (h * kRawDim + pc * 16);
+                    ring_blocks<0, 8>(base, v, lb);
                 } else {
-                    // block sr: position jst + sr % 8 of kv head sr / 8
                     const unsigned char *r0 = reinterpret_cast<const unsigned char *>(kbase + (size_t) (sv.first + jst) * kRawDim);
-                    const unsigned char *r1 = r0 + (size_t) p.head_stride * sizeof(uint16_t);
-                    const uint64_t base[4] = {sbase64(r0), sbase64(r0 + 4096), sbase64(r1), sbase64(r1 + 4096)};
+                    const uint64_t base[4] = {sbase64(r0), sbase64(r0 + 4096), sbase64(r0 + 8192), sbase64(r0 + 12288)};
                     ring_blocks<0, 16>(base, (unsigned) (lane * 16), lb);
                 }
             } else {
-                // The segment's last stage: rows past its end repeat its last row (their scores
-                // are masked); the new token's raw row comes from k_new.
-#pragma unroll
-                for (int bt = 0; bt < 2; ++bt) {
-                    const int j = min(jst + 4 * bt + rib, j1 - 1);
-                    lds_dma16<false>(p.rope_tab + (size_t) (sv.first + j) * kRopePairs + c * 4, tdst + bt * kBlk);
-                }
                 if constexpr (Q8) {
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
-                        const int j = min(jst + ((2 * i) & 7) + h, j1 - 1);
-                        lds_dma16(q8base + (size_t) (i >> 2) * p.head_stride + (size_t) (sv.first + j) * kRawDim + pc * 16,
-                                  lb + i * kBlk);
+                        const int j = min(jst + 2 * i + h, j1 - 1);
+                        lds_dma16(q8base + (size_t) (sv.first + j) * kRawDim + pc * 16, lb + i * kBlk);
                     }
                 } else {
 #pragma unroll
-                    for (int sr = 0; sr < 16; ++sr) {
-                        const int pr = sr >> 3, j = min(jst + (sr & 7), j1 - 1);
-                        const uint16_t *src = (append && j == sv.nvis - 1)
-                                                  ? knew + pr * kRawDim
-                                                  : kbase + (size_t) pr * p.head_stride + (size_t) (sv.first + j) * kRawDim;
-                        lds_dma16(src + lane * 8, lb + sr * kBlk);
+                    for (int r = 0; r < 16; ++r) {
+                        const int j = min(jst + r, j1 - 1);
+                        const uint16_t *src = (append && j == sv.nvis - 1) ? knew : kbase + (size_t) (sv.first + j) * kRawDim;
+                        lds_dma16(src + lane * 8, lb + r * kBlk);
                     }
                 }
             }
             if constexpr (Q8) {
+                // scales (lanes 0..15) and biases (16..31) of the stage's rows
                 if (lane < 32) {
-                    const int sr = lane & 15, pr = sr >> 3;
-                    const int j = min(jst + (sr & 7), j1 - 1);
-                    lds_dma4((lane < 16 ? p.qsc : p.qbs) + sb_off + (size_t) pr * p.sb_head_stride + (size_t) (sv.first + j),
-                             lb + W::ROWS);
+                    const int j = min(jst + (lane & 15), j1 - 1);
+                    lds_dma4((lane < 16 ? p.qsc : p.qbs) + sb_off + (size_t) (sv.first + j), lb + W::ROWS);
+                }
+            }
+        };
+        // DMA of stage st's 16 table rows into the wave's table buffer: block bt holds positions
+        // 4bt .. 4bt + 3, piece c of position rib at 16 * (16 rib + (c + 4 rib) mod 16).  Loaded
+        // temporal (the rows non-temporal): the workgroups of the other kv heads at the same
+        // positions run on the same XCD and read them from the L2.
+        auto dma_tab = [&](int st) {
+            const int jst = j0 + 16 * st;
+            const int rib = lane >> 4, c = (lane - 4 * rib) & 15;
+            const unsigned tdst = lds_addr(wl + 2 * W::SLOT + W::STG);
+            if (jst + 16 <= j1) {
+                const uint64_t tb = sbase64(p.rope_tab + (size_t) (sv.first + jst) * kRopePairs);
+                const unsigned tvoff = (unsigned) (rib * 256 + c * 16);
+                lds_dma16_o<0, 0, false>(tb, tvoff, tdst);
+                lds_dma16_o<1024, kBlk - 1024, false>(tb, tvoff, tdst);
+                lds_dma16_o<2048, 2 * kBlk - 2048, false>(tb, tvoff, tdst);
+                lds_dma16_o<3072, 3 * kBlk - 3072, false>(tb, tvoff, tdst);
+            } else {
+#pragma unroll
+                for (int bt = 0; bt < 4; ++bt) {
+                    const int j = min(jst + 4 * bt + rib, j1 - 1);
+                    lds_dma16<false>(p.rope_tab + (size_t) (sv.first + j) * kRopePairs + c * 4, tdst + bt * kBlk);
                 }
             }
         };
@@ -1294,7 +1263,10 @@ void raw_attend_kernel(AttendParams p) {
         // while waiting measured slower (c4raw attend 96.4 against 94.5 us, c4q8 110.1
         // against 108.5): the loads of all waves together then oversubscribe the memory system.
         const int st0 = wave;
-        if (st0 < nst) dma(st0, wl);
+        if (st0 < nst) {
+            dma_rows(st0, wl);
+            dma_tab(st0);
+        }
 
         float m = -INFINITY, l = 0.0f;
         float bt = 0.0f;  // q8: sum of P * bias / scale of this lane's head
@@ -1302,27 +1274,25 @@ void raw_attend_kernel(AttendParams p) {
 #pragma unroll
         for (int dt = 0; dt < 32; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         float *const xfw = &xf[wave][0][0];
-        // stage row 4lg + r belongs to kv head lg / 2; head li to kv head min(li / gk, 1)
-        const bool hmatch = (lg >> 1) == min(li / p.gk, 1);
 
         for (int st = st0, it = 0; st < nst; st += kWaves, ++it) {
             unsigned char *const sl = wl + (it & 1) * W::SLOT;
-            ESDA_WAIT_VM(0);  // this stage landed
+            ESDA_WAIT_VM(0);  // this stage's rows and table rows landed
             if (st + kWaves < nst) {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the other slot's reads are done
-                dma(st + kWaves, wl + ((it + 1) & 1) * W::SLOT);
+                dma_rows(st + kWaves, wl + ((it + 1) & 1) * W::SLOT);
             }
             // Scores S^T[16 rows x 16 heads] of K = bf16(rope(x * rinv * kw)) (q8: x = q * scale
             // + bias), rounded where ESDecodeAttn.mm:51-93 rounds it.
             f32x4 sp0 = {0.0f, 0.0f, 0.0f, 0.0f}, sp1 = {0.0f, 0.0f, 0.0f, 0.0f};
             // cos / sin of row li's position for the rotary pairs this lane holds
             auto load_tab = [&](u32x4 (&tab)[4]) {
-                const int pos = li & 7, bt2 = pos >> 2, rib = pos & 3;
+                const int bt2 = li >> 2, rib = li & 3;  // row li: position li of the stage
 #pragma unroll
                 for (int c4 = 0; c4 < 4; ++c4) {
                     // the pieces (4 frequencies each) of the lane's rotary dims kdim(kr, lg) .. + 7
                     const int c = 8 * (c4 >> 1) + 2 * lg + (c4 & 1);
-                    tab[c4] = *reinterpret_cast<const u32x4 *>(sl + W::ROWS + W::SB + bt2 * kBlk +
+                    tab[c4] = *reinterpret_cast<const u32x4 *>(wl + 2 * W::SLOT + W::STG + bt2 * kBlk +
                                                                16 * (16 * rib + ((c + 4 * rib) & 15)));
                 }
             };
@@ -1462,6 +1432,11 @@ void raw_attend_kernel(AttendParams p) {
                 sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(lo), qv[kr], sp0, 0, 0, 0);
                 sp1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(hi), qv[kr + 8], sp1, 0, 0, 0);
             }
+            // the table buffer is read (the rotary k-steps above): the next stage's rows may land
+            if (st + kWaves < nst) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                dma_tab(st + kWaves);
+            }
 #pragma unroll
             for (int kk = 2; kk < 16; ++kk) {
                 if (rot_step(kk)) continue;
@@ -1472,10 +1447,10 @@ void raw_attend_kernel(AttendParams p) {
             }
             f32x4 sc = sp0 + sp1;
             // Online softmax (log2 domain) over stage rows 4lg .. 4lg + 3: rows past the
-            // segment end and rows of the other kv head are masked.
-            const int jt = j0 + 8 * st + ((4 * lg) & 7);
+            // segment end are masked.
+            const int jt = j0 + 16 * st + 4 * lg;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sc[r] = hmatch && (jt + r) < j1 ? sc[r] * p.scale_log2e : -INFINITY;
+            for (int r = 0; r < 4; ++r) sc[r] = (jt + r) < j1 ? sc[r] * p.scale_log2e : -INFINITY;
             const float tmax = wave_max_across_groups(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
             m = m == -INFINITY ? tmax : m;  // first stage: nothing accumulated to rescale
             if (__builtin_expect(__any(tmax > m + kRawRescaleSlack), 0)) {
@@ -1523,9 +1498,9 @@ void raw_attend_kernel(AttendParams p) {
 
         // Fused append (raw): the workgroup whose rows end at the new token copies k_new
         // into its cache row (its DMA read the row from k_new; no other workgroup reads it).
-        if (!Q8 && append && j1 == sv.nvis && wave < 2) {
-            const size_t row = (size_t) wave * p.head_stride + (size_t) sv.newrow * kRawDim;
-            *reinterpret_cast<u32x4 *>(kbase + row + lane * 8) = *reinterpret_cast<const u32x4 *>(knew + wave * kRawDim + lane * 8);
+        if (!Q8 && append && j1 == sv.nvis && wave == 0) {
+            const size_t row = (size_t) sv.newrow * kRawDim;
+            *reinterpret_cast<u32x4 *>(kbase + row + lane * 8) = *reinterpret_cast<const u32x4 *>(knew + lane * 8);
         }
 
         // This wave's (m, l, O): l and (q8) the bias term summed over the lane groups.
@@ -1958,8 +1933,7 @@ int choose_pack(const esda_decode_desc *d, int G, long long S, int target) {
     return pk;
 }
 
-// raw: the raw-K kernel packs two kv heads whenever their query heads fit the MFMA's N
-// dimension (their rows share positions, so they share the stage's cos/sin table).
+// raw: the raw-K kernels take one kv head per workgroup.
 int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
     if (!d) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_decode: null description");
     if (d->batch <= 0 || d->num_q_heads <= 0 || d->num_kv_heads <= 0)
@@ -1997,9 +1971,6 @@ int make_plan(const esda_decode_desc *d, Plan *pl, bool raw = false) {
     pl->per_cu = (!raw && d->head_dim == 256) ? kOcc256 : 1;
     const int target = pl->per_cu * kTargetGroups;  // workgroups that fill the GPU
     pl->pk = 1;
-    if (raw && G * 2 <= kMaxGroup && d->num_kv_heads % 2 == 0 &&
-        (long long) d->head_stride * 2 * 2 + 16LL * d->head_dim * 2 < (1LL << 31))
-        pl->pk = 2;
     // Work split.  Sizing uses the upper bound on rows (the kernels see the real ones),
     // counted per packed kv head (a row of a pk-packed head is pk cache rows).
     // Automatic: about one workgroup per CU, no fewer than 64 rows each; split_rows > 0
@@ -2066,10 +2037,10 @@ constexpr int ring_waves() { return D == 256 ? kWaves256 : 4; }
 // reconstruction work.
 constexpr int kRawWaves = 8;
 
-template <int D, bool SHARED, bool RAW = false, int RPK = 1, bool Q8 = false, bool TAB = false, int OCC = 1>
+template <int D, bool SHARED, bool RAW = false, bool Q8 = false, int OCC = 1>
 hipError_t launch_attend(const AttendParams &ap, dim3 grid, hipStream_t st) {
     constexpr int NW = RAW ? kRawWaves : ring_waves<D>();
-    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW, RPK, Q8, TAB, OCC>), grid, dim3(64 * NW), 0, st, ap);
+    hipLaunchKernelGGL((attend_kernel<D, SHARED, NW, RAW, Q8, OCC>), grid, dim3(64 * NW), 0, st, ap);
     return hipGetLastError();
 }
 
@@ -2086,10 +2057,10 @@ hipError_t dispatch_attend(int D, bool shared, const AttendParams &ap, dim3 grid
     switch (D) {
         case 128: return shared ? launch_attend<128, true>(ap, grid, st) : launch_attend<128, false>(ap, grid, st);
         case 256:
-            return shared ? launch_attend<256, true, false, 1, false, false, O256>(ap, grid, st)
-                          : launch_attend<256, false, false, 1, false, false, O256>(ap, grid, st);
+            return shared ? launch_attend<256, true, false, false, O256>(ap, grid, st)
+                          : launch_attend<256, false, false, false, O256>(ap, grid, st);
         default:
-            return shared ? launch_attend<512, true, false, 1, false, false, O512>(ap, grid, st)
+            return shared ? launch_attend<512, true, false, false, O512>(ap, grid, st)
                           : launch_attend<512, false>(ap, grid, st);
     }
 }
@@ -2153,19 +2124,17 @@ int run_stages(const esda_decode_desc *d, const Plan &pl, const AttendParams &ap
         hipError_t e;
         if (mode == 0) {
             e = dispatch_attend(d->head_dim, d->kv_shared != 0, ap, grid, st);
-        } else if (pl.pk == 2 && ap.rope_tab) {
-            // two kv heads per workgroup with the precomputed cos/sin table (the ES layer's
-            // form): the wave-private-ring kernel
+        } else if (ap.rope_tab) {
+            // with the precomputed cos/sin table (the ES layer's form): the wave-private-ring
+            // kernel, one kv head per workgroup
             if (mode == 1) hipLaunchKernelGGL(raw_attend_kernel<false>, grid, dim3(64 * kWaves), 0, st, ap);
             else hipLaunchKernelGGL(raw_attend_kernel<true>, grid, dim3(64 * kWaves), 0, st, ap);
             e = hipGetLastError();
         } else if (mode == 1) {
-            // without a table (or with one kv head per workgroup) the 8-wave kernel computes
-            // its cos/sin per stage
-            e = pl.pk == 2 ? launch_attend<kRawDim, true, true, 2>(ap, grid, st) : launch_attend<kRawDim, true, true, 1>(ap, grid, st);
+            // without a table the 8-wave kernel computes its cos/sin per stage
+            e = launch_attend<kRawDim, true, true>(ap, grid, st);
         } else {
-            e = pl.pk == 2 ? launch_attend<kRawDim, true, true, 2, true>(ap, grid, st)
-                           : launch_attend<kRawDim, true, true, 1, true>(ap, grid, st);
+            e = launch_attend<kRawDim, true, true, true>(ap, grid, st);
         }
         if (e != hipSuccess) return hip_fail(e, "attend_kernel launch");
     }
