@@ -221,10 +221,29 @@ def rms_norm_rows(x: np.ndarray, w: np.ndarray | None, eps: float) -> np.ndarray
     return y
 
 
+def _other_groups(q, Hkv, call):
+    """GQA groups other than the reference kernel's 8 query heads per kv head: each query
+    head's output depends only on its own q row and its kv head's rows, so the group is run
+    in calls of 8 heads on that kv head alone (q padded with zero heads, their outputs
+    dropped).  call(kvh, q8) returns the [8, 512] outputs of q8 against kv head kvh."""
+    G = q.shape[0] // Hkv
+    out = np.empty((Hkv * G, 512), dtype=np.float64)
+    for kvh in range(Hkv):
+        for g0 in range(0, G, 8):
+            n = min(8, G - g0)
+            q8 = np.zeros((8, 512), dtype=np.uint16)
+            q8[:n] = q[kvh * G + g0:kvh * G + g0 + n]
+            out[kvh * G + g0:kvh * G + g0 + n] = call(kvh, q8)[:n]
+    return out
+
+
 def decode_raw_f64(q, raw, len_: int, kw, eps: float, inv_freq, scale: float = 1.0,
                    threads=None) -> np.ndarray:
     Hkv, pitch, D = raw.shape
-    assert D == 512 and q.shape == (Hkv * 8, 512)
+    assert D == 512 and q.shape[1] == 512 and q.shape[0] % Hkv == 0
+    if q.shape[0] != Hkv * 8:
+        return _other_groups(q, Hkv, lambda kvh, q8: decode_raw_f64(
+            q8, raw[kvh:kvh + 1], len_, kw, eps, inv_freq, scale, threads))
     out = np.empty((Hkv * 8, 512), dtype=np.float64)
     inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
     rc = lib().orc_decode_raw_f64(_ptr(q), _ptr(raw), Hkv, int(len_), pitch, _ptr(kw),
@@ -239,10 +258,13 @@ def decode_raw_q8_f64(q, qraw, sc, bs, len_: int, kw, eps: float, inv_freq, scal
                       threads=None) -> np.ndarray:
     """q8 raw stream: qraw [Hkv, pitch, 512] u8, sc / bs [Hkv, pitch] (or [Hkv, pitch, 1]) f32."""
     Hkv, pitch, D = qraw.shape
-    assert D == 512 and q.shape == (Hkv * 8, 512)
+    assert D == 512 and q.shape[1] == 512 and q.shape[0] % Hkv == 0
     qraw = np.ascontiguousarray(qraw, dtype=np.uint8)
     sc = np.ascontiguousarray(sc, dtype=np.float32).reshape(Hkv, pitch)
     bs = np.ascontiguousarray(bs, dtype=np.float32).reshape(Hkv, pitch)
+    if q.shape[0] != Hkv * 8:
+        return _other_groups(q, Hkv, lambda kvh, q8: decode_raw_q8_f64(
+            q8, qraw[kvh:kvh + 1], sc[kvh:kvh + 1], bs[kvh:kvh + 1], len_, kw, eps, inv_freq, scale, threads))
     out = np.empty((Hkv * 8, 512), dtype=np.float64)
     inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
     rc = lib().orc_decode_raw_q8_f64(_ptr(q), _ptr(qraw), _ptr(sc), _ptr(bs), Hkv, int(len_), pitch,

@@ -441,10 +441,11 @@ def _hf_raw_reference(q, raw, len_, kw, eps, inv, scale):
     s = torch.sin(emb).to(torch.bfloat16).float()
     k = (kn * c + rotate_half(kn) * s).to(torch.bfloat16).double()
     v = (x * rinv).double()
-    qq = torch.from_numpy(orc.from_bf16(q)).double().view(Hkv, 8, D)
+    G = q.shape[0] // Hkv
+    qq = torch.from_numpy(orc.from_bf16(q)).double().view(Hkv, G, D)
     sc = torch.einsum("hgd,htd->hgt", qq, k) * scale
     w = torch.softmax(sc, -1)
-    return torch.einsum("hgt,htd->hgd", w, v).reshape(Hkv * 8, D).numpy()
+    return torch.einsum("hgt,htd->hgd", w, v).reshape(Hkv * G, D).numpy()
 
 
 def test_raw_decode_matches_hf_rope_composition():
@@ -457,6 +458,31 @@ def test_raw_decode_matches_hf_rope_composition():
     ours = orc.decode_raw_f64(q, raw, L, kw, 1e-6, inv, scale=512 ** -0.5)
     ref = _hf_raw_reference(q, raw, L, kw, 1e-6, inv, 512 ** -0.5)
     assert np.abs(ours - ref).max() < 2e-3
+
+
+@pytest.mark.parametrize("G", [1, 3, 16])
+def test_raw_decode_other_gqa_groups(G):
+    """Groups other than 8 query heads per kv head (run as calls of 8 heads on one kv head):
+    every head against the HF composition, and each head's output the same as in a call that
+    holds it among 8 heads of the group-8 form."""
+    rng = np.random.default_rng(50 + G)
+    Hkv, pitch, L = 2, 48, 41
+    raw = orc.to_bf16(rng.standard_normal((Hkv, pitch, 512)).astype(np.float32) * 3)
+    q = rms_rows(rng, (Hkv * G, 512))
+    kw = orc.to_bf16((1.0 + 0.1 * rng.standard_normal(512)).astype(np.float32))
+    inv = orc.rope_inv_freq(512, 1.0e6, 0.25)
+    ours = orc.decode_raw_f64(q, raw, L, kw, 1e-6, inv, scale=512 ** -0.5)
+    assert ours.shape == (Hkv * G, 512)
+    assert np.abs(ours - _hf_raw_reference(q, raw, L, kw, 1e-6, inv, 512 ** -0.5)).max() < 2e-3
+    # head h of kv head 1 placed at slot 5 of a group-8 call on both kv heads
+    h = Hkv * G - 1
+    q8 = rms_rows(rng, (Hkv * 8, 512))
+    q8[8 + 5] = q[h]
+    assert np.array_equal(orc.decode_raw_f64(q8, raw, L, kw, 1e-6, inv, scale=512 ** -0.5)[8 + 5], ours[h])
+    qraw, sc, bs = orc.quantize_rows(raw)
+    a = orc.decode_raw_q8_f64(q, qraw, sc, bs, L, kw, 1e-6, inv, scale=512 ** -0.5)
+    b = orc.decode_raw_q8_f64(q8, qraw, sc, bs, L, kw, 1e-6, inv, scale=512 ** -0.5)
+    assert a.shape == (Hkv * G, 512) and np.array_equal(b[8 + 5], a[h])
 
 
 def test_rinv_nudge_moves_the_row_norm_by_whole_ulps():

@@ -104,8 +104,8 @@ def run_raw(name, *, B=1, Hq=32, Hkv=4, cap, pos, scale=1.0, seed=0, split_rows=
     return o, errs
 
 
-# table=True is the ES layer's form (precomputed rotary table, two kv heads per workgroup):
-# the wave-private-ring kernel; table=False the 8-wave kernel that computes its cos / sin.
+# table=True is the ES layer's form (precomputed rotary table): the wave-private-ring kernel;
+# table=False the 8-wave kernel that computes its cos / sin.
 TABLE = pytest.mark.parametrize("table", [False, True], ids=["own-sincos", "table"])
 
 
@@ -199,7 +199,7 @@ def test_raw_randomized_configurations(seed):
 
 @pytest.mark.parametrize("seed", [23, 29])
 def test_raw_table_in_model_scale_one_ragged_batch(seed):
-    """The ES layer's raw-K form (precomputed rotary table, two kv heads per workgroup) at the
+    """The ES layer's raw-K form (precomputed rotary table) at the
     in-model scale 1.0 over a ragged batch with appends, each sequence against the fp64 oracle
     with the conditioning allowance of _check_conditioned: on seed 23 one sequence has a
     near-tied pair of keys where a one-ulp change of rinv alone moves the oracle's output by
@@ -214,14 +214,25 @@ def test_raw_batched_ragged_positions(table):
     run_raw("batched", B=3, cap=4096, pos=[17, 2500, 4095], scale=512 ** -0.5, seed=7, table=table)
 
 
-def test_raw_unpacked_odd_kv_heads():
-    """Three kv heads cannot pair up: one kv head per workgroup (16 rows per stage)."""
-    run_raw("unpacked-hkv3", B=2, Hq=24, Hkv=3, cap=1024, pos=[1000, 333], scale=512 ** -0.5, seed=19)
+@TABLE
+def test_raw_odd_kv_heads(table):
+    """Three kv heads over a two-sequence batch: workgroups of every kv head of each sequence."""
+    run_raw("hkv3", B=2, Hq=24, Hkv=3, cap=1024, pos=[1000, 333], scale=512 ** -0.5, seed=19, table=table)
 
 
-def test_raw_unpacked_single_kv_head():
-    """One kv head (8 query heads, the reference kernel's group): nothing to pair with."""
-    run_raw("unpacked-hkv1", Hq=8, Hkv=1, cap=1500, pos=[1499], scale=512 ** -0.5, seed=21)
+@TABLE
+def test_raw_single_kv_head(table):
+    """One kv head with the reference kernel's group of 8 query heads."""
+    run_raw("hkv1", Hq=8, Hkv=1, cap=1500, pos=[1499], scale=512 ** -0.5, seed=21, table=table)
+
+
+@TABLE
+@pytest.mark.parametrize("G", [1, 3, 16])
+def test_raw_gqa_group_sizes(G, table):
+    """GQA groups other than 8: the query heads fill G of the MFMA's 16 columns (the rest are
+    zero padding), from one query head per kv head to the full 16."""
+    run_raw(f"gqa{G}", B=2, Hq=2 * G, Hkv=2, cap=1024, pos=[1023, 611], scale=512 ** -0.5, seed=31 + G,
+            table=table)
 
 
 @TABLE

@@ -102,8 +102,8 @@ def run_q8(name, *, B=1, Hq=32, Hkv=4, cap, pos, scale=1.0, seed=0, split_rows=0
     return o, errs
 
 
-# table=True is the ES layer's form (precomputed rotary table, two kv heads per workgroup):
-# the wave-private-ring kernel; table=False the 8-wave kernel that computes its cos / sin.
+# table=True is the ES layer's form (precomputed rotary table): the wave-private-ring kernel;
+# table=False the 8-wave kernel that computes its cos / sin.
 TABLE = pytest.mark.parametrize("table", [False, True], ids=["own-sincos", "table"])
 
 
@@ -118,7 +118,7 @@ def test_q8_in_model_scale_one(table):
 
 
 def test_q8_long_context_131072():
-    """The C4 shape over a q8 raw stream: 131072 rows, two kv heads per workgroup."""
+    """The C4 shape over a q8 raw stream: 131072 rows (the 8-wave kernel, its own cos / sin)."""
     run_q8("c4-q8", cap=131072, pos=[131071], scale=512 ** -0.5, seed=5)
 
 
@@ -138,8 +138,17 @@ def test_q8_split_sizes(split_rows, table):
     run_q8(f"split{split_rows}", cap=1024, pos=[777], split_rows=split_rows, seed=11, table=table)
 
 
-def test_q8_unpacked_odd_kv_heads():
-    run_q8("unpacked-hkv3", B=2, Hq=24, Hkv=3, cap=1024, pos=[1000, 333], scale=512 ** -0.5, seed=19)
+@TABLE
+def test_q8_odd_kv_heads(table):
+    run_q8("hkv3", B=2, Hq=24, Hkv=3, cap=1024, pos=[1000, 333], scale=512 ** -0.5, seed=19, table=table)
+
+
+@TABLE
+@pytest.mark.parametrize("G", [1, 16])
+def test_q8_gqa_group_sizes(G, table):
+    """GQA groups other than 8 (the kernels take any group up to the MFMA's 16 columns)."""
+    run_q8(f"gqa{G}", B=2, Hq=2 * G, Hkv=2, cap=1024, pos=[1023, 611], scale=512 ** -0.5, seed=41 + G,
+           table=table)
 
 
 def _degenerate_rows(x, rng):
