@@ -36,7 +36,7 @@ EXPORTS = (
     "esda_cache_decode_raw_q8", "esda_decode_attn_global_q8",
     # include/esda_prefill.h
     "esda_prefill_workspace_size", "esda_prefill", "esda_prefill_stages", "esda_raw_prefill_kv",
-    "esda_raw_q8_prefill_kv", "esda_cache_prefill", "esda_cache_prefill_raw",
+    "esda_raw_q8_prefill_kv", "esda_cache_prefill", "esda_cache_prefill_raw", "esda_lds_read",
 )
 _VOID = ("esda_cache_destroy", "esda_cache_mark_step", "esda_cache_reset", "esda_cache_clear_rewind_mark")
 
@@ -168,6 +168,7 @@ def lib() -> ctypes.CDLL:
         L.esda_rope_table.argtypes = [P, i32, P, P]
         L.esda_fill_i32.argtypes = [P, i32, i32, P]
         L.esda_stream_read.argtypes = [P, sz, i32, P, P]
+        L.esda_lds_read.argtypes = [i32, i32, i32, i32, P, P]
         L.esda_last_error.restype = ctypes.c_char_p
         L.esda_last_error.argtypes = []
         L.esda_version.argtypes = []

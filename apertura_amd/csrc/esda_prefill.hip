@@ -540,6 +540,52 @@ __global__ __launch_bounds__(256) void raw_prefill_kv_kernel(RawKvParams p) {
     }
 }
 
+// ------------------------------------------------------------ LDS read ceiling
+//
+// The read rate of the LDS on the prefill kernel's two read forms, for its roofline: each
+// wave of W reads its 4 KB share of a 64 KB array, 8 reads in flight per round, with the
+// QK operand's 128-bit row reads (TR = false) or the PV operand's 64-bit transpose reads
+// ds_read_b64_tr_b16 (TR = true), every lane group of a read on consecutive addresses
+// (bank-conflict-free).  Every address is masked into the array.
+template <int W, bool TR>
+__global__ __launch_bounds__(64 * W, 1) void lds_read_kernel(int iters, unsigned *sink) {
+    __shared__ __attribute__((aligned(16))) unsigned char buf[65536];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < 65536 / 4; i += 64 * W) reinterpret_cast<unsigned *>(buf)[i] = (unsigned) i * 2654435761u;
+    __syncthreads();
+    const unsigned base = lds_addr(buf);
+    constexpr unsigned kStep = TR ? 512u : 1024u, kLane = TR ? 8u : 16u;
+    unsigned acc = 0u;
+    // The wait names the read registers as operands, so that no use of them is scheduled
+    // above it (the compiler does not count the assembly reads).
+    for (int it = 0; it < iters; ++it) {
+        unsigned a[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            a[u] = base + (((unsigned) (it * 8 + u) * kStep + (unsigned) wave * 4096u + (unsigned) lane * kLane) & 65535u);
+        if constexpr (TR) {
+            u32x2 y[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(y[u]) : "v"(a[u]));
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]), "+v"(y[4]), "+v"(y[5]), "+v"(y[6]), "+v"(y[7])
+                         :: "memory");
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc ^= y[u][0] ^ y[u][1];
+        } else {
+            u32x4 x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) asm volatile("ds_read_b128 %0, %1" : "=v"(x[u]) : "v"(a[u]));
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7])
+                         :: "memory");
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc ^= x[u][0] ^ x[u][1] ^ x[u][2] ^ x[u][3];
+        }
+    }
+    sink[(size_t) blockIdx.x * 64 * W + tid] = acc;
+}
+
 // ------------------------------------------------------------ host side
 
 int fail(int code, const std::string &msg) {
@@ -788,6 +834,26 @@ int esda_raw_q8_prefill_kv(const void *q8, int64_t q_head_stride, const float *s
     p.k = static_cast<uint16_t *>(k_out);
     p.v = static_cast<uint16_t *>(v_out);
     return run_raw_kv(p, 512, true, static_cast<hipStream_t>(stream));
+}
+
+int esda_lds_read(int32_t waves, int32_t transpose, int32_t iters, int32_t workgroups, uint32_t *sink,
+                  void *stream) {
+    if (!sink) return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_lds_read: null sink");
+    if (iters <= 0 || workgroups <= 0 || workgroups > 65535)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_lds_read: iters must be positive, workgroups in 1 .. 65535");
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid(workgroups);
+    const bool tr = transpose != 0;
+    if (waves != 4 && waves != 8 && waves != 16)
+        return fail(ESDA_ERR_INVALID_ARGUMENT, "esda_lds_read: waves must be 4, 8 or 16");
+    if (waves == 4 && tr) hipLaunchKernelGGL((lds_read_kernel<4, true>), grid, dim3(256), 0, st, iters, sink);
+    if (waves == 4 && !tr) hipLaunchKernelGGL((lds_read_kernel<4, false>), grid, dim3(256), 0, st, iters, sink);
+    if (waves == 8 && tr) hipLaunchKernelGGL((lds_read_kernel<8, true>), grid, dim3(512), 0, st, iters, sink);
+    if (waves == 8 && !tr) hipLaunchKernelGGL((lds_read_kernel<8, false>), grid, dim3(512), 0, st, iters, sink);
+    if (waves == 16 && tr) hipLaunchKernelGGL((lds_read_kernel<16, true>), grid, dim3(1024), 0, st, iters, sink);
+    if (waves == 16 && !tr) hipLaunchKernelGGL((lds_read_kernel<16, false>), grid, dim3(1024), 0, st, iters, sink);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? ESDA_OK : fail(ESDA_ERR_HIP, std::string("lds_read_kernel launch: ") + hipGetErrorString(e));
 }
 
 }  // extern "C"

@@ -167,6 +167,9 @@ def main() -> int:
                          "the measured read ceiling and the counter calibration for that path")
     ap.add_argument("--read-workgroups", type=int, default=0,
                     help="calibrate-read: workgroups per launch (0: sweep 256 .. 2048)")
+    ap.add_argument("--calibrate-lds", action="store_true",
+                    help="measure the LDS read rate of the prefill kernel's operand reads instead "
+                         "(esda_lds_read: 128-bit row reads and 64-bit transpose reads, 4 / 8 / 16 waves per CU)")
     args = ap.parse_args()
     if args.cpu_threads <= 0:
         args.cpu_threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or os.cpu_count() or 1
@@ -184,6 +187,8 @@ def main() -> int:
         return calibrate_copy(args)
     if args.calibrate_read:
         return calibrate_read(args)
+    if args.calibrate_lds:
+        return calibrate_lds(args)
     if args.workload == "c5":
         return bench_c5(args)
     if args.workload in PREFILL_WORKLOADS:
@@ -451,6 +456,42 @@ def calibrate_read(args) -> int:
     print(json.dumps({"calibration": "stream read (global_load_lds_dwordx4 nt, esda_stream_read)",
                       "bytes_read": n, "best": best, "sweep": results,
                       "frac_of_8TBs": round(best["GB/s"] / PEAK_HBM_GBS, 4)}), flush=True)
+    return 0
+
+
+def calibrate_lds(args) -> int:
+    """LDS read rate of the prefill kernel's two operand read forms (esda_lds_read), one
+    workgroup per CU of 4, 8 or 16 waves, timed with HIP events on the launch stream: the
+    ceiling its per-stage LDS bytes are priced against."""
+    import torch
+
+    from apertura_amd._lib import check, lib
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 4000
+    stream = torch.cuda.current_stream()
+    results = []
+    for tr in (0, 1):
+        for waves in (4, 8, 16):
+            sink = torch.zeros(cus * waves * 64, dtype=torch.int32, device="cuda:0")
+
+            def launch():
+                check(lib().esda_lds_read(waves, tr, iters, cus, sink.data_ptr(), stream.cuda_stream))
+
+            warm_up(launch, max(1, args.warmup), 0.5)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(args.steps):
+                launch()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / args.steps
+            n = cus * waves * 64 * iters * 8 * (8 if tr else 16)
+            results.append({"read": "ds_read_b64_tr_b16" if tr else "ds_read_b128", "waves_per_cu": waves,
+                            "us": round(ms * 1e3, 3), "TB/s": round(n / (ms * 1e-3) / 1e12, 2),
+                            "GB/s_per_cu": round(n / (ms * 1e-3) / 1e9 / cus, 1)})
+    print(json.dumps({"calibration": "LDS read rate (esda_lds_read)", "cus": cus, "workgroups": cus,
+                      "results": results}), flush=True)
     return 0
 
 

@@ -96,6 +96,16 @@ int esda_raw_q8_prefill_kv(const void *q8, int64_t q_head_stride, const float *s
                            int32_t pos0, void *k_out, void *v_out, int64_t out_head_stride,
                            void *stream);
 
+/* LDS read ceiling of the prefill kernel's two operand read forms (no counterpart in the
+ * reference: a measurement for the prefill kernel's roofline, like esda_stream_read for
+ * the decode rings).  Each of `workgroups` workgroups of `waves` waves (4, 8 or 16) reads
+ * a 64 KB LDS array for iters rounds of 8 reads per lane: 128-bit row reads
+ * (transpose = 0) or 64-bit transpose reads ds_read_b64_tr_b16 (transpose != 0), 1 KB
+ * (512 B) per wave per read, bank-conflict-free.  Bytes read: workgroups * waves * 64 *
+ * iters * 8 * (16 or 8).  sink: workgroups * waves * 64 words (a checksum per thread). */
+int esda_lds_read(int32_t waves, int32_t transpose, int32_t iters, int32_t workgroups, uint32_t *sink,
+                  void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -276,3 +276,32 @@ def test_raw_prefill_end_to_end():
     err = np.abs(orc.from_bf16(_host(out)).astype(np.float64) - ref)
     print(f"[raw-prefill] max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
     assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN
+
+
+def test_lds_read_probe_reads_the_array():
+    """esda_lds_read (the LDS read-rate probe priced against in the prefill roofline) reads
+    what it wrote: each thread's checksum of its 128-bit row reads equals the host's
+    restatement of the array (word i = i * 2654435761 mod 2^32) over the same addresses; the
+    transpose-read form gives the same checksums on two calls."""
+    from apertura_amd._lib import check, lib
+    W, iters, wgs = 8, 3, 2
+    words = (np.arange(16384, dtype=np.uint64) * 2654435761 % (1 << 32)).astype(np.uint32)
+    want = np.zeros(W * 64, dtype=np.uint32)
+    for tid in range(W * 64):
+        wave, lane = tid >> 6, tid & 63
+        acc = np.uint32(0)
+        for it in range(iters):
+            for u in range(8):
+                a = ((it * 8 + u) * 1024 + wave * 4096 + lane * 16) & 65535
+                acc ^= np.bitwise_xor.reduce(words[a // 4:a // 4 + 4])
+        want[tid] = acc
+    stream = torch.cuda.current_stream().cuda_stream
+    sink = torch.zeros(wgs * W * 64, dtype=torch.int32, device="cuda")
+    check(lib().esda_lds_read(W, 0, iters, wgs, sink.data_ptr(), stream))
+    got = sink.cpu().numpy().view(np.uint32).reshape(wgs, W * 64)
+    assert (got == want[None]).all()
+    tr = [torch.zeros(wgs * W * 64, dtype=torch.int32, device="cuda") for _ in range(2)]
+    for t in tr:
+        check(lib().esda_lds_read(W, 1, iters, wgs, t.data_ptr(), stream))
+    assert torch.equal(tr[0], tr[1]) and bool((tr[0] != 0).any())
+    assert lib().esda_lds_read(5, 0, iters, wgs, sink.data_ptr(), stream) != 0  # waves 4, 8 or 16 only
