@@ -34,8 +34,36 @@ def _host(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
+def _decode_every_row(qd, kd, vd, out, q_pos0, scale):
+    """Every query row of a causal global prefill (keys at positions 0 ..) against the decode
+    kernel at that row's position: a B = 1 decode of the row's q over the keys as a
+    [1, Hkv, Sk, D] cache, appending the row at its own position as itself (the same bytes).
+    The two kernels tile the work differently (query tiles and key stages against split-K
+    rows); each is held to the fp64 oracle separately, and here to each other at the same
+    bars over every row."""
+    from apertura_amd.decode import DecodeStep, decode_step, new_workspace
+    Hq, Sq, D = qd.shape
+    Hkv, Sk, _ = kd.shape
+    step = DecodeStep(batch=1, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D, cap=Sk, scale=scale)
+    ws = new_workspace(step, "cuda")
+    kc, vc = kd.reshape(1, Hkv, Sk, D), vd.reshape(1, Hkv, Sk, D)
+    worst, total = 0.0, 0.0
+    for i in range(Sq):
+        p = q_pos0 + i
+        o = decode_step(step, qd[:, i].contiguous().view(1, Hq, D), kd[:, p].contiguous().view(1, Hkv, D),
+                        vd[:, p].contiguous().view(1, Hkv, D), kc, vc,
+                        torch.tensor([p], dtype=torch.int32, device="cuda"), None, workspace=ws)
+        d = (out[i].float() - o[0].float()).abs()
+        worst = max(worst, float(d.max()))
+        total += float(d.sum())
+    torch.cuda.synchronize()
+    mean = total / (Sq * Hq * D)
+    print(f"[prefill] every row against decode: max_abs={worst:.3e} mean_abs={mean:.3e}", flush=True)
+    assert worst <= TOL_MAX and mean <= TOL_MEAN
+
+
 def run_prefill(name, *, Hq, Hkv, D, Sq, Sk, q_pos0, k_pos0, window=0, split_keys=0, seed=0,
-                layout="dense", shared=False, rows=None, fault=0):
+                layout="dense", shared=False, rows=None, fault=0, decode_rows=False):
     from apertura_amd.prefill import PrefillStep, prefill
     print(f"\n[prefill] {name}: Hq={Hq} Hkv={Hkv} D={D} Sq={Sq} Sk={Sk} q_pos0={q_pos0} k_pos0={k_pos0} "
           f"window={window} split_keys={split_keys} layout={layout} shared={shared}", flush=True)
@@ -80,6 +108,9 @@ def run_prefill(name, *, Hq, Hkv, D, Sq, Sk, q_pos0, k_pos0, window=0, split_key
     print(f"[prefill] {name}: max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
     if not fault:
         assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN, name
+    if decode_rows:
+        assert layout == "dense" and k_pos0 == 0 and window == 0 and Sk == q_pos0 + Sq
+        _decode_every_row(qd, kd, vd, out, q_pos0, scale)
     return err
 
 
@@ -160,18 +191,21 @@ def test_single_query_and_single_key():
 
 def test_chunked_prefill_benchmark_shape_sampled_rows():
     """512 queries over a 16384-key global cache (the p512g benchmark shape, two key splits):
-    25 query rows (all heads) on the 16-position tile edges, in the middle and at both ends; a
-    full check would take ~1 min of fp64 host time (541 GFLOP)."""
+    25 query rows (all heads) against the fp64 oracle, on the 16-position tile edges, in the
+    middle and at both ends (a full fp64 check would take ~1 min of host time, 541 GFLOP),
+    and every row against the decode kernel at its position."""
     run_prefill("bench-global", Hq=32, Hkv=4, D=512, Sq=512, Sk=16384, q_pos0=15872, k_pos0=0, seed=10,
                 rows=[0, 1, 15, 16, 17, 31, 32, 100, 127, 128, 200, 255, 256, 300, 383, 384, 400, 447, 448,
-                      480, 495, 496, 500, 510, 511])
+                      480, 495, 496, 500, 510, 511], decode_rows=True)
 
 
 def test_global_fresh_prefill_benchmark_shape_sampled_rows():
     """4096 fresh tokens of a global layer (causal, D=512, GQA 32/4; the p4kg benchmark
-    shape): 16 query rows (all heads) on tile edges, in the middle and at both ends."""
+    shape): 16 query rows (all heads) against the fp64 oracle on tile edges, in the middle and
+    at both ends, and every row against the decode kernel at its position."""
     run_prefill("bench-global-fresh", Hq=32, Hkv=4, D=512, Sq=4096, Sk=4096, q_pos0=0, k_pos0=0, seed=17,
-                rows=[0, 1, 15, 16, 17, 127, 128, 1000, 2047, 2048, 2049, 3000, 4079, 4080, 4094, 4095])
+                rows=[0, 1, 15, 16, 17, 127, 128, 1000, 2047, 2048, 2049, 3000, 4079, 4080, 4094, 4095],
+                decode_rows=True)
 
 
 @pytest.mark.parametrize("seed", range(14))
