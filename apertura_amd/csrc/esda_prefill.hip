@@ -104,22 +104,24 @@ __host__ __device__ inline void tile_keys(const PrefillParams &p, int tile, int 
 // each wave's work per stage and the barriers per stage stay those of the plain kernel.
 constexpr int kWaves = 8;
 
-template <int D, int NSL>
+template <int D, int NSL, int NT = 2>
 struct PRing {
     static constexpr int NI = D / 32;                 // DMA blocks per 16-key half
     static constexpr int HB = NI * kBlk;              // one half stage of one tensor
-    static constexpr int BYTES = 4 * NSL * HB;        // NSL K stages, then NSL V stages
+    static constexpr int BYTES = 2 * NT * NSL * HB;   // NSL K stages, then NSL V stages (NT = 2)
     static constexpr int CPR = D / 8;                 // 16-byte chunks per row
     static_assert(BYTES <= kRingBudget, "the K / V slots must fit the LDS budget");
     __host__ __device__ static constexpr int off(int r) { return (r % NI) * kBlk + (r / NI) * 2 * D; }
 };
 
-template <int D, int QB, bool KH = false>
+// SH: V is the K buffer (attention_k_eq_v): one tensor streams, and PV reads V^T from the
+// stage's K slot.
+template <int D, int QB, bool KH = false, bool SH = false>
 __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p) {
     constexpr int NQW = KH ? kWaves / 2 : kWaves;  // waves with distinct query blocks
     constexpr int NSL = KH ? 4 : 2;                // ring stages per tensor
     constexpr int SPI = KH ? 2 : 1;                // stages per iteration (one per wave group)
-    using R = PRing<D, NSL>;
+    using R = PRing<D, NSL, SH ? 1 : 2>;
     constexpr int QT = 16 * QB * NQW;   // query rows per tile
     constexpr int KS = D / 32;          // QK k-steps
     constexpr int DT = D / 16;          // PV dim tiles
@@ -210,7 +212,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
     }
     static_assert((NSL & (NSL - 1)) == 0, "stage slots: a power of two");
     auto kslot = [&](int s) { return ring + (s & (NSL - 1)) * 2 * R::HB; };
-    auto vslot = [&](int s) { return ring + 2 * NSL * R::HB + (s & (NSL - 1)) * 2 * R::HB; };
+    auto vslot = [&](int s) { return SH ? kslot(s) : ring + 2 * NSL * R::HB + (s & (NSL - 1)) * 2 * R::HB; };
     auto issue = [&](const uint16_t *head, int s, unsigned char *slot) {
         const int jb = j0 + s * kStageKeys;
         if (jb + kStageKeys <= j1) {
@@ -266,10 +268,10 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
     };
 
     issue(kvb, 0, kslot(0));  // nst >= 1 here
-    issue(vvb, 0, vslot(0));
+    if (!SH) issue(vvb, 0, vslot(0));
     if (KH && nst > 1) {
         issue(kvb, 1, kslot(1));
-        issue(vvb, 1, vslot(1));
+        if (!SH) issue(vvb, 1, vslot(1));
     }
 
     for (int s0 = 0; s0 < nst; s0 += SPI) {
@@ -279,11 +281,11 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
         lds_barrier();
         if (s0 + SPI < nst) {
             issue(kvb, s0 + SPI, kslot(s0 + SPI));
-            issue(vvb, s0 + SPI, vslot(s0 + SPI));
+            if (!SH) issue(vvb, s0 + SPI, vslot(s0 + SPI));
         }
         if (KH && s0 + SPI + 1 < nst) {
             issue(kvb, s0 + SPI + 1, kslot(s0 + SPI + 1));
-            issue(vvb, s0 + SPI + 1, vslot(s0 + SPI + 1));
+            if (!SH) issue(vvb, s0 + SPI + 1, vslot(s0 + SPI + 1));
         }
         const int s = s0 + kh;  // this wave group's stage
         if (KH && s >= nst) continue;  // an odd stage count: the odd group's last iteration is empty
@@ -697,8 +699,10 @@ template <int D>
 void launch_prefill(const PrefillParams &p, int stages, hipStream_t st) {
     if (stages & 1) {
         const dim3 grid(p.tiles * p.Hkv * p.splits), block(64 * kWaves);
-        if constexpr (D == 512)
-            hipLaunchKernelGGL((prefill_kernel<512, 1>), grid, block, 0, st, p);
+        if constexpr (D == 512) {
+            if (p.k == p.v) hipLaunchKernelGGL((prefill_kernel<512, 1, false, true>), grid, block, 0, st, p);
+            else hipLaunchKernelGGL((prefill_kernel<512, 1>), grid, block, 0, st, p);
+        }
         else if constexpr (D == 128)
             hipLaunchKernelGGL((prefill_kernel<128, 2>), grid, block, 0, st, p);
         else if (p.qb == 2)

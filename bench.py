@@ -13,7 +13,7 @@ write + new-row read and write.  `roofline` prices the dominant kernel (the spli
 attend kernel, timed alone with HIP events on the launch stream); `cpu_baseline` times
 the CPU oracle's reference-rounding restatement on the same inputs.
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c2|c1|c3|c4raw|c4q8|c5|p512g|p4kg|p512l|p4kl] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c2|c1|c3|c4raw|c4q8|c5|p512g|p4kg|p512gs|p4kgs|p512l|p4kl] [--no-cpu]
 
 Workload c5 is the full Gemma-4-31B-shaped attention step: 60 layers (every 6th
 global: D=512, Hkv=4, k_eq_v, linear caches; the rest local: D=256, Hkv=16, window
@@ -25,8 +25,10 @@ Workloads p512g / p4kg / p512l / p4kl are the prefill side (esda_prefill): a 512
 chunk over a 16384-token global cache (the reference's own prefill decomposition shape:
 d512, nKV 4, groups 8, seqQ 512 at 16K, WIDE_HEAD_ATTENTION.md), a fresh 4096-token
 global prefill, a 512-token chunk of a local layer (D=256, Hkv=16, window 1024 over
-window + chunk keys) and a fresh 4096-token local prefill (window 1024).  They report TFLOP/s of algorithmic attention FLOPs (4 * D per
-visible (query head, key) pair) against the bf16 MFMA peak.
+window + chunk keys) and a fresh 4096-token local prefill (window 1024); p512gs / p4kgs are
+the two global shapes over one K = V buffer (attention_k_eq_v).  They report TFLOP/s of
+algorithmic attention FLOPs (4 * D per visible (query head, key) pair) against the bf16 MFMA
+peak.
 """
 from __future__ import annotations
 
@@ -71,6 +73,14 @@ PREFILL_WORKLOADS = {
                   name="global-layer prefill chunk: 512 queries over 16384 keys (causal), D=512, GQA 32/4"),
     "p4kg": dict(Hq=32, Hkv=4, D=512, Sq=4096, Sk=4096, q_pos0=0, k_pos0=0, window=0, scale=512 ** -0.5,
                  name="global-layer fresh prefill: 4096 tokens (causal), D=512, GQA 32/4"),
+    # the same two over one K = V buffer (attention_k_eq_v, the global layers' layout): the
+    # kernel streams the buffer once and reads V^T from the K stage
+    "p512gs": dict(Hq=32, Hkv=4, D=512, Sq=512, Sk=16384, q_pos0=15872, k_pos0=0, window=0, scale=512 ** -0.5,
+                   shared=True, name="global-layer prefill chunk, k_eq_v (V = K): 512 queries over 16384 keys "
+                                     "(causal), D=512, GQA 32/4"),
+    "p4kgs": dict(Hq=32, Hkv=4, D=512, Sq=4096, Sk=4096, q_pos0=0, k_pos0=0, window=0, scale=512 ** -0.5,
+                  shared=True, name="global-layer fresh prefill, k_eq_v (V = K): 4096 tokens (causal), D=512, "
+                                    "GQA 32/4"),
     "p4kl": dict(Hq=32, Hkv=16, D=256, Sq=4096, Sk=4096, q_pos0=0, k_pos0=0, window=1024, scale=1 / 16,
                  name="local-layer fresh prefill: 4096 tokens, window 1024, D=256, GQA 32/16"),
     "p512l": dict(Hq=32, Hkv=16, D=256, Sq=512, Sk=1536, q_pos0=15872, k_pos0=15872 + 512 - 1536, window=1024,
@@ -522,7 +532,8 @@ def bench_prefill(args) -> int:
         return x.to(torch.bfloat16)
 
     Hq, Hkv, D, Sq, Sk = w["Hq"], w["Hkv"], w["D"], w["Sq"], w["Sk"]
-    q, k, v = rms_bf16((Hq, Sq, D)), rms_bf16((Hkv, Sk, D)), rms_bf16((Hkv, Sk, D))
+    q, k = rms_bf16((Hq, Sq, D)), rms_bf16((Hkv, Sk, D))
+    v = k if w.get("shared") else rms_bf16((Hkv, Sk, D))
     out = torch.empty((Sq, Hq, D), dtype=torch.bfloat16, device=dev)
     step = PrefillStep(num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D, seq_q=Sq, seq_k=Sk, q_pos0=w["q_pos0"],
                        k_pos0=w["k_pos0"], window=w["window"], scale=w["scale"])

@@ -7,7 +7,8 @@ ESAttention.mm:188, ESGemma4TextModel.mm:68-83, ESAttention.mm:17-22).  Shapes c
 Gemma-4's global (D=512, 8 query heads per kv head) and local (D=256, 2 per kv head,
 sliding window with evicted keys) layers, fresh causal prefill and chunks after a cached
 past, tiles padded past the last query, key splits (automatic, forced, empty), strided
-query / cache / output layouts, a shared K = V buffer, and both query-block
+query / cache / output layouts, a shared K = V buffer (the single-stream kernel at D = 512,
+with key splits, at the p512gs benchmark shape and in the randomized cases), and both query-block
 configurations of head dim 256 (one and two 16-query blocks per wave).  At the local
 benchmark shapes (4096 fresh tokens of a sliding layer; 512 queries over window + chunk) every
 row is checked; at 512 queries over 16384 global keys 25 sampled query rows (query rows are
@@ -44,14 +45,16 @@ def _decode_every_row(qd, kd, vd, out, q_pos0, scale):
     from apertura_amd.decode import DecodeStep, decode_step, new_workspace
     Hq, Sq, D = qd.shape
     Hkv, Sk, _ = kd.shape
-    step = DecodeStep(batch=1, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D, cap=Sk, scale=scale)
+    shared = vd.data_ptr() == kd.data_ptr()  # one K = V buffer: the decode's k_eq_v form
+    step = DecodeStep(batch=1, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D, cap=Sk, kv_shared=shared,
+                      scale=scale)
     ws = new_workspace(step, "cuda")
     kc, vc = kd.reshape(1, Hkv, Sk, D), vd.reshape(1, Hkv, Sk, D)
     worst, total = 0.0, 0.0
     for i in range(Sq):
         p = q_pos0 + i
         o = decode_step(step, qd[:, i].contiguous().view(1, Hq, D), kd[:, p].contiguous().view(1, Hkv, D),
-                        vd[:, p].contiguous().view(1, Hkv, D), kc, vc,
+                        None if shared else vd[:, p].contiguous().view(1, Hkv, D), kc, vc,
                         torch.tensor([p], dtype=torch.int32, device="cuda"), None, workspace=ws)
         d = (out[i].float() - o[0].float()).abs()
         worst = max(worst, float(d.max()))
@@ -184,6 +187,14 @@ def test_shared_k_equals_v_buffer():
                 layout="strided")
 
 
+@pytest.mark.parametrize("split_keys", [0, 32, 96, 4096])
+def test_shared_k_equals_v_with_key_splits(split_keys):
+    """One K = V buffer (the kernel's single-stream form: V^T read from the K stage) over a
+    cached past, with automatic, forced and empty key splits."""
+    run_prefill(f"shared-splits{split_keys}", Hq=32, Hkv=4, D=512, Sq=70, Sk=700, q_pos0=630, k_pos0=0,
+                seed=31 + split_keys, shared=True, split_keys=split_keys)
+
+
 def test_single_query_and_single_key():
     run_prefill("one-by-one", Hq=4, Hkv=1, D=256, Sq=1, Sk=1, q_pos0=0, k_pos0=0, seed=8)
     run_prefill("one-query", Hq=32, Hkv=4, D=512, Sq=1, Sk=513, q_pos0=512, k_pos0=0, seed=9)
@@ -195,6 +206,16 @@ def test_chunked_prefill_benchmark_shape_sampled_rows():
     middle and at both ends (a full fp64 check would take ~1 min of host time, 541 GFLOP),
     and every row against the decode kernel at its position."""
     run_prefill("bench-global", Hq=32, Hkv=4, D=512, Sq=512, Sk=16384, q_pos0=15872, k_pos0=0, seed=10,
+                rows=[0, 1, 15, 16, 17, 31, 32, 100, 127, 128, 200, 255, 256, 300, 383, 384, 400, 447, 448,
+                      480, 495, 496, 500, 510, 511], decode_rows=True)
+
+
+def test_shared_chunk_benchmark_shape_sampled_rows():
+    """The p512gs benchmark shape (512 queries over 16384 keys of one K = V buffer): 25
+    query rows against the fp64 oracle and every row against the decode kernel at its
+    position."""
+    run_prefill("bench-global-shared", Hq=32, Hkv=4, D=512, Sq=512, Sk=16384, q_pos0=15872, k_pos0=0, seed=12,
+                shared=True,
                 rows=[0, 1, 15, 16, 17, 31, 32, 100, 127, 128, 200, 255, 256, 300, 383, 384, 400, 447, 448,
                       480, 495, 496, 500, 510, 511], decode_rows=True)
 
@@ -223,9 +244,12 @@ def test_randomized_shapes_sampled_rows(seed):
     k_pos0 = max(0, past - window) if window else 0
     Sk = past + Sq - k_pos0
     rows = sorted({int(x) for x in r.integers(0, Sq, 8)} | {Sq - 1})
+    split_keys = int(r.choice([0, 0, 32, 96]))
+    layout = "dense" if r.integers(0, 2) == 0 else "strided"
+    shared = bool(r.integers(0, 2))  # one K = V buffer (drawn last: the other draws stay as they were)
     run_prefill(f"random-{seed}", Hq=Hq, Hkv=Hkv, D=D, Sq=Sq, Sk=Sk, q_pos0=past, k_pos0=k_pos0,
-                window=window, split_keys=int(r.choice([0, 0, 32, 96])), seed=4000 + seed,
-                layout="dense" if r.integers(0, 2) == 0 else "strided", rows=rows)
+                window=window, split_keys=split_keys, seed=4000 + seed, layout=layout, rows=rows,
+                shared=shared)
 
 
 def test_diagonal_fault_in_the_oracle_is_detected():
