@@ -115,12 +115,14 @@ struct PRing {
 };
 
 // SH: V is the K buffer (attention_k_eq_v): one tensor streams, and PV reads V^T from the
-// stage's K slot.
-template <int D, int QB, bool KH = false, bool SH = false>
+// stage's K slot.  S2 (with SH, in the LDS the second tensor leaves free): every wave computes
+// two stages per iteration, so the workgroup meets at one barrier per 64 keys.
+template <int D, int QB, bool KH = false, bool SH = false, bool S2 = false>
 __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p) {
+    static_assert(!S2 || !KH, "two stages per iteration: all waves on both");
     constexpr int NQW = KH ? kWaves / 2 : kWaves;  // waves with distinct query blocks
-    constexpr int NSL = KH ? 4 : 2;                // ring stages per tensor
-    constexpr int SPI = KH ? 2 : 1;                // stages per iteration (one per wave group)
+    constexpr int NSL = KH || S2 ? 4 : 2;          // ring stages per tensor
+    constexpr int SPI = KH || S2 ? 2 : 1;          // stages per iteration (KH: one per wave group)
     using R = PRing<D, NSL, SH ? 1 : 2>;
     constexpr int QT = 16 * QB * NQW;   // query rows per tile
     constexpr int KS = D / 32;          // QK k-steps
@@ -269,7 +271,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
 
     issue(kvb, 0, kslot(0));  // nst >= 1 here
     if (!SH) issue(vvb, 0, vslot(0));
-    if (KH && nst > 1) {
+    if ((KH || S2) && nst > 1) {
         issue(kvb, 1, kslot(1));
         if (!SH) issue(vvb, 1, vslot(1));
     }
@@ -283,12 +285,11 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
             issue(kvb, s0 + SPI, kslot(s0 + SPI));
             if (!SH) issue(vvb, s0 + SPI, vslot(s0 + SPI));
         }
-        if (KH && s0 + SPI + 1 < nst) {
+        if ((KH || S2) && s0 + SPI + 1 < nst) {
             issue(kvb, s0 + SPI + 1, kslot(s0 + SPI + 1));
             if (!SH) issue(vvb, s0 + SPI + 1, vslot(s0 + SPI + 1));
         }
-        const int s = s0 + kh;  // this wave group's stage
-        if (KH && s >= nst) continue;  // an odd stage count: the odd group's last iteration is empty
+        auto stage = [&](const int s) {
         const Scores cur = qk(kslot(s));
         const unsigned char *vb = vslot(s);
         const int jb = j0 + s * kStageKeys;
@@ -379,6 +380,15 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb)
                 acc[qb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qb], acc[qb][dt], 0, 0, 0);
+        }
+        };
+        if constexpr (S2) {
+            stage(s0);
+            if (s0 + 1 < nst) stage(s0 + 1);
+        } else {
+            const int s = s0 + kh;  // this wave group's stage
+            if (KH && s >= nst) continue;  // an odd stage count: the odd group's last iteration is empty
+            stage(s);
         }
     }
 
@@ -700,13 +710,13 @@ void launch_prefill(const PrefillParams &p, int stages, hipStream_t st) {
     if (stages & 1) {
         const dim3 grid(p.tiles * p.Hkv * p.splits), block(64 * kWaves);
         if constexpr (D == 512) {
-            if (p.k == p.v) hipLaunchKernelGGL((prefill_kernel<512, 1, false, true>), grid, block, 0, st, p);
+            if (p.k == p.v) hipLaunchKernelGGL((prefill_kernel<512, 1, false, true, true>), grid, block, 0, st, p);
             else hipLaunchKernelGGL((prefill_kernel<512, 1>), grid, block, 0, st, p);
         }
         else if constexpr (D == 128)
             hipLaunchKernelGGL((prefill_kernel<128, 2>), grid, block, 0, st, p);
         else if (p.qb == 2)
-            hipLaunchKernelGGL((prefill_kernel<256, 2>), grid, block, 0, st, p);
+            hipLaunchKernelGGL((prefill_kernel<256, 2, false, false, true>), grid, block, 0, st, p);
         else if (p.kh)
             hipLaunchKernelGGL((prefill_kernel<256, 1, true>), grid, block, 0, st, p);
         else

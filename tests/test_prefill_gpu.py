@@ -155,6 +155,14 @@ def test_local_chunk_benchmark_shape_stage_halves_all_rows():
                 window=1024, seed=14)
 
 
+def test_two_blocks_per_wave_two_stages_per_iteration_after_odd_past():
+    """Head dim 256 with two 16-query blocks per wave (the tiles fill the CUs), where each
+    iteration computes two stages: a causal chunk after an odd-length past, so the tiles'
+    key ranges start and end off the 32-key stage grid and their stage counts are odd and even."""
+    run_prefill("d256-qb2-odd-past", Hq=32, Hkv=16, D=256, Sq=2048, Sk=2048 + 317, q_pos0=317, k_pos0=0, seed=41,
+                rows=[0, 1, 63, 64, 127, 128, 255, 256, 700, 1023, 1024, 1500, 2000, 2046, 2047])
+
+
 def test_local_one_block_per_wave_without_stage_halves():
     """1024 queries at GQA 32/16: the 128-row tiles alone fill the 256 CUs and two-block
     tiles would not, so eight waves of one block each on distinct rows."""
