@@ -103,6 +103,9 @@ __host__ __device__ inline void tile_keys(const PrefillParams &p, int tile, int 
 // twice the tiles instead of key splits -- no fp32 partials and no merge launch -- while
 // each wave's work per stage and the barriers per stage stay those of the plain kernel.
 constexpr int kWaves = 8;
+#ifndef PV_DEPTH
+#define PV_DEPTH 4
+#endif
 
 template <int D, int NSL, int NT = 2>
 struct PRing {
@@ -369,17 +372,27 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
 
         // O^T += V^T . P^T: lane (li, lg) gets dim 16dt + li of keys 4lg .. 4lg+3 (first
         // half) and 16 + 4lg .. (second half): the k order of the P^T registers.
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+        // The V^T tiles are read PD ahead of their MFMAs (the scheduler alone kept one in flight).
+        auto vtile = [&](int dt) {
             const short4v a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) short4v *) (vb + tr_off + 32 * dt));
             const short4v a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) short4v *) (vb + R::HB + tr_off + 32 * dt));
             const short8v a8 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-            const bf16x8 a = __builtin_bit_cast(bf16x8, a8);
+            return __builtin_bit_cast(bf16x8, a8);
+        };
+        constexpr int PD = PV_DEPTH;
+        bf16x8 vf[PD];
+#pragma unroll
+        for (int i = 0; i < PD && i < DT; ++i) vf[i] = vtile(i);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const bf16x8 a = vf[dt % PD];
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb)
                 acc[qb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qb], acc[qb][dt], 0, 0, 0);
+            if (dt + PD < DT) vf[dt % PD] = vtile(dt + PD);
+            __builtin_amdgcn_sched_barrier(0);
         }
         };
         if constexpr (S2) {
