@@ -284,16 +284,27 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
         // the other waves') and every wave is done with the previous iteration
         ESDA_WAIT_VM(0);
         lds_barrier();
-        if (s0 + SPI < nst) {
-            issue(kvb, s0 + SPI, kslot(s0 + SPI));
-            if (!SH) issue(vvb, s0 + SPI, vslot(s0 + SPI));
-        }
-        if ((KH || S2) && s0 + SPI + 1 < nst) {
-            issue(kvb, s0 + SPI + 1, kslot(s0 + SPI + 1));
-            if (!SH) issue(vvb, s0 + SPI + 1, vslot(s0 + SPI + 1));
-        }
-        auto stage = [&](const int s) {
+        auto issue_first = [&]() {
+            if (s0 + SPI < nst) {
+                issue(kvb, s0 + SPI, kslot(s0 + SPI));
+                if (!SH) issue(vvb, s0 + SPI, vslot(s0 + SPI));
+            }
+        };
+        // The next iteration's stages: at once (plain, KH), or spread over this iteration (S2)
+        // so that the workgroup's DMAs do not all queue at the barrier: the second after this
+        // iteration's first stage, and (one K = V stream) the first after that stage's QK.
+        constexpr bool kFirstAfterQK = S2 && SH;
+        if (!kFirstAfterQK) issue_first();
+        auto issue_second = [&]() {
+            if (s0 + SPI + 1 < nst) {
+                issue(kvb, s0 + SPI + 1, kslot(s0 + SPI + 1));
+                if (!SH) issue(vvb, s0 + SPI + 1, vslot(s0 + SPI + 1));
+            }
+        };
+        if (KH) issue_second();
+        auto stage = [&](const int s, auto after_qk) {
         const Scores cur = qk(kslot(s));
+        after_qk();
         const unsigned char *vb = vslot(s);
         const int jb = j0 + s * kStageKeys;
 
@@ -396,12 +407,14 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
         }
         };
         if constexpr (S2) {
-            stage(s0);
-            if (s0 + 1 < nst) stage(s0 + 1);
+            if constexpr (kFirstAfterQK) stage(s0, issue_first);
+            else stage(s0, [] {});
+            issue_second();
+            if (s0 + 1 < nst) stage(s0 + 1, [] {});
         } else {
             const int s = s0 + kh;  // this wave group's stage
             if (KH && s >= nst) continue;  // an odd stage count: the odd group's last iteration is empty
-            stage(s);
+            stage(s, [] {});
         }
     }
 
