@@ -284,24 +284,33 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
         // the other waves') and every wave is done with the previous iteration
         ESDA_WAIT_VM(0);
         lds_barrier();
-        auto issue_first = [&]() {
-            if (s0 + SPI < nst) {
-                issue(kvb, s0 + SPI, kslot(s0 + SPI));
-                if (!SH) issue(vvb, s0 + SPI, vslot(s0 + SPI));
-            }
+        // The next iteration's DMAs, spread over this iteration so that the workgroup's loads
+        // do not all queue at the barrier (each slot is free once the barrier has passed):
+        //  - separate K and V (plain, S2): K of the next stage at the barrier, its V after
+        //    this iteration's first QK;
+        //  - one K = V stream (S2): the next stage after the first QK;
+        //  - S2: the stage after that once this iteration's first stage is done;
+        //  - KH: all at the barrier (spreading measured slower there).
+        constexpr bool kVLate = !SH && !KH;
+        auto issue_k = [&]() {
+            if (s0 + SPI < nst) issue(kvb, s0 + SPI, kslot(s0 + SPI));
         };
-        // The next iteration's stages: at once (plain, KH), or spread over this iteration (S2)
-        // so that the workgroup's DMAs do not all queue at the barrier: the second after this
-        // iteration's first stage, and (one K = V stream) the first after that stage's QK.
-        constexpr bool kFirstAfterQK = S2 && SH;
-        if (!kFirstAfterQK) issue_first();
+        auto issue_v = [&]() {
+            if (!SH && s0 + SPI < nst) issue(vvb, s0 + SPI, vslot(s0 + SPI));
+        };
         auto issue_second = [&]() {
             if (s0 + SPI + 1 < nst) {
                 issue(kvb, s0 + SPI + 1, kslot(s0 + SPI + 1));
                 if (!SH) issue(vvb, s0 + SPI + 1, vslot(s0 + SPI + 1));
             }
         };
-        if (KH) issue_second();
+        auto after_first_qk = [&]() {
+            if constexpr (SH) issue_k();
+            if constexpr (kVLate) issue_v();
+        };
+        if constexpr (!SH) issue_k();
+        if constexpr (!kVLate && !SH) issue_v();
+        if constexpr (KH) issue_second();
         auto stage = [&](const int s, auto after_qk) {
         const Scores cur = qk(kslot(s));
         after_qk();
@@ -407,14 +416,13 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
         }
         };
         if constexpr (S2) {
-            if constexpr (kFirstAfterQK) stage(s0, issue_first);
-            else stage(s0, [] {});
+            stage(s0, after_first_qk);
             issue_second();
             if (s0 + 1 < nst) stage(s0 + 1, [] {});
         } else {
             const int s = s0 + kh;  // this wave group's stage
             if (KH && s >= nst) continue;  // an odd stage count: the odd group's last iteration is empty
-            stage(s, [] {});
+            stage(s, after_first_qk);
         }
     }
 
