@@ -36,7 +36,8 @@ extern "C" {
  * k/v: element (kvh, j, d) at k[kvh*kv_head_stride + j*head_dim + d], key j < seq_k at
  *      absolute position k_pos0 + j (a cache view: rows dense, head stride free; with
  *      sliding eviction k_pos0 = pastLen + seq_q - seq_k, as alignMask keeps the last
- *      seq_k columns).  k == v is allowed.
+ *      seq_k columns).  k == v is allowed (attention_k_eq_v): at head_dim 512 the call
+ *      then streams the one buffer once and reads V from it.
  * out: element (i, h, d) at out[i*out_row_stride + h*out_head_stride + d] (bf16); the
  *      reference's [seq, numQ * headDim] is out_row_stride = numQ*headDim,
  *      out_head_stride = headDim.
