@@ -1233,6 +1233,27 @@ void raw_attend_kernel(AttendParams p) {
                 }
             }
         };
+        // raw: chunk c (of 4) of stage st's row DMAs, rows 4c .. 4c + 3.  The next stage's rows
+        // go out in four chunks over the iteration (at the top, after the Gram pass, beside the
+        // table rows, after the scores) rather than sixteen DMAs at once, which stalled their
+        // issue behind the other waves' loads (c4raw attend 91.3 -> 90.8 us).
+        auto dma_rows_part = [&](int st, unsigned char *sl, auto cc) {
+            constexpr int c = decltype(cc)::value;
+            const int jst = j0 + 16 * st;
+            const unsigned lb = lds_addr(sl);
+            if (jst + 16 < j1) {
+                const unsigned char *r0 = reinterpret_cast<const unsigned char *>(kbase + (size_t) (sv.first + jst) * kRawDim);
+                const uint64_t base[4] = {sbase64(r0), sbase64(r0 + 4096), sbase64(r0 + 8192), sbase64(r0 + 12288)};
+                ring_blocks<4 * c, 4 * c + 4>(base, (unsigned) (lane * 16), lb);
+            } else {
+#pragma unroll
+                for (int r = 4 * c; r < 4 * c + 4; ++r) {
+                    const int j = min(jst + r, j1 - 1);
+                    const uint16_t *src = (append && j == sv.nvis - 1) ? knew : kbase + (size_t) (sv.first + j) * kRawDim;
+                    lds_dma16(src + lane * 8, lb + r * kBlk);
+                }
+            }
+        };
         // DMA of stage st's 16 table rows into the wave's table buffer: block bt holds positions
         // 4bt .. 4bt + 3, piece c of position rib at 16 * (16 rib + (c + 4 rib) mod 16).  Loaded
         // temporal (the rows non-temporal): the workgroups of the other kv heads at the same
@@ -1278,9 +1299,12 @@ void raw_attend_kernel(AttendParams p) {
         for (int st = st0, it = 0; st < nst; st += kWaves, ++it) {
             unsigned char *const sl = wl + (it & 1) * W::SLOT;
             ESDA_WAIT_VM(0);  // this stage's rows and table rows landed
-            if (st + kWaves < nst) {
+            unsigned char *const nsl = wl + ((it + 1) & 1) * W::SLOT;
+            const bool more = st + kWaves < nst;
+            if (more) {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the other slot's reads are done
-                dma_rows(st + kWaves, wl + ((it + 1) & 1) * W::SLOT);
+                if constexpr (Q8) dma_rows(st + kWaves, nsl);
+                else dma_rows_part(st + kWaves, nsl, std::integral_constant<int, 0>{});
             }
             // Scores S^T[16 rows x 16 heads] of K = bf16(rope(x * rinv * kw)) (q8: x = q * scale
             // + bias), rounded where ESDecodeAttn.mm:51-93 rounds it.
@@ -1385,6 +1409,9 @@ void raw_attend_kernel(AttendParams p) {
 #pragma unroll
                 for (int kk = 0; kk < 16; ++kk) asm volatile("" : "+v"(w8[kk]));
             }
+            if constexpr (!Q8) {
+                if (more) dma_rows_part(st + kWaves, nsl, std::integral_constant<int, 1>{});
+            }
             // Other lanes read the factors back: a compiler memory barrier keeps those loads
             // after the stores above (the lanes' LDS accesses then run in order).
             asm volatile("" ::: "memory");
@@ -1436,6 +1463,7 @@ void raw_attend_kernel(AttendParams p) {
             if (st + kWaves < nst) {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                 dma_tab(st + kWaves);
+                if constexpr (!Q8) dma_rows_part(st + kWaves, nsl, std::integral_constant<int, 2>{});
             }
 #pragma unroll
             for (int kk = 2; kk < 16; ++kk) {
@@ -1446,6 +1474,9 @@ void raw_attend_kernel(AttendParams p) {
                 else sp0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack(v), qv[kk], sp0, 0, 0, 0);
             }
             f32x4 sc = sp0 + sp1;
+            if constexpr (!Q8) {
+                if (more) dma_rows_part(st + kWaves, nsl, std::integral_constant<int, 3>{});
+            }
             // Online softmax (log2 domain) over stage rows 4lg .. 4lg + 3: rows past the
             // segment end are masked.
             const int jt = j0 + 16 * st + 4 * lg;
