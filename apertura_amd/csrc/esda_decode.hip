@@ -846,8 +846,11 @@ void attend_kernel(AttendParams p) {
         const int st = s0 + u;
         if (st >= nst) return;
         if (st + AHEAD < nst) {
-            // own DMA for stage st+AHEAD done; the stages behind it may stay in flight
-            if (nst - st - AHEAD - 1 >= NS - 2 - AHEAD) {
+            // own DMA for stage st+AHEAD done; the stages behind it may stay in flight --
+            // except at D = 256, whose two workgroups per CU then keep twice the 512-dim
+            // kernel's bytes in flight (16.8 MB over the GPU, past the 6-15 MB at which the
+            // read probe peaks): waiting for every issued stage there took C5 7.50 -> 7.44 ms
+            if (D != 256 && nst - st - AHEAD - 1 >= NS - 2 - AHEAD) {
                 ESDA_WAIT_VM((NS - 2 - AHEAD) * DPW);
             } else {
                 ESDA_WAIT_VM(0);
