@@ -106,6 +106,7 @@ constexpr int kWaves = 8;
 #ifndef PV_DEPTH
 #define PV_DEPTH 4
 #endif
+constexpr int kPairSpin = 1 << 20;  // PS: polls of the partner's flag before a wave gives up
 
 template <int D, int NSL, int NT = 2>
 struct PRing {
@@ -120,9 +121,21 @@ struct PRing {
 // SH: V is the K buffer (attention_k_eq_v): one tensor streams, and PV reads V^T from the
 // stage's K slot.  S2 (with SH, in the LDS the second tensor leaves free): every wave computes
 // two stages per iteration, so the workgroup meets at one barrier per 64 keys.
-template <int D, int QB, bool KH = false, bool SH = false, bool S2 = false>
+//
+// PS (pair split, one block per wave): waves w and w^1 (on different SIMDs) each score and
+// softmax their own query block over the whole head dim, as above, but accumulate O^T for
+// both blocks of the pair over half of the head dim each (wave w: dims D/2 (w & 1) on).
+// Each V^T tile read from LDS then feeds two MFMAs, which halves the kernel's transpose
+// reads for an exchange of P^T (1 KB per wave and stage) through LDS: the wave writes its
+// P^T (and, after a rescale, its factors), then a flag, and reads its partner's once the
+// partner's flag shows the stage.  The buffers alternate by stage parity: a wave rewrites a
+// parity only after reading its partner's next flag, which the partner writes after reading
+// this stage's P^T.  Used by the K = V kernel at D = 512 (p512gs 436 -> 422 us on one box);
+// with separate K and V -- one stage per barrier -- it measured 1-3% slower and is not used.
+template <int D, int QB, bool KH = false, bool SH = false, bool S2 = false, bool PS = false>
 __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p) {
     static_assert(!S2 || !KH, "two stages per iteration: all waves on both");
+    static_assert(!PS || (QB == 1 && !KH), "pair split: one block per wave, every wave on every stage");
     constexpr int NQW = KH ? kWaves / 2 : kWaves;  // waves with distinct query blocks
     constexpr int NSL = KH || S2 ? 4 : 2;          // ring stages per tensor
     constexpr int SPI = KH || S2 ? 2 : 1;          // stages per iteration (KH: one per wave group)
@@ -130,13 +143,21 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
     constexpr int QT = 16 * QB * NQW;   // query rows per tile
     constexpr int KS = D / 32;          // QK k-steps
     constexpr int DT = D / 16;          // PV dim tiles
+    constexpr int NB = PS ? 2 : QB;     // O^T blocks per wave
+    constexpr int DW = PS ? DT / 2 : DT;  // O^T dim tiles per wave
     __shared__ __attribute__((aligned(16))) unsigned char ring[R::BYTES];
+    // PS exchange, per stage parity: each wave's P^T (16 B per lane) and rescale factors
+    // (4 B per lane), then one flag per wave; after both parities, each wave's row sums.
+    constexpr int XP = 64 * 16 + 64 * 4;
+    constexpr int XPAR = kWaves * XP + kWaves * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char xch[PS ? 2 * XPAR + kWaves * 16 * 4 : 16];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int li = lane & 15, lg = lane >> 4;
     // Query-block wave and stage parity (both constant for the plain kernel, whose code
     // does not change: a wave-dependent parity there measured 3% slower).
     const int wq = KH ? wave % NQW : wave, kh = KH ? wave / NQW : 0;
+    const int hd = PS ? (wave & 1) : 0;  // PS: this wave's half of the head dim
     // Workgroup -> (tile, kv head, split): consecutive workgroups go to consecutive XCDs
     // (dispatch is round-robin over the 8), so the (kv head, split) pair is the fastest
     // index and the workgroups on one XCD share one K / V stream in its L2; tiles run
@@ -237,13 +258,23 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
     const int tr_off = R::off(4 * lg + li / 4) + (li % 4) * 8;  // + 32 dt (+ HB)
 
     float m[QB], l[QB];
-    f32x4 acc[QB][DT];
+    f32x4 acc[NB][DW];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         m[qb] = -INFINITY;
         l[qb] = 0.0f;
+    }
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[qb][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int dt = 0; dt < DW; ++dt) acc[nb][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // PS flags start at 0 (stage s shows as 2 (s + 1), plus 1 after a rescale); the loop's
+    // first barrier orders these stores before any wave reads them.
+    // (Flags are read and written through LDS pointers: a generic volatile access would be
+    // a flat one, whose wait also drains the ring's DMAs.)
+    using lds_flag = __attribute__((address_space(3))) volatile unsigned;
+    if constexpr (PS) {
+        if (lane < 2) *(lds_flag *) (xch + lane * XPAR + kWaves * XP + wave * 4) = 0u;
     }
     // Positions of the tile's first and last rows (the host keeps positions below 2^31).
     const int qa_min = p.q_pos0 + (int) ((long long) tile * QT / p.G);
@@ -363,16 +394,20 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
 
         // Raise the running max where a score exceeds it by the slack (rare): one
         // wave-uniform branch; lanes that do not need it scale by 1.
+        unsigned char *const xs = xch + (PS ? (s & 1) * XPAR : 0);  // PS: this stage's exchange
+        bool resc = false;
         if (__builtin_expect(__builtin_amdgcn_ballot_w64(need) != 0, 0)) {
             asm volatile("" ::: "memory");  // keeps the rare rescale a branch (no if-conversion)
+            resc = true;
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
                 const bool up = mt[qb] > m[qb] + kRescaleSlack;
                 const float corr = up ? __builtin_amdgcn_exp2f(m[qb] - mt[qb]) : 1.0f;  // 0 while m is -inf
                 l[qb] *= corr;
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt) acc[qb][dt] *= corr;
+                for (int dt = 0; dt < DW; ++dt) acc[qb][dt] *= corr;
                 m[qb] = up ? mt[qb] : m[qb];
+                if constexpr (PS) *reinterpret_cast<float *>(xs + wave * XP + 1024 + lane * 4) = corr;
             }
         }
 
@@ -389,29 +424,58 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
             for (int e = 0; e < 8; e += 2) l[qb] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pv[e], pv[e + 1]}, one2, l[qb], false);
             pb[qb] = pv;
         }
+        if constexpr (PS) {  // P^T (and factors) to the partner, then the flag
+            *reinterpret_cast<bf16x8 *>(xs + wave * XP + lane * 16) = pb[0];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0)
+                *(lds_flag *) (xs + kWaves * XP + wave * 4) = 2u * (unsigned) (s + 1) + (resc ? 1u : 0u);
+        }
 
         // O^T += V^T . P^T: lane (li, lg) gets dim 16dt + li of keys 4lg .. 4lg+3 (first
         // half) and 16 + 4lg .. (second half): the k order of the P^T registers.
         // The V^T tiles are read PD ahead of their MFMAs (the scheduler alone kept one in flight).
+        const unsigned char *const vbh = vb + 32 * DW * hd;  // PS: this wave's dims
         auto vtile = [&](int dt) {
             const short4v a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) short4v *) (vb + tr_off + 32 * dt));
+                (__attribute__((address_space(3))) short4v *) (vbh + tr_off + 32 * dt));
             const short4v a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) short4v *) (vb + R::HB + tr_off + 32 * dt));
+                (__attribute__((address_space(3))) short4v *) (vbh + R::HB + tr_off + 32 * dt));
             const short8v a8 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
             return __builtin_bit_cast(bf16x8, a8);
         };
         constexpr int PD = PV_DEPTH;
         bf16x8 vf[PD];
 #pragma unroll
-        for (int i = 0; i < PD && i < DT; ++i) vf[i] = vtile(i);
+        for (int i = 0; i < PD && i < DW; ++i) vf[i] = vtile(i);
+        bf16x8 pq[NB];  // B operands: the wave's blocks (PS: its own, then its partner's)
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+        for (int qb = 0; qb < QB; ++qb) pq[qb] = pb[qb];
+        if constexpr (PS) {
+            // The partner's flag for this stage (bounded: a wave that gave up would compute
+            // garbage, not hang), then its P^T and, after its rescale, its factors.
+            const unsigned want = 2u * (unsigned) (s + 1);
+            lds_flag *fl = (lds_flag *) (xs + kWaves * XP + (wave ^ 1) * 4);
+            unsigned f = __builtin_amdgcn_readfirstlane(*fl);
+            for (int it = 0; (f & ~1u) != want && it < kPairSpin; ++it) {
+                __builtin_amdgcn_s_sleep(1);
+                f = __builtin_amdgcn_readfirstlane(*fl);
+            }
+            asm volatile("" ::: "memory");
+            const unsigned char *const xp = xs + (wave ^ 1) * XP;
+            pq[1] = *reinterpret_cast<const bf16x8 *>(xp + lane * 16);
+            if (f & 1u) {
+                const float pc = *reinterpret_cast<const float *>(xp + 1024 + lane * 4);
+#pragma unroll
+                for (int dt = 0; dt < DW; ++dt) acc[1][dt] *= pc;
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < DW; ++dt) {
             const bf16x8 a = vf[dt % PD];
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb)
-                acc[qb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qb], acc[qb][dt], 0, 0, 0);
-            if (dt + PD < DT) vf[dt % PD] = vtile(dt + PD);
+            for (int nb = 0; nb < NB; ++nb)
+                acc[nb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pq[nb], acc[nb][dt], 0, 0, 0);
+            if (dt + PD < DW) vf[dt % PD] = vtile(dt + PD);
             __builtin_amdgcn_sched_barrier(0);
         }
         };
@@ -463,29 +527,44 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillParams p
     }
 
     // Row totals over the four lane groups; then the output (one split) or the partial.
+    float lb[NB];  // row sums of the wave's O^T blocks
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         l[qb] += __shfl_xor(l[qb], 16);
         l[qb] += __shfl_xor(l[qb], 32);
-        if (!qvalid(qb)) continue;
-        const long long gr = qrow(qb);
+        lb[qb] = l[qb];
+    }
+    if constexpr (PS) {  // the partner's row sums, through LDS past every wave's last stage
+        float *xl = reinterpret_cast<float *>(xch + 2 * XPAR);
+        if (lg == 0) xl[wave * 16 + li] = l[0];
+        lds_barrier();
+        lb[1] = xl[(wave ^ 1) * 16 + li];
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        // the block's first tile row (PS: the wave's own block, then its partner's)
+        const int br = PS ? (nb == 0 ? wave : wave ^ 1) * 16 : wq * 16 * QB + nb * 16;
+        const long long gr0 = (long long) tile * QT + br + li;
+        if (gr0 >= nq) continue;
+        const long long gr = gr0;
         const int qi = (int) (gr / p.G), qh = kvh * p.G + (int) (gr % p.G);
         const long long row = (long long) qi * p.Hq + qh;
+        const int d0 = 16 * DW * hd;  // the wave's first O^T dim
         if (p.splits == 1) {
-            const float inv = 1.0f / l[qb];
-            uint16_t *o = p.out + (size_t) qi * p.o_rs + (size_t) qh * p.o_hs + 4 * lg;
+            const float inv = 1.0f / lb[nb];
+            uint16_t *o = p.out + (size_t) qi * p.o_rs + (size_t) qh * p.o_hs + d0 + 4 * lg;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const f32x4 v4 = acc[qb][dt] * inv;
+            for (int dt = 0; dt < DW; ++dt) {
+                const f32x4 v4 = acc[nb][dt] * inv;
                 bf16x4 b4 = {(__bf16) v4[0], (__bf16) v4[1], (__bf16) v4[2], (__bf16) v4[3]};
                 *reinterpret_cast<bf16x4 *>(o + 16 * dt) = b4;
             }
         } else {
-            float *pa = p.part_acc + ((long long) split * nrows + row) * D + 4 * lg;
+            float *pa = p.part_acc + ((long long) split * nrows + row) * D + d0 + 4 * lg;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4 *>(pa + 16 * dt) = acc[qb][dt];
-            if (lg == 0)
-                *reinterpret_cast<f32x2 *>(p.part_ml + 2 * ((long long) split * nrows + row)) = f32x2{m[qb], l[qb]};
+            for (int dt = 0; dt < DW; ++dt) *reinterpret_cast<f32x4 *>(pa + 16 * dt) = acc[nb][dt];
+            if (lg == 0 && nb < QB)  // (m, l) from the block's owner
+                *reinterpret_cast<f32x2 *>(p.part_ml + 2 * ((long long) split * nrows + row)) = f32x2{m[nb < QB ? nb : 0], l[nb < QB ? nb : 0]};
         }
     }
 }
@@ -744,7 +823,7 @@ void launch_prefill(const PrefillParams &p, int stages, hipStream_t st) {
     if (stages & 1) {
         const dim3 grid(p.tiles * p.Hkv * p.splits), block(64 * kWaves);
         if constexpr (D == 512) {
-            if (p.k == p.v) hipLaunchKernelGGL((prefill_kernel<512, 1, false, true, true>), grid, block, 0, st, p);
+            if (p.k == p.v) hipLaunchKernelGGL((prefill_kernel<512, 1, false, true, true, true>), grid, block, 0, st, p);
             else hipLaunchKernelGGL((prefill_kernel<512, 1>), grid, block, 0, st, p);
         }
         else if constexpr (D == 128)

@@ -66,13 +66,15 @@ def _decode_every_row(qd, kd, vd, out, q_pos0, scale):
 
 
 def run_prefill(name, *, Hq, Hkv, D, Sq, Sk, q_pos0, k_pos0, window=0, split_keys=0, seed=0,
-                layout="dense", shared=False, rows=None, fault=0, decode_rows=False):
+                layout="dense", shared=False, rows=None, fault=0, decode_rows=False, peaks=()):
     from apertura_amd.prefill import PrefillStep, prefill
     print(f"\n[prefill] {name}: Hq={Hq} Hkv={Hkv} D={D} Sq={Sq} Sk={Sk} q_pos0={q_pos0} k_pos0={k_pos0} "
           f"window={window} split_keys={split_keys} layout={layout} shared={shared}", flush=True)
     rng = np.random.default_rng(seed)
     q = rms_rows(rng, (Hq, Sq, D))
     k = rms_rows(rng, (Hkv, Sk, D))
+    for h, i, j in peaks:  # key j := query (h, i): a score of |q|^2 / sqrt(D) = sqrt(D) for that row
+        k[h // (Hq // Hkv), j] = q[h, i]
     v = k if shared else rms_rows(rng, (Hkv, Sk, D))
     scale = D ** -0.5
     if layout == "dense":
@@ -201,6 +203,22 @@ def test_shared_k_equals_v_with_key_splits(split_keys):
     cached past, with automatic, forced and empty key splits."""
     run_prefill(f"shared-splits{split_keys}", Hq=32, Hkv=4, D=512, Sq=70, Sk=700, q_pos0=630, k_pos0=0,
                 seed=31 + split_keys, shared=True, split_keys=split_keys)
+
+
+# (query head, query row, key) triples: rows 0, 2, 5 and 7 of a GQA-8 group fall in tile
+# blocks 0, 1, 2 and 3 -- both waves of the two first pairs -- and each key sits in a stage
+# after the row's first, so the row's running max rises by ~30 in log2 units mid-stream.
+PEAKS = [(3, 0, 70), (9, 2, 200), (17, 5, 333), (30, 7, 446), (0, 40, 120), (12, 63, 500)]
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_mid_stream_rescale_reaches_both_dim_halves(shared):
+    """Keys equal to a query row (score sqrt(512) ~ 22.6) in a later stage than the row's
+    first force the online softmax to rescale mid-stream.  In the K = V kernel the row's
+    P^T and rescale factors go to the partner wave, which holds the other half of the row's
+    O^T: a factor that did not reach it would leave that half unscaled, by O(1)."""
+    run_prefill(f"peaks-shared{int(shared)}", Hq=32, Hkv=4, D=512, Sq=64, Sk=512, q_pos0=448, k_pos0=0,
+                seed=41, shared=shared, peaks=PEAKS)
 
 
 def test_single_query_and_single_key():
